@@ -1,0 +1,289 @@
+// C ABI of libesa.so: argument checks on the host, then kernel launches.
+// Declarations and contracts: include/esa.h.
+#include <algorithm>
+#include <cmath>
+#include <numeric>
+#include <vector>
+
+#include "../../include/esa.h"
+#include "esa_internal.hpp"
+
+using namespace esa;
+
+namespace {
+
+constexpr int64_t kMaxSeqLen = int64_t(1) << 26;  // int32 work items and LDS bitmap bounds
+constexpr int kMaxW = 1 << 16;
+
+// The two scalars the reference's layout formula casts to float32
+// (elastic_sparse_attention.py:488-496): alpha = layer_idx / max(nl - 1, 1)
+// and w * (1 - alpha), both formed in double as Python does.
+PatternConsts make_consts(const esa_pattern& p) {
+  PatternConsts pc;
+  const double denom = p.num_hidden_layers > 1 ? (double)(p.num_hidden_layers - 1) : 1.0;
+  volatile double alpha = (double)p.layer_idx / denom;
+  volatile double one_minus = 1.0 - alpha;
+  volatile double cw = (double)p.attention_length * one_minus;
+  pc.a = (float)alpha;
+  pc.c = (float)cw;
+  pc.w = p.attention_length;
+  pc.H = p.num_heads;
+  return pc;
+}
+
+esa_status check_pattern(const esa_pattern* p) {
+  if (!p) return ESA_ERR_NULL;
+  if (p->seq_len < 1 || p->seq_len > kMaxSeqLen) return ESA_ERR_SHAPE;
+  if (p->attention_length < 1 || p->attention_length > kMaxW) return ESA_ERR_SHAPE;
+  if (p->num_hidden_layers < 1 || p->num_heads < 1) return ESA_ERR_SHAPE;
+  if (p->block_m < 1 || p->block_n < 1 || p->block_m > 4096 || p->block_n > 4096)
+    return ESA_ERR_SHAPE;
+  return ESA_OK;
+}
+
+LayoutDims dims_of(const esa_pattern& p) {
+  LayoutDims d;
+  d.seq_len = p.seq_len;
+  d.bm = p.block_m;
+  d.bn = p.block_n;
+  d.nqb = (p.seq_len + p.block_m - 1) / p.block_m;
+  d.nkb = (p.seq_len + p.block_n - 1) / p.block_n;
+  d.nwords = (d.nkb + 31) / 32;
+  return d;
+}
+
+// Upper bound on active tiles: block qb can only reach keys <= its last row
+// (valid indices are causal), and holds at most rows * w entries.
+int64_t max_tiles_of(const esa_pattern& p, const LayoutDims& d) {
+  int64_t per_head = 0;
+  for (int qb = 0; qb < d.nqb; ++qb) {
+    const int64_t last = std::min<int64_t>(p.seq_len, (int64_t)(qb + 1) * p.block_m) - 1;
+    const int64_t rows = last - (int64_t)qb * p.block_m + 1;
+    per_head += std::min<int64_t>(last / p.block_n + 1, rows * p.attention_length);
+  }
+  return per_head * p.num_heads;
+}
+
+size_t workspace_of(const esa_pattern& p, const LayoutDims& d) {
+  const int64_t rows = (int64_t)p.num_heads * d.nqb;
+  return (size_t)(rows * d.nwords * 4 + rows * 4 + 256);
+}
+
+bool aligned(const void* ptr, size_t a) { return ((uintptr_t)ptr % a) == 0; }
+
+esa_status check_fwd_common(const esa_fwd_args* a) {
+  if (!a || !a->q || !a->k || !a->v || !a->o) return ESA_ERR_NULL;
+  if (a->dtype != ESA_F32 && a->dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (a->batch < 0 || a->num_heads < 1 || a->num_kv_heads < 1 || a->q_len < 0 || a->kv_len < 1 ||
+      a->head_dim < 1)
+    return ESA_ERR_SHAPE;
+  if (a->num_heads % a->num_kv_heads != 0) return ESA_ERR_SHAPE;
+  if (a->kv_len > kMaxSeqLen || a->q_len > kMaxSeqLen) return ESA_ERR_SHAPE;
+  return ESA_OK;
+}
+
+GatherArgs gather_args_of(const esa_fwd_args* a) {
+  GatherArgs g{};
+  g.q = a->q; g.k = a->k; g.v = a->v; g.o = a->o; g.lse = a->lse;
+  g.qsb = a->q_stride_b; g.qsh = a->q_stride_h; g.qss = a->q_stride_s;
+  g.ksb = a->k_stride_b; g.ksh = a->k_stride_h; g.kss = a->k_stride_s;
+  g.vsb = a->v_stride_b; g.vsh = a->v_stride_h; g.vss = a->v_stride_s;
+  g.osb = a->o_stride_b; g.osh = a->o_stride_h; g.oss = a->o_stride_s;
+  g.lsb = a->lse_stride_b; g.lsh = a->lse_stride_h;
+  g.B = a->batch; g.H = a->num_heads; g.groups = a->num_heads / a->num_kv_heads;
+  g.q_len = a->q_len; g.kv_len = a->kv_len; g.D = a->head_dim;
+  g.sm_scale = a->sm_scale;
+  return g;
+}
+
+esa_status check_gather_layout(const esa_fwd_args* a) {
+  if (a->head_dim % 4 != 0 || a->head_dim > 256) return ESA_ERR_UNSUPPORTED;
+  const size_t es = a->dtype == ESA_F32 ? 4 : 2;
+  // K rows are read 4 elements at a time.
+  if (!aligned(a->k, 4 * es) || a->k_stride_s % 4 != 0 || a->k_stride_h % 4 != 0 ||
+      a->k_stride_b % 4 != 0)
+    return ESA_ERR_ALIGN;
+  return ESA_OK;
+}
+
+esa_status hip_status(hipError_t e) { return e == hipSuccess ? ESA_OK : ESA_ERR_HIP; }
+
+}  // namespace
+
+extern "C" {
+
+const char* esa_status_string(esa_status s) {
+  switch (s) {
+    case ESA_OK: return "ok";
+    case ESA_ERR_NULL: return "null pointer";
+    case ESA_ERR_SHAPE: return "invalid or inconsistent shape";
+    case ESA_ERR_DTYPE: return "unsupported dtype";
+    case ESA_ERR_ALIGN: return "misaligned pointer or stride";
+    case ESA_ERR_UNSUPPORTED: return "unsupported configuration";
+    case ESA_ERR_CAPACITY: return "buffer too small";
+    case ESA_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+const char* esa_version(void) { return "esa-gfx950 0.1.0"; }
+
+esa_status esa_layout_sizes(const esa_pattern* p, int32_t* num_qblocks, int32_t* num_kblocks,
+                            int64_t* max_tiles, size_t* workspace_bytes) {
+  esa_status s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  const LayoutDims d = dims_of(*p);
+  if ((int64_t)d.nwords * 4 > 65536) return ESA_ERR_SHAPE;  // LDS bitmap bound
+  if (num_qblocks) *num_qblocks = d.nqb;
+  if (num_kblocks) *num_kblocks = d.nkb;
+  if (max_tiles) *max_tiles = max_tiles_of(*p, d);
+  if (workspace_bytes) *workspace_bytes = workspace_of(*p, d);
+  return ESA_OK;
+}
+
+esa_status esa_build_indices(const esa_pattern* p, int32_t row0, int32_t nrows, void* indices,
+                             void* mask, int32_t elem_bytes, void* stream) {
+  esa_status s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  if (elem_bytes != 4 && elem_bytes != 8) return ESA_ERR_DTYPE;
+  if (row0 < 0 || nrows < 0 || (int64_t)row0 + nrows > p->seq_len) return ESA_ERR_SHAPE;
+  if (!indices && !mask) return ESA_OK;
+  if (nrows == 0) return ESA_OK;
+  if ((int64_t)nrows * p->attention_length > (int64_t(1) << 40)) return ESA_ERR_SHAPE;
+  return hip_status(launch_indices(make_consts(*p), row0, nrows, indices, mask, elem_bytes,
+                                   (hipStream_t)stream));
+}
+
+esa_status esa_build_layout(const esa_pattern* p, int32_t* row_ptr, int32_t* col_idx,
+                            int64_t col_capacity, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  esa_status s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  if (!row_ptr || !col_idx || !workspace) return ESA_ERR_NULL;
+  const LayoutDims d = dims_of(*p);
+  if ((int64_t)d.nwords * 4 > 65536) return ESA_ERR_SHAPE;
+  if (col_capacity < max_tiles_of(*p, d)) return ESA_ERR_CAPACITY;
+  if (workspace_bytes < workspace_of(*p, d)) return ESA_ERR_CAPACITY;
+  if (!aligned(workspace, 4)) return ESA_ERR_ALIGN;
+  return hip_status(
+      launch_layout(make_consts(*p), d, row_ptr, col_idx, workspace, (hipStream_t)stream));
+}
+
+esa_status esa_plan_schedule(const esa_pattern* p, const int32_t* row_ptr_host, int32_t q_len,
+                             int32_t batch, int32_t* items_host, int64_t items_capacity,
+                             int64_t* num_items) {
+  esa_status s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  if (!row_ptr_host || !items_host || !num_items) return ESA_ERR_NULL;
+  if (q_len < 0 || q_len > p->seq_len || batch < 0) return ESA_ERR_SHAPE;
+  const LayoutDims d = dims_of(*p);
+  const int nq = (q_len + p->block_m - 1) / p->block_m;
+  const int64_t n = (int64_t)batch * p->num_heads * nq;
+  if ((int64_t)batch * p->num_heads * d.nqb > INT32_MAX) return ESA_ERR_SHAPE;
+  if (items_capacity < n) return ESA_ERR_CAPACITY;
+  // (cost, head-major position) pairs over (h, qb); the batch index repeats
+  // each pair, so sort once and expand.
+  std::vector<int64_t> order((size_t)p->num_heads * nq);
+  std::iota(order.begin(), order.end(), 0);
+  auto cost = [&](int64_t hq) {
+    const int64_t h = hq / nq, qb = hq % nq;
+    const int64_t row = h * d.nqb + qb;
+    return row_ptr_host[row + 1] - row_ptr_host[row];
+  };
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int64_t x, int64_t y) { return cost(x) > cost(y); });
+  int64_t k = 0;
+  for (int64_t hq : order) {
+    const int64_t h = hq / nq, qb = hq % nq;
+    for (int b = 0; b < batch; ++b)
+      items_host[k++] = (int32_t)(((int64_t)b * p->num_heads + h) * d.nqb + qb);
+  }
+  *num_items = n;
+  return ESA_OK;
+}
+
+esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const int32_t* row_ptr,
+                           const int32_t* col_idx, const int32_t* items, int64_t num_items,
+                           void* stream) {
+  esa_status s = check_fwd_common(a);
+  if (s != ESA_OK) return s;
+  s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  if (!row_ptr || !col_idx || !items) return ESA_ERR_NULL;
+  if (a->dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (a->head_dim != 64 && a->head_dim != 128) return ESA_ERR_UNSUPPORTED;
+  if (p->block_m != 128 || p->block_n != 128) return ESA_ERR_UNSUPPORTED;
+  // The per-tile key masks assume strictly rising indices, which holds for
+  // 0 <= alpha <= 1.
+  if (p->layer_idx < 0 || p->layer_idx > std::max(p->num_hidden_layers - 1, 0))
+    return ESA_ERR_UNSUPPORTED;
+  if (p->num_heads != a->num_heads) return ESA_ERR_SHAPE;
+  if (a->q_len > a->kv_len || a->q_len > p->seq_len) return ESA_ERR_SHAPE;
+  const LayoutDims d = dims_of(*p);
+  const int nq = (a->q_len + 127) / 128;
+  if (num_items != (int64_t)a->batch * a->num_heads * nq) return ESA_ERR_SHAPE;
+  // 16-byte row loads and 8-byte output stores.
+  if (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16) || !aligned(a->o, 8))
+    return ESA_ERR_ALIGN;
+  const int64_t st[] = {a->q_stride_b, a->q_stride_h, a->q_stride_s, a->k_stride_b,
+                        a->k_stride_h, a->k_stride_s, a->v_stride_b, a->v_stride_h,
+                        a->v_stride_s};
+  for (int64_t x : st)
+    if (x % 8 != 0) return ESA_ERR_ALIGN;
+  if (a->o_stride_b % 4 || a->o_stride_h % 4 || a->o_stride_s % 4) return ESA_ERR_ALIGN;
+  if (num_items == 0 || a->batch == 0 || a->q_len == 0) return ESA_OK;
+
+  TileArgs t{};
+  t.q = (const uint16_t*)a->q; t.k = (const uint16_t*)a->k; t.v = (const uint16_t*)a->v;
+  t.o = (uint16_t*)a->o; t.lse = a->lse;
+  t.qsb = a->q_stride_b; t.qsh = a->q_stride_h; t.qss = a->q_stride_s;
+  t.ksb = a->k_stride_b; t.ksh = a->k_stride_h; t.kss = a->k_stride_s;
+  t.vsb = a->v_stride_b; t.vsh = a->v_stride_h; t.vss = a->v_stride_s;
+  t.osb = a->o_stride_b; t.osh = a->o_stride_h; t.oss = a->o_stride_s;
+  t.lsb = a->lse_stride_b; t.lsh = a->lse_stride_h;
+  t.H = a->num_heads; t.groups = a->num_heads / a->num_kv_heads;
+  t.q_len = a->q_len; t.kv_len = a->kv_len; t.nqb = d.nqb;
+  t.scale_log2 = a->sm_scale * 1.4426950408889634f;
+  t.pc = make_consts(*p);
+  t.row_ptr = row_ptr; t.col_idx = col_idx; t.items = items;
+  return hip_status(launch_tile_fwd(t, a->head_dim, num_items, (hipStream_t)stream));
+}
+
+esa_status esa_elastic_fwd_rows(const esa_fwd_args* a, const esa_pattern* p,
+                                const int64_t* positions, void* stream) {
+  esa_status s = check_fwd_common(a);
+  if (s != ESA_OK) return s;
+  s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  if (p->num_heads != a->num_heads) return ESA_ERR_SHAPE;
+  if (!positions && a->q_len > a->kv_len) return ESA_ERR_SHAPE;
+  s = check_gather_layout(a);
+  if (s != ESA_OK) return s;
+  GatherArgs g = gather_args_of(a);
+  g.w = p->attention_length;
+  g.pc = make_consts(*p);
+  g.positions = positions;
+  return hip_status(launch_gather_fwd(g, a->dtype == ESA_F32, true, (hipStream_t)stream));
+}
+
+esa_status esa_sparse_fwd(const esa_fwd_args* a, const void* indices, int32_t index_bytes,
+                          int64_t idx_stride_h, int64_t idx_stride_s, const void* mask,
+                          int32_t mask_bytes, int64_t mask_stride_h, int64_t mask_stride_s,
+                          int32_t attn_length, void* stream) {
+  esa_status s = check_fwd_common(a);
+  if (s != ESA_OK) return s;
+  if (!indices || !mask) return ESA_ERR_NULL;
+  if (index_bytes != 4 && index_bytes != 8) return ESA_ERR_DTYPE;
+  if (mask_bytes != 1 && mask_bytes != 4 && mask_bytes != 8) return ESA_ERR_DTYPE;
+  if (attn_length < 1 || attn_length > kMaxW) return ESA_ERR_SHAPE;
+  s = check_gather_layout(a);
+  if (s != ESA_OK) return s;
+  GatherArgs g = gather_args_of(a);
+  g.w = attn_length;
+  g.indices = indices; g.mask = mask;
+  g.index_bytes = index_bytes; g.mask_bytes = mask_bytes;
+  g.ish = idx_stride_h; g.iss = idx_stride_s; g.msh = mask_stride_h; g.mss = mask_stride_s;
+  return hip_status(launch_gather_fwd(g, a->dtype == ESA_F32, false, (hipStream_t)stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,186 @@
+// Per-row gather forward (gfx950): one wave per (batch, head, query row).
+//
+// Two index sources share the kernel:
+//   explicit  indices / mask arrays, the operator
+//             ElasticSparseAttentionFunction.forward (elastic_sparse_attention.py:241-297)
+//             with the Triton kernel's semantics (:117-166): a valid entry
+//             whose index is outside [0, kv_len) scores 0 against zero K/V;
+//             duplicates count once per entry.
+//   pattern   each row's w indices regenerated on the device for query
+//             position positions[r] (or r), masked entries set to 0 and
+//             clamped to [0, kv_len - 1] as _triton_forward does (:602-615).
+//
+// Lanes split the row's entries 64 at a time for QK (each lane one key, a
+// full dot product over D in float32), then split D for PV (each lane up to
+// four d columns, one 64-key chunk at a time with p and the key broadcast
+// through LDS).  Online softmax in float32 with accurate expf, so float32
+// inputs meet a 1e-4 bound.
+#include "esa_internal.hpp"
+
+namespace esa {
+
+template <typename T>
+__device__ __forceinline__ float ld(const T* p);
+template <>
+__device__ __forceinline__ float ld<float>(const float* p) { return *p; }
+template <>
+__device__ __forceinline__ float ld<uint16_t>(const uint16_t* p) { return bf16_to_f32(*p); }
+
+template <typename T>
+__device__ __forceinline__ void st(T* p, float v);
+template <>
+__device__ __forceinline__ void st<float>(float* p, float v) { *p = v; }
+template <>
+__device__ __forceinline__ void st<uint16_t>(uint16_t* p, float v) { *p = f32_to_bf16_bits(v); }
+
+// dot(q, k_row) over D (D % 4 == 0); q in LDS as float.
+template <typename T>
+__device__ __forceinline__ float row_dot(const float* __restrict__ qs, const T* __restrict__ kr,
+                                         int D);
+template <>
+__device__ __forceinline__ float row_dot<float>(const float* __restrict__ qs,
+                                                const float* __restrict__ kr, int D) {
+  float acc = 0.f;
+  for (int d = 0; d < D; d += 4) {
+    const f32x4 kv = *(const f32x4*)(kr + d);
+    acc += qs[d] * kv[0];
+    acc += qs[d + 1] * kv[1];
+    acc += qs[d + 2] * kv[2];
+    acc += qs[d + 3] * kv[3];
+  }
+  return acc;
+}
+template <>
+__device__ __forceinline__ float row_dot<uint16_t>(const float* __restrict__ qs,
+                                                   const uint16_t* __restrict__ kr, int D) {
+  float acc = 0.f;
+  for (int d = 0; d < D; d += 4) {
+    const u32x2 kv = *(const u32x2*)(kr + d);
+    acc += qs[d] * __uint_as_float(kv[0] << 16);
+    acc += qs[d + 1] * __uint_as_float(kv[0] & 0xffff0000u);
+    acc += qs[d + 2] * __uint_as_float(kv[1] << 16);
+    acc += qs[d + 3] * __uint_as_float(kv[1] & 0xffff0000u);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ int64_t load_int(const void* base, int bytes, int64_t off) {
+  if (bytes == 8) return ((const int64_t*)base)[off];
+  if (bytes == 4) return ((const int32_t*)base)[off];
+  return ((const uint8_t*)base)[off];
+}
+
+template <typename T, bool PATTERN>
+__global__ __launch_bounds__(256) void gather_fwd_kernel(GatherArgs A) {
+  __shared__ float qs_all[4][256];
+  __shared__ float ps_all[4][64];
+  __shared__ int ks_all[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = blockIdx.x * 4 + wave;
+  const int h = blockIdx.y, b = blockIdx.z;
+  if (r >= A.q_len) return;  // whole wave leaves; no block-level barrier below
+  const int kvh = h / A.groups;
+  const int D = A.D;
+  float* qs = qs_all[wave];
+  float* ps = ps_all[wave];
+  int* ks = ks_all[wave];
+
+  const T* qrow = (const T*)A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)r * A.qss;
+  for (int d = lane; d < D; d += 64) qs[d] = ld<T>(qrow + d);
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  const T* kbase = (const T*)A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh;
+  const T* vbase = (const T*)A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh;
+
+  int pos = r;
+  HeadWeights hw{};
+  RowParams rp{};
+  if (PATTERN) {
+    pos = A.positions ? (int)A.positions[r] : r;
+    hw = head_weights(A.pc, h);
+    rp = row_params(A.pc, pos);
+  }
+
+  float m = -INFINITY, l = 0.f;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0; c0 < A.w; c0 += 64) {
+    const int j = c0 + lane;
+    bool valid = false;
+    int64_t key = 0;
+    if (j < A.w) {
+      if (PATTERN) {
+        const int idx = interp_index(oversized(rp, j), oversized(rp, j + 1), hw);
+        valid = idx <= pos;
+        key = valid ? idx : 0;
+        key = key < 0 ? 0 : (key > A.kv_len - 1 ? A.kv_len - 1 : key);
+      } else {
+        key = load_int(A.indices, A.index_bytes, (int64_t)h * A.ish + (int64_t)r * A.iss + j);
+        valid = load_int(A.mask, A.mask_bytes, (int64_t)h * A.msh + (int64_t)r * A.mss + j) != 0;
+      }
+    }
+    const bool in_range = key >= 0 && key < A.kv_len;
+    float s = -INFINITY;
+    if (valid) s = in_range ? row_dot<T>(qs, kbase + key * A.kss, D) * A.sm_scale : 0.f;
+    const float cmax = wave_max(s);
+    const float m_new = fmaxf(m, cmax);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float p = valid ? expf(s - m_use) : 0.f;
+    const float alpha = expf(m - m_use);
+    l = l * alpha + wave_sum(p);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] *= alpha;
+    m = m_new;
+    ps[lane] = p;
+    ks[lane] = (valid && in_range) ? (int)key : -1;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int nj = min(64, A.w - c0);
+    for (int jj = 0; jj < nj; ++jj) {
+      const float pj = ps[jj];
+      const int kj = ks[jj];
+      if (kj >= 0 && pj != 0.f) {
+        const T* vr = vbase + (int64_t)kj * A.vss;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int d = lane + 64 * e;
+          if (d < D) acc[e] += pj * ld<T>(vr + d);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  T* orow = (T*)A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)r * A.oss;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int d = lane + 64 * e;
+    if (d < D) st<T>(orow + d, acc[e] * inv);
+  }
+  if (A.lse && lane == 0)
+    A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + r] = l > 0.f ? m + logf(l) : -INFINITY;
+}
+
+hipError_t launch_gather_fwd(const GatherArgs& a, bool f32, bool pattern, hipStream_t stream) {
+  if (a.q_len <= 0 || a.B <= 0 || a.H <= 0) return hipSuccess;
+  dim3 grid((unsigned)((a.q_len + 3) / 4), (unsigned)a.H, (unsigned)a.B);
+  if (f32) {
+    if (pattern)
+      gather_fwd_kernel<float, true><<<grid, 256, 0, stream>>>(a);
+    else
+      gather_fwd_kernel<float, false><<<grid, 256, 0, stream>>>(a);
+  } else {
+    if (pattern)
+      gather_fwd_kernel<uint16_t, true><<<grid, 256, 0, stream>>>(a);
+    else
+      gather_fwd_kernel<uint16_t, false><<<grid, 256, 0, stream>>>(a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace esa

@@ -1,0 +1,463 @@
+"""Elastic sparse attention for AMD MI355X: drop-in for the reference module.
+
+Same class names, constructor arguments, forward signature, return values and
+errors as the reference's ``elastic_sparse_attention.py``
+(HighCWu/elastic-sparse-attention):
+
+* ``ElasticSparseAttention(layer_idx, num_hidden_layers, num_attention_heads,
+  head_dim, attention_length, max_seq_len, num_key_value_heads=None,
+  attention_dropout=0.0, implementation="triton")``   (:375-386)
+* ``forward(query_states, key_states, value_states, cache_position=None)
+  -> (attn_output [B, Lq, H * D], None)``             (:728-765)
+* ``ElasticSparseAttentionFunction.apply(q, k, v, sparse_indices,
+  sparse_mask, sm_scale, num_kv_groups) -> o [B, H, Lq, D]``  (:241-297)
+
+Underneath, every call goes through libesa.so's C ABI (include/esa.h) to
+hand-written gfx950 HIP kernels:
+
+* prefill (``cache_position is None``), bf16, head_dim 64 or 128: the
+  block-sparse MFMA kernel over the block layout (CSR of active 128x128
+  tiles) built once per device by the HIP layout builder;
+* decode (``cache_position`` given), float32, or other head dims: the
+  per-row gather kernel that regenerates each row's elastic indices on the
+  device.
+
+The index cache the reference keeps as two int64 buffers
+(``sparse_attention_indices``, ``sparse_causal_mask``, :454-468) is not held
+by default: the kernels regenerate indices from the pattern.  The two
+attributes are still available and are materialised on first access, on the
+GPU, by the HIP index builder.
+
+Differences from the reference, all deliberate:
+* ``implementation`` accepts "triton", "naive" and "dense" (anything else is
+  the reference's ValueError); all three run the HIP kernels and return
+  ``None`` attention weights.  There is no CPU path: CPU tensors raise.
+* ``attention_dropout`` is ignored, as the reference's Triton path ignores it.
+* Backward is not built: calling ``backward`` through the output raises
+  NotImplementedError.
+* A query row with no valid entry (impossible for the elastic pattern, only
+  reachable through explicit masks) gives output 0 rather than NaN.
+"""
+from __future__ import annotations
+
+import ctypes
+import logging
+from typing import Dict, Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from esa_native import (ESA_BF16, ESA_F32, EsaFwdArgs, EsaPattern, check, load)
+
+logger = logging.getLogger(__name__)
+
+BLOCK_M = 128
+BLOCK_N = 128
+
+__all__ = [
+    "ElasticSparseAttention",
+    "ElasticSparseAttentionFunction",
+    "ElasticLayout",
+    "make_pattern",
+    "build_indices",
+    "elastic_attention_fwd",
+    "elastic_attention_rows",
+    "sparse_attention_fwd",
+]
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return ESA_BF16
+    if dt == torch.float32:
+        return ESA_F32
+    raise ValueError(f"unsupported dtype {dt}: the HIP kernels take bfloat16 or float32")
+
+
+def _require_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if not t.is_cuda:
+            raise RuntimeError(
+                "elastic sparse attention runs on the GPU through libesa.so (HIP); "
+                f"got a tensor on {t.device}")
+
+
+def _prep(t: torch.Tensor, align_elems: int) -> torch.Tensor:
+    """Innermost dim contiguous, base and strides aligned for row loads."""
+    es = t.element_size()
+    ok = (t.stride(-1) == 1 and t.data_ptr() % (align_elems * es) == 0
+          and all(s % align_elems == 0 for s in t.stride()[:-1]))
+    if ok:
+        return t
+    t = t.contiguous()
+    if t.data_ptr() % (align_elems * es) != 0:
+        t = t.clone()
+    return t
+
+
+def make_pattern(seq_len: int, attention_length: int, layer_idx: int, num_hidden_layers: int,
+                 num_heads: int, block_m: int = BLOCK_M, block_n: int = BLOCK_N) -> EsaPattern:
+    """The pattern parameters the C ABI takes (esa_pattern)."""
+    return EsaPattern(int(seq_len), int(attention_length), int(layer_idx),
+                      int(num_hidden_layers), int(num_heads), int(block_m), int(block_n))
+
+
+def build_indices(pattern: EsaPattern, device: torch.device, dtype: torch.dtype = torch.int64,
+                  row0: int = 0, nrows: Optional[int] = None
+                  ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Index set and mask ``[H, nrows, w]`` on ``device``, as
+    ``_create_elastic_sparse_indices`` (:470-535) returns them (bit-exact)."""
+    lib = load()
+    device = torch.device(device)
+    _require_gpu(torch.empty(0, device=device))
+    nrows = pattern.seq_len - row0 if nrows is None else nrows
+    if dtype not in (torch.int64, torch.int32):
+        raise ValueError("index dtype must be int64 or int32")
+    shape = (pattern.num_heads, nrows, pattern.attention_length)
+    idx = torch.empty(shape, dtype=dtype, device=device)
+    msk = torch.empty(shape, dtype=dtype, device=device)
+    check(lib.esa_build_indices(ctypes.byref(pattern), row0, nrows, ctypes.c_void_p(idx.data_ptr()),
+                                ctypes.c_void_p(msk.data_ptr()), idx.element_size(),
+                                _stream(device)), "esa_build_indices")
+    return idx, msk
+
+
+class ElasticLayout:
+    """Block layout of one elastic pattern on one device.
+
+    ``row_ptr`` (int32 ``[H * nqb + 1]``) and ``col_idx`` (int32) list, for
+    every (head, 128-row query block), the ascending 128-key tiles holding at
+    least one valid entry.  Built by the HIP layout builder; the host keeps a
+    copy of ``row_ptr`` for the LPT work lists (``schedule``), one per
+    (q_len, batch), cached.
+    """
+
+    def __init__(self, pattern: EsaPattern, device: torch.device):
+        lib = load()
+        self.pattern = pattern
+        self.device = torch.device(device)
+        nqb = ctypes.c_int32()
+        nkb = ctypes.c_int32()
+        max_tiles = ctypes.c_int64()
+        ws = ctypes.c_size_t()
+        check(lib.esa_layout_sizes(ctypes.byref(pattern), ctypes.byref(nqb), ctypes.byref(nkb),
+                                   ctypes.byref(max_tiles), ctypes.byref(ws)), "esa_layout_sizes")
+        self.num_qblocks = nqb.value
+        self.num_kblocks = nkb.value
+        H = pattern.num_heads
+        self.row_ptr = torch.empty(H * self.num_qblocks + 1, dtype=torch.int32, device=self.device)
+        self.col_idx = torch.empty(max(1, max_tiles.value), dtype=torch.int32, device=self.device)
+        work = torch.empty(ws.value, dtype=torch.uint8, device=self.device)
+        check(lib.esa_build_layout(ctypes.byref(pattern), ctypes.c_void_p(self.row_ptr.data_ptr()),
+                                   ctypes.c_void_p(self.col_idx.data_ptr()),
+                                   self.col_idx.numel(), ctypes.c_void_p(work.data_ptr()),
+                                   ws.value, _stream(self.device)), "esa_build_layout")
+        self.row_ptr_host = self.row_ptr.cpu()  # one synchronisation per layout
+        del work
+        self.num_tiles = int(self.row_ptr_host[-1])
+        self._schedules: Dict[Tuple[int, int], Tuple[torch.Tensor, int]] = {}
+
+    def tiles_for(self, q_len: int) -> int:
+        """Active tiles over the query blocks a q_len-row prefill visits,
+        summed over heads (one batch element)."""
+        nq = (q_len + self.pattern.block_m - 1) // self.pattern.block_m
+        rp = self.row_ptr_host.view(-1)[:-1].view(self.pattern.num_heads, self.num_qblocks)
+        nxt = self.row_ptr_host.view(-1)[1:].view(self.pattern.num_heads, self.num_qblocks)
+        return int((nxt[:, :nq] - rp[:, :nq]).sum())
+
+    def schedule(self, q_len: int, batch: int) -> Tuple[torch.Tensor, int]:
+        key = (int(q_len), int(batch))
+        got = self._schedules.get(key)
+        if got is not None:
+            return got
+        lib = load()
+        nq = (q_len + self.pattern.block_m - 1) // self.pattern.block_m
+        cap = max(1, batch * self.pattern.num_heads * nq)
+        items = torch.empty(cap, dtype=torch.int32)
+        n = ctypes.c_int64()
+        check(lib.esa_plan_schedule(ctypes.byref(self.pattern),
+                                    ctypes.c_void_p(self.row_ptr_host.data_ptr()), q_len, batch,
+                                    ctypes.c_void_p(items.data_ptr()), cap, ctypes.byref(n)),
+              "esa_plan_schedule")
+        got = (items.to(self.device), n.value)
+        self._schedules[key] = got
+        return got
+
+
+def _fwd_args(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+              o_strides: Tuple[int, int, int], lse: Optional[torch.Tensor],
+              scaling: float) -> EsaFwdArgs:
+    B, H, Lq, D = q.shape
+    a = EsaFwdArgs()
+    a.dtype = _dtype_code(q.dtype)
+    a.batch, a.num_heads, a.num_kv_heads = B, H, k.shape[1]
+    a.q_len, a.kv_len, a.head_dim = Lq, k.shape[2], D
+    a.q = q.data_ptr()
+    a.q_stride_b, a.q_stride_h, a.q_stride_s = q.stride(0), q.stride(1), q.stride(2)
+    a.k = k.data_ptr()
+    a.k_stride_b, a.k_stride_h, a.k_stride_s = k.stride(0), k.stride(1), k.stride(2)
+    a.v = v.data_ptr()
+    a.v_stride_b, a.v_stride_h, a.v_stride_s = v.stride(0), v.stride(1), v.stride(2)
+    a.o = o.data_ptr()
+    a.o_stride_b, a.o_stride_h, a.o_stride_s = o_strides
+    if lse is not None:
+        a.lse = lse.data_ptr()
+        a.lse_stride_b, a.lse_stride_h = lse.stride(0), lse.stride(1)
+    else:
+        a.lse = None
+    a.sm_scale = float(scaling)
+    return a
+
+
+def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+    _require_gpu(q, k, v)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be 4-D [B, heads, seq, head_dim]")
+    if k.shape != v.shape:
+        raise ValueError(f"key {tuple(k.shape)} and value {tuple(v.shape)} shapes differ")
+    if q.shape[0] != k.shape[0] or q.shape[3] != k.shape[3]:
+        raise ValueError(f"query {tuple(q.shape)} and key {tuple(k.shape)} disagree on batch "
+                         "or head_dim")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError("q, k and v must share one dtype")
+    if q.shape[1] % k.shape[1] != 0:
+        raise ValueError(f"query heads ({q.shape[1]}) must be divisible by key/value heads "
+                         f"({k.shape[1]})")
+
+
+def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                          layout: ElasticLayout, scaling: float, return_lse: bool = True,
+                          out: Optional[torch.Tensor] = None
+                          ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Block-sparse MFMA forward (prefill: query row r is position r).
+
+    Returns ``o`` as ``[B, Lq, H, D]`` (so ``o.view(B, Lq, H * D)`` is the
+    module output, :761-763) and, if asked, ``lse`` float32 ``[B, H, Lq]``.
+    """
+    _check_qkv(q, k, v)
+    B, H, Lq, D = q.shape
+    q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
+    o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
+    lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
+    items, n = layout.schedule(Lq, B)
+    a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
+    check(load().esa_elastic_fwd(ctypes.byref(a), ctypes.byref(layout.pattern),
+                                 ctypes.c_void_p(layout.row_ptr.data_ptr()),
+                                 ctypes.c_void_p(layout.col_idx.data_ptr()),
+                                 ctypes.c_void_p(items.data_ptr()), n, _stream(q.device)),
+          "esa_elastic_fwd")
+    return o, lse
+
+
+def elastic_attention_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                           pattern: EsaPattern, scaling: float,
+                           positions: Optional[torch.Tensor] = None, return_lse: bool = True
+                           ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Per-row gather forward over the pattern; query row r is position
+    ``positions[r]`` (int64 on the device) or r.  Output ``[B, Lq, H, D]``."""
+    _check_qkv(q, k, v)
+    B, H, Lq, D = q.shape
+    q, k, v = _prep(q, 4), _prep(k, 4), _prep(v, 4)
+    o = torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
+    lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
+    pos_ptr = None
+    if positions is not None:
+        if positions.dtype != torch.int64 or positions.device != q.device or positions.numel() != Lq:
+            raise ValueError("positions must be an int64 tensor of q_len entries on q's device")
+        positions = positions.contiguous()
+        pos_ptr = ctypes.c_void_p(positions.data_ptr())
+    a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
+    check(load().esa_elastic_fwd_rows(ctypes.byref(a), ctypes.byref(pattern), pos_ptr,
+                                      _stream(q.device)), "esa_elastic_fwd_rows")
+    return o, lse
+
+
+def sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                         sparse_indices: torch.Tensor, sparse_mask: torch.Tensor,
+                         sm_scale: float, num_kv_groups: int
+                         ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Gather forward over explicit ``[H, Lq, w]`` index lists (the reference
+    operator, :241-297).  Returns ``o [B, H, Lq, D]`` (q's shape and dtype)
+    and ``lse [B, H, Lq]``."""
+    _check_qkv(q, k, v)
+    _require_gpu(sparse_indices, sparse_mask)
+    B, H, Lq, D = q.shape
+    if num_kv_groups != H // k.shape[1]:
+        raise ValueError(f"num_kv_groups ({num_kv_groups}) != query heads / key heads "
+                         f"({H} / {k.shape[1]})")
+    if sparse_indices.shape != sparse_mask.shape or sparse_indices.dim() != 3 or \
+            sparse_indices.shape[0] != H or sparse_indices.shape[1] != Lq:
+        raise ValueError(f"sparse_indices/sparse_mask must be [H={H}, Lq={Lq}, w]; got "
+                         f"{tuple(sparse_indices.shape)} and {tuple(sparse_mask.shape)}")
+    if sparse_indices.dtype not in (torch.int64, torch.int32):
+        raise ValueError("sparse_indices must be int64 or int32")
+    q, k, v = _prep(q, 4), _prep(k, 4), _prep(v, 4)
+    idx = sparse_indices.contiguous()
+    msk = sparse_mask
+    if msk.dtype == torch.bool:
+        msk = msk.to(torch.uint8)
+    elif msk.dtype not in (torch.int64, torch.int32, torch.uint8):
+        msk = msk.to(torch.int32)
+    msk = msk.contiguous()
+    o = torch.empty(B, H, Lq, D, dtype=q.dtype, device=q.device)
+    lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device)
+    a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(1), o.stride(2)), lse, sm_scale)
+    check(load().esa_sparse_fwd(ctypes.byref(a), ctypes.c_void_p(idx.data_ptr()),
+                                idx.element_size(), idx.stride(0), idx.stride(1),
+                                ctypes.c_void_p(msk.data_ptr()), msk.element_size(),
+                                msk.stride(0), msk.stride(1), idx.shape[2], _stream(q.device)),
+          "esa_sparse_fwd")
+    return o, lse
+
+
+class ElasticSparseAttentionFunction(torch.autograd.Function):
+    """The reference's operator (:235-339): ``apply(q, k, v, sparse_indices,
+    sparse_mask, sm_scale, num_kv_groups) -> o [B, H, Lq, D]``.  Forward only;
+    ``backward`` raises NotImplementedError."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, sparse_indices, sparse_mask, sm_scale, num_kv_groups):
+        o, _ = sparse_attention_fwd(q, k, v, sparse_indices, sparse_mask, sm_scale,
+                                    num_kv_groups)
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        raise NotImplementedError("the elastic sparse attention backward is not built")
+
+
+class _ForwardOnly(torch.autograd.Function):
+    """Marks a module output as not differentiable through this op."""
+
+    @staticmethod
+    def forward(ctx, out, *inputs):
+        return out
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError("the elastic sparse attention backward is not built")
+
+
+class ElasticSparseAttention(nn.Module):
+    """Drop-in for the reference's ElasticSparseAttention (:345-765), on HIP.
+
+    Args mirror :375-386.  ``scaling = head_dim ** -0.5`` (:444),
+    ``num_kv_groups = H // Hkv`` (:442); query head h reads kv head
+    ``h // num_kv_groups`` (:89).
+    """
+
+    def __init__(self, layer_idx: int, num_hidden_layers: int, num_attention_heads: int,
+                 head_dim: int, attention_length: int, max_seq_len: int,
+                 num_key_value_heads: Optional[int] = None, attention_dropout: float = 0.0,
+                 implementation: str = "triton"):
+        super().__init__()
+        valid_implementations = ["triton", "naive", "dense"]
+        if implementation not in valid_implementations:                   # :412-417
+            raise ValueError(
+                f"Invalid implementation '{implementation}'. Must be one of "
+                f"{valid_implementations}.")
+        self.layer_idx = layer_idx
+        self.num_hidden_layers = num_hidden_layers
+        self.num_attention_heads = num_attention_heads
+        self.head_dim = head_dim
+        self.attention_length = attention_length
+        self.attention_dropout = attention_dropout
+        self.implementation = implementation
+        self.max_seq_len = max_seq_len
+        self.num_key_value_heads = (num_key_value_heads if num_key_value_heads is not None
+                                    else num_attention_heads)
+        if self.num_attention_heads % self.num_key_value_heads != 0:      # :435-441
+            raise ValueError(
+                f"`num_attention_heads` ({self.num_attention_heads}) must be divisible by "
+                f"`num_key_value_heads` ({self.num_key_value_heads}) for GQA.")
+        self.num_kv_groups = self.num_attention_heads // self.num_key_value_heads  # :442
+        self.scaling = self.head_dim ** -0.5                                  # :444
+        self.pattern = make_pattern(max_seq_len, attention_length, layer_idx,
+                                    num_hidden_layers, num_attention_heads)
+        self._layouts: Dict[torch.device, ElasticLayout] = {}
+        self._index_cache: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+        self._last_device: Optional[torch.device] = None
+        self.full_attention_mask = None
+
+    # -- the reference's cached buffers, built on the GPU on first access --
+    def _indices(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        dev = self._last_device or torch.device("cuda", torch.cuda.current_device())
+        if self._index_cache is None or self._index_cache[0].device != dev:
+            self._index_cache = build_indices(self.pattern, dev, torch.int64)
+        return self._index_cache
+
+    @property
+    def sparse_attention_indices(self) -> torch.Tensor:
+        """int64 ``[H, max_seq_len, w]``, as the reference caches (:465-466)."""
+        return self._indices()[0]
+
+    @property
+    def sparse_causal_mask(self) -> torch.Tensor:
+        """int64 ``[H, max_seq_len, w]`` 0/1, as the reference caches (:465-467)."""
+        return self._indices()[1]
+
+    def layout(self, device: torch.device) -> ElasticLayout:
+        """The block layout on ``device`` (built once, cached)."""
+        device = torch.device(device)
+        if device.index is None:
+            device = torch.device(device.type, torch.cuda.current_device())
+        lay = self._layouts.get(device)
+        if lay is None:
+            lay = ElasticLayout(self.pattern, device)
+            self._layouts[device] = lay
+        return lay
+
+    def _get_prepared_indices_and_mask(self, kv_seq_len: int):
+        """Rows ``[:kv_seq_len]`` of the cached index set (:574-590)."""
+        if kv_seq_len > self.max_seq_len:
+            raise ValueError(
+                f"Input sequence length ({kv_seq_len}) exceeds the maximum length initialized "
+                f"in the module ({self.max_seq_len}).")
+        idx, msk = self._indices()
+        return idx[:, :kv_seq_len, :], msk[:, :kv_seq_len, :]
+
+    def forward(self, query_states: torch.Tensor, key_states: torch.Tensor,
+                value_states: torch.Tensor, cache_position: Optional[torch.LongTensor] = None
+                ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        q, k, v = query_states, key_states, value_states
+        _check_qkv(q, k, v)
+        B, H, Lq, D = q.shape
+        kv_len = k.shape[2]
+        if kv_len > self.max_seq_len:                                     # :579-584
+            raise ValueError(
+                f"Input sequence length ({kv_len}) exceeds the maximum length initialized "
+                f"in the module ({self.max_seq_len}).")
+        if H != self.num_attention_heads or k.shape[1] != self.num_key_value_heads:
+            raise ValueError(
+                f"expected {self.num_attention_heads} query heads and "
+                f"{self.num_key_value_heads} key/value heads; got {H} and {k.shape[1]}")
+        self._last_device = q.device
+        if cache_position is None:
+            if Lq > kv_len:
+                raise ValueError(f"q_len ({Lq}) exceeds kv_len ({kv_len}) without cache_position")
+            if q.dtype == torch.bfloat16 and D in (64, 128):
+                o, _ = elastic_attention_fwd(q, k, v, self.layout(q.device), self.scaling,
+                                             return_lse=False)
+            else:
+                o, _ = elastic_attention_rows(q, k, v, self.pattern, self.scaling, None,
+                                              return_lse=False)
+        else:
+            pos = torch.as_tensor(cache_position, device=q.device).to(torch.int64).reshape(-1)
+            if pos.numel() != Lq:
+                raise ValueError(f"cache_position has {pos.numel()} entries for {Lq} query rows")
+            pos = torch.where(pos < 0, pos + kv_len, pos)
+            if bool(((pos < 0) | (pos >= kv_len)).any()):
+                raise IndexError(f"cache_position out of range for kv_len {kv_len}")
+            o, _ = elastic_attention_rows(q, k, v, self.pattern, self.scaling, pos,
+                                          return_lse=False)
+        out = o.view(B, Lq, H * D)                                         # :761-763
+        if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+            out = _ForwardOnly.apply(out, q, k, v)
+        return out, None

@@ -1,0 +1,169 @@
+/*
+ * Elastic sparse attention forward for AMD MI355X (gfx950) -- C ABI.
+ *
+ * Library: libesa.so (built from elastic-sparse-attention_amd/csrc).
+ *
+ * Conventions shared by every entry point:
+ *   - Every function returns an esa_status; 0 (ESA_OK) means success.  Invalid
+ *     arguments are rejected on the host before anything is launched.
+ *   - Device pointers are plain addresses of device memory the caller owns.
+ *     The library never allocates device memory and keeps no mutable global
+ *     state, so calls on different streams may run concurrently.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Launch functions are asynchronous and never synchronise the host.
+ *   - Strides are in elements.  The innermost (head_dim / w) dimension of
+ *     every tensor is contiguous.
+ *
+ * Each entry point names the part of the reference's
+ * elastic_sparse_attention.py (HighCWu/elastic-sparse-attention) it replaces.
+ */
+#ifndef ESA_H_
+#define ESA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t esa_status;
+#define ESA_OK 0
+#define ESA_ERR_NULL 1        /* a required pointer is NULL */
+#define ESA_ERR_SHAPE 2       /* inconsistent or out-of-range sizes */
+#define ESA_ERR_DTYPE 3       /* unsupported element type */
+#define ESA_ERR_ALIGN 4       /* pointer or stride misaligned for the kernel */
+#define ESA_ERR_UNSUPPORTED 5 /* valid request this build has no kernel for */
+#define ESA_ERR_CAPACITY 6    /* output or workspace buffer too small */
+#define ESA_ERR_HIP 7         /* a HIP runtime call failed */
+
+typedef int32_t esa_dtype;
+#define ESA_F32 0
+#define ESA_BF16 1
+
+/* Elastic pattern parameters: the constructor arguments that fix the index
+ * set (elastic_sparse_attention.py:375-386, used at :477-535) plus the tile
+ * shape of the block layout. */
+typedef struct esa_pattern {
+  int32_t seq_len;           /* rows (query positions 0..seq_len-1) covered */
+  int32_t attention_length;  /* w: keys per query row */
+  int32_t layer_idx;         /* 0-based layer index */
+  int32_t num_hidden_layers; /* layers in the model */
+  int32_t num_heads;         /* query heads H */
+  int32_t block_m;           /* query rows per tile (layout granularity) */
+  int32_t block_n;           /* keys per tile (layout granularity) */
+} esa_pattern;
+
+/* q, k, v, o and the log-sum-exp of one forward call.  Mirrors the tensors
+ * ElasticSparseAttentionFunction.forward receives and allocates
+ * (elastic_sparse_attention.py:241-257): q [B, H, Lq, D], k and v
+ * [B, Hkv, Lk, D]; o has q's shape and dtype but any (b, h, s) strides, so
+ * [B, Lq, H, D] can be written directly; lse is float32 [B, H, Lq] with
+ * contiguous s (may be NULL). */
+typedef struct esa_fwd_args {
+  esa_dtype dtype; /* element type of q, k, v and o */
+  int32_t batch, num_heads, num_kv_heads, q_len, kv_len, head_dim;
+  const void* q;
+  int64_t q_stride_b, q_stride_h, q_stride_s;
+  const void* k;
+  int64_t k_stride_b, k_stride_h, k_stride_s;
+  const void* v;
+  int64_t v_stride_b, v_stride_h, v_stride_s;
+  void* o;
+  int64_t o_stride_b, o_stride_h, o_stride_s;
+  float* lse;
+  int64_t lse_stride_b, lse_stride_h;
+  float sm_scale; /* the module's scaling = head_dim ** -0.5 (:444) */
+} esa_fwd_args;
+
+/* Human-readable name of a status code. */
+const char* esa_status_string(esa_status s);
+
+/* Library version string. */
+const char* esa_version(void);
+
+/* Host only.  Checks an esa_pattern and reports the sizes of its block
+ * layout: query blocks per head, key blocks, an upper bound on the number of
+ * active tiles (the col_idx capacity esa_build_layout needs) and the
+ * workspace esa_build_layout needs.  No reference counterpart: the reference
+ * never forms a block layout. */
+esa_status esa_layout_sizes(const esa_pattern* p, int32_t* num_qblocks,
+                            int32_t* num_kblocks, int64_t* max_tiles,
+                            size_t* workspace_bytes);
+
+/* Replaces ElasticSparseAttention._create_elastic_sparse_indices
+ * (elastic_sparse_attention.py:470-535).  Writes rows [row0, row0 + nrows)
+ * of the index set as indices[H, nrows, w] (masked entries 0, :533) and
+ * mask[H, nrows, w] (1 = valid), each with elem_bytes = 4 (int32) or 8
+ * (int64, the reference's dtype).  Either output may be NULL.  Bit-exact with
+ * the reference's torch float32 evaluation. */
+esa_status esa_build_indices(const esa_pattern* p, int32_t row0, int32_t nrows,
+                             void* indices, void* mask, int32_t elem_bytes,
+                             void* stream);
+
+/* Block layout builder (derived from :470-535; no reference counterpart).
+ * For every (head h, query block qb) writes the ascending list of active key
+ * tiles -- tiles kb with some valid index idx of a row in the block and
+ * idx / block_n == kb -- as CSR: row_ptr[H * nqb + 1] (rows ordered
+ * h * nqb + qb) and col_idx[row_ptr[H * nqb]].  col_capacity is the length
+ * of col_idx; the workspace is at least esa_layout_sizes' figure. */
+esa_status esa_build_layout(const esa_pattern* p, int32_t* row_ptr,
+                            int32_t* col_idx, int64_t col_capacity,
+                            void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/* Host only.  Work list for esa_elastic_fwd: the (batch, head, query block)
+ * items of a forward over q_len query rows, ordered for the device.  Replaces
+ * the implicit Triton grid (q_len, H, B) (elastic_sparse_attention.py:261).
+ * row_ptr_host is esa_build_layout's row_ptr copied to host memory.  Items
+ * are ordered longest first (LPT), so the tail of the launch holds the
+ * shortest query blocks.  Writes *num_items entries (batch * H *
+ * ceil(q_len / block_m)) into items_host. */
+esa_status esa_plan_schedule(const esa_pattern* p, const int32_t* row_ptr_host,
+                             int32_t q_len, int32_t batch, int32_t* items_host,
+                             int64_t items_capacity, int64_t* num_items);
+
+/* Block-sparse forward over the elastic pattern, query rows at positions
+ * 0..q_len-1.  Replaces _triton_forward + ElasticSparseAttentionFunction
+ * .forward (elastic_sparse_attention.py:592-622, 241-297) for prefill.
+ * Visits only the active tiles of the layout, runs QK^T and PV on bf16 MFMA
+ * with float32 accumulation and online softmax.  Requires dtype ESA_BF16,
+ * head_dim 64 or 128, block_m = block_n = 128, q_len <= kv_len,
+ * q_len <= p->seq_len, 16-byte aligned rows.  items/num_items come from
+ * esa_plan_schedule (copied to device memory). */
+esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p,
+                           const int32_t* row_ptr, const int32_t* col_idx,
+                           const int32_t* items, int64_t num_items,
+                           void* stream);
+
+/* Per-row gather forward over the elastic pattern for arbitrary query
+ * positions: row r of q is position positions[r] (int64 device array, as
+ * cache_position, :602-608), or r when positions is NULL.  Replaces the
+ * decode branch of _triton_forward (:602-619).  Each row's w indices are
+ * regenerated on the device (bit-exact with :470-535) and clamped to
+ * [0, kv_len - 1] (:615).  Positions must lie in [0, kv_len); the caller
+ * checks.  dtype ESA_F32 or ESA_BF16, head_dim a multiple of 4, <= 256. */
+esa_status esa_elastic_fwd_rows(const esa_fwd_args* a, const esa_pattern* p,
+                                const int64_t* positions, void* stream);
+
+/* Gather forward over explicit index lists: the operator
+ * ElasticSparseAttentionFunction.forward(q, k, v, sparse_indices,
+ * sparse_mask, sm_scale, num_kv_groups) (elastic_sparse_attention.py:241-297).
+ * indices [H, q_len, attn_length] with index_bytes 4 or 8, mask
+ * [H, q_len, attn_length] with mask_bytes 1, 4 or 8 (nonzero = valid).
+ * Query head h reads kv head h / (H / Hkv) (:89).  Semantics of the Triton
+ * kernel (:117-166): a valid entry whose index lies outside [0, kv_len)
+ * scores 0 against a zero key and value; an entry listed twice counts twice.
+ * A row with no valid entry gets output 0 and lse -inf. */
+esa_status esa_sparse_fwd(const esa_fwd_args* a, const void* indices,
+                          int32_t index_bytes, int64_t idx_stride_h,
+                          int64_t idx_stride_s, const void* mask,
+                          int32_t mask_bytes, int64_t mask_stride_h,
+                          int64_t mask_stride_s, int32_t attn_length,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ESA_H_ */

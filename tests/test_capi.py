@@ -1,0 +1,171 @@
+"""The C ABI on the CPU: the library loads, exports every entry point
+include/esa.h declares, rejects invalid arguments on the host with the
+documented status codes (nothing is launched), and plans LPT work lists.
+No test here calls a kernel."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import esa_native as en
+from esa_oracle import block_layout, elastic_indices
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "esa.h")).read()
+    return re.findall(r"^(?:esa_status|const char\*)\s+(esa_\w+)\(", text, re.M)
+
+
+def test_library_exports_header_symbols():
+    lib = en.load()
+    names = header_functions()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(en.EXPORTED)
+    assert lib.esa_version().decode().startswith("esa-gfx950")
+    assert lib.esa_status_string(en.ESA_ERR_ALIGN).decode() == "misaligned pointer or stride"
+
+
+def pat(L=32768, w=64, layer=4, nl=8, H=32, bm=128, bn=128):
+    return en.EsaPattern(L, w, layer, nl, H, bm, bn)
+
+
+def test_layout_sizes():
+    lib = en.load()
+    nqb, nkb, mt, ws = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64(), ctypes.c_size_t()
+    p = pat()
+    assert lib.esa_layout_sizes(ctypes.byref(p), ctypes.byref(nqb), ctypes.byref(nkb),
+                                ctypes.byref(mt), ctypes.byref(ws)) == en.ESA_OK
+    assert (nqb.value, nkb.value) == (256, 256)
+    assert mt.value == 32 * sum(qb + 1 for qb in range(256))
+    assert mt.value >= 633512
+    assert ws.value >= 32 * 256 * 8 * 4 + 32 * 256 * 4
+    for bad in [pat(L=0), pat(w=0), pat(nl=0), pat(H=0), pat(bm=0)]:
+        assert lib.esa_layout_sizes(ctypes.byref(bad), None, None, None, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_layout_sizes(None, None, None, None, None) == en.ESA_ERR_NULL
+
+
+def test_layout_capacity_bound_holds():
+    """The col_idx bound esa_layout_sizes reports covers the real layout."""
+    lib = en.load()
+    for (L, H, w, nl, layer, bm, bn) in [(1000, 3, 48, 6, 5, 128, 128), (777, 2, 16, 4, 3, 64, 32),
+                                         (1024, 4, 64, 8, 7, 128, 128)]:
+        p = en.EsaPattern(L, w, layer, nl, H, bm, bn)
+        mt = ctypes.c_int64()
+        assert lib.esa_layout_sizes(ctypes.byref(p), None, None, ctypes.byref(mt), None) == 0
+        idx, msk = elastic_indices(L, layer, nl, H, w)
+        rp, _ = block_layout(idx, msk, bm, bn)
+        assert int(rp[-1]) <= mt.value
+
+
+def test_build_entry_points_reject_bad_arguments():
+    lib = en.load()
+    p = pat(L=1024, H=4)
+    fake = ctypes.c_void_p(4096)
+    assert lib.esa_build_indices(ctypes.byref(p), 0, 10, fake, fake, 2, None) == en.ESA_ERR_DTYPE
+    assert lib.esa_build_indices(ctypes.byref(p), 1000, 100, fake, fake, 8, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_build_indices(ctypes.byref(p), 0, 0, fake, fake, 8, None) == en.ESA_OK
+    assert lib.esa_build_layout(ctypes.byref(p), None, fake, 1 << 20, fake, 1 << 20, None) == en.ESA_ERR_NULL
+    assert lib.esa_build_layout(ctypes.byref(p), fake, fake, 1, fake, 1 << 20, None) == en.ESA_ERR_CAPACITY
+    assert lib.esa_build_layout(ctypes.byref(p), fake, fake, 1 << 20, fake, 4, None) == en.ESA_ERR_CAPACITY
+
+
+def fwd_args(dtype=en.ESA_BF16, B=1, H=4, Hkv=4, Lq=256, Lk=256, D=128, ptr=4096):
+    a = en.EsaFwdArgs()
+    a.dtype, a.batch, a.num_heads, a.num_kv_heads = dtype, B, H, Hkv
+    a.q_len, a.kv_len, a.head_dim = Lq, Lk, D
+    a.q = a.k = a.v = a.o = ptr
+    for t in "qkvo":
+        setattr(a, f"{t}_stride_b", H * Lk * D)
+        setattr(a, f"{t}_stride_h", Lk * D)
+        setattr(a, f"{t}_stride_s", D)
+    a.lse = None
+    a.sm_scale = D ** -0.5
+    return a
+
+
+def test_forward_entry_points_reject_bad_arguments():
+    lib = en.load()
+    p = pat(L=1024, H=4)
+    fake = ctypes.c_void_p(4096)
+    n = 4 * 2
+
+    def call(a, pp=p, items=n):
+        return lib.esa_elastic_fwd(ctypes.byref(a), ctypes.byref(pp), fake, fake, fake, items, None)
+
+    a = fwd_args()
+    a.q = None
+    assert call(a) == en.ESA_ERR_NULL
+    assert call(fwd_args(dtype=en.ESA_F32)) == en.ESA_ERR_DTYPE
+    assert call(fwd_args(dtype=7)) == en.ESA_ERR_DTYPE
+    assert call(fwd_args(D=96)) == en.ESA_ERR_UNSUPPORTED
+    assert call(fwd_args(Hkv=3)) == en.ESA_ERR_SHAPE
+    assert call(fwd_args(Lq=512, Lk=256)) == en.ESA_ERR_SHAPE
+    assert call(fwd_args(H=8, Hkv=8)) == en.ESA_ERR_SHAPE  # pattern has 4 heads
+    assert call(fwd_args(), items=7) == en.ESA_ERR_SHAPE
+    assert call(fwd_args(ptr=4100)) == en.ESA_ERR_ALIGN
+    a = fwd_args()
+    a.k_stride_s = 130
+    assert call(a) == en.ESA_ERR_ALIGN
+    assert call(fwd_args(), pp=pat(L=1024, H=4, bm=64)) == en.ESA_ERR_UNSUPPORTED
+    assert call(fwd_args(), pp=pat(L=1024, H=4, layer=9)) == en.ESA_ERR_UNSUPPORTED
+
+    assert lib.esa_elastic_fwd_rows(ctypes.byref(fwd_args(D=258)), ctypes.byref(p), None, None) \
+        == en.ESA_ERR_UNSUPPORTED
+    assert lib.esa_elastic_fwd_rows(ctypes.byref(fwd_args(Lq=300, Lk=256)), ctypes.byref(p), None,
+                                    None) == en.ESA_ERR_SHAPE
+    assert lib.esa_sparse_fwd(ctypes.byref(fwd_args()), fake, 2, 0, 0, fake, 1, 0, 0, 64, None) \
+        == en.ESA_ERR_DTYPE
+    assert lib.esa_sparse_fwd(ctypes.byref(fwd_args()), fake, 8, 0, 0, fake, 2, 0, 0, 64, None) \
+        == en.ESA_ERR_DTYPE
+    assert lib.esa_sparse_fwd(ctypes.byref(fwd_args()), None, 8, 0, 0, fake, 1, 0, 0, 64, None) \
+        == en.ESA_ERR_NULL
+    assert lib.esa_sparse_fwd(ctypes.byref(fwd_args()), fake, 8, 0, 0, fake, 1, 0, 0, 0, None) \
+        == en.ESA_ERR_SHAPE
+
+
+def plan(p, row_ptr, q_len, batch):
+    lib = en.load()
+    nq = (q_len + p.block_m - 1) // p.block_m
+    cap = batch * p.num_heads * nq
+    items = torch.empty(max(cap, 1), dtype=torch.int32)
+    n = ctypes.c_int64()
+    rp = row_ptr.contiguous()
+    st = lib.esa_plan_schedule(ctypes.byref(p), ctypes.c_void_p(rp.data_ptr()), q_len, batch,
+                               ctypes.c_void_p(items.data_ptr()), cap, ctypes.byref(n))
+    return st, items[:n.value]
+
+
+@pytest.mark.parametrize("L,Lq,B,layer", [(1024, 1024, 1, 4), (1024, 700, 3, 7), (2048, 2048, 2, 0)])
+def test_plan_schedule_is_lpt_permutation(L, Lq, B, layer):
+    H, w = 4, 64
+    p = en.EsaPattern(L, w, layer, 8, H, 128, 128)
+    idx, msk = elastic_indices(L, layer, 8, H, w)
+    rp, _ = block_layout(idx, msk, 128, 128)
+    st, items = plan(p, rp, Lq, B)
+    assert st == en.ESA_OK
+    nqb = (L + 127) // 128
+    nq = (Lq + 127) // 128
+    expect = sorted(((b * H + h) * nqb + qb) for b in range(B) for h in range(H) for qb in range(nq))
+    assert sorted(items.tolist()) == expect
+    cost = [int(rp[(it // nqb) % H * nqb + it % nqb + 1] - rp[(it // nqb) % H * nqb + it % nqb])
+            for it in items.tolist()]
+    assert all(cost[i] >= cost[i + 1] for i in range(len(cost) - 1))
+
+
+def test_plan_schedule_rejects():
+    p = en.EsaPattern(1024, 64, 4, 8, 4, 128, 128)
+    rp = torch.zeros(4 * 8 + 1, dtype=torch.int32)
+    st, _ = plan(p, rp, 2048, 1)
+    assert st == en.ESA_ERR_SHAPE
+    lib = en.load()
+    n = ctypes.c_int64()
+    items = torch.empty(4, dtype=torch.int32)
+    assert lib.esa_plan_schedule(ctypes.byref(p), ctypes.c_void_p(rp.data_ptr()), 1024, 1,
+                                 ctypes.c_void_p(items.data_ptr()), 4, ctypes.byref(n)) \
+        == en.ESA_ERR_CAPACITY
