@@ -51,8 +51,7 @@ def cpu_baseline(cfg_name: str, layer: int, counted_flops: float, rows_per_run: 
     from esa_oracle import elastic_indices, naive_forward, seeded_inputs
 
     B, H, L, D, scale, outl = CONFIGS[cfg_name]
-    torch.set_num_threads(torch.get_num_threads())
-    cores = torch.get_num_threads()
+    cores = torch.get_num_threads()  # OMP_NUM_THREADS, else the host's cores
     q, k, v = seeded_inputs(B, H, H, L, D, torch.bfloat16, seed=0, scale=scale,
                             outlier_frac=outl)
     t0 = time.perf_counter()
@@ -79,6 +78,34 @@ def cpu_baseline(cfg_name: str, layer: int, counted_flops: float, rows_per_run: 
             "seconds_per_forward": full_s, "layout_build_s": layout_s}
 
 
+COPY_BYTES = 1 << 30
+
+
+def copy_calibration(torch) -> None:
+    """A plain device-to-device copy of COPY_BYTES, three times: the kernel
+    whose FETCH_SIZE / WRITE_SIZE readings scale the counters to bytes."""
+    dev = torch.device("cuda", 0)
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "copies": 3}), flush=True)
+
+
+def traffic_from_profile(name: str):
+    """HBM bytes per launch of the forward kernel, from the committed rocprofv3
+    --pmc summary for this workload (profiles/<name>), or None."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1].strip()))
+    return None
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -87,6 +114,8 @@ def main() -> None:
     ap.add_argument("--config", default="32k", choices=sorted(CONFIGS))
     ap.add_argument("--layer", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain device copy of known size (HBM counter scale)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU; the forward is a "
@@ -95,6 +124,9 @@ def main() -> None:
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        copy_calibration(torch)
+        return
     from elastic_sparse_attention import ElasticSparseAttention
 
     B, H, L, D, scale, outl = CONFIGS[args.config]
@@ -132,34 +164,34 @@ def main() -> None:
     for _ in range(args.warmup):
         m(q, k, v)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        m(q, k, v)
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / args.steps
-
-    # kernel duration: events around each launch on the launch (current) stream
+    # timed region: K forwards, each bracketed by HIP events on the stream the
+    # module launches on (torch's current stream), wall clock around all K
     stream = torch.cuda.current_stream(dev)
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
     for s_ev, e_ev in evs:
         s_ev.record(stream)
         m(q, k, v)
         e_ev.record(stream)
     torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
     kern_ms = statistics.mean(s.elapsed_time(e) for s, e in evs)
 
     achieved = counted / (kern_ms * 1e-3) / 1e12
     value = counted / wall / 1e12
+    traffic = traffic_from_profile(
+        f"tile_fwd_kernel_bf16_B{B}_H{H}_L{L}_D{D}_layer{args.layer}_pmc.md")
     if args.layer == 0:
         # a plain sliding window: ~127 flop/B, below the MFMA ridge -> HBM-bound
         gbs = alg_bytes / (kern_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
-                    "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None}
+                    "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic}
     else:
         roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                    "traffic": None}
+                    "traffic": traffic}
     out = {
         "metric": METRIC,
         "value": round(value, 3),
