@@ -106,6 +106,50 @@ esa_status check_gather_layout(const esa_fwd_args* a) {
   return ESA_OK;
 }
 
+// Work list of the block-sparse forward, laid out for the 8 XCDs of MI355X.
+//
+// Consecutive workgroup ids are dispatched round-robin over the XCDs
+// (id % 8), and each XCD has its own L2.  Every (batch, head) stream -- all
+// query blocks of one head -- is a run of items; streams are walked in
+// (batch, head) order (heads that share a kv head stay adjacent), each
+// stream's query blocks longest first, and the walk is cut into 8 runs of
+// equal tile count.  Run x goes to grid slots x, x + 8, x + 16, ..., so one
+// XCD works through one or two heads' K/V at a time (their tiles stay in
+// its L2) and ends on the cheapest blocks of its last stream.  Runs shorter
+// than the longest are padded with -1 (an empty workgroup).
+void plan_xcd_grid(const int32_t* row_ptr, int nqb, int nq, int batch, int H,
+                   std::vector<int32_t>& grid) {
+  constexpr int kXcd = 8;
+  int64_t total = 0;
+  for (int h = 0; h < H; ++h)
+    total += (int64_t)(row_ptr[(int64_t)h * nqb + nq] - row_ptr[(int64_t)h * nqb]) * batch;
+  const int64_t n = (int64_t)batch * H * nq;
+  std::vector<std::vector<int32_t>> runs(kXcd);
+  int64_t cum = 0;
+  int x = 0;
+  for (int b = 0; b < batch; ++b) {
+    for (int h = 0; h < H; ++h) {
+      for (int qb = nq - 1; qb >= 0; --qb) {
+        const int64_t row = (int64_t)h * nqb + qb;
+        const int64_t c = row_ptr[row + 1] - row_ptr[row];
+        // move on once this run holds its share of the tiles (by item count
+        // when the layout has no tiles at all)
+        while (x < kXcd - 1 &&
+               (total > 0 ? cum * kXcd >= (int64_t)(x + 1) * total
+                          : (int64_t)runs[x].size() * kXcd >= n))
+          ++x;
+        runs[x].push_back((int32_t)(((int64_t)b * H + h) * nqb + qb));
+        cum += c;
+      }
+    }
+  }
+  size_t len = 0;
+  for (auto& r : runs) len = std::max(len, r.size());
+  grid.assign(len * kXcd, -1);
+  for (int r = 0; r < kXcd; ++r)
+    for (size_t i = 0; i < runs[r].size(); ++i) grid[i * kXcd + r] = runs[r][i];
+}
+
 esa_status hip_status(hipError_t e) { return e == hipSuccess ? ESA_OK : ESA_ERR_HIP; }
 
 }  // namespace
@@ -174,31 +218,19 @@ esa_status esa_plan_schedule(const esa_pattern* p, const int32_t* row_ptr_host, 
                              int64_t* num_items) {
   esa_status s = check_pattern(p);
   if (s != ESA_OK) return s;
-  if (!row_ptr_host || !items_host || !num_items) return ESA_ERR_NULL;
+  if (!row_ptr_host || !num_items) return ESA_ERR_NULL;
   if (q_len < 0 || q_len > p->seq_len || batch < 0) return ESA_ERR_SHAPE;
   const LayoutDims d = dims_of(*p);
+  if ((int64_t)batch * p->num_heads * d.nqb > INT32_MAX) return ESA_ERR_SHAPE;
   const int nq = (q_len + p->block_m - 1) / p->block_m;
   const int64_t n = (int64_t)batch * p->num_heads * nq;
-  if ((int64_t)batch * p->num_heads * d.nqb > INT32_MAX) return ESA_ERR_SHAPE;
-  if (items_capacity < n) return ESA_ERR_CAPACITY;
-  // (cost, head-major position) pairs over (h, qb); the batch index repeats
-  // each pair, so sort once and expand.
-  std::vector<int64_t> order((size_t)p->num_heads * nq);
-  std::iota(order.begin(), order.end(), 0);
-  auto cost = [&](int64_t hq) {
-    const int64_t h = hq / nq, qb = hq % nq;
-    const int64_t row = h * d.nqb + qb;
-    return row_ptr_host[row + 1] - row_ptr_host[row];
-  };
-  std::stable_sort(order.begin(), order.end(),
-                   [&](int64_t x, int64_t y) { return cost(x) > cost(y); });
-  int64_t k = 0;
-  for (int64_t hq : order) {
-    const int64_t h = hq / nq, qb = hq % nq;
-    for (int b = 0; b < batch; ++b)
-      items_host[k++] = (int32_t)(((int64_t)b * p->num_heads + h) * d.nqb + qb);
-  }
-  *num_items = n;
+  std::vector<int32_t> grid;
+  plan_xcd_grid(row_ptr_host, d.nqb, nq, batch, p->num_heads, grid);
+  *num_items = (int64_t)grid.size();
+  if (!items_host) return ESA_OK;  // size query
+  if (items_capacity < (int64_t)grid.size()) return ESA_ERR_CAPACITY;
+  std::copy(grid.begin(), grid.end(), items_host);
+  (void)n;
   return ESA_OK;
 }
 
@@ -221,7 +253,10 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
   if (a->q_len > a->kv_len || a->q_len > p->seq_len) return ESA_ERR_SHAPE;
   const LayoutDims d = dims_of(*p);
   const int nq = (a->q_len + 127) / 128;
-  if (num_items != (int64_t)a->batch * a->num_heads * nq) return ESA_ERR_SHAPE;
+  // a plan from esa_plan_schedule holds every item once plus at most 7 pads
+  // per item slot row
+  const int64_t n_real = (int64_t)a->batch * a->num_heads * nq;
+  if (num_items < n_real || num_items > 8 * std::max<int64_t>(n_real, 1)) return ESA_ERR_SHAPE;
   // 16-byte row loads and 8-byte output stores.
   if (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16) || !aligned(a->o, 8))
     return ESA_ERR_ALIGN;
@@ -242,7 +277,8 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
   t.osb = a->o_stride_b; t.osh = a->o_stride_h; t.oss = a->o_stride_s;
   t.lsb = a->lse_stride_b; t.lsh = a->lse_stride_h;
   t.H = a->num_heads; t.groups = a->num_heads / a->num_kv_heads;
-  t.q_len = a->q_len; t.kv_len = a->kv_len; t.nqb = d.nqb;
+  t.q_len = a->q_len; t.kv_len = a->kv_len; t.nqb = d.nqb; t.nq = nq;
+  t.num_bh = a->batch * a->num_heads;
   t.scale_log2 = a->sm_scale * 1.4426950408889634f;
   t.pc = make_consts(*p);
   t.row_ptr = row_ptr; t.col_idx = col_idx; t.items = items;

@@ -3,23 +3,36 @@
 // Replaces the forward branch of the reference's per-token Triton kernel
 // (elastic_sparse_attention.py:117-166) for prefill.  One workgroup (4 waves,
 // 256 lanes) owns one (batch, head, 128-row query block) work item and visits
-// only the 128-key tiles the block layout lists as active for it.
+// only the 128-key tiles the block layout lists as active for it; every
+// active tile is computed densely (128 x 128 x D on MFMA), so the executed
+// tile equals the layout tile.
 //
-// Per tile and wave (32 query rows):
-//   S^T = K Q^T    32 x v_mfma_f32_32x32x16_bf16 (A = K rows from LDS,
+// Per tile (workgroup) and wave (32 query rows):
+//   prefetch       the next tile's K and V rows are loaded into registers
+//                  (16-byte loads) while this tile computes, and written to
+//                  LDS after it
+//   mask           each lane owns one query row; rows whose index list is a
+//                  contiguous run (the sliding window of layer 0, and the
+//                  first w - 1 rows of every layer) set a bit range, the
+//                  others walk their elastic indices (the same float32
+//                  sequence as the layout builder) through the tile
+// then for each 32-key block of the tile:
+//   S^T = K Q^T    8 (D=128) x v_mfma_f32_32x32x16_bf16 (A = K rows from LDS,
 //                  B = Q kept in registers for the whole item)
-//   mask           each lane regenerates its row's elastic indices inside the
-//                  tile (the same float32 sequence as the layout builder)
-//   softmax        online, per lane: the S^T accumulator layout gives every
-//                  lane one query row (lane % 32) and 64 of the tile's keys,
-//                  so the row max needs one cross-half exchange and nothing
-//                  else; the running max and sum stay in registers
-//   O^T += V^T P^T 32 x v_mfma_f32_32x32x16_bf16 (A = V^T read with
+//   softmax        online, in registers, log2 domain.  The S^T accumulator
+//                  layout gives each lane one row and 16 of the block's keys
+//                  in 4 groups of 4; a group that holds no valid key in any
+//                  lane of the wave is skipped (its probabilities are 0).  At
+//                  dilated layers a row has about one valid key per tile, so
+//                  most groups are skipped.  The running max is raised only
+//                  when a row's block max exceeds it by more than 8 (log2), so
+//                  the O rescale is rare; probabilities stay below 2^8.
+//   O^T += V^T P^T 8 (D=128) x v_mfma_f32_32x32x16_bf16 (A = V^T read with
 //                  ds_read_b64_tr_b16 from row-major V in LDS, B = P straight
 //                  from the S^T accumulators: a key permutation shared by
 //                  both operands leaves the contraction unchanged)
 //
-// MFMA 32x32x16 register layouts (checked on gfx950):
+// MFMA 32x32x16 register layouts (gfx950):
 //   A[i][k]: lane l holds i = l%32, k = 8*(l/32) + e, e = 0..7
 //   B[k][j]: lane l holds k = 8*(l/32) + e, j = l%32
 //   C[i][j]: lane l, reg r holds i = 8*(r/4) + 4*(l/32) + r%4, j = l%32
@@ -33,16 +46,45 @@ template <int D>
 struct TileCfg {
   static constexpr int BM = 128;
   static constexpr int BN = 128;
-  static constexpr int KSTR = D + 8;   // K row pitch (elements): conflict-free b128 reads
-  static constexpr int VSTR = D + 16;  // V row pitch: conflict-free transposed reads
-  static constexpr int NS = D / 16;    // k-steps of QK^T
-  static constexpr int ND = D / 32;    // 32-wide d blocks of PV
-  static constexpr int CPR = D / 8;    // 16-byte chunks per row
+  static constexpr int KSTR = D + 8;     // K row pitch (elements): conflict-free b128 reads
+  static constexpr int VSTR = D + 16;    // V row pitch: conflict-free transposed reads
+  static constexpr int NS = D / 16;      // k-steps of QK^T
+  static constexpr int ND = D / 32;      // 32-wide d blocks of PV
+  static constexpr int CPR = D / 8;      // 16-byte chunks per row
   static constexpr int RPP = 256 / CPR;  // rows staged per pass
+  static constexpr int NP = BN / RPP;    // staging passes per tile
 };
+
+// Rows whose index list is a contiguous run and whose indices are exact in
+// float32 (the interpolation of equal integers x reproduces x when x < 2^21).
+constexpr int kContigLimit = 1 << 21;
+// Lazy rescale threshold (log2 units): the running max moves only when a
+// tile raises a row's max by more than this, so probabilities stay <= 2^8.
+constexpr float kRescaleSlack = 8.0f;
 
 __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 v;
+  v[0] = (__bf16)lo;
+  v[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Bits [a - 32 w, b - 32 w] of word w of a 128-bit mask (a <= b, both in [0, 127]).
+__device__ __forceinline__ uint32_t range_word(int a, int b, int w) {
+  const int lo = max(a - 32 * w, 0);
+  const int hi = min(b - 32 * w, 31);
+  const int n = hi - lo;
+  const uint32_t bits = (0xffffffffu >> ((31 - n) & 31)) << (lo & 31);
+  return n >= 0 ? bits : 0u;
+}
+
+__device__ __forceinline__ bool wave_any(bool p) {
+  return __builtin_amdgcn_ballot_w64(p) != 0;
 }
 
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -53,16 +95,19 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[C::BN * C::KSTR];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[C::BN * C::VSTR];
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int hf = lane >> 5, l32 = lane & 31;
-
+  // ---- work item (uniform over the workgroup; -1 pads the XCD runs)
   const int item = A.items[blockIdx.x];
+  if (item < 0 || item >= A.num_bh * A.nqb) return;
   const int qb = item % A.nqb;
+  if (qb >= A.nq) return;
   const int bh = item / A.nqb;
   const int h = bh % A.H;
   const int b = bh / A.H;
   const int kvh = h / A.groups;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int hf = lane >> 5, l32 = lane & 31;
 
   const int i = qb * C::BM + wave * 32 + l32;  // this lane's query row = position
   const bool row_ok = i < A.q_len;
@@ -79,13 +124,18 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
     }
   }
 
+  // ---- this row's index list
   const HeadWeights hw = head_weights(A.pc, h);
   const RowParams rp = row_params(A.pc, i);
-  int jp = row_ok ? 0 : A.pc.w;  // next unread entry of this row's index list
-  int o_cur = rp.st;             // o_jp
+  const bool contig = row_ok && rp.sp == 1.0f && i < kContigLimit;
+  const int c_lo = rp.st;                                // contiguous run [c_lo, c_hi]
+  const int c_hi = min(rp.st + A.pc.w - 1, i);
+  int jp = (row_ok && !contig) ? 0 : A.pc.w;  // next unread entry of a dilated list
+  int o_cur = rp.st;                          // o_jp
 
-  float m_run = -INFINITY;  // running max, log2 units
-  float l_run = 0.f;        // running sum over this lane's half of the keys
+  float m_run = -INFINITY;  // running max, log2 units (the same in both halves)
+  float l_run = 0.f;        // running sum of p over this lane's half of the keys (-> lse)
+  float n_run = 0.f;        // the same sum of p rounded to bf16, as PV sees it (-> O)
   f32x16 oacc[C::ND];
 #pragma unroll
   for (int d = 0; d < C::ND; ++d) oacc[d] = f32x16{};
@@ -95,38 +145,49 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   const int64_t lrow = (int64_t)h * A.nqb + qb;
   const int t0 = A.row_ptr[lrow], t1 = A.row_ptr[lrow + 1];
 
+  // ---- K/V staging: registers <- HBM (one tile ahead), LDS <- registers.
+  // Keys past kv_len read the last row instead: they are never valid (valid
+  // indices are <= the query position < q_len <= kv_len), so their
+  // probabilities are 0 and the values only need to be finite.
+  const int srow = tid / C::CPR, scol = 8 * (tid % C::CPR);
+  u32x4 kpre[C::NP], vpre[C::NP];
+  auto load_tile = [&](int kt) {
+    const int kbase = A.col_idx[kt] * C::BN;
+#pragma unroll
+    for (int p = 0; p < C::NP; ++p) {
+      const int key = min(kbase + p * C::RPP + srow, A.kv_len - 1);
+      kpre[p] = *(const u32x4*)(kg + (int64_t)key * A.kss + scol);
+      vpre[p] = *(const u32x4*)(vg + (int64_t)key * A.vss + scol);
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int p = 0; p < C::NP; ++p) {
+      const int r = p * C::RPP + srow;
+      *(u32x4*)(Ks + r * C::KSTR + scol) = kpre[p];
+      *(u32x4*)(Vs + r * C::VSTR + scol) = vpre[p];
+    }
+  };
+
+  if (t0 < t1) {
+    load_tile(t0);
+    store_tile();
+  }
+  __syncthreads();
+
   for (int t = t0; t < t1; ++t) {
     const int k0 = A.col_idx[t] * C::BN;
-
-    // ---- stage the K and V tiles (row-major) in LDS; rows past kv_len are 0
-#pragma unroll
-    for (int p = 0; p < C::BN / C::RPP; ++p) {
-      const int r = p * C::RPP + tid / C::CPR, c = tid % C::CPR;
-      const int key = k0 + r;
-      u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-      if (key < A.kv_len) {
-        kv = *(const u32x4*)(kg + (int64_t)key * A.kss + 8 * c);
-        vv = *(const u32x4*)(vg + (int64_t)key * A.vss + 8 * c);
-      }
-      *(u32x4*)(Ks + r * C::KSTR + 8 * c) = kv;
-      *(u32x4*)(Vs + r * C::VSTR + 8 * c) = vv;
-    }
-    __syncthreads();
-
-    // ---- S^T = K Q^T: block kb holds keys 32kb..32kb+31 x this wave's 32 rows
-    f32x16 sacc[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      sacc[kb] = f32x16{};
-#pragma unroll
-      for (int s = 0; s < C::NS; ++s) {
-        const bf16x8 a = *(const bf16x8*)(Ks + (32 * kb + l32) * C::KSTR + 16 * s + 8 * hf);
-        sacc[kb] = mfma32(a, qop[s], sacc[kb]);
-      }
-    }
+    if (t + 1 < t1) load_tile(t + 1);
 
     // ---- this row's valid keys inside [k0, k0 + 128) as a 128-bit mask
-    uint32_t mb0 = 0u, mb1 = 0u, mb2 = 0u, mb3 = 0u;
+    uint32_t mb[4] = {0u, 0u, 0u, 0u};
+    if (contig) {
+      const int a = max(c_lo, k0) - k0, e = min(c_hi, k0 + C::BN - 1) - k0;
+      if (a <= e) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) mb[w] = range_word(a, e, w);
+      }
+    }
     while (jp < A.pc.w) {
       const int o_next = oversized(rp, jp + 1);
       const int idx = interp_index(o_cur, o_next, hw);
@@ -139,84 +200,117 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
       if (rel >= 0) {
         const uint32_t bit = 1u << (rel & 31);
         const int wsel = rel >> 5;
-        mb0 |= wsel == 0 ? bit : 0u;
-        mb1 |= wsel == 1 ? bit : 0u;
-        mb2 |= wsel == 2 ? bit : 0u;
-        mb3 |= wsel == 3 ? bit : 0u;
+        mb[0] |= wsel == 0 ? bit : 0u;
+        mb[1] |= wsel == 1 ? bit : 0u;
+        mb[2] |= wsel == 2 ? bit : 0u;
+        mb[3] |= wsel == 3 ? bit : 0u;
       }
       o_cur = o_next;
       ++jp;
     }
-    // lane half hf holds keys 32kb + 8*(r/4) + 4*hf + r%4: pre-shift by 4*hf
-    const uint32_t mk[4] = {mb0 >> (4 * hf), mb1 >> (4 * hf), mb2 >> (4 * hf), mb3 >> (4 * hf)};
 
-    // ---- online softmax (log2 domain)
-    float smax = -INFINITY;
+    // ---- per 32-key block kb: S^T = K Q^T, online softmax, O^T += V^T P^T
+    const int g4 = lane >> 4, lam = lane & 15;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
+      f32x16 sacc = f32x16{};
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const bool on = (mk[kb] >> (8 * (r / 4) + (r % 4))) & 1u;
-        const float s = on ? sacc[kb][r] * A.scale_log2 : -INFINITY;
-        sacc[kb][r] = s;
-        smax = fmaxf(smax, s);
+      for (int s = 0; s < C::NS; ++s) {
+        const bf16x8 a = *(const bf16x8*)(Ks + (32 * kb + l32) * C::KSTR + 16 * s + 8 * hf);
+        sacc = mfma32(a, qop[s], sacc);
       }
-    }
-    smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
-    const float m_new = fmaxf(m_run, smax);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    float psum = 0.f;
-    bf16x8 pb[4][2];
+      // lane half hf holds keys 32kb + 8*(r/4) + 4*hf + r%4
+      const uint32_t mk = mb[kb] >> (4 * hf);
+      bool act[4];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(sacc[kb][r] - m_use);
-        psum += p;
-        pb[kb][r / 8][r % 8] = (__bf16)p;
-      }
-    }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int d = 0; d < C::ND; ++d) oacc[d] *= alpha;
+      for (int g = 0; g < 4; ++g) act[g] = wave_any(((mk >> (8 * g)) & 0xfu) != 0u);
 
-    // ---- O^T += V^T P^T
-    const int g = lane >> 4, lam = lane & 15;
+      float smax = -INFINITY;
 #pragma unroll
-    for (int d = 0; d < C::ND; ++d) {
+      for (int g = 0; g < 4; ++g) {
+        if (act[g]) {
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g + e;
+            const bool on = (mk >> (8 * g + e)) & 1u;
+            const float x = on ? sacc[r] * A.scale_log2 : -INFINITY;
+            sacc[r] = x;
+            smax = fmaxf(smax, x);
+          }
+        }
+      }
+      smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
+      const bool grow = smax > m_run + kRescaleSlack;
+      if (wave_any(grow)) {
+        // rows that do not grow keep alpha = 1 (m_run may still be -inf there)
+        const float m_new = grow ? smax : m_run;
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 from -inf
+        l_run *= alpha;
+        n_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < C::ND; ++d) oacc[d] *= alpha;
+        m_run = m_new;
+      }
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+
+      uint32_t pw[8];  // P as packed bf16 pairs: pw[q] holds regs 2q, 2q+1
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        if (act[g]) {
+          float p[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            p[e] = __builtin_amdgcn_exp2f(sacc[4 * g + e] - m_use);
+            l_run += p[e];
+          }
+          pw[2 * g] = pack_bf16x2(p[0], p[1]);
+          pw[2 * g + 1] = pack_bf16x2(p[2], p[3]);
+          // normalise O by the probabilities PV actually used, so a row led
+          // by one key reproduces that key's value row
+          n_run += __uint_as_float(pw[2 * g] << 16) + __uint_as_float(pw[2 * g] & 0xffff0000u);
+          n_run += __uint_as_float(pw[2 * g + 1] << 16) +
+                   __uint_as_float(pw[2 * g + 1] & 0xffff0000u);
+        } else {
+          pw[2 * g] = 0u;
+          pw[2 * g + 1] = 0u;
+        }
+      }
+
+#pragma unroll
+      for (int d = 0; d < C::ND; ++d) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int key = 32 * kb + 16 * u + 4 * hf + (lam >> 2);
-          const int col = 32 * d + 16 * (g & 1) + 4 * (lam & 3);
+          const int col = 32 * d + 16 * (g4 & 1) + 4 * (lam & 3);
           const uint16_t* p1 = Vs + key * C::VSTR + col;
           const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p1);
           const s16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1 + 8 * C::VSTR));
           const s16x4 vv[2] = {v1, v2};
           const bf16x8 a = __builtin_bit_cast(bf16x8, vv);
-          oacc[d] = mfma32(a, pb[kb][u], oacc[d]);
+          const u32x4 pq = {pw[4 * u], pw[4 * u + 1], pw[4 * u + 2], pw[4 * u + 3]};
+          oacc[d] = mfma32(a, __builtin_bit_cast(bf16x8, pq), oacc[d]);
         }
       }
     }
+    __syncthreads();
+    if (t + 1 < t1) store_tile();
     __syncthreads();
   }
 
   // ---- epilogue: normalise and store O rows and the log-sum-exp
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float n_tot = n_run + __shfl_xor(n_run, 32, 64);
   if (row_ok) {
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const float inv = n_tot > 0.f ? 1.f / n_tot : 0.f;
     uint16_t* orow = A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)i * A.oss;
 #pragma unroll
     for (int d = 0; d < C::ND; ++d) {
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
+      for (int q4 = 0; q4 < 4; ++q4) {
         bf16x4 ov;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) ov[e] = (__bf16)(oacc[d][4 * g4 + e] * inv);
-        *(bf16x4*)(orow + 32 * d + 8 * g4 + 4 * hf) = ov;
+        for (int e = 0; e < 4; ++e) ov[e] = (__bf16)(oacc[d][4 * q4 + e] * inv);
+        *(bf16x4*)(orow + 32 * d + 8 * q4 + 4 * hf) = ov;
       }
     }
     if (A.lse && hf == 0) {

@@ -23,7 +23,10 @@ struct TileArgs {
   int64_t vsb, vsh, vss;
   int64_t osb, osh, oss;
   int64_t lsb, lsh;
-  int H, groups, q_len, kv_len, nqb;
+  int H, groups, q_len, kv_len;
+  int nqb;     // query blocks per head in the layout
+  int nq;      // query blocks a q_len-row forward visits (<= nqb)
+  int num_bh;  // batch * H
   float scale_log2;  // sm_scale * log2(e)
   PatternConsts pc;
   const int32_t* row_ptr;

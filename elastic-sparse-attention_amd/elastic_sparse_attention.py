@@ -135,8 +135,8 @@ class ElasticLayout:
     ``row_ptr`` (int32 ``[H * nqb + 1]``) and ``col_idx`` (int32) list, for
     every (head, 128-row query block), the ascending 128-key tiles holding at
     least one valid entry.  Built by the HIP layout builder; the host keeps a
-    copy of ``row_ptr`` for the LPT work lists (``schedule``), one per
-    (q_len, batch), cached.
+    copy of ``row_ptr`` for the work lists (``schedule``, XCD-ordered), one
+    per (q_len, batch), cached.
     """
 
     def __init__(self, pattern: EsaPattern, device: torch.device):
@@ -178,12 +178,13 @@ class ElasticLayout:
         if got is not None:
             return got
         lib = load()
-        nq = (q_len + self.pattern.block_m - 1) // self.pattern.block_m
-        cap = max(1, batch * self.pattern.num_heads * nq)
-        items = torch.empty(cap, dtype=torch.int32)
         n = ctypes.c_int64()
-        check(lib.esa_plan_schedule(ctypes.byref(self.pattern),
-                                    ctypes.c_void_p(self.row_ptr_host.data_ptr()), q_len, batch,
+        rp = ctypes.c_void_p(self.row_ptr_host.data_ptr())
+        check(lib.esa_plan_schedule(ctypes.byref(self.pattern), rp, q_len, batch, None, 0,
+                                    ctypes.byref(n)), "esa_plan_schedule")
+        cap = max(1, n.value)
+        items = torch.empty(cap, dtype=torch.int32)
+        check(lib.esa_plan_schedule(ctypes.byref(self.pattern), rp, q_len, batch,
                                     ctypes.c_void_p(items.data_ptr()), cap, ctypes.byref(n)),
               "esa_plan_schedule")
         got = (items.to(self.device), n.value)

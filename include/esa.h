@@ -113,12 +113,15 @@ esa_status esa_build_layout(const esa_pattern* p, int32_t* row_ptr,
                             void* stream);
 
 /* Host only.  Work list for esa_elastic_fwd: the (batch, head, query block)
- * items of a forward over q_len query rows, ordered for the device.  Replaces
- * the implicit Triton grid (q_len, H, B) (elastic_sparse_attention.py:261).
- * row_ptr_host is esa_build_layout's row_ptr copied to host memory.  Items
- * are ordered longest first (LPT), so the tail of the launch holds the
- * shortest query blocks.  Writes *num_items entries (batch * H *
- * ceil(q_len / block_m)) into items_host. */
+ * items of a forward over q_len query rows, laid out for the device.
+ * Replaces the implicit Triton grid (q_len, H, B)
+ * (elastic_sparse_attention.py:261).  row_ptr_host is esa_build_layout's
+ * row_ptr copied to host memory.  Item b * H * nqb + h * nqb + qb appears
+ * exactly once; the list is cut into 8 runs of equal tile count, one per
+ * XCD (workgroup id % 8), each run walking whole (batch, head) streams with
+ * their query blocks longest first, and shorter runs padded with -1 (an
+ * idle workgroup).  With items_host NULL only *num_items (the list length,
+ * at most 8 * batch * H * ceil(q_len / block_m)) is written. */
 esa_status esa_plan_schedule(const esa_pattern* p, const int32_t* row_ptr_host,
                              int32_t q_len, int32_t batch, int32_t* items_host,
                              int64_t items_capacity, int64_t* num_items);
@@ -130,7 +133,8 @@ esa_status esa_plan_schedule(const esa_pattern* p, const int32_t* row_ptr_host,
  * with float32 accumulation and online softmax.  Requires dtype ESA_BF16,
  * head_dim 64 or 128, block_m = block_n = 128, q_len <= kv_len,
  * q_len <= p->seq_len, 16-byte aligned rows.  items/num_items come from
- * esa_plan_schedule (copied to device memory). */
+ * esa_plan_schedule (copied to device memory); item ids outside the forward
+ * are skipped. */
 esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p,
                            const int32_t* row_ptr, const int32_t* col_idx,
                            const int32_t* items, int64_t num_items,

@@ -108,6 +108,7 @@ def test_forward_entry_points_reject_bad_arguments():
     assert call(fwd_args(Lq=512, Lk=256)) == en.ESA_ERR_SHAPE
     assert call(fwd_args(H=8, Hkv=8)) == en.ESA_ERR_SHAPE  # pattern has 4 heads
     assert call(fwd_args(), items=7) == en.ESA_ERR_SHAPE
+    assert call(fwd_args(), items=65) == en.ESA_ERR_SHAPE
     assert call(fwd_args(ptr=4100)) == en.ESA_ERR_ALIGN
     a = fwd_args()
     a.k_stride_s = 130
@@ -131,19 +132,25 @@ def test_forward_entry_points_reject_bad_arguments():
 
 def plan(p, row_ptr, q_len, batch):
     lib = en.load()
-    nq = (q_len + p.block_m - 1) // p.block_m
-    cap = batch * p.num_heads * nq
-    items = torch.empty(max(cap, 1), dtype=torch.int32)
     n = ctypes.c_int64()
     rp = row_ptr.contiguous()
     st = lib.esa_plan_schedule(ctypes.byref(p), ctypes.c_void_p(rp.data_ptr()), q_len, batch,
-                               ctypes.c_void_p(items.data_ptr()), cap, ctypes.byref(n))
+                               None, 0, ctypes.byref(n))
+    if st != en.ESA_OK:
+        return st, None
+    items = torch.empty(max(n.value, 1), dtype=torch.int32)
+    st = lib.esa_plan_schedule(ctypes.byref(p), ctypes.c_void_p(rp.data_ptr()), q_len, batch,
+                               ctypes.c_void_p(items.data_ptr()), n.value, ctypes.byref(n))
     return st, items[:n.value]
 
 
-@pytest.mark.parametrize("L,Lq,B,layer", [(1024, 1024, 1, 4), (1024, 700, 3, 7), (2048, 2048, 2, 0)])
-def test_plan_schedule_is_lpt_permutation(L, Lq, B, layer):
-    H, w = 4, 64
+@pytest.mark.parametrize("L,Lq,B,H,layer", [(1024, 1024, 1, 4, 4), (1024, 700, 3, 4, 7),
+                                            (2048, 2048, 2, 4, 0), (4096, 4096, 1, 32, 4),
+                                            (1000, 1000, 1, 1, 3), (300, 100, 1, 2, 5)])
+def test_plan_schedule_xcd_runs(L, Lq, B, H, layer):
+    """Every item once, -1 pads, 8 interleaved runs (slot % 8) of whole
+    streams walked longest block first, with balanced tile counts."""
+    w = 64
     p = en.EsaPattern(L, w, layer, 8, H, 128, 128)
     idx, msk = elastic_indices(L, layer, 8, H, w)
     rp, _ = block_layout(idx, msk, 128, 128)
@@ -151,11 +158,33 @@ def test_plan_schedule_is_lpt_permutation(L, Lq, B, layer):
     assert st == en.ESA_OK
     nqb = (L + 127) // 128
     nq = (Lq + 127) // 128
+    got = items.tolist()
+    assert len(got) % 8 == 0 and len(got) <= 8 * B * H * nq
     expect = sorted(((b * H + h) * nqb + qb) for b in range(B) for h in range(H) for qb in range(nq))
-    assert sorted(items.tolist()) == expect
-    cost = [int(rp[(it // nqb) % H * nqb + it % nqb + 1] - rp[(it // nqb) % H * nqb + it % nqb])
-            for it in items.tolist()]
-    assert all(cost[i] >= cost[i + 1] for i in range(len(cost) - 1))
+    assert sorted(x for x in got if x >= 0) == expect
+    assert all(x == -1 or x >= 0 for x in got)
+
+    def cost(it):
+        row = (it // nqb) % H * nqb + it % nqb
+        return int(rp[row + 1] - rp[row])
+
+    runs = [[x for x in got[r::8]] for r in range(8)]
+    flat = []
+    for run in runs:
+        real = [x for x in run if x >= 0]
+        assert run[:len(real)] == real  # pads only at the end of a run
+        flat += real
+        # within a stream, query blocks descend
+        for a, b in zip(real, real[1:]):
+            if a // nqb == b // nqb:
+                assert a % nqb > b % nqb
+    # the runs concatenated walk (batch, head) streams in order
+    assert [x // nqb for x in flat] == sorted(x // nqb for x in flat)
+    total = sum(cost(x) for x in expect)
+    biggest = max(cost(x) for x in expect)
+    for run in runs:
+        c = sum(cost(x) for x in run if x >= 0)
+        assert c <= total / 8 + biggest + 1
 
 
 def test_plan_schedule_rejects():
@@ -169,3 +198,5 @@ def test_plan_schedule_rejects():
     assert lib.esa_plan_schedule(ctypes.byref(p), ctypes.c_void_p(rp.data_ptr()), 1024, 1,
                                  ctypes.c_void_p(items.data_ptr()), 4, ctypes.byref(n)) \
         == en.ESA_ERR_CAPACITY
+    assert lib.esa_plan_schedule(ctypes.byref(p), None, 1024, 1, None, 0, ctypes.byref(n)) \
+        == en.ESA_ERR_NULL

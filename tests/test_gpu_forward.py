@@ -106,13 +106,20 @@ def full_size_check(B, H, L, D, layer, scale, outlier, seed, n_rows=384):
                       torch.randint(0, L, (n_rows,), generator=g)]).unique()
     ro, rl = oracle(q, k, v, idx, msk, sc, 1, rows)
     oc = to_bhsd(o)[:, :, rows.to(DEV)].float().cpu()
-    assert (oc - ro).abs().max().item() <= BF16_TOL
-    assert (lse[:, :, rows.to(DEV)].cpu() - rl).abs().max().item() <= BF16_LSE_TOL
-    # every row: MFMA kernel vs the independent gather kernel
-    og, lg = elastic_attention_rows(qd, kd, vd, make_pattern(L, 64, layer, 8, H), sc)
+    e_o = (oc - ro).abs().max().item()
+    e_l = (lse[:, :, rows.to(DEV)].cpu() - rl).abs().max().item()
+    print(f"  sampled rows vs oracle: o {e_o:.3e} lse {e_l:.3e}", flush=True)
+    assert e_o <= BF16_TOL and e_l <= BF16_LSE_TOL
+    # every row: against the per-row gather kernel run in float32 on the same
+    # (bf16-valued) inputs, itself held to 1e-4 of the oracle
+    # (test_rows_fp32_all_layers)
+    og, lg = elastic_attention_rows(qd.float(), kd.float(), vd.float(),
+                                    make_pattern(L, 64, layer, 8, H), sc)
     assert bool(torch.isfinite(o.float()).all())
-    assert (o.float() - og.float()).abs().max().item() <= BF16_TOL
-    assert (lse - lg).abs().max().item() <= BF16_LSE_TOL
+    e_o = (o.float() - og).abs().max().item()
+    e_l = (lse - lg).abs().max().item()
+    print(f"  every row vs fp32 gather: o {e_o:.3e} lse {e_l:.3e}", flush=True)
+    assert e_o <= BF16_TOL and e_l <= BF16_LSE_TOL
 
 
 @pytest.mark.parametrize("layer", [0, 4, 7])
@@ -120,7 +127,7 @@ def test_full_size_8k(layer):
     full_size_check(1, 32, 8192, 128, layer, 128 ** -0.25, 0.0, seed=20 + layer)
 
 
-@pytest.mark.parametrize("layer", [4])
+@pytest.mark.parametrize("layer", [0, 4, 7])
 def test_full_size_headline_32k(layer):
     full_size_check(1, 32, 32768, 128, layer, 128 ** -0.25, 0.0, seed=30 + layer, n_rows=256)
 
@@ -130,7 +137,7 @@ def test_full_size_batched_4k(layer):
     full_size_check(8, 16, 4096, 64, layer, 1.0, 0.0, seed=40 + layer, n_rows=128)
 
 
-@pytest.mark.parametrize("layer", [4, 7])
+@pytest.mark.parametrize("layer", [0, 4, 7])
 def test_full_size_long_outliers_128k(layer):
     full_size_check(1, 8, 131072, 128, layer, 1.0, 0.01, seed=50 + layer, n_rows=128)
 
