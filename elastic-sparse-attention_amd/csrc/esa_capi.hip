@@ -5,7 +5,7 @@
 #include <numeric>
 #include <vector>
 
-#include "../../include/esa.h"
+#include "esa.h"
 #include "esa_internal.hpp"
 
 using namespace esa;
@@ -251,6 +251,8 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
     return ESA_ERR_UNSUPPORTED;
   if (p->num_heads != a->num_heads) return ESA_ERR_SHAPE;
   if (a->q_len > a->kv_len || a->q_len > p->seq_len) return ESA_ERR_SHAPE;
+  // the kernel folds the key mask into the scaled score as -inf
+  if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale)) return ESA_ERR_UNSUPPORTED;
   const LayoutDims d = dims_of(*p);
   const int nq = (a->q_len + 127) / 128;
   // a plan from esa_plan_schedule holds every item once plus at most 7 pads

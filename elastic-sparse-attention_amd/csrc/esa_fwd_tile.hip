@@ -83,6 +83,13 @@ __device__ __forceinline__ uint32_t range_word(int a, int b, int w) {
   return n >= 0 ? bits : 0u;
 }
 
+// c + lo + hi of a packed bf16 pair, in float32 (v_dot2 with (1, 1))
+__device__ __forceinline__ float dot2_bf16(uint32_t pair, float c) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), one, c, false);
+}
+
 __device__ __forceinline__ bool wave_any(bool p) {
   return __builtin_amdgcn_ballot_w64(p) != 0;
 }
@@ -130,8 +137,17 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   const bool contig = row_ok && rp.sp == 1.0f && i < kContigLimit;
   const int c_lo = rp.st;                                // contiguous run [c_lo, c_hi]
   const int c_hi = min(rp.st + A.pc.w - 1, i);
-  int jp = (row_ok && !contig) ? 0 : A.pc.w;  // next unread entry of a dilated list
-  int o_cur = rp.st;                          // o_jp
+  // dilated rows: entry jp (index `pend`) is the next one not yet placed in a
+  // tile; kNone once the valid entries are used up
+  constexpr int kNone = 0x7fffffff;
+  int jp = 0;
+  int o_cur = rp.st, o_next = rp.st;
+  int pend = kNone;
+  if (row_ok && !contig) {
+    o_next = oversized(rp, 1);
+    pend = interp_index(o_cur, o_next, hw);
+    if (pend > i) pend = kNone;
+  }
 
   float m_run = -INFINITY;  // running max, log2 units (the same in both halves)
   float l_run = 0.f;        // running sum of p over this lane's half of the keys (-> lse)
@@ -140,8 +156,6 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
 #pragma unroll
   for (int d = 0; d < C::ND; ++d) oacc[d] = f32x16{};
 
-  const uint16_t* kg = A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh;
-  const uint16_t* vg = A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh;
   const int64_t lrow = (int64_t)h * A.nqb + qb;
   const int t0 = A.row_ptr[lrow], t1 = A.row_ptr[lrow + 1];
 
@@ -150,14 +164,27 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   // indices are <= the query position < q_len <= kv_len), so their
   // probabilities are 0 and the values only need to be finite.
   const int srow = tid / C::CPR, scol = 8 * (tid % C::CPR);
+  const uint16_t* kg = A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh + scol;
+  const uint16_t* vg = A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh + scol;
+  const int64_t kstep = (int64_t)C::RPP * A.kss, vstep = (int64_t)C::RPP * A.vss;
   u32x4 kpre[C::NP], vpre[C::NP];
   auto load_tile = [&](int kt) {
     const int kbase = A.col_idx[kt] * C::BN;
+    if (kbase + C::BN <= A.kv_len) {  // whole tile in range: strided rows
+      const uint16_t* kr = kg + (int64_t)(kbase + srow) * A.kss;
+      const uint16_t* vr = vg + (int64_t)(kbase + srow) * A.vss;
 #pragma unroll
-    for (int p = 0; p < C::NP; ++p) {
-      const int key = min(kbase + p * C::RPP + srow, A.kv_len - 1);
-      kpre[p] = *(const u32x4*)(kg + (int64_t)key * A.kss + scol);
-      vpre[p] = *(const u32x4*)(vg + (int64_t)key * A.vss + scol);
+      for (int p = 0; p < C::NP; ++p) {
+        kpre[p] = *(const u32x4*)(kr + p * kstep);
+        vpre[p] = *(const u32x4*)(vr + p * vstep);
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < C::NP; ++p) {
+        const int key = min(kbase + p * C::RPP + srow, A.kv_len - 1);
+        kpre[p] = *(const u32x4*)(kg + (int64_t)key * A.kss);
+        vpre[p] = *(const u32x4*)(vg + (int64_t)key * A.vss);
+      }
     }
   };
   auto store_tile = [&]() {
@@ -175,9 +202,13 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   }
   __syncthreads();
 
+  const float scale = A.scale_log2;  // > 0 (checked on the host)
+  const int g4 = lane >> 4, lam = lane & 15;
   for (int t = t0; t < t1; ++t) {
     const int k0 = A.col_idx[t] * C::BN;
-    if (t + 1 < t1) load_tile(t + 1);
+    // the next tile (the last one again on the final pass, so the loop body
+    // has no branch around its loads and stores)
+    load_tile(min(t + 1, t1 - 1));
 
     // ---- this row's valid keys inside [k0, k0 + 128) as a 128-bit mask
     uint32_t mb[4] = {0u, 0u, 0u, 0u};
@@ -188,70 +219,80 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
         for (int w = 0; w < 4; ++w) mb[w] = range_word(a, e, w);
       }
     }
-    while (jp < A.pc.w) {
-      const int o_next = oversized(rp, jp + 1);
-      const int idx = interp_index(o_cur, o_next, hw);
-      if (idx > i) {  // indices rise with j: every later entry is masked too
-        jp = A.pc.w;
-        break;
+    // tiles come in ascending order and hold every valid entry, so the
+    // pending entry is never below k0
+    while (pend < k0 + C::BN) {
+      const int rel = pend - k0;
+      const uint32_t bit = 1u << (rel & 31);
+      const int wsel = rel >> 5;
+      mb[0] |= wsel == 0 ? bit : 0u;
+      mb[1] |= wsel == 1 ? bit : 0u;
+      mb[2] |= wsel == 2 ? bit : 0u;
+      mb[3] |= wsel == 3 ? bit : 0u;
+      if (++jp == A.pc.w) {
+        pend = kNone;
+      } else {
+        o_cur = o_next;
+        o_next = oversized(rp, jp + 1);
+        pend = interp_index(o_cur, o_next, hw);
+        if (pend > i) pend = kNone;  // indices rise with j: the rest are masked
       }
-      if (idx >= k0 + C::BN) break;
-      const int rel = idx - k0;
-      if (rel >= 0) {
-        const uint32_t bit = 1u << (rel & 31);
-        const int wsel = rel >> 5;
-        mb[0] |= wsel == 0 ? bit : 0u;
-        mb[1] |= wsel == 1 ? bit : 0u;
-        mb[2] |= wsel == 2 ? bit : 0u;
-        mb[3] |= wsel == 3 ? bit : 0u;
-      }
-      o_cur = o_next;
-      ++jp;
     }
 
     // ---- per 32-key block kb: S^T = K Q^T, online softmax, O^T += V^T P^T
-    const int g4 = lane >> 4, lam = lane & 15;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
+      // lane half hf holds keys 32kb + 8*(r/4) + 4*hf + r%4
+      const uint32_t mk = mb[kb] >> (4 * hf);
+      bool act[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) act[g] = wave_any(((mk >> (8 * g)) & 0xfu) != 0u);
       f32x16 sacc = f32x16{};
 #pragma unroll
       for (int s = 0; s < C::NS; ++s) {
         const bf16x8 a = *(const bf16x8*)(Ks + (32 * kb + l32) * C::KSTR + 16 * s + 8 * hf);
         sacc = mfma32(a, qop[s], sacc);
       }
-      // lane half hf holds keys 32kb + 8*(r/4) + 4*hf + r%4
-      const uint32_t mk = mb[kb] >> (4 * hf);
-      bool act[4];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) act[g] = wave_any(((mk >> (8 * g)) & 0xfu) != 0u);
 
+      // x = scaled score relative to the running max (log2 units), -inf for
+      // a masked key: fma(s, scale, valid ? -m : -inf)
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+      const uint32_t neg_m = __float_as_uint(-m_use);
       float smax = -INFINITY;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         if (act[g]) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int r = 4 * g + e;
-            const bool on = (mk >> (8 * g + e)) & 1u;
-            const float x = on ? sacc[r] * A.scale_log2 : -INFINITY;
-            sacc[r] = x;
+            const uint32_t on = (uint32_t)__builtin_amdgcn_sbfe((int)mk, 8 * g + e, 1);
+            const uint32_t add = (on & neg_m) | (~on & 0xff800000u);
+            const float x = __builtin_fmaf(sacc[4 * g + e], scale, __uint_as_float(add));
+            sacc[4 * g + e] = x;
             smax = fmaxf(smax, x);
           }
         }
       }
       smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
-      const bool grow = smax > m_run + kRescaleSlack;
+      // raise the running max of a row when this block exceeds it by more
+      // than the slack (or when the row sees its first valid key)
+      const bool grow = m_run == -INFINITY ? smax != -INFINITY : smax > kRescaleSlack;
       if (wave_any(grow)) {
+        const float delta = grow ? smax : 0.f;
         // rows that do not grow keep alpha = 1 (m_run may still be -inf there)
-        const float m_new = grow ? smax : m_run;
-        const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;  // 0 from -inf
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - (m_use + delta)) : 1.0f;
         l_run *= alpha;
         n_run *= alpha;
 #pragma unroll
         for (int d = 0; d < C::ND; ++d) oacc[d] *= alpha;
-        m_run = m_new;
+        m_run = grow ? m_use + delta : m_run;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          if (act[g]) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sacc[4 * g + e] -= delta;
+          }
+        }
       }
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;
 
       uint32_t pw[8];  // P as packed bf16 pairs: pw[q] holds regs 2q, 2q+1
 #pragma unroll
@@ -260,16 +301,15 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
           float p[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            p[e] = __builtin_amdgcn_exp2f(sacc[4 * g + e] - m_use);
+            p[e] = __builtin_amdgcn_exp2f(sacc[4 * g + e]);
             l_run += p[e];
           }
           pw[2 * g] = pack_bf16x2(p[0], p[1]);
           pw[2 * g + 1] = pack_bf16x2(p[2], p[3]);
           // normalise O by the probabilities PV actually used, so a row led
           // by one key reproduces that key's value row
-          n_run += __uint_as_float(pw[2 * g] << 16) + __uint_as_float(pw[2 * g] & 0xffff0000u);
-          n_run += __uint_as_float(pw[2 * g + 1] << 16) +
-                   __uint_as_float(pw[2 * g + 1] & 0xffff0000u);
+          n_run = dot2_bf16(pw[2 * g], n_run);
+          n_run = dot2_bf16(pw[2 * g + 1], n_run);
         } else {
           pw[2 * g] = 0u;
           pw[2 * g + 1] = 0u;
@@ -293,7 +333,7 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
       }
     }
     __syncthreads();
-    if (t + 1 < t1) store_tile();
+    store_tile();
     __syncthreads();
   }
 

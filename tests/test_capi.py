@@ -114,6 +114,10 @@ def test_forward_entry_points_reject_bad_arguments():
     a.k_stride_s = 130
     assert call(a) == en.ESA_ERR_ALIGN
     assert call(fwd_args(), pp=pat(L=1024, H=4, bm=64)) == en.ESA_ERR_UNSUPPORTED
+    for bad_scale in (0.0, -0.1, float("inf"), float("nan")):
+        a = fwd_args()
+        a.sm_scale = bad_scale
+        assert call(a) == en.ESA_ERR_UNSUPPORTED
     assert call(fwd_args(), pp=pat(L=1024, H=4, layer=9)) == en.ESA_ERR_UNSUPPORTED
 
     assert lib.esa_elastic_fwd_rows(ctypes.byref(fwd_args(D=258)), ctypes.byref(p), None, None) \
