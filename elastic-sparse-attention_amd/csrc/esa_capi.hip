@@ -253,6 +253,11 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
   if (a->q_len > a->kv_len || a->q_len > p->seq_len) return ESA_ERR_SHAPE;
   // the kernel folds the key mask into the scaled score as -inf
   if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale)) return ESA_ERR_UNSUPPORTED;
+  // K/V rows are addressed through 32-bit buffer offsets per (batch, kv head)
+  if ((int64_t)a->kv_len * a->k_stride_s * 2 >= (int64_t(1) << 31) ||
+      (int64_t)a->kv_len * a->v_stride_s * 2 >= (int64_t(1) << 31) ||
+      a->k_stride_s < a->head_dim || a->v_stride_s < a->head_dim)
+    return ESA_ERR_UNSUPPORTED;
   const LayoutDims d = dims_of(*p);
   const int nq = (a->q_len + 127) / 128;
   // a plan from esa_plan_schedule holds every item once plus at most 7 pads

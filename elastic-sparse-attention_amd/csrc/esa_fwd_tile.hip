@@ -7,17 +7,23 @@
 // active tile is computed densely (128 x 128 x D on MFMA), so the executed
 // tile equals the layout tile.
 //
-// Per tile (workgroup) and wave (32 query rows):
-//   prefetch       the next tile's K and V rows are loaded into registers
-//                  (16-byte loads) while this tile computes, and written to
-//                  LDS after it
+// K/V staging: a tile is consumed in two 64-key stages.  Each stage's K and V
+// rows are copied HBM -> LDS by buffer_load_dwordx4 ... lds (no registers),
+// one stage ahead, into two stage buffers (64 KB per workgroup at D = 128, so
+// two workgroups share a CU).  Rows past kv_len fall outside the buffer
+// resource and read as zeros.  Within a buffer, 16-byte chunks of a row are
+// XOR-swizzled (K: 16 consecutive rows hit 16 distinct bank groups for the
+// 16-byte MFMA operand reads; V: the 4 rows of a ds_read_b64_tr_b16 group hit
+// distinct bank groups), since the direct loads write whole rows unpadded.
+//
+// Per tile and wave (32 query rows):
 //   mask           each lane owns one query row; rows whose index list is a
 //                  contiguous run (the sliding window of layer 0, and the
 //                  first w - 1 rows of every layer) set a bit range, the
 //                  others walk their elastic indices (the same float32
 //                  sequence as the layout builder) through the tile
 // then for each 32-key block of the tile:
-//   S^T = K Q^T    8 (D=128) x v_mfma_f32_32x32x16_bf16 (A = K rows from LDS,
+//   S^T = K Q^T    NS x v_mfma_f32_32x32x16_bf16 (A = K rows from LDS,
 //                  B = Q kept in registers for the whole item)
 //   softmax        online, in registers, log2 domain.  The S^T accumulator
 //                  layout gives each lane one row and 16 of the block's keys
@@ -27,7 +33,7 @@
 //                  most groups are skipped.  The running max is raised only
 //                  when a row's block max exceeds it by more than 8 (log2), so
 //                  the O rescale is rare; probabilities stay below 2^8.
-//   O^T += V^T P^T 8 (D=128) x v_mfma_f32_32x32x16_bf16 (A = V^T read with
+//   O^T += V^T P^T 2 ND x v_mfma_f32_32x32x16_bf16 (A = V^T read with
 //                  ds_read_b64_tr_b16 from row-major V in LDS, B = P straight
 //                  from the S^T accumulators: a key permutation shared by
 //                  both operands leaves the contraction unchanged)
@@ -38,6 +44,8 @@
 //   C[i][j]: lane l, reg r holds i = 8*(r/4) + 4*(l/32) + r%4, j = l%32
 // ds_read_b64_tr_b16 in each 16-lane group: lane g receives element r from
 // lane 4r + g/4's 8-byte chunk, element g%4.
+// buffer_load_dwordx4 ... lds: lane l's 16 bytes land at M0 + 16 l; offsets
+// (voffset + soffset) at or past num_records read as zero.
 #include "esa_internal.hpp"
 
 namespace esa {
@@ -46,21 +54,34 @@ template <int D>
 struct TileCfg {
   static constexpr int BM = 128;
   static constexpr int BN = 128;
-  static constexpr int KSTR = D + 8;     // K row pitch (elements): conflict-free b128 reads
-  static constexpr int VSTR = D + 16;    // V row pitch: conflict-free transposed reads
-  static constexpr int NS = D / 16;      // k-steps of QK^T
-  static constexpr int ND = D / 32;      // 32-wide d blocks of PV
-  static constexpr int CPR = D / 8;      // 16-byte chunks per row
-  static constexpr int RPP = 256 / CPR;  // rows staged per pass
-  static constexpr int NP = BN / RPP;    // staging passes per tile
+  static constexpr int HALF = 64;                 // keys per stage
+  static constexpr int CPR = D / 8;               // 16-byte chunks per row
+  static constexpr int STAGE = HALF * D;          // elements per stage buffer (one matrix)
+  static constexpr int LOADS = HALF * CPR / 256;  // 16-byte loads per lane per matrix per stage
+  static constexpr int NS = D / 16;               // k-steps of QK^T
+  static constexpr int ND = D / 32;               // 32-wide d blocks of PV
 };
+
+// Chunk swizzles (chunk index XOR f(row)); both depend only on row bits the
+// kernel's row offsets (multiples of 8 for V, 32 for K) leave unchanged.
+template <int D>
+__device__ __forceinline__ int swz_k(int row) {
+  return D == 128 ? (((row & 3) << 2) ^ ((row >> 2) & 3))
+                  : ((((row >> 1) & 1) << 2) ^ ((row >> 2) & 3));
+}
+template <int D>
+__device__ __forceinline__ int swz_v(int row) {
+  return D == 128 ? ((row & 3) << 2) : (((row >> 1) & 1) << 2);
+}
 
 // Rows whose index list is a contiguous run and whose indices are exact in
 // float32 (the interpolation of equal integers x reproduces x when x < 2^21).
 constexpr int kContigLimit = 1 << 21;
 // Lazy rescale threshold (log2 units): the running max moves only when a
-// tile raises a row's max by more than this, so probabilities stay <= 2^8.
+// block raises a row's max by more than this, so probabilities stay <= 2^8.
 constexpr float kRescaleSlack = 8.0f;
+// s_waitcnt with vmcnt(0) and the other counters left alone (gfx9 encoding)
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -74,6 +95,20 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// c + lo + hi of a packed bf16 pair, in float32 (v_dot2 with (1, 1))
+__device__ __forceinline__ float dot2_bf16(uint32_t pair, float c) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), one, c, false);
+}
+
+// max of v over lanes l and l ^ 32 (v_permlane32_swap)
+__device__ __forceinline__ float half_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Bits [a - 32 w, b - 32 w] of word w of a 128-bit mask (a <= b, both in [0, 127]).
 __device__ __forceinline__ uint32_t range_word(int a, int b, int w) {
   const int lo = max(a - 32 * w, 0);
@@ -83,27 +118,38 @@ __device__ __forceinline__ uint32_t range_word(int a, int b, int w) {
   return n >= 0 ? bits : 0u;
 }
 
-// c + lo + hi of a packed bf16 pair, in float32 (v_dot2 with (1, 1))
-__device__ __forceinline__ float dot2_bf16(uint32_t pair, float c) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), one, c, false);
-}
-
 __device__ __forceinline__ bool wave_any(bool p) {
   return __builtin_amdgcn_ballot_w64(p) != 0;
 }
 
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(4))) int32_t* cptr_i32;
+
+// 16 bytes per lane from a buffer resource at voffset + soffset straight into
+// LDS at dst + 16 * lane (dst uniform)
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t rsrc, uint16_t* dst, int voffset,
+                                           int soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)dst, 16, voffset, soffset, 0, 0);
+}
 
 template <int D>
 __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   using C = TileCfg<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[C::BN * C::KSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[C::BN * C::VSTR];
+  // stage buffers (HALF rows x D, rows unpadded, chunks swizzled); separate
+  // objects, so the compiler can tell reads of one buffer from the direct
+  // loads into the other
+  __shared__ __attribute__((aligned(1024))) uint16_t k_st0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_st0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t k_st1[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_st1[C::STAGE];
+  // the layout and the work list are read-only here: scalar loads
+  const cptr_i32 items = (cptr_i32)A.items;
+  const cptr_i32 row_ptr = (cptr_i32)A.row_ptr;
+  const cptr_i32 col_idx = (cptr_i32)A.col_idx;
 
   // ---- work item (uniform over the workgroup; -1 pads the XCD runs)
-  const int item = A.items[blockIdx.x];
+  const int item = items[blockIdx.x];
   if (item < 0 || item >= A.num_bh * A.nqb) return;
   const int qb = item % A.nqb;
   if (qb >= A.nq) return;
@@ -113,7 +159,7 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   const int kvh = h / A.groups;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hf = lane >> 5, l32 = lane & 31;
 
   const int i = qb * C::BM + wave * 32 + l32;  // this lane's query row = position
@@ -157,58 +203,154 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   for (int d = 0; d < C::ND; ++d) oacc[d] = f32x16{};
 
   const int64_t lrow = (int64_t)h * A.nqb + qb;
-  const int t0 = A.row_ptr[lrow], t1 = A.row_ptr[lrow + 1];
+  const int t0 = row_ptr[lrow], t1 = row_ptr[lrow + 1];
 
-  // ---- K/V staging: registers <- HBM (one tile ahead), LDS <- registers.
-  // Keys past kv_len read the last row instead: they are never valid (valid
-  // indices are <= the query position < q_len <= kv_len), so their
-  // probabilities are 0 and the values only need to be finite.
-  const int srow = tid / C::CPR, scol = 8 * (tid % C::CPR);
-  const uint16_t* kg = A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh + scol;
-  const uint16_t* vg = A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh + scol;
-  const int64_t kstep = (int64_t)C::RPP * A.kss, vstep = (int64_t)C::RPP * A.vss;
-  u32x4 kpre[C::NP], vpre[C::NP];
-  auto load_tile = [&](int kt) {
-    const int kbase = A.col_idx[kt] * C::BN;
-    if (kbase + C::BN <= A.kv_len) {  // whole tile in range: strided rows
-      const uint16_t* kr = kg + (int64_t)(kbase + srow) * A.kss;
-      const uint16_t* vr = vg + (int64_t)(kbase + srow) * A.vss;
+  // ---- staging: buffer resources over this (batch, kv head)'s rows; keys at
+  // or past kv_len are outside num_records and load as zeros (the host keeps
+  // kv_len * row stride * 2 below 2^31)
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh), (short)0,
+      (int)((int64_t)A.kv_len * A.kss * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh), (short)0,
+      (int)((int64_t)A.kv_len * A.vss * 2), 0x00020000);
+  // load j of this lane fills chunk slot (LOADS wave + j) * 64 + lane of a
+  // stage buffer: row slot / CPR, physical chunk slot % CPR
+  int koff[C::LOADS], voff[C::LOADS];
 #pragma unroll
-      for (int p = 0; p < C::NP; ++p) {
-        kpre[p] = *(const u32x4*)(kr + p * kstep);
-        vpre[p] = *(const u32x4*)(vr + p * vstep);
-      }
-    } else {
-#pragma unroll
-      for (int p = 0; p < C::NP; ++p) {
-        const int key = min(kbase + p * C::RPP + srow, A.kv_len - 1);
-        kpre[p] = *(const u32x4*)(kg + (int64_t)key * A.kss);
-        vpre[p] = *(const u32x4*)(vg + (int64_t)key * A.vss);
-      }
-    }
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int p = 0; p < C::NP; ++p) {
-      const int r = p * C::RPP + srow;
-      *(u32x4*)(Ks + r * C::KSTR + scol) = kpre[p];
-      *(u32x4*)(Vs + r * C::VSTR + scol) = vpre[p];
-    }
-  };
-
-  if (t0 < t1) {
-    load_tile(t0);
-    store_tile();
+  for (int j = 0; j < C::LOADS; ++j) {
+    const int slot = (C::LOADS * wave + j) * 64 + lane;
+    const int row = slot / C::CPR, pc = slot % C::CPR;
+    koff[j] = (row * (int)A.kss + 8 * (pc ^ swz_k<D>(row))) * 2;
+    voff[j] = (row * (int)A.vss + 8 * (pc ^ swz_v<D>(row))) * 2;
   }
-  __syncthreads();
+  // stage hh (keys 64 hh .. 64 hh + 63) of tile kt -> buffers (kd, vd)
+  auto issue = [&](int kt, int hh, uint16_t* kd, uint16_t* vd) {
+    const int key0 = col_idx[kt] * C::BN + C::HALF * hh;
+    const int ks = key0 * (int)A.kss * 2, vs = key0 * (int)A.vss * 2;
+#pragma unroll
+    for (int j = 0; j < C::LOADS; ++j) {
+      // each load writes 64 lanes x 16 bytes = 512 elements
+      load_lds16(krs, kd + (C::LOADS * wave + j) * 512, koff[j], ks);
+      load_lds16(vrs, vd + (C::LOADS * wave + j) * 512, voff[j], vs);
+    }
+  };
+
+  // ---- LDS read addresses (elements), fixed for the whole item: K rows
+  // 32 kbl + l32 at chunk 2 s + hf; V rows 4 hf + lam / 4 (+ 32 kbl + 16 u,
+  // + 8) at column 32 d + 16 (g4 & 1) + 4 (lam & 3)
+  const int g4 = lane >> 4, lam = lane & 15;
+  int kaddr[C::NS], vaddr[C::ND];
+#pragma unroll
+  for (int s = 0; s < C::NS; ++s) kaddr[s] = l32 * D + 8 * ((2 * s + hf) ^ swz_k<D>(l32));
+  {
+    const int vrow = 4 * hf + (lam >> 2);
+#pragma unroll
+    for (int d = 0; d < C::ND; ++d) {
+      const int col = 32 * d + 16 * (g4 & 1) + 4 * (lam & 3);
+      vaddr[d] = vrow * D + 8 * ((col >> 3) ^ swz_v<D>(vrow)) + (col & 7);
+    }
+  }
 
   const float scale = A.scale_log2;  // > 0 (checked on the host)
-  const int g4 = lane >> 4, lam = lane & 15;
+
+  // One 32-key block: keys 32 kbl .. 32 kbl + 31 of a stage buffer (Kb, Vb),
+  // whose valid-key bits for this row are mbits.
+  auto block = [&](const uint16_t* Kb, const uint16_t* Vb, int kbl, uint32_t mbits) {
+    // lane half hf holds keys 8*(r/4) + 4*hf + r%4 of the block
+    const uint32_t mk = mbits >> (4 * hf);
+    bool act[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) act[g] = wave_any(((mk >> (8 * g)) & 0xfu) != 0u);
+
+    f32x16 sacc = f32x16{};
+#pragma unroll
+    for (int s = 0; s < C::NS; ++s) {
+      const bf16x8 a = *(const bf16x8*)(Kb + kaddr[s] + 32 * kbl * D);
+      sacc = mfma32(a, qop[s], sacc);
+    }
+
+    // x = scaled score relative to the running max (log2 units), -inf for a
+    // masked key: fma(s, scale, valid ? -m : -inf)
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    const uint32_t neg_m = __float_as_uint(-m_use);
+    float smax = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      if (act[g]) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t on = (uint32_t)__builtin_amdgcn_sbfe((int)mk, 8 * g + e, 1);
+          const uint32_t add = (on & neg_m) | (~on & 0xff800000u);
+          const float x = __builtin_fmaf(sacc[4 * g + e], scale, __uint_as_float(add));
+          sacc[4 * g + e] = x;
+          smax = fmaxf(smax, x);
+        }
+      }
+    }
+    smax = half_max(smax);
+    // raise the running max of a row when this block exceeds it by more than
+    // the slack (or when the row sees its first valid key)
+    const bool grow = m_run == -INFINITY ? smax != -INFINITY : smax > kRescaleSlack;
+    if (wave_any(grow)) {
+      const float delta = grow ? smax : 0.f;
+      // rows that do not grow keep alpha = 1 (m_run may still be -inf there)
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - (m_use + delta)) : 1.0f;
+      l_run *= alpha;
+      n_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < C::ND; ++d) oacc[d] *= alpha;
+      m_run = grow ? m_use + delta : m_run;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        if (act[g]) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sacc[4 * g + e] -= delta;
+        }
+      }
+    }
+
+    uint32_t pw[8];  // P as packed bf16 pairs: pw[q] holds regs 2q, 2q+1
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      if (act[g]) {
+        float p[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          p[e] = __builtin_amdgcn_exp2f(sacc[4 * g + e]);
+          l_run += p[e];
+        }
+        pw[2 * g] = pack_bf16x2(p[0], p[1]);
+        pw[2 * g + 1] = pack_bf16x2(p[2], p[3]);
+        // normalise O by the probabilities PV actually used, so a row led by
+        // one key reproduces that key's value row
+        n_run = dot2_bf16(pw[2 * g], n_run);
+        n_run = dot2_bf16(pw[2 * g + 1], n_run);
+      } else {
+        pw[2 * g] = 0u;
+        pw[2 * g + 1] = 0u;
+      }
+    }
+
+#pragma unroll
+    for (int d = 0; d < C::ND; ++d) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint16_t* p1 = Vb + vaddr[d] + (32 * kbl + 16 * u) * D;
+        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p1);
+        const s16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1 + 8 * D));
+        const s16x4 vv[2] = {v1, v2};
+        const bf16x8 a = __builtin_bit_cast(bf16x8, vv);
+        const u32x4 pq = {pw[4 * u], pw[4 * u + 1], pw[4 * u + 2], pw[4 * u + 3]};
+        oacc[d] = mfma32(a, __builtin_bit_cast(bf16x8, pq), oacc[d]);
+      }
+    }
+  };
+
+  if (t0 < t1) issue(t0, 0, k_st0, v_st0);
+
   for (int t = t0; t < t1; ++t) {
-    const int k0 = A.col_idx[t] * C::BN;
-    // the next tile (the last one again on the final pass, so the loop body
-    // has no branch around its loads and stores)
-    load_tile(min(t + 1, t1 - 1));
+    const int k0 = col_idx[t] * C::BN;
 
     // ---- this row's valid keys inside [k0, k0 + 128) as a 128-bit mask
     uint32_t mb[4] = {0u, 0u, 0u, 0u};
@@ -239,102 +381,21 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
       }
     }
 
-    // ---- per 32-key block kb: S^T = K Q^T, online softmax, O^T += V^T P^T
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      // lane half hf holds keys 32kb + 8*(r/4) + 4*hf + r%4
-      const uint32_t mk = mb[kb] >> (4 * hf);
-      bool act[4];
-#pragma unroll
-      for (int g = 0; g < 4; ++g) act[g] = wave_any(((mk >> (8 * g)) & 0xfu) != 0u);
-      f32x16 sacc = f32x16{};
-#pragma unroll
-      for (int s = 0; s < C::NS; ++s) {
-        const bf16x8 a = *(const bf16x8*)(Ks + (32 * kb + l32) * C::KSTR + 16 * s + 8 * hf);
-        sacc = mfma32(a, qop[s], sacc);
-      }
-
-      // x = scaled score relative to the running max (log2 units), -inf for
-      // a masked key: fma(s, scale, valid ? -m : -inf)
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;
-      const uint32_t neg_m = __float_as_uint(-m_use);
-      float smax = -INFINITY;
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        if (act[g]) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t on = (uint32_t)__builtin_amdgcn_sbfe((int)mk, 8 * g + e, 1);
-            const uint32_t add = (on & neg_m) | (~on & 0xff800000u);
-            const float x = __builtin_fmaf(sacc[4 * g + e], scale, __uint_as_float(add));
-            sacc[4 * g + e] = x;
-            smax = fmaxf(smax, x);
-          }
-        }
-      }
-      smax = fmaxf(smax, __shfl_xor(smax, 32, 64));
-      // raise the running max of a row when this block exceeds it by more
-      // than the slack (or when the row sees its first valid key)
-      const bool grow = m_run == -INFINITY ? smax != -INFINITY : smax > kRescaleSlack;
-      if (wave_any(grow)) {
-        const float delta = grow ? smax : 0.f;
-        // rows that do not grow keep alpha = 1 (m_run may still be -inf there)
-        const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - (m_use + delta)) : 1.0f;
-        l_run *= alpha;
-        n_run *= alpha;
-#pragma unroll
-        for (int d = 0; d < C::ND; ++d) oacc[d] *= alpha;
-        m_run = grow ? m_use + delta : m_run;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          if (act[g]) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sacc[4 * g + e] -= delta;
-          }
-        }
-      }
-
-      uint32_t pw[8];  // P as packed bf16 pairs: pw[q] holds regs 2q, 2q+1
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        if (act[g]) {
-          float p[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            p[e] = __builtin_amdgcn_exp2f(sacc[4 * g + e]);
-            l_run += p[e];
-          }
-          pw[2 * g] = pack_bf16x2(p[0], p[1]);
-          pw[2 * g + 1] = pack_bf16x2(p[2], p[3]);
-          // normalise O by the probabilities PV actually used, so a row led
-          // by one key reproduces that key's value row
-          n_run = dot2_bf16(pw[2 * g], n_run);
-          n_run = dot2_bf16(pw[2 * g + 1], n_run);
-        } else {
-          pw[2 * g] = 0u;
-          pw[2 * g + 1] = 0u;
-        }
-      }
-
-#pragma unroll
-      for (int d = 0; d < C::ND; ++d) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int key = 32 * kb + 16 * u + 4 * hf + (lam >> 2);
-          const int col = 32 * d + 16 * (g4 & 1) + 4 * (lam & 3);
-          const uint16_t* p1 = Vs + key * C::VSTR + col;
-          const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p1);
-          const s16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1 + 8 * C::VSTR));
-          const s16x4 vv[2] = {v1, v2};
-          const bf16x8 a = __builtin_bit_cast(bf16x8, vv);
-          const u32x4 pq = {pw[4 * u], pw[4 * u + 1], pw[4 * u + 2], pw[4 * u + 3]};
-          oacc[d] = mfma32(a, __builtin_bit_cast(bf16x8, pq), oacc[d]);
-        }
-      }
-    }
+    // ---- stage 0: keys k0 .. k0 + 63 (buffer 0); stage 1 loads meanwhile.
+    // The barrier also retires every wave's reads of buffer 1.
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
-    store_tile();
+    issue(t, 1, k_st1, v_st1);
+    block(k_st0, v_st0, 0, mb[0]);
+    block(k_st0, v_st0, 1, mb[1]);
+
+    // ---- stage 1: keys k0 + 64 .. k0 + 127 (buffer 1); the next tile's
+    // stage 0 loads meanwhile
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
+    if (t + 1 < t1) issue(t + 1, 0, k_st0, v_st0);
+    block(k_st1, v_st1, 0, mb[2]);
+    block(k_st1, v_st1, 1, mb[3]);
   }
 
   // ---- epilogue: normalise and store O rows and the log-sum-exp

@@ -132,7 +132,9 @@ esa_status esa_plan_schedule(const esa_pattern* p, const int32_t* row_ptr_host,
  * Visits only the active tiles of the layout, runs QK^T and PV on bf16 MFMA
  * with float32 accumulation and online softmax.  Requires dtype ESA_BF16,
  * head_dim 64 or 128, block_m = block_n = 128, a finite sm_scale > 0
- * (ESA_ERR_UNSUPPORTED otherwise; esa_elastic_fwd_rows takes any), q_len <= kv_len,
+ * (ESA_ERR_UNSUPPORTED otherwise; esa_elastic_fwd_rows takes any), K and V
+ * row strides >= head_dim with kv_len * row stride * 2 < 2^31 (one head's
+ * rows within a 2 GiB window), q_len <= kv_len,
  * q_len <= p->seq_len, 16-byte aligned rows.  items/num_items come from
  * esa_plan_schedule (copied to device memory); item ids outside the forward
  * are skipped. */
