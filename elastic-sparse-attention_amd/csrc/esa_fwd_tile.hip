@@ -26,13 +26,14 @@
 //   S^T = K Q^T    NS x v_mfma_f32_32x32x16_bf16 (A = K rows from LDS,
 //                  B = Q kept in registers for the whole item)
 //   softmax        online, in registers, log2 domain.  The S^T accumulator
-//                  layout gives each lane one row and 16 of the block's keys
-//                  in 4 groups of 4; a group that holds no valid key in any
-//                  lane of the wave is skipped (its probabilities are 0).  At
-//                  dilated layers a row has about one valid key per tile, so
-//                  most groups are skipped.  The running max is raised only
-//                  when a row's block max exceeds it by more than 8 (log2), so
-//                  the O rescale is rare; probabilities stay below 2^8.
+//                  layout gives each lane one row and 16 of the block's keys;
+//                  the mask enters as the accumulator's initial value (0 or
+//                  -inf).  A block that holds no valid key for any row of the
+//                  wave is skipped (its probabilities are 0): at dilated
+//                  layers the 32 rows' keys cluster, so about half the blocks
+//                  are skipped.  The running max is raised only when a row's
+//                  block max exceeds it by more than 8 (log2), so the O
+//                  rescale is rare; probabilities stay below 2^8.
 //   O^T += V^T P^T 2 ND x v_mfma_f32_32x32x16_bf16 (A = V^T read with
 //                  ds_read_b64_tr_b16 from row-major V in LDS, B = P straight
 //                  from the S^T accumulators: a key permutation shared by
@@ -259,87 +260,88 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   auto block = [&](const uint16_t* Kb, const uint16_t* Vb, int kbl, uint32_t mbits) {
     // lane half hf holds keys 8*(r/4) + 4*hf + r%4 of the block
     const uint32_t mk = mbits >> (4 * hf);
-    bool act[4];
-#pragma unroll
-    for (int g = 0; g < 4; ++g) act[g] = wave_any(((mk >> (8 * g)) & 0xfu) != 0u);
+    // a block no row of the wave has a valid key in contributes p = 0: its
+    // softmax is skipped (its MFMAs still run: the tile is computed densely)
+    const bool active = wave_any(mk != 0u);
 
+    // all K operand reads first, so their LDS latency overlaps
+    bf16x8 ka[C::NS];
+#pragma unroll
+    for (int s = 0; s < C::NS; ++s) ka[s] = *(const bf16x8*)(Kb + kaddr[s] + 32 * kbl * D);
+    // the mask enters as the accumulator's initial value: 0 for a valid key,
+    // -inf for a masked one
     f32x16 sacc = f32x16{};
+    if (active) {
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) {
-      const bf16x8 a = *(const bf16x8*)(Kb + kaddr[s] + 32 * kbl * D);
-      sacc = mfma32(a, qop[s], sacc);
-    }
-
-    // x = scaled score relative to the running max (log2 units), -inf for a
-    // masked key: fma(s, scale, valid ? -m : -inf)
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    const uint32_t neg_m = __float_as_uint(-m_use);
-    float smax = -INFINITY;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      if (act[g]) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t on = (uint32_t)__builtin_amdgcn_sbfe((int)mk, 8 * g + e, 1);
-          const uint32_t add = (on & neg_m) | (~on & 0xff800000u);
-          const float x = __builtin_fmaf(sacc[4 * g + e], scale, __uint_as_float(add));
-          sacc[4 * g + e] = x;
-          smax = fmaxf(smax, x);
-        }
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t on = (uint32_t)__builtin_amdgcn_sbfe((int)mk, 8 * (r / 4) + r % 4, 1);
+        sacc[r] = __uint_as_float(~on & 0xff800000u);
       }
     }
-    smax = half_max(smax);
-    // raise the running max of a row when this block exceeds it by more than
-    // the slack (or when the row sees its first valid key)
-    const bool grow = m_run == -INFINITY ? smax != -INFINITY : smax > kRescaleSlack;
-    if (wave_any(grow)) {
-      const float delta = grow ? smax : 0.f;
-      // rows that do not grow keep alpha = 1 (m_run may still be -inf there)
-      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - (m_use + delta)) : 1.0f;
-      l_run *= alpha;
-      n_run *= alpha;
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int d = 0; d < C::ND; ++d) oacc[d] *= alpha;
-      m_run = grow ? m_use + delta : m_run;
+    for (int s = 0; s < C::NS; ++s) sacc = mfma32(ka[s], qop[s], sacc);
+    // the V^T operands of this block, read while the softmax runs
+    s16x4 va[C::ND][4];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        if (act[g]) {
+    for (int d = 0; d < C::ND; ++d) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) sacc[4 * g + e] -= delta;
-        }
+      for (int u = 0; u < 2; ++u) {
+        const uint16_t* p1 = Vb + vaddr[d] + (32 * kbl + 16 * u) * D;
+        va[d][2 * u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p1);
+        va[d][2 * u + 1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1 + 8 * D));
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
 
     uint32_t pw[8];  // P as packed bf16 pairs: pw[q] holds regs 2q, 2q+1
+    if (active) {
+      // x = scaled score relative to the running max (log2 units); a masked
+      // key stays -inf (scale > 0)
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+      float smax = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      if (act[g]) {
-        float p[4];
+      for (int r = 0; r < 16; ++r) {
+        sacc[r] = __builtin_fmaf(sacc[r], scale, -m_use);
+        smax = fmaxf(smax, sacc[r]);
+      }
+      smax = half_max(smax);
+      // raise the running max of a row when this block exceeds it by more
+      // than the slack (or when the row sees its first valid key)
+      const bool grow = m_run == -INFINITY ? smax != -INFINITY : smax > kRescaleSlack;
+      if (wave_any(grow)) {
+        const float delta = grow ? smax : 0.f;
+        // rows that do not grow keep alpha = 1 (m_run may still be -inf there)
+        const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - (m_use + delta)) : 1.0f;
+        l_run *= alpha;
+        n_run *= alpha;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          p[e] = __builtin_amdgcn_exp2f(sacc[4 * g + e]);
-          l_run += p[e];
-        }
-        pw[2 * g] = pack_bf16x2(p[0], p[1]);
-        pw[2 * g + 1] = pack_bf16x2(p[2], p[3]);
+        for (int d = 0; d < C::ND; ++d) oacc[d] *= alpha;
+        m_run = grow ? m_use + delta : m_run;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[r] -= delta;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float p0 = __builtin_amdgcn_exp2f(sacc[2 * q]);
+        const float p1 = __builtin_amdgcn_exp2f(sacc[2 * q + 1]);
+        l_run += p0;
+        l_run += p1;
+        pw[q] = pack_bf16x2(p0, p1);
         // normalise O by the probabilities PV actually used, so a row led by
         // one key reproduces that key's value row
-        n_run = dot2_bf16(pw[2 * g], n_run);
-        n_run = dot2_bf16(pw[2 * g + 1], n_run);
-      } else {
-        pw[2 * g] = 0u;
-        pw[2 * g + 1] = 0u;
+        n_run = dot2_bf16(pw[q], n_run);
       }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) pw[q] = 0u;
     }
 
 #pragma unroll
     for (int d = 0; d < C::ND; ++d) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const uint16_t* p1 = Vb + vaddr[d] + (32 * kbl + 16 * u) * D;
-        const s16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p1);
-        const s16x4 v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1 + 8 * D));
-        const s16x4 vv[2] = {v1, v2};
+        const s16x4 vv[2] = {va[d][2 * u], va[d][2 * u + 1]};
         const bf16x8 a = __builtin_bit_cast(bf16x8, vv);
         const u32x4 pq = {pw[4 * u], pw[4 * u + 1], pw[4 * u + 2], pw[4 * u + 3]};
         oacc[d] = mfma32(a, __builtin_bit_cast(bf16x8, pq), oacc[d]);
