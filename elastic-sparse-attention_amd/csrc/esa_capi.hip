@@ -106,41 +106,37 @@ esa_status check_gather_layout(const esa_fwd_args* a) {
   return ESA_OK;
 }
 
-// Work list of the block-sparse forward, laid out for the 8 XCDs of MI355X.
+// Work lists of the block-sparse kernels, laid out for the 8 XCDs of MI355X.
 //
 // Consecutive workgroup ids are dispatched round-robin over the XCDs
-// (id % 8), and each XCD has its own L2.  Every (batch, head) stream -- all
-// query blocks of one head -- is a run of items; streams are walked in
-// (batch, head) order (heads that share a kv head stay adjacent), each
-// stream's query blocks longest first, and the walk is cut into 8 runs of
-// equal tile count.  Run x goes to grid slots x, x + 8, x + 16, ..., so one
-// XCD works through one or two heads' K/V at a time (their tiles stay in
-// its L2) and ends on the cheapest blocks of its last stream.  Runs shorter
-// than the longest are padded with -1 (an empty workgroup).
-void plan_xcd_grid(const int32_t* row_ptr, int nqb, int nq, int batch, int H,
-                   std::vector<int32_t>& grid) {
+// (id % 8), and each XCD has its own L2.  Items come in streams (all query
+// blocks of one (batch, head) for the forward; all key blocks of one
+// (batch, kv head) for the backward's dK/dV), each walked from its last item
+// to its first (the costliest first: later blocks see longer prefixes).
+// The walk is cut into 8 runs of equal cost; run x goes to grid slots x,
+// x + 8, x + 16, ..., so one XCD works through one or two streams' K/V (or
+// Q/dO) at a time, their tiles staying in its L2, and ends on the cheapest
+// items of its last stream.  Runs shorter than the longest are padded with
+// -1 (an empty workgroup).
+template <typename Cost, typename Id>
+void plan_xcd_runs(int64_t streams, int per_stream, Cost cost, Id id, std::vector<int32_t>& grid) {
   constexpr int kXcd = 8;
   int64_t total = 0;
-  for (int h = 0; h < H; ++h)
-    total += (int64_t)(row_ptr[(int64_t)h * nqb + nq] - row_ptr[(int64_t)h * nqb]) * batch;
-  const int64_t n = (int64_t)batch * H * nq;
+  for (int64_t st = 0; st < streams; ++st)
+    for (int j = 0; j < per_stream; ++j) total += cost(st, j);
+  const int64_t n = streams * per_stream;
   std::vector<std::vector<int32_t>> runs(kXcd);
   int64_t cum = 0;
   int x = 0;
-  for (int b = 0; b < batch; ++b) {
-    for (int h = 0; h < H; ++h) {
-      for (int qb = nq - 1; qb >= 0; --qb) {
-        const int64_t row = (int64_t)h * nqb + qb;
-        const int64_t c = row_ptr[row + 1] - row_ptr[row];
-        // move on once this run holds its share of the tiles (by item count
-        // when the layout has no tiles at all)
-        while (x < kXcd - 1 &&
-               (total > 0 ? cum * kXcd >= (int64_t)(x + 1) * total
-                          : (int64_t)runs[x].size() * kXcd >= n))
-          ++x;
-        runs[x].push_back((int32_t)(((int64_t)b * H + h) * nqb + qb));
-        cum += c;
-      }
+  for (int64_t st = 0; st < streams; ++st) {
+    for (int j = per_stream - 1; j >= 0; --j) {
+      // move on once this run holds its share of the cost (by item count
+      // when every item is free)
+      while (x < kXcd - 1 && (total > 0 ? cum * kXcd >= (int64_t)(x + 1) * total
+                                        : (int64_t)runs[x].size() * kXcd >= n))
+        ++x;
+      runs[x].push_back(id(st, j));
+      cum += cost(st, j);
     }
   }
   size_t len = 0;
@@ -148,6 +144,18 @@ void plan_xcd_grid(const int32_t* row_ptr, int nqb, int nq, int batch, int H,
   grid.assign(len * kXcd, -1);
   for (int r = 0; r < kXcd; ++r)
     for (size_t i = 0; i < runs[r].size(); ++i) grid[i * kXcd + r] = runs[r][i];
+}
+
+// Forward: streams (b, h), items qb < nq, cost = active tiles.
+void plan_xcd_grid(const int32_t* row_ptr, int nqb, int nq, int batch, int H,
+                   std::vector<int32_t>& grid) {
+  plan_xcd_runs(
+      (int64_t)batch * H, nq,
+      [&](int64_t st, int qb) {
+        const int64_t row = (st % H) * nqb + qb;
+        return (int64_t)(row_ptr[row + 1] - row_ptr[row]);
+      },
+      [&](int64_t st, int qb) { return (int32_t)(st * nqb + qb); }, grid);
 }
 
 esa_status hip_status(hipError_t e) { return e == hipSuccess ? ESA_OK : ESA_ERR_HIP; }
@@ -254,8 +262,9 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
   // the kernel folds the key mask into the scaled score as -inf
   if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale)) return ESA_ERR_UNSUPPORTED;
   // K/V rows are addressed through 32-bit buffer offsets per (batch, kv head)
-  if ((int64_t)a->kv_len * a->k_stride_s * 2 >= (int64_t(1) << 31) ||
-      (int64_t)a->kv_len * a->v_stride_s * 2 >= (int64_t(1) << 31) ||
+  // (rows up to one tile past kv_len are addressed, and read as zeros)
+  if ((int64_t)(a->kv_len + 128) * a->k_stride_s * 2 >= (int64_t(1) << 31) ||
+      (int64_t)(a->kv_len + 128) * a->v_stride_s * 2 >= (int64_t(1) << 31) ||
       a->k_stride_s < a->head_dim || a->v_stride_s < a->head_dim)
     return ESA_ERR_UNSUPPORTED;
   const LayoutDims d = dims_of(*p);
@@ -327,6 +336,160 @@ esa_status esa_sparse_fwd(const esa_fwd_args* a, const void* indices, int32_t in
   g.index_bytes = index_bytes; g.mask_bytes = mask_bytes;
   g.ish = idx_stride_h; g.iss = idx_stride_s; g.msh = mask_stride_h; g.mss = mask_stride_s;
   return hip_status(launch_gather_fwd(g, a->dtype == ESA_F32, false, (hipStream_t)stream));
+}
+
+esa_status esa_plan_bwd(const esa_pattern* p, const int32_t* row_ptr_host,
+                        const int32_t* col_idx_host, int32_t q_len, int32_t batch,
+                        int32_t num_kv_heads, int32_t* tile_row, int32_t* kv_ptr,
+                        int32_t* kv_tiles, int64_t kv_tiles_capacity, int32_t* kv_items,
+                        int64_t kv_items_capacity, int64_t* num_kv_tiles,
+                        int64_t* num_kv_items) {
+  esa_status s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  if (!row_ptr_host || !col_idx_host || !num_kv_tiles || !num_kv_items) return ESA_ERR_NULL;
+  if (q_len < 0 || q_len > p->seq_len || batch < 0 || num_kv_heads < 1 ||
+      p->num_heads % num_kv_heads != 0)
+    return ESA_ERR_SHAPE;
+  const LayoutDims d = dims_of(*p);
+  const int H = p->num_heads, groups = H / num_kv_heads;
+  const int nq = (q_len + p->block_m - 1) / p->block_m;
+  if ((int64_t)batch * num_kv_heads * d.nkb > INT32_MAX) return ESA_ERR_SHAPE;
+  // tiles per (kv head, key block) over query blocks below nq
+  const int64_t nrow = (int64_t)num_kv_heads * d.nkb;
+  std::vector<int64_t> cnt(nrow + 1, 0);
+  for (int h = 0; h < H; ++h)
+    for (int qb = 0; qb < nq; ++qb)
+      for (int32_t t = row_ptr_host[(int64_t)h * d.nqb + qb]; t < row_ptr_host[(int64_t)h * d.nqb + qb + 1]; ++t)
+        ++cnt[(int64_t)(h / groups) * d.nkb + col_idx_host[t] + 1];
+  for (int64_t r = 0; r < nrow; ++r) cnt[r + 1] += cnt[r];
+  const int64_t ntiles = cnt[nrow];
+  std::vector<int32_t> grid;
+  plan_xcd_runs(
+      (int64_t)batch * num_kv_heads, d.nkb,
+      [&](int64_t st, int kb) {
+        const int64_t r = (st % num_kv_heads) * d.nkb + kb;
+        return cnt[r + 1] - cnt[r];
+      },
+      [&](int64_t st, int kb) { return (int32_t)(st * d.nkb + kb); }, grid);
+  *num_kv_tiles = ntiles;
+  *num_kv_items = (int64_t)grid.size();
+  if (!tile_row || !kv_ptr || !kv_tiles || !kv_items) return ESA_OK;  // size query
+  if (kv_tiles_capacity < ntiles || kv_items_capacity < (int64_t)grid.size())
+    return ESA_ERR_CAPACITY;
+  for (int h = 0; h < H; ++h)
+    for (int qb = 0; qb < d.nqb; ++qb)
+      for (int32_t t = row_ptr_host[(int64_t)h * d.nqb + qb]; t < row_ptr_host[(int64_t)h * d.nqb + qb + 1]; ++t)
+        tile_row[t] = h * d.nqb + qb;
+  std::vector<int64_t> fill(cnt.begin(), cnt.end() - 1);
+  for (int h = 0; h < H; ++h)
+    for (int qb = 0; qb < nq; ++qb)
+      for (int32_t t = row_ptr_host[(int64_t)h * d.nqb + qb]; t < row_ptr_host[(int64_t)h * d.nqb + qb + 1]; ++t)
+        kv_tiles[fill[(int64_t)(h / groups) * d.nkb + col_idx_host[t]]++] = t;
+  for (int64_t r = 0; r <= nrow; ++r) kv_ptr[r] = (int32_t)cnt[r];
+  std::copy(grid.begin(), grid.end(), kv_items);
+  return ESA_OK;
+}
+
+esa_status esa_build_tile_masks(const esa_pattern* p, const int32_t* row_ptr,
+                                const int32_t* col_idx, int32_t q_len, uint32_t* mask_t,
+                                int64_t mask_capacity, void* stream) {
+  esa_status s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  if (!row_ptr || !col_idx || !mask_t) return ESA_ERR_NULL;
+  if (p->block_m != 128 || p->block_n != 128) return ESA_ERR_UNSUPPORTED;
+  if (q_len < 0 || q_len > p->seq_len) return ESA_ERR_SHAPE;
+  const LayoutDims d = dims_of(*p);
+  if (mask_capacity < max_tiles_of(*p, d) * 512) return ESA_ERR_CAPACITY;
+  if (!aligned(mask_t, 4)) return ESA_ERR_ALIGN;
+  return hip_status(launch_tile_masks(make_consts(*p), row_ptr, col_idx, d.nqb, q_len, mask_t,
+                                      (hipStream_t)stream));
+}
+
+esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes) {
+  if (!a || !workspace_bytes) return ESA_ERR_NULL;
+  if (a->batch < 0 || a->num_heads < 1 || a->q_len < 0) return ESA_ERR_SHAPE;
+  *workspace_bytes = (size_t)2 * a->batch * a->num_heads * a->q_len * sizeof(float);
+  return ESA_OK;
+}
+
+esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const int32_t* row_ptr,
+                           const int32_t* col_idx, const int32_t* q_items, int64_t num_q_items,
+                           const int32_t* tile_row, const int32_t* kv_ptr,
+                           const int32_t* kv_tiles, const int32_t* kv_items,
+                           int64_t num_kv_items, const uint32_t* mask_t, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (!a || !a->q || !a->k || !a->v || !a->o || !a->dout || !a->dq || !a->dk || !a->dv || !a->lse)
+    return ESA_ERR_NULL;
+  esa_status s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  if (!row_ptr || !col_idx || !q_items || !tile_row || !kv_ptr || !kv_tiles || !kv_items ||
+      !mask_t || !workspace)
+    return ESA_ERR_NULL;
+  if (a->dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (a->batch < 0 || a->num_heads < 1 || a->num_kv_heads < 1 || a->q_len < 0 || a->kv_len < 1 ||
+      a->num_heads % a->num_kv_heads != 0 || a->num_heads != p->num_heads)
+    return ESA_ERR_SHAPE;
+  if (a->head_dim != 64 && a->head_dim != 128) return ESA_ERR_UNSUPPORTED;
+  if (p->block_m != 128 || p->block_n != 128) return ESA_ERR_UNSUPPORTED;
+  if (p->layer_idx < 0 || p->layer_idx > std::max(p->num_hidden_layers - 1, 0))
+    return ESA_ERR_UNSUPPORTED;
+  if (a->q_len > a->kv_len || a->q_len > p->seq_len || a->kv_len > kMaxSeqLen) return ESA_ERR_SHAPE;
+  if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale)) return ESA_ERR_UNSUPPORTED;
+  const int64_t lim = int64_t(1) << 31;
+  // (rows up to one tile past the length are addressed, and read as zeros)
+  if ((int64_t)(a->kv_len + 128) * a->k_stride_s * 2 >= lim ||
+      (int64_t)(a->kv_len + 128) * a->v_stride_s * 2 >= lim ||
+      (int64_t)(a->q_len + 128) * a->q_stride_s * 2 >= lim ||
+      (int64_t)(a->q_len + 128) * a->dout_stride_s * 2 >= lim || a->q_stride_s < a->head_dim ||
+      a->dout_stride_s < a->head_dim || a->k_stride_s < a->head_dim || a->v_stride_s < a->head_dim)
+    return ESA_ERR_UNSUPPORTED;
+  const void* ptrs[] = {a->q, a->k, a->v, a->o, a->dout, a->dq, a->dk, a->dv};
+  for (const void* x : ptrs)
+    if (!aligned(x, 16)) return ESA_ERR_ALIGN;
+  const int64_t st[] = {a->q_stride_b,  a->q_stride_h,  a->q_stride_s,  a->k_stride_b,
+                        a->k_stride_h,  a->k_stride_s,  a->v_stride_b,  a->v_stride_h,
+                        a->v_stride_s,  a->o_stride_b,  a->o_stride_h,  a->o_stride_s,
+                        a->dout_stride_b, a->dout_stride_h, a->dout_stride_s, a->dq_stride_b,
+                        a->dq_stride_h, a->dq_stride_s, a->dk_stride_b, a->dk_stride_h,
+                        a->dk_stride_s, a->dv_stride_b, a->dv_stride_h, a->dv_stride_s};
+  for (int64_t x : st)
+    if (x % 8 != 0) return ESA_ERR_ALIGN;
+  size_t need = 0;
+  esa_bwd_workspace_size(a, &need);
+  if (workspace_bytes < need) return ESA_ERR_CAPACITY;
+  if (!aligned(workspace, 16)) return ESA_ERR_ALIGN;
+  const LayoutDims d = dims_of(*p);
+  const int nq = (a->q_len + 127) / 128;
+  const int64_t n_real = (int64_t)a->batch * a->num_heads * nq;
+  if (num_q_items < n_real || num_q_items > 8 * std::max<int64_t>(n_real, 1)) return ESA_ERR_SHAPE;
+  const int64_t kv_real = (int64_t)a->batch * a->num_kv_heads * d.nkb;
+  if (num_kv_items < kv_real || num_kv_items > 8 * std::max<int64_t>(kv_real, 1))
+    return ESA_ERR_SHAPE;
+  if (a->batch == 0 || a->q_len == 0) return ESA_OK;
+
+  BwdArgs t{};
+  t.q = (const uint16_t*)a->q; t.k = (const uint16_t*)a->k; t.v = (const uint16_t*)a->v;
+  t.o = (const uint16_t*)a->o; t.dout = (const uint16_t*)a->dout;
+  t.dq = (uint16_t*)a->dq; t.dk = (uint16_t*)a->dk; t.dv = (uint16_t*)a->dv;
+  t.lse = a->lse; t.delta = (float*)workspace; t.mask_t = mask_t;
+  t.qsb = a->q_stride_b; t.qsh = a->q_stride_h; t.qss = a->q_stride_s;
+  t.ksb = a->k_stride_b; t.ksh = a->k_stride_h; t.kss = a->k_stride_s;
+  t.vsb = a->v_stride_b; t.vsh = a->v_stride_h; t.vss = a->v_stride_s;
+  t.osb = a->o_stride_b; t.osh = a->o_stride_h; t.oss = a->o_stride_s;
+  t.dosb = a->dout_stride_b; t.dosh = a->dout_stride_h; t.doss = a->dout_stride_s;
+  t.dqsb = a->dq_stride_b; t.dqsh = a->dq_stride_h; t.dqss = a->dq_stride_s;
+  t.dksb = a->dk_stride_b; t.dksh = a->dk_stride_h; t.dkss = a->dk_stride_s;
+  t.dvsb = a->dv_stride_b; t.dvsh = a->dv_stride_h; t.dvss = a->dv_stride_s;
+  t.lsb = a->lse_stride_b; t.lsh = a->lse_stride_h;
+  t.B = a->batch; t.H = a->num_heads; t.Hkv = a->num_kv_heads;
+  t.groups = a->num_heads / a->num_kv_heads;
+  t.q_len = a->q_len; t.kv_len = a->kv_len;
+  t.nqb = d.nqb; t.nq = nq; t.nkb = d.nkb;
+  t.sm_scale = a->sm_scale; t.scale_log2 = a->sm_scale * 1.4426950408889634f;
+  t.pc = make_consts(*p);
+  t.row_ptr = row_ptr; t.col_idx = col_idx; t.q_items = q_items;
+  t.tile_row = tile_row; t.kv_ptr = kv_ptr; t.kv_tiles = kv_tiles; t.kv_items = kv_items;
+  return hip_status(launch_tile_bwd(t, a->head_dim, num_q_items, num_kv_items, (hipStream_t)stream));
 }
 
 }  // extern "C"

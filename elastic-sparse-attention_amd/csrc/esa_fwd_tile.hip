@@ -47,7 +47,7 @@
 // lane 4r + g/4's 8-byte chunk, element g%4.
 // buffer_load_dwordx4 ... lds: lane l's 16 bytes land at M0 + 16 l; offsets
 // (voffset + soffset) at or past num_records read as zero.
-#include "esa_internal.hpp"
+#include "esa_tile.hpp"
 
 namespace esa {
 
@@ -62,77 +62,6 @@ struct TileCfg {
   static constexpr int NS = D / 16;               // k-steps of QK^T
   static constexpr int ND = D / 32;               // 32-wide d blocks of PV
 };
-
-// Chunk swizzles (chunk index XOR f(row)); both depend only on row bits the
-// kernel's row offsets (multiples of 8 for V, 32 for K) leave unchanged.
-template <int D>
-__device__ __forceinline__ int swz_k(int row) {
-  return D == 128 ? (((row & 3) << 2) ^ ((row >> 2) & 3))
-                  : ((((row >> 1) & 1) << 2) ^ ((row >> 2) & 3));
-}
-template <int D>
-__device__ __forceinline__ int swz_v(int row) {
-  return D == 128 ? ((row & 3) << 2) : (((row >> 1) & 1) << 2);
-}
-
-// Rows whose index list is a contiguous run and whose indices are exact in
-// float32 (the interpolation of equal integers x reproduces x when x < 2^21).
-constexpr int kContigLimit = 1 << 21;
-// Lazy rescale threshold (log2 units): the running max moves only when a
-// block raises a row's max by more than this, so probabilities stay <= 2^8.
-constexpr float kRescaleSlack = 8.0f;
-// s_waitcnt with vmcnt(0) and the other counters left alone (gfx9 encoding)
-constexpr int kWaitVmcnt0 = 0x0F70;
-
-__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  bf16x2 v;
-  v[0] = (__bf16)lo;
-  v[1] = (__bf16)hi;
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// c + lo + hi of a packed bf16 pair, in float32 (v_dot2 with (1, 1))
-__device__ __forceinline__ float dot2_bf16(uint32_t pair, float c) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), one, c, false);
-}
-
-// max of v over lanes l and l ^ 32 (v_permlane32_swap)
-__device__ __forceinline__ float half_max(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
-                                                  false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
-// Bits [a - 32 w, b - 32 w] of word w of a 128-bit mask (a <= b, both in [0, 127]).
-__device__ __forceinline__ uint32_t range_word(int a, int b, int w) {
-  const int lo = max(a - 32 * w, 0);
-  const int hi = min(b - 32 * w, 31);
-  const int n = hi - lo;
-  const uint32_t bits = (0xffffffffu >> ((31 - n) & 31)) << (lo & 31);
-  return n >= 0 ? bits : 0u;
-}
-
-__device__ __forceinline__ bool wave_any(bool p) {
-  return __builtin_amdgcn_ballot_w64(p) != 0;
-}
-
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-typedef __attribute__((address_space(3))) void lds_void;
-typedef const __attribute__((address_space(4))) int32_t* cptr_i32;
-
-// 16 bytes per lane from a buffer resource at voffset + soffset straight into
-// LDS at dst + 16 * lane (dst uniform)
-__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t rsrc, uint16_t* dst, int voffset,
-                                           int soffset) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)dst, 16, voffset, soffset, 0, 0);
-}
 
 template <int D>
 __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
@@ -179,22 +108,8 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   }
 
   // ---- this row's index list
-  const HeadWeights hw = head_weights(A.pc, h);
-  const RowParams rp = row_params(A.pc, i);
-  const bool contig = row_ok && rp.sp == 1.0f && i < kContigLimit;
-  const int c_lo = rp.st;                                // contiguous run [c_lo, c_hi]
-  const int c_hi = min(rp.st + A.pc.w - 1, i);
-  // dilated rows: entry jp (index `pend`) is the next one not yet placed in a
-  // tile; kNone once the valid entries are used up
-  constexpr int kNone = 0x7fffffff;
-  int jp = 0;
-  int o_cur = rp.st, o_next = rp.st;
-  int pend = kNone;
-  if (row_ok && !contig) {
-    o_next = oversized(rp, 1);
-    pend = interp_index(o_cur, o_next, hw);
-    if (pend > i) pend = kNone;
-  }
+  RowWalker walk;
+  walk.init(A.pc, h, i, row_ok);
 
   float m_run = -INFINITY;  // running max, log2 units (the same in both halves)
   float l_run = 0.f;        // running sum of p over this lane's half of the keys (-> lse)
@@ -355,33 +270,8 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
     const int k0 = col_idx[t] * C::BN;
 
     // ---- this row's valid keys inside [k0, k0 + 128) as a 128-bit mask
-    uint32_t mb[4] = {0u, 0u, 0u, 0u};
-    if (contig) {
-      const int a = max(c_lo, k0) - k0, e = min(c_hi, k0 + C::BN - 1) - k0;
-      if (a <= e) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) mb[w] = range_word(a, e, w);
-      }
-    }
-    // tiles come in ascending order and hold every valid entry, so the
-    // pending entry is never below k0
-    while (pend < k0 + C::BN) {
-      const int rel = pend - k0;
-      const uint32_t bit = 1u << (rel & 31);
-      const int wsel = rel >> 5;
-      mb[0] |= wsel == 0 ? bit : 0u;
-      mb[1] |= wsel == 1 ? bit : 0u;
-      mb[2] |= wsel == 2 ? bit : 0u;
-      mb[3] |= wsel == 3 ? bit : 0u;
-      if (++jp == A.pc.w) {
-        pend = kNone;
-      } else {
-        o_cur = o_next;
-        o_next = oversized(rp, jp + 1);
-        pend = interp_index(o_cur, o_next, hw);
-        if (pend > i) pend = kNone;  // indices rise with j: the rest are masked
-      }
-    }
+    uint32_t mb[4];
+    walk.tile(k0, mb);
 
     // ---- stage 0: keys k0 .. k0 + 63 (buffer 0); stage 1 loads meanwhile.
     // The barrier also retires every wave's reads of buffer 1.

@@ -59,6 +59,41 @@ struct GatherArgs {
   int64_t ish, iss, msh, mss;
 };
 
+// Arguments of the block-sparse MFMA backward (bf16).
+struct BwdArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* o;     // forward output (q's layout strides below)
+  const uint16_t* dout;  // gradient of o
+  uint16_t* dq;
+  uint16_t* dk;
+  uint16_t* dv;
+  const float* lse;      // forward log-sum-exp, natural log, [B, H, q_len]
+  float* delta;          // workspace [B, H, q_len]: rowsum(dO * O)
+  const uint32_t* mask_t;  // [tiles][4 query sub-blocks][128 keys] key-major tile masks
+  int64_t qsb, qsh, qss;
+  int64_t ksb, ksh, kss;
+  int64_t vsb, vsh, vss;
+  int64_t osb, osh, oss;
+  int64_t dosb, dosh, doss;
+  int64_t dqsb, dqsh, dqss;
+  int64_t dksb, dksh, dkss;
+  int64_t dvsb, dvsh, dvss;
+  int64_t lsb, lsh;
+  int B, H, Hkv, groups, q_len, kv_len;
+  int nqb, nq, nkb;
+  float sm_scale, scale_log2;
+  PatternConsts pc;
+  const int32_t* row_ptr;   // forward layout (CSR of key tiles per (h, qb))
+  const int32_t* col_idx;
+  const int32_t* q_items;   // dQ work list (esa_plan_schedule)
+  const int32_t* tile_row;  // per layout tile t: h * nqb + qb
+  const int32_t* kv_ptr;    // [Hkv * nkb + 1]: tiles of each (kv head, key block)
+  const int32_t* kv_tiles;  // layout tile ids, grouped by (kv head, key block)
+  const int32_t* kv_items;  // dK/dV work list: (b * Hkv + kvh) * nkb + kb, -1 = idle
+};
+
 hipError_t launch_indices(const PatternConsts& pc, int row0, int nrows, void* indices, void* mask,
                           int elem_bytes, hipStream_t stream);
 hipError_t launch_layout(const PatternConsts& pc, const LayoutDims& ld, int32_t* row_ptr,
@@ -66,5 +101,9 @@ hipError_t launch_layout(const PatternConsts& pc, const LayoutDims& ld, int32_t*
 hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
                            hipStream_t stream);
 hipError_t launch_gather_fwd(const GatherArgs& a, bool f32, bool pattern, hipStream_t stream);
+hipError_t launch_tile_masks(const PatternConsts& pc, const int32_t* row_ptr, const int32_t* col_idx,
+                             int nqb, int q_len, uint32_t* mask_t, hipStream_t stream);
+hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,
+                           int64_t num_kv_items, hipStream_t stream);
 
 }  // namespace esa

@@ -33,8 +33,10 @@ Differences from the reference, all deliberate:
   the reference's ValueError); all three run the HIP kernels and return
   ``None`` attention weights.  There is no CPU path: CPU tensors raise.
 * ``attention_dropout`` is ignored, as the reference's Triton path ignores it.
-* Backward is not built: calling ``backward`` through the output raises
-  NotImplementedError.
+* Backward: the prefill bf16 path (head_dim 64 or 128) backpropagates
+  through hand-written block-sparse MFMA kernels (deterministic, no
+  atomics); the other paths (decode rows, float32, explicit index lists)
+  raise NotImplementedError in backward.
 * A query row with no valid entry (impossible for the elastic pattern, only
   reachable through explicit masks) gives output 0 rather than NaN.
 """
@@ -47,7 +49,7 @@ from typing import Dict, Optional, Tuple
 import torch
 import torch.nn as nn
 
-from esa_native import (ESA_BF16, ESA_F32, EsaFwdArgs, EsaPattern, check, load)
+from esa_native import (ESA_BF16, ESA_F32, EsaBwdArgs, EsaFwdArgs, EsaPattern, check, load)
 
 logger = logging.getLogger(__name__)
 
@@ -63,6 +65,7 @@ __all__ = [
     "elastic_attention_fwd",
     "elastic_attention_rows",
     "sparse_attention_fwd",
+    "elastic_attention_bwd",
 ]
 
 
@@ -163,6 +166,9 @@ class ElasticLayout:
         del work
         self.num_tiles = int(self.row_ptr_host[-1])
         self._schedules: Dict[Tuple[int, int], Tuple[torch.Tensor, int]] = {}
+        self._col_idx_host: Optional[torch.Tensor] = None
+        self._bwd_plans: Dict[Tuple[int, int, int], Tuple[torch.Tensor, ...]] = {}
+        self._masks: Dict[int, torch.Tensor] = {}
 
     def tiles_for(self, q_len: int) -> int:
         """Active tiles over the query blocks a q_len-row prefill visits,
@@ -190,6 +196,56 @@ class ElasticLayout:
         got = (items.to(self.device), n.value)
         self._schedules[key] = got
         return got
+
+
+    def bwd_plan(self, q_len: int, batch: int, num_kv_heads: int) -> Tuple[torch.Tensor, ...]:
+        """(tile_row, kv_ptr, kv_tiles, kv_items, num_kv_items) of esa_plan_bwd on
+        the device, cached per (q_len, batch, kv heads)."""
+        key = (int(q_len), int(batch), int(num_kv_heads))
+        got = self._bwd_plans.get(key)
+        if got is not None:
+            return got
+        lib = load()
+        if self._col_idx_host is None:
+            self._col_idx_host = self.col_idx[:max(self.num_tiles, 1)].cpu()
+        rp = ctypes.c_void_p(self.row_ptr_host.data_ptr())
+        ci = ctypes.c_void_p(self._col_idx_host.data_ptr())
+        nt, ni = ctypes.c_int64(), ctypes.c_int64()
+        check(lib.esa_plan_bwd(ctypes.byref(self.pattern), rp, ci, q_len, batch, num_kv_heads,
+                               None, None, None, 0, None, 0, ctypes.byref(nt), ctypes.byref(ni)),
+              "esa_plan_bwd")
+        nkb = self.num_kblocks
+        tile_row = torch.empty(max(self.num_tiles, 1), dtype=torch.int32)
+        kv_ptr = torch.empty(num_kv_heads * nkb + 1, dtype=torch.int32)
+        kv_tiles = torch.empty(max(nt.value, 1), dtype=torch.int32)
+        kv_items = torch.empty(max(ni.value, 1), dtype=torch.int32)
+        check(lib.esa_plan_bwd(ctypes.byref(self.pattern), rp, ci, q_len, batch, num_kv_heads,
+                               ctypes.c_void_p(tile_row.data_ptr()),
+                               ctypes.c_void_p(kv_ptr.data_ptr()),
+                               ctypes.c_void_p(kv_tiles.data_ptr()), kv_tiles.numel(),
+                               ctypes.c_void_p(kv_items.data_ptr()), kv_items.numel(),
+                               ctypes.byref(nt), ctypes.byref(ni)), "esa_plan_bwd")
+        got = (tile_row.to(self.device), kv_ptr.to(self.device), kv_tiles.to(self.device),
+               kv_items.to(self.device), ni.value)
+        self._bwd_plans[key] = got
+        return got
+
+    def tile_masks(self, q_len: int) -> torch.Tensor:
+        """Key-major masks of every active tile for q_len query rows
+        (esa_build_tile_masks), built once per q_len and cached: 2 KB per
+        tile."""
+        got = self._masks.get(int(q_len))
+        if got is not None:
+            return got
+        n = max(self.col_idx.numel(), 1) * 512
+        masks = torch.empty(n, dtype=torch.int32, device=self.device)
+        check(load().esa_build_tile_masks(ctypes.byref(self.pattern),
+                                          ctypes.c_void_p(self.row_ptr.data_ptr()),
+                                          ctypes.c_void_p(self.col_idx.data_ptr()), q_len,
+                                          ctypes.c_void_p(masks.data_ptr()), n,
+                                          _stream(self.device)), "esa_build_tile_masks")
+        self._masks[int(q_len)] = masks
+        return masks
 
 
 def _fwd_args(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
@@ -318,6 +374,80 @@ def sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return o, lse
 
 
+def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                          lse: torch.Tensor, dout: torch.Tensor, layout: ElasticLayout,
+                          scaling: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Block-sparse MFMA backward of ``elastic_attention_fwd`` (prefill, bf16).
+
+    ``o`` and ``dout`` are ``[B, Lq, H, D]`` (the forward's output layout),
+    ``lse`` float32 ``[B, H, Lq]``.  Returns ``dq`` ``[B, H, Lq, D]`` and
+    ``dk``, ``dv`` ``[B, Hkv, Lk, D]``: the gradients the reference's
+    ElasticSparseAttentionFunction.backward returns (:299-339), computed
+    without atomics.
+    """
+    _check_qkv(q, k, v)
+    B, H, Lq, D = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
+    o = _prep(o, 8)
+    dout = _prep(dout, 8)
+    lse = lse.contiguous()
+    dq = torch.empty_like(q)
+    dk = torch.empty(B, Hkv, Lk, D, dtype=k.dtype, device=k.device)
+    dv = torch.empty(B, Hkv, Lk, D, dtype=v.dtype, device=v.device)
+    a = EsaBwdArgs()
+    a.dtype = _dtype_code(q.dtype)
+    a.batch, a.num_heads, a.num_kv_heads = B, H, Hkv
+    a.q_len, a.kv_len, a.head_dim = Lq, Lk, D
+    for name, t, strides in (("q", q, q.stride()[:3]), ("k", k, k.stride()[:3]),
+                             ("v", v, v.stride()[:3]),
+                             ("o", o, (o.stride(0), o.stride(2), o.stride(1))),
+                             ("dout", dout, (dout.stride(0), dout.stride(2), dout.stride(1))),
+                             ("dq", dq, dq.stride()[:3]), ("dk", dk, dk.stride()[:3]),
+                             ("dv", dv, dv.stride()[:3])):
+        setattr(a, name, t.data_ptr())
+        for ax, st in zip("bhs", strides):
+            setattr(a, f"{name}_stride_{ax}", st)
+    a.lse = lse.data_ptr()
+    a.lse_stride_b, a.lse_stride_h = lse.stride(0), lse.stride(1)
+    a.sm_scale = float(scaling)
+    lib = load()
+    ws = ctypes.c_size_t()
+    check(lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(ws)), "esa_bwd_workspace_size")
+    work = torch.empty(max(ws.value // 4, 4), dtype=torch.float32, device=q.device)
+    items, n_items = layout.schedule(Lq, B)
+    tile_row, kv_ptr, kv_tiles, kv_items, n_kv = layout.bwd_plan(Lq, B, Hkv)
+    masks = layout.tile_masks(Lq)
+    vp = ctypes.c_void_p
+    check(lib.esa_elastic_bwd(ctypes.byref(a), ctypes.byref(layout.pattern),
+                              vp(layout.row_ptr.data_ptr()), vp(layout.col_idx.data_ptr()),
+                              vp(items.data_ptr()), n_items, vp(tile_row.data_ptr()),
+                              vp(kv_ptr.data_ptr()), vp(kv_tiles.data_ptr()),
+                              vp(kv_items.data_ptr()), n_kv, vp(masks.data_ptr()),
+                              vp(work.data_ptr()), work.numel() * 4, _stream(q.device)),
+          "esa_elastic_bwd")
+    return dq, dk, dv
+
+
+class _ElasticTileAttention(torch.autograd.Function):
+    """Prefill forward (block-sparse MFMA) with its block-sparse backward:
+    ``apply(q, k, v, layout, scaling) -> o [B, Lq, H, D]``."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, layout, scaling):
+        o, lse = elastic_attention_fwd(q, k, v, layout, scaling, return_lse=True)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.layout = layout
+        ctx.scaling = scaling
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = elastic_attention_bwd(q, k, v, o, lse, do, ctx.layout, ctx.scaling)
+        return dq, dk, dv, None, None
+
+
 class ElasticSparseAttentionFunction(torch.autograd.Function):
     """The reference's operator (:235-339): ``apply(q, k, v, sparse_indices,
     sparse_mask, sm_scale, num_kv_groups) -> o [B, H, Lq, D]``.  Forward only;
@@ -444,6 +574,10 @@ class ElasticSparseAttention(nn.Module):
             if Lq > kv_len:
                 raise ValueError(f"q_len ({Lq}) exceeds kv_len ({kv_len}) without cache_position")
             if q.dtype == torch.bfloat16 and D in (64, 128):
+                if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or
+                                                v.requires_grad):
+                    o = _ElasticTileAttention.apply(q, k, v, self.layout(q.device), self.scaling)
+                    return o.reshape(B, Lq, H * D), None
                 o, _ = elastic_attention_fwd(q, k, v, self.layout(q.device), self.scaling,
                                              return_lse=False)
             else:

@@ -28,7 +28,8 @@ ESA_BF16 = 1
 EXPORTED = (
     "esa_status_string", "esa_version", "esa_layout_sizes", "esa_build_indices",
     "esa_build_layout", "esa_plan_schedule", "esa_elastic_fwd", "esa_elastic_fwd_rows",
-    "esa_sparse_fwd",
+    "esa_sparse_fwd", "esa_plan_bwd", "esa_build_tile_masks", "esa_bwd_workspace_size",
+    "esa_elastic_bwd",
 )
 
 
@@ -61,6 +62,24 @@ class EsaFwdArgs(ctypes.Structure):
         ("v_stride_b", ctypes.c_int64), ("v_stride_h", ctypes.c_int64), ("v_stride_s", ctypes.c_int64),
         ("o", ctypes.c_void_p),
         ("o_stride_b", ctypes.c_int64), ("o_stride_h", ctypes.c_int64), ("o_stride_s", ctypes.c_int64),
+        ("lse", ctypes.c_void_p),
+        ("lse_stride_b", ctypes.c_int64), ("lse_stride_h", ctypes.c_int64),
+        ("sm_scale", ctypes.c_float),
+    ]
+
+
+class EsaBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("q_len", ctypes.c_int32),
+        ("kv_len", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+    ] + [f for name in ("q", "k", "v", "o", "dout", "dq", "dk", "dv")
+         for f in ((name, ctypes.c_void_p), (f"{name}_stride_b", ctypes.c_int64),
+                   (f"{name}_stride_h", ctypes.c_int64), (f"{name}_stride_s", ctypes.c_int64))] + [
         ("lse", ctypes.c_void_p),
         ("lse_stride_b", ctypes.c_int64), ("lse_stride_h", ctypes.c_int64),
         ("sm_scale", ctypes.c_float),
@@ -107,6 +126,17 @@ def load() -> ctypes.CDLL:
     lib.esa_sparse_fwd.argtypes = [P(EsaFwdArgs), vp, ctypes.c_int32, ctypes.c_int64,
                                    ctypes.c_int64, vp, ctypes.c_int32, ctypes.c_int64,
                                    ctypes.c_int64, ctypes.c_int32, vp]
+    i64, i32 = ctypes.c_int64, ctypes.c_int32
+    lib.esa_plan_bwd.restype = st
+    lib.esa_plan_bwd.argtypes = [P(EsaPattern), vp, vp, i32, i32, i32, vp, vp, vp, i64, vp, i64,
+                                 P(i64), P(i64)]
+    lib.esa_build_tile_masks.restype = st
+    lib.esa_build_tile_masks.argtypes = [P(EsaPattern), vp, vp, i32, vp, i64, vp]
+    lib.esa_bwd_workspace_size.restype = st
+    lib.esa_bwd_workspace_size.argtypes = [P(EsaBwdArgs), P(ctypes.c_size_t)]
+    lib.esa_elastic_bwd.restype = st
+    lib.esa_elastic_bwd.argtypes = [P(EsaBwdArgs), P(EsaPattern), vp, vp, vp, i64, vp, vp, vp, vp,
+                                    i64, vp, vp, ctypes.c_size_t, vp]
     _lib = lib
     return lib
 

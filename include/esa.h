@@ -169,6 +169,93 @@ esa_status esa_sparse_fwd(const esa_fwd_args* a, const void* indices,
                           int64_t mask_stride_s, int32_t attn_length,
                           void* stream);
 
+/* Tensors of one backward call over the elastic pattern: the forward's
+ * inputs, its output o (any strides, as esa_elastic_fwd wrote it) and
+ * log-sum-exp, the incoming gradient dout (o's shape), and the gradients to
+ * write: dq (q's shape), dk and dv (k's shape).  Mirrors what
+ * ElasticSparseAttentionFunction.backward receives and returns
+ * (elastic_sparse_attention.py:299-339).  All bf16 except lse (float32,
+ * natural log, [B, H, q_len] with contiguous rows). */
+typedef struct esa_bwd_args {
+  esa_dtype dtype; /* ESA_BF16 */
+  int32_t batch, num_heads, num_kv_heads, q_len, kv_len, head_dim;
+  const void* q;
+  int64_t q_stride_b, q_stride_h, q_stride_s;
+  const void* k;
+  int64_t k_stride_b, k_stride_h, k_stride_s;
+  const void* v;
+  int64_t v_stride_b, v_stride_h, v_stride_s;
+  const void* o;
+  int64_t o_stride_b, o_stride_h, o_stride_s;
+  const void* dout;
+  int64_t dout_stride_b, dout_stride_h, dout_stride_s;
+  void* dq;
+  int64_t dq_stride_b, dq_stride_h, dq_stride_s;
+  void* dk;
+  int64_t dk_stride_b, dk_stride_h, dk_stride_s;
+  void* dv;
+  int64_t dv_stride_b, dv_stride_h, dv_stride_s;
+  const float* lse;
+  int64_t lse_stride_b, lse_stride_h;
+  float sm_scale;
+} esa_bwd_args;
+
+/* Host only.  Work lists of the backward (no reference counterpart: the
+ * reference scatters dK and dV with atomics from a (q_len, H, B) grid,
+ * :299-339).  From esa_build_layout's row_ptr and col_idx (host copies) and
+ * q_len, batch and num_kv_heads, writes
+ *   tile_row[T]         T = row_ptr[H * nqb]: h * nqb + qb of layout tile t
+ *   kv_ptr[Hkv * nkb + 1], kv_tiles[*num_kv_tiles]: for each (kv head,
+ *                       key block), the layout tiles of query blocks below
+ *                       ceil(q_len / 128) of its query heads that hold the
+ *                       key block, in (head, query block) order
+ *   kv_items[*num_kv_items]: (b * Hkv + kvh) * nkb + kb work items laid out
+ *                       for the 8 XCDs like esa_plan_schedule's, -1 = idle.
+ * With any of tile_row, kv_ptr, kv_tiles, kv_items NULL only the two counts
+ * are written. */
+esa_status esa_plan_bwd(const esa_pattern* p, const int32_t* row_ptr_host,
+                        const int32_t* col_idx_host, int32_t q_len,
+                        int32_t batch, int32_t num_kv_heads,
+                        int32_t* tile_row, int32_t* kv_ptr,
+                        int32_t* kv_tiles, int64_t kv_tiles_capacity,
+                        int32_t* kv_items, int64_t kv_items_capacity,
+                        int64_t* num_kv_tiles, int64_t* num_kv_items);
+
+/* Key-major masks of every active layout tile for a backward over q_len
+ * query rows: mask_t[t * 512 + qs * 128 + k] bit r is set when query row
+ * qb * 128 + 32 qs + r (< q_len) has key col_idx[t] * 128 + k among its
+ * valid elastic entries (:470-535).  mask_t holds row_ptr[H * nqb] * 512
+ * uint32 (mask_capacity).  Depends only on the pattern and q_len, so it can
+ * be built once and reused. */
+esa_status esa_build_tile_masks(const esa_pattern* p, const int32_t* row_ptr,
+                                const int32_t* col_idx, int32_t q_len,
+                                uint32_t* mask_t, int64_t mask_capacity,
+                                void* stream);
+
+/* Host only.  Bytes of float32 workspace esa_elastic_bwd needs
+ * (2 * batch * num_heads * q_len floats). */
+esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes);
+
+/* Block-sparse backward over the elastic pattern: replaces the backward
+ * branch of the Triton kernel (elastic_sparse_attention.py:168-233) and
+ * ElasticSparseAttentionFunction.backward (:299-339) for the prefill
+ * forward of esa_elastic_fwd.  Writes dq, dk and dv (every element; no
+ * zero-initialisation needed, no atomics: each gradient row is accumulated
+ * by one workgroup in a fixed order, so results are deterministic).
+ * q_items/num_q_items: esa_plan_schedule's list for (q_len, batch);
+ * tile_row, kv_ptr, kv_tiles, kv_items/num_kv_items: esa_plan_bwd's;
+ * mask_t: esa_build_tile_masks' for this q_len (all device memory).
+ * Requires dtype ESA_BF16, head_dim 64 or 128, block 128 x 128, a finite
+ * sm_scale > 0, q_len <= kv_len, 16-byte aligned rows. */
+esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p,
+                           const int32_t* row_ptr, const int32_t* col_idx,
+                           const int32_t* q_items, int64_t num_q_items,
+                           const int32_t* tile_row, const int32_t* kv_ptr,
+                           const int32_t* kv_tiles, const int32_t* kv_items,
+                           int64_t num_kv_items, const uint32_t* mask_t,
+                           void* workspace, size_t workspace_bytes,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

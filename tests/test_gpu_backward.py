@@ -1,0 +1,103 @@
+"""Block-sparse MFMA backward against autograd through the float32 oracle (GPU).
+
+The reference's ElasticSparseAttentionFunction.backward
+(elastic_sparse_attention.py:299-339) returns dq, dk, dv of the forward; the
+oracle's forward_fp32 restates that forward in differentiable torch ops, so
+torch autograd through it (float32, on the bf16-valued inputs) is the
+reference gradient.  bf16 bar: max |err| <= 2e-2 * max |ref| per tensor (P
+and dS enter the MFMAs rounded to bf16, the gradients are stored in bf16).
+The backward accumulates every gradient in one workgroup in a fixed order,
+so two runs agree bit for bit.
+"""
+import pytest
+import torch
+
+from esa_oracle import elastic_indices, forward_fp32, prepared_rows, scaling_for, seeded_inputs
+from elastic_sparse_attention import (ElasticLayout, ElasticSparseAttention, elastic_attention_bwd,
+                                      elastic_attention_fwd, make_pattern)
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+REL = 2e-2
+
+
+def reference_grads(q, k, v, idx, msk, sc, groups, g):
+    qf, kf, vf = (t.float().requires_grad_() for t in (q, k, v))
+    o, _ = forward_fp32(qf, kf, vf, idx, msk, sc, groups, chunk_rows=512)
+    (o * g).sum().backward()
+    return qf.grad, kf.grad, vf.grad
+
+
+def rel_err(got, ref):
+    return ((got.float().cpu() - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+
+
+@pytest.mark.parametrize("B,H,Hkv,L,Lq,D,layer", [
+    (1, 4, 4, 1024, 1024, 128, 4),
+    (1, 4, 4, 1024, 1024, 128, 0),
+    (1, 4, 4, 1024, 1024, 128, 7),
+    (1, 4, 4, 1024, 1024, 64, 3),
+    (2, 8, 2, 640, 640, 128, 5),     # GQA, batch
+    (1, 4, 4, 1000, 700, 128, 6),    # q_len < kv_len, ragged blocks
+    (1, 2, 1, 200, 200, 64, 2),      # MQA, short
+])
+def test_backward_matches_autograd(B, H, Hkv, L, Lq, D, layer):
+    print(f"bwd B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} layer={layer}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=layer + 3, scale=1.0, Lq=Lq)
+    idx, msk = elastic_indices(L, layer, 8, H, 64)
+    pi, pm = prepared_rows(idx, msk, Lq, L, L)
+    sc = scaling_for(D)
+    g = torch.randn(B, H, Lq, D, generator=torch.Generator().manual_seed(layer)).to(torch.bfloat16)
+    rq, rk, rv = reference_grads(q, k, v, pi, pm, sc, H // Hkv, g.float())
+
+    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc)
+    do = g.to(DEV).permute(0, 2, 1, 3).contiguous()  # [B, Lq, H, D] like o
+    dq, dk, dv = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc)
+    e = (rel_err(dq, rq), rel_err(dk, rk), rel_err(dv, rv))
+    print(f"  rel err dq {e[0]:.3e} dk {e[1]:.3e} dv {e[2]:.3e}", flush=True)
+    assert all(torch.isfinite(t.float()).all() for t in (dq, dk, dv))
+    assert max(e) <= REL
+    # deterministic: a second run is bit-identical
+    dq2, dk2, dv2 = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc)
+    assert torch.equal(dq, dq2) and torch.equal(dk, dk2) and torch.equal(dv, dv2)
+
+
+def test_module_autograd():
+    """The drop-in module's output backpropagates through the HIP backward."""
+    B, H, L, D, layer = 1, 4, 768, 128, 4
+    m = ElasticSparseAttention(layer, 8, H, D, 64, 1024)
+    q, k, v = seeded_inputs(B, H, H, L, D, torch.bfloat16, seed=12, scale=1.0)
+    idx, msk = elastic_indices(L, layer, 8, H, 64)
+    g = torch.randn(B, L, H * D, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    out, _ = m(qd, kd, vd)
+    (out.float() * g.to(DEV).float()).sum().backward()
+    gref = g.float().view(B, L, H, D).permute(0, 2, 1, 3)
+    rq, rk, rv = reference_grads(q, k, v, idx, msk, m.scaling, 1, gref)
+    e = (rel_err(qd.grad, rq), rel_err(kd.grad, rk), rel_err(vd.grad, rv))
+    print(f"  module rel err dq {e[0]:.3e} dk {e[1]:.3e} dv {e[2]:.3e}", flush=True)
+    assert max(e) <= REL
+
+
+def test_backward_full_size_8k_layer4():
+    """H = 32, L = 8192, D = 128 at layer 4: every gradient against autograd
+    through the oracle on a 4-head slice (heads are independent)."""
+    B, H, L, D, layer = 1, 32, 8192, 128, 4
+    q, k, v = seeded_inputs(B, H, H, L, D, torch.bfloat16, seed=77, scale=128 ** -0.25)
+    sc = scaling_for(D)
+    g = torch.randn(B, H, L, D, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc)
+    dq, dk, dv = elastic_attention_bwd(qd, kd, vd, o, lse, g.to(DEV).permute(0, 2, 1, 3).contiguous(),
+                                       lay, sc)
+    idx, msk = elastic_indices(L, layer, 8, H, 64)
+    heads = [0, 13, 31]
+    for h in heads:
+        rq, rk, rv = reference_grads(q[:, h:h + 1], k[:, h:h + 1], v[:, h:h + 1], idx[h:h + 1],
+                                     msk[h:h + 1], sc, 1, g[:, h:h + 1].float())
+        e = (rel_err(dq[:, h:h + 1], rq), rel_err(dk[:, h:h + 1], rk), rel_err(dv[:, h:h + 1], rv))
+        print(f"  head {h} rel err dq {e[0]:.3e} dk {e[1]:.3e} dv {e[2]:.3e}", flush=True)
+        assert max(e) <= REL
