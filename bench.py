@@ -93,6 +93,39 @@ def copy_calibration(torch) -> None:
     print(json.dumps({"copy_bytes": COPY_BYTES, "copies": 3}), flush=True)
 
 
+def time_backward(torch, m, q, k, v, lay, counted_fwd, steps, warmup) -> dict:
+    """The block-sparse backward (dQ, dK, dV from the forward's O and LSE) on
+    the same inputs: mean of `steps` launches (HIP events on the launch
+    stream) after `warmup`; the tile masks and work lists are built (and
+    cached) before timing, as the layout is.  TFLOP/s counts 2.5x the
+    forward's active-tile flops (QK^T, dP, dV, dK, dQ)."""
+    from elastic_sparse_attention import elastic_attention_bwd, elastic_attention_fwd
+    B, H, L, D = q.shape
+    o, lse = elastic_attention_fwd(q, k, v, lay, m.scaling)
+    g = torch.Generator(device="cpu").manual_seed(1)
+    do = torch.randn(B, L, H, D, generator=g).to(q.dtype).to(q.device)
+    t0 = time.perf_counter()
+    lay.tile_masks(L)
+    lay.bwd_plan(L, B, k.shape[1])
+    torch.cuda.synchronize()
+    setup_ms = (time.perf_counter() - t0) * 1e3
+    for _ in range(warmup):
+        elastic_attention_bwd(q, k, v, o, lse, do, lay, m.scaling)
+    stream = torch.cuda.current_stream(q.device)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    torch.cuda.synchronize()
+    for s_ev, e_ev in evs:
+        s_ev.record(stream)
+        elastic_attention_bwd(q, k, v, o, lse, do, lay, m.scaling)
+        e_ev.record(stream)
+    torch.cuda.synchronize()
+    ms = statistics.mean(a.elapsed_time(b) for a, b in evs)
+    return {"ms": round(ms, 4), "tflops": round(2.5 * counted_fwd / (ms * 1e-3) / 1e12, 3),
+            "flops_convention": "2.5 x forward active-tile flops",
+            "mask_and_plan_setup_ms": round(setup_ms, 2)}
+
+
 def traffic_from_profile(name: str):
     """HBM bytes per launch of the forward kernel, from the committed rocprofv3
     --pmc summary for this workload (profiles/<name>), or None."""
@@ -114,6 +147,8 @@ def main() -> None:
     ap.add_argument("--config", default="32k", choices=sorted(CONFIGS))
     ap.add_argument("--layer", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--backward", action="store_true",
+                    help="also time the block-sparse backward (reported beside the forward)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of known size (HBM counter scale)")
     args = ap.parse_args()
@@ -219,6 +254,8 @@ def main() -> None:
         "roofline": roofline,
         "cpu_baseline": None,
     }
+    if args.backward:
+        out["backward"] = time_backward(torch, m, q, k, v, lay, counted, args.steps, args.warmup)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.config, args.layer, counted)
     print(json.dumps(out), flush=True)

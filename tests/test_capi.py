@@ -204,3 +204,106 @@ def test_plan_schedule_rejects():
         == en.ESA_ERR_CAPACITY
     assert lib.esa_plan_schedule(ctypes.byref(p), None, 1024, 1, None, 0, ctypes.byref(n)) \
         == en.ESA_ERR_NULL
+
+
+def plan_bwd(p, rp, ci, q_len, batch, hkv):
+    lib = en.load()
+    nt, ni = ctypes.c_int64(), ctypes.c_int64()
+    rp, ci = rp.contiguous(), ci.contiguous()
+    vp = ctypes.c_void_p
+    st = lib.esa_plan_bwd(ctypes.byref(p), vp(rp.data_ptr()), vp(ci.data_ptr()), q_len, batch, hkv,
+                          None, None, None, 0, None, 0, ctypes.byref(nt), ctypes.byref(ni))
+    assert st == en.ESA_OK
+    nkb = (p.seq_len + 127) // 128
+    tile_row = torch.empty(max(int(rp[-1]), 1), dtype=torch.int32)
+    kv_ptr = torch.empty(hkv * nkb + 1, dtype=torch.int32)
+    kv_tiles = torch.empty(max(nt.value, 1), dtype=torch.int32)
+    kv_items = torch.empty(max(ni.value, 1), dtype=torch.int32)
+    st = lib.esa_plan_bwd(ctypes.byref(p), vp(rp.data_ptr()), vp(ci.data_ptr()), q_len, batch, hkv,
+                          vp(tile_row.data_ptr()), vp(kv_ptr.data_ptr()), vp(kv_tiles.data_ptr()),
+                          kv_tiles.numel(), vp(kv_items.data_ptr()), kv_items.numel(),
+                          ctypes.byref(nt), ctypes.byref(ni))
+    return st, tile_row, kv_ptr, kv_tiles[:nt.value], kv_items[:ni.value]
+
+
+@pytest.mark.parametrize("L,Lq,B,H,Hkv,layer", [(1024, 1024, 1, 4, 4, 4), (1000, 700, 2, 8, 2, 6),
+                                                (2048, 2048, 1, 4, 1, 0), (300, 300, 3, 2, 2, 7)])
+def test_plan_bwd_transposes_the_layout(L, Lq, B, H, Hkv, layer):
+    """kv lists = for each (kv head, key block), the layout tiles of the group's
+    query heads (query blocks below ceil(Lq/128)) holding that key block, in
+    (head, query block) order; tile_row inverts the CSR; the kv work list holds
+    every (b, kv head, key block) once, in 8 interleaved runs."""
+    w = 64
+    p = en.EsaPattern(L, w, layer, 8, H, 128, 128)
+    idx, msk = elastic_indices(L, layer, 8, H, w)
+    rp, ci = block_layout(idx, msk, 128, 128)
+    st, tile_row, kv_ptr, kv_tiles, kv_items = plan_bwd(p, rp, ci, Lq, B, Hkv)
+    assert st == en.ESA_OK
+    nqb = (L + 127) // 128
+    nkb = nqb
+    nq = (Lq + 127) // 128
+    groups = H // Hkv
+    for h in range(H):
+        for qb in range(nqb):
+            for t in range(int(rp[h * nqb + qb]), int(rp[h * nqb + qb + 1])):
+                assert int(tile_row[t]) == h * nqb + qb
+    for kvh in range(Hkv):
+        for kb in range(nkb):
+            expect = [t for h in range(kvh * groups, (kvh + 1) * groups) for qb in range(nq)
+                      for t in range(int(rp[h * nqb + qb]), int(rp[h * nqb + qb + 1]))
+                      if int(ci[t]) == kb]
+            r = kvh * nkb + kb
+            assert kv_tiles[int(kv_ptr[r]):int(kv_ptr[r + 1])].tolist() == expect
+    items = kv_items.tolist()
+    assert len(items) % 8 == 0
+    assert sorted(x for x in items if x >= 0) == list(range(B * Hkv * nkb))
+
+
+def test_bwd_entry_points_reject_bad_arguments():
+    lib = en.load()
+    p = pat(L=1024, H=4)
+    fake = ctypes.c_void_p(4096)
+    a = en.EsaBwdArgs()
+    a.dtype, a.batch, a.num_heads, a.num_kv_heads = en.ESA_BF16, 1, 4, 4
+    a.q_len, a.kv_len, a.head_dim = 256, 256, 128
+    for name in ("q", "k", "v", "o", "dout", "dq", "dk", "dv"):
+        setattr(a, name, 4096)
+        setattr(a, f"{name}_stride_b", 4 * 256 * 128)
+        setattr(a, f"{name}_stride_h", 256 * 128)
+        setattr(a, f"{name}_stride_s", 128)
+    a.lse = 4096
+    a.lse_stride_b, a.lse_stride_h = 4 * 256, 256
+    a.sm_scale = 128 ** -0.5
+    ws = ctypes.c_size_t()
+    assert lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(ws)) == en.ESA_OK
+    assert ws.value == 2 * 1 * 4 * 256 * 4
+
+    def call(args, items=8, kv_items=64, wsb=ws.value):
+        return lib.esa_elastic_bwd(ctypes.byref(args), ctypes.byref(p), fake, fake, fake, items,
+                                   fake, fake, fake, fake, kv_items, fake, fake, wsb, None)
+
+    assert call(a, wsb=16) == en.ESA_ERR_CAPACITY
+    assert call(a, items=7) == en.ESA_ERR_SHAPE
+    assert call(a, kv_items=31) == en.ESA_ERR_SHAPE
+    b = en.EsaBwdArgs.from_buffer_copy(a)
+    b.dtype = en.ESA_F32
+    assert call(b) == en.ESA_ERR_DTYPE
+    b = en.EsaBwdArgs.from_buffer_copy(a)
+    b.head_dim = 96
+    assert call(b) == en.ESA_ERR_UNSUPPORTED
+    b = en.EsaBwdArgs.from_buffer_copy(a)
+    b.sm_scale = -1.0
+    assert call(b) == en.ESA_ERR_UNSUPPORTED
+    b = en.EsaBwdArgs.from_buffer_copy(a)
+    b.dk = None
+    assert call(b) == en.ESA_ERR_NULL
+    b = en.EsaBwdArgs.from_buffer_copy(a)
+    b.q_len = 300
+    assert call(b) == en.ESA_ERR_SHAPE  # q_len > kv_len
+    b = en.EsaBwdArgs.from_buffer_copy(a)
+    b.dq_stride_s = 130
+    assert call(b) == en.ESA_ERR_ALIGN
+    assert lib.esa_build_tile_masks(ctypes.byref(p), fake, fake, 256, fake, 1, None) \
+        == en.ESA_ERR_CAPACITY
+    assert lib.esa_build_tile_masks(ctypes.byref(p), fake, fake, 2048, fake, 1 << 30, None) \
+        == en.ESA_ERR_SHAPE
