@@ -12,7 +12,9 @@ time is reported separately.
 Prints ONE JSON line.  value = counted active-tile flops / wall time per
 step, where counted flops = active 128x128 tiles x 4 * 128 * 128 * D.
 roofline.achieved uses the same flops over the kernel's own average duration
-(HIP events on the launch stream).  cpu_baseline times the reference's
+(HIP events on the launch stream).  Inside an active tile the kernel issues
+MFMAs only for the 32 x 32 blocks that hold a valid key for one of a wave's
+rows; executed_flop_fraction and executed_mfma_tflops report that work.  cpu_baseline times the reference's
 PyTorch fallback (_naive_forward, restated in oracle/) on the host cores on a
 bounded sample of query rows of the same workload, extrapolated linearly
 (every row costs the same w-key gather there).
@@ -126,6 +128,16 @@ def time_backward(torch, m, q, k, v, lay, counted_fwd, steps, warmup) -> dict:
             "mask_and_plan_setup_ms": round(setup_ms, 2)}
 
 
+def executed_blocks(torch, lay, L: int) -> int:
+    """Number of (active tile, 32-row block, 32-key block) triples in which
+    some row has a valid key, per batch element: the blocks the forward
+    issues MFMAs for.  From the layout's key-major tile masks (32 row bits per
+    key), built here after the timed region."""
+    masks = lay.tile_masks(L)
+    n = lay.num_tiles  # every tile of the layout; rows at or past L carry no bits
+    return int(masks[:n * 512].view(n, 4, 4, 32).ne(0).any(-1).sum().item())
+
+
 def traffic_from_profile(name: str):
     """HBM bytes per launch of the forward kernel, from the committed rocprofv3
     --pmc summary for this workload (profiles/<name>), or None."""
@@ -216,6 +228,9 @@ def main() -> None:
 
     achieved = counted / (kern_ms * 1e-3) / 1e12
     value = counted / wall / 1e12
+    # MFMA work actually issued: inside each active tile a wave skips the
+    # 32 x 32 (rows x keys) blocks where none of its rows has a valid key
+    executed = B * executed_blocks(torch, lay, L) * 4.0 * 32 * 32 * D
     traffic = traffic_from_profile(
         f"tile_fwd_kernel_bf16_B{B}_H{H}_L{L}_D{D}_layer{args.layer}_pmc.md")
     if args.layer == 0:
@@ -248,6 +263,8 @@ def main() -> None:
                    "block": [128, 128], "active_tiles": tiles},
         "pct_of_bf16_mfma_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
         "kernel_ms": round(kern_ms, 4),
+        "executed_flop_fraction": round(executed / counted, 4),
+        "executed_mfma_tflops": round(executed / (kern_ms * 1e-3) / 1e12, 3),
         "useful_tflops": round(useful / wall / 1e12, 4),
         "hbm_gbs_algorithmic": round(alg_bytes / (kern_ms * 1e-3) / 1e9, 1),
         "layout_build_ms": round(layout_ms, 2),

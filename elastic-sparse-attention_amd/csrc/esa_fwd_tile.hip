@@ -3,9 +3,12 @@
 // Replaces the forward branch of the reference's per-token Triton kernel
 // (elastic_sparse_attention.py:117-166) for prefill.  One workgroup (4 waves,
 // 256 lanes) owns one (batch, head, 128-row query block) work item and visits
-// only the 128-key tiles the block layout lists as active for it; every
-// active tile is computed densely (128 x 128 x D on MFMA), so the executed
-// tile equals the layout tile.
+// only the 128-key tiles the block layout lists as active for it.  The
+// executed tile is the layout tile: every active tile's K and V are staged
+// whole and its mask is built whole; inside it, each wave issues MFMAs only
+// for the 32 x 32 (rows x keys) blocks where one of its rows has a valid key
+// (about 36% of them at dilated layers), since the others contribute exactly
+// zero.
 //
 // K/V staging: a tile is consumed in two 64-key stages.  Each stage's K and V
 // rows are copied HBM -> LDS by buffer_load_dwordx4 ... lds (no registers),
@@ -29,9 +32,8 @@
 //                  layout gives each lane one row and 16 of the block's keys;
 //                  the mask enters as the accumulator's initial value (0 or
 //                  -inf).  A block that holds no valid key for any row of the
-//                  wave is skipped (its probabilities are 0): at dilated
-//                  layers the 32 rows' keys cluster, so about half the blocks
-//                  are skipped.  The running max is raised only when a row's
+//                  wave is skipped whole (K reads, both products, softmax).
+//                  The running max is raised only when a row's
 //                  block max exceeds it by more than 8 (log2), so the O
 //                  rescale is rare; probabilities stay below 2^8.
 //   O^T += V^T P^T 2 ND x v_mfma_f32_32x32x16_bf16 (A = V^T read with
@@ -175,9 +177,10 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   auto block = [&](const uint16_t* Kb, const uint16_t* Vb, int kbl, uint32_t mbits) {
     // lane half hf holds keys 8*(r/4) + 4*hf + r%4 of the block
     const uint32_t mk = mbits >> (4 * hf);
-    // a block no row of the wave has a valid key in contributes p = 0: its
-    // softmax is skipped (its MFMAs still run: the tile is computed densely)
-    const bool active = wave_any(mk != 0u);
+    // a 32 x 32 block in which no row of the wave has a valid key contributes
+    // p = 0 to every row: its reads, MFMAs and softmax are all skipped (O, the
+    // running max and the sums are unchanged, bit for bit)
+    if (!wave_any(mk != 0u)) return;
 
     // all K operand reads first, so their LDS latency overlaps
     bf16x8 ka[C::NS];
@@ -185,13 +188,11 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
     for (int s = 0; s < C::NS; ++s) ka[s] = *(const bf16x8*)(Kb + kaddr[s] + 32 * kbl * D);
     // the mask enters as the accumulator's initial value: 0 for a valid key,
     // -inf for a masked one
-    f32x16 sacc = f32x16{};
-    if (active) {
+    f32x16 sacc;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const uint32_t on = (uint32_t)__builtin_amdgcn_sbfe((int)mk, 8 * (r / 4) + r % 4, 1);
-        sacc[r] = __uint_as_float(~on & 0xff800000u);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const uint32_t on = (uint32_t)__builtin_amdgcn_sbfe((int)mk, 8 * (r / 4) + r % 4, 1);
+      sacc[r] = __uint_as_float(~on & 0xff800000u);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -210,46 +211,41 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
     __builtin_amdgcn_sched_barrier(0);
 
     uint32_t pw[8];  // P as packed bf16 pairs: pw[q] holds regs 2q, 2q+1
-    if (active) {
-      // x = scaled score relative to the running max (log2 units); a masked
-      // key stays -inf (scale > 0)
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;
-      float smax = -INFINITY;
+    // x = scaled score relative to the running max (log2 units); a masked
+    // key stays -inf (scale > 0)
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float smax = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        sacc[r] = __builtin_fmaf(sacc[r], scale, -m_use);
-        smax = fmaxf(smax, sacc[r]);
-      }
-      smax = half_max(smax);
-      // raise the running max of a row when this block exceeds it by more
-      // than the slack (or when the row sees its first valid key)
-      const bool grow = m_run == -INFINITY ? smax != -INFINITY : smax > kRescaleSlack;
-      if (wave_any(grow)) {
-        const float delta = grow ? smax : 0.f;
-        // rows that do not grow keep alpha = 1 (m_run may still be -inf there)
-        const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - (m_use + delta)) : 1.0f;
-        l_run *= alpha;
-        n_run *= alpha;
+    for (int r = 0; r < 16; ++r) {
+      sacc[r] = __builtin_fmaf(sacc[r], scale, -m_use);
+      smax = fmaxf(smax, sacc[r]);
+    }
+    smax = half_max(smax);
+    // raise the running max of a row when this block exceeds it by more
+    // than the slack (or when the row sees its first valid key)
+    const bool grow = m_run == -INFINITY ? smax != -INFINITY : smax > kRescaleSlack;
+    if (wave_any(grow)) {
+      const float delta = grow ? smax : 0.f;
+      // rows that do not grow keep alpha = 1 (m_run may still be -inf there)
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - (m_use + delta)) : 1.0f;
+      l_run *= alpha;
+      n_run *= alpha;
 #pragma unroll
-        for (int d = 0; d < C::ND; ++d) oacc[d] *= alpha;
-        m_run = grow ? m_use + delta : m_run;
+      for (int d = 0; d < C::ND; ++d) oacc[d] *= alpha;
+      m_run = grow ? m_use + delta : m_run;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[r] -= delta;
-      }
+      for (int r = 0; r < 16; ++r) sacc[r] -= delta;
+    }
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const float p0 = __builtin_amdgcn_exp2f(sacc[2 * q]);
-        const float p1 = __builtin_amdgcn_exp2f(sacc[2 * q + 1]);
-        l_run += p0;
-        l_run += p1;
-        pw[q] = pack_bf16x2(p0, p1);
-        // normalise O by the probabilities PV actually used, so a row led by
-        // one key reproduces that key's value row
-        n_run = dot2_bf16(pw[q], n_run);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) pw[q] = 0u;
+    for (int q = 0; q < 8; ++q) {
+      const float p0 = __builtin_amdgcn_exp2f(sacc[2 * q]);
+      const float p1 = __builtin_amdgcn_exp2f(sacc[2 * q + 1]);
+      l_run += p0;
+      l_run += p1;
+      pw[q] = pack_bf16x2(p0, p1);
+      // normalise O by the probabilities PV actually used, so a row led by
+      // one key reproduces that key's value row
+      n_run = dot2_bf16(pw[q], n_run);
     }
 
 #pragma unroll
