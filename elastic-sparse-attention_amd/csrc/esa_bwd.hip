@@ -115,11 +115,12 @@ __global__ __launch_bounds__(256) void tile_mask_kernel(PatternConsts pc, const 
 }
 
 // ---------------------------------------------------------------------------
-// One workgroup per CU: the K and V operands (64 VGPRs at D = 128) and the
+// At D = 128 one workgroup per CU: the K and V operands (64 VGPRs) and the
 // dK^T, dV^T accumulators (128) stay resident, which leaves no room for the
 // per-block operands at two workgroups per CU (the compiler spills there).
+// D = 64 needs half of that and keeps two.
 template <int D>
-__global__ __launch_bounds__(256, 1) void dkdv_kernel(BwdArgs A, const float* lse2) {
+__global__ __launch_bounds__(256, D == 128 ? 1 : 2) void dkdv_kernel(BwdArgs A, const float* lse2) {
   using C = BwdCfg<D>;
   __shared__ __attribute__((aligned(1024))) uint16_t q_st0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint16_t o_st0[C::STAGE];  // dO rows

@@ -492,4 +492,30 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
   return hip_status(launch_tile_bwd(t, a->head_dim, num_q_items, num_kv_items, (hipStream_t)stream));
 }
 
+esa_status esa_reachability(int32_t seq_len, int32_t attention_length,
+                            int32_t num_hidden_layers, int32_t num_heads, int32_t position,
+                            uint32_t* reach, uint32_t* work, int32_t* layer_counts,
+                            void* stream) {
+  if (!reach || !work) return ESA_ERR_NULL;
+  if (reach == work) return ESA_ERR_SHAPE;
+  esa_pattern p{};
+  p.seq_len = seq_len;
+  p.attention_length = attention_length;
+  p.num_hidden_layers = num_hidden_layers;
+  p.num_heads = num_heads;
+  p.block_m = p.block_n = 128;
+  esa_status st = check_pattern(&p);
+  if (st != ESA_OK) return st;
+  if (position < 0 || position >= seq_len) return ESA_ERR_SHAPE;
+  if (!aligned(reach, 4) || !aligned(work, 4) || !aligned(layer_counts, 4)) return ESA_ERR_ALIGN;
+  // layers in processing order: the last layer first
+  std::vector<PatternConsts> layers((size_t)num_hidden_layers);
+  for (int k = 0; k < num_hidden_layers; ++k) {
+    p.layer_idx = num_hidden_layers - 1 - k;
+    layers[(size_t)k] = make_consts(p);
+  }
+  return hip_status(launch_reachability(layers.data(), num_hidden_layers, position, reach, work,
+                                        layer_counts, (hipStream_t)stream));
+}
+
 }  // extern "C"

@@ -103,6 +103,9 @@ hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
 hipError_t launch_gather_fwd(const GatherArgs& a, bool f32, bool pattern, hipStream_t stream);
 hipError_t launch_tile_masks(const PatternConsts& pc, const int32_t* row_ptr, const int32_t* col_idx,
                              int nqb, int q_len, uint32_t* mask_t, hipStream_t stream);
+hipError_t launch_reachability(const PatternConsts* layers, int num_layers, int position,
+                               uint32_t* reach, uint32_t* work, int32_t* counts,
+                               hipStream_t stream);
 hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,
                            int64_t num_kv_items, hipStream_t stream);
 

@@ -29,7 +29,7 @@ EXPORTED = (
     "esa_status_string", "esa_version", "esa_layout_sizes", "esa_build_indices",
     "esa_build_layout", "esa_plan_schedule", "esa_elastic_fwd", "esa_elastic_fwd_rows",
     "esa_sparse_fwd", "esa_plan_bwd", "esa_build_tile_masks", "esa_bwd_workspace_size",
-    "esa_elastic_bwd",
+    "esa_elastic_bwd", "esa_reachability",
 )
 
 
@@ -137,6 +137,9 @@ def load() -> ctypes.CDLL:
     lib.esa_elastic_bwd.restype = st
     lib.esa_elastic_bwd.argtypes = [P(EsaBwdArgs), P(EsaPattern), vp, vp, vp, i64, vp, vp, vp, vp,
                                     i64, vp, vp, ctypes.c_size_t, vp]
+    i32 = ctypes.c_int32
+    lib.esa_reachability.restype = st
+    lib.esa_reachability.argtypes = [i32, i32, i32, i32, i32, vp, vp, vp, vp]
     _lib = lib
     return lib
 

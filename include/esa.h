@@ -256,6 +256,23 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p,
                            void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* Replaces check_attention_holes_pytorch (check_attn_hole.py:53-180): the
+ * tokens `position` reaches through num_hidden_layers elastic layers of
+ * num_heads heads (each layer's index set is the pattern of
+ * esa_build_indices at that layer_idx).  The last layer starts the set with
+ * the position and its valid indices over all heads; every earlier layer, from
+ * num_hidden_layers - 2 down to 0, adds the valid indices of every token
+ * already in the set.  reach (device, (position + 32) / 32 words) receives bit
+ * j % 32 of word j / 32 set iff token j is reachable; work is a device buffer
+ * of the same size.  layer_counts (device, num_hidden_layers int32, or NULL)
+ * receives the set size after each layer, last layer first.  0 <= position <
+ * seq_len (the reference's ValueError).  No index buffers: each pass
+ * regenerates the indices.  Asynchronous on `stream`. */
+esa_status esa_reachability(int32_t seq_len, int32_t attention_length,
+                            int32_t num_hidden_layers, int32_t num_heads,
+                            int32_t position, uint32_t* reach, uint32_t* work,
+                            int32_t* layer_counts, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -27,6 +27,9 @@ It restates, with the same torch CPU ops, the reference's
                                from ``elastic_indices``.
 * ``dense_mask``            <- ``_create_full_sparse_mask`` (:537-572), used as
                                a brute-force cross-check at small sizes.
+* ``attention_reachability`` <- ``check_attention_holes_pytorch`` in
+                               ``check_attn_hole.py`` (:53-180): the tokens one
+                               position reaches through all layers.
 
 How each function is pinned (beyond restating the reference's ops):
   elastic_indices  golden SHA-256 hashes and slices written by importing the
@@ -44,6 +47,12 @@ How each function is pinned (beyond restating the reference's ops):
   naive_forward    used only as the CPU baseline; its bf16 rounding points are
                    the reference's, checked against forward_fp32 within the
                    bf16 tolerance.
+  attention_reachability  boolean products of the ``dense_mask`` adjacency
+                   matrices at small sizes; closed forms (one layer = the
+                   sliding window; a position below w reaches its whole
+                   prefix; position 0 reaches only itself); the reference's
+                   stated result (no holes at L = 131072, 8 layers, 8 heads,
+                   w = 64, theory/note.md:85).
 """
 from __future__ import annotations
 
@@ -53,6 +62,7 @@ from typing import Optional, Tuple
 import torch
 
 __all__ = [
+    "attention_reachability",
     "elastic_indices",
     "prepared_rows",
     "block_layout",
@@ -174,6 +184,42 @@ def dense_mask(indices: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
     valid = mask.bool()
     full[h_i[valid], q_i[valid], k_i[valid]] = True
     return full
+
+
+def attention_reachability(num_hidden_layers: int, num_attention_heads: int,
+                           attn_length: int, position: int):
+    """Tokens ``position`` reaches through the layers, as
+    ``check_attention_holes_pytorch`` (check_attn_hole.py:53-180) tracks them.
+
+    The last layer starts the set with the position itself and its valid
+    indices over all heads (:102-114); each earlier layer, from nl - 2 down to
+    0, adds the valid indices of every token already in the set (:134-156).
+    The reference stops once the set is the whole history (:161-163); a full
+    set stays full, so running every layer gives the same final set.
+
+    Returns ``(reach, counts)``: ``reach`` bool ``[position + 1]`` and the set
+    size after each layer, last layer first.  A row's indices do not depend on
+    the sequence length, so they come from ``elastic_indices`` over rows
+    ``0..position``; the checker's own copy of the formula (:5-51) also
+    requires idx >= 0 and leaves masked entries unfilled, which does not
+    change the valid set.
+    """
+    n = position + 1
+    reach = torch.zeros(n, dtype=torch.bool)
+    reach[position] = True                                               # :114
+    counts = []
+    for layer in range(num_hidden_layers - 1, -1, -1):
+        idx, msk = elastic_indices(n, layer, num_hidden_layers, num_attention_heads, attn_length)
+        if layer == num_hidden_layers - 1:
+            sources = torch.tensor([position])                           # :106-107
+        else:
+            sources = torch.where(reach)[0]                              # :141
+        new = idx[:, sources, :][msk[:, sources, :].bool()].unique()     # :145-150
+        new = new[new < n]                                               # :154
+        reach[new] = True                                                # :156
+        counts.append(int(reach.sum()))                                  # :158
+        del idx, msk
+    return reach, counts
 
 
 def forward_fp32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

@@ -307,3 +307,27 @@ def test_bwd_entry_points_reject_bad_arguments():
         == en.ESA_ERR_CAPACITY
     assert lib.esa_build_tile_masks(ctypes.byref(p), fake, fake, 2048, fake, 1 << 30, None) \
         == en.ESA_ERR_SHAPE
+
+
+def test_reachability_rejects_bad_arguments():
+    lib = en.load()
+    f1, f2 = ctypes.c_void_p(4096), ctypes.c_void_p(8192)
+    call = lambda L, w, nl, H, pos, r=f1, wk=f2, c=None: lib.esa_reachability(L, w, nl, H, pos, r,
+                                                                            wk, c, None)
+    assert call(1024, 64, 8, 8, 1024) == en.ESA_ERR_SHAPE   # position == seq_len
+    assert call(1024, 64, 8, 8, -1) == en.ESA_ERR_SHAPE
+    assert call(1024, 0, 8, 8, 10) == en.ESA_ERR_SHAPE      # attn_length <= 0
+    assert call(1024, 64, 0, 8, 10) == en.ESA_ERR_SHAPE     # no layers
+    assert call(1024, 64, 8, 0, 10) == en.ESA_ERR_SHAPE     # no heads
+    assert call(1024, 64, 8, 8, 10, r=None) == en.ESA_ERR_NULL
+    assert call(1024, 64, 8, 8, 10, wk=None) == en.ESA_ERR_NULL
+    assert call(1024, 64, 8, 8, 10, wk=f1) == en.ESA_ERR_SHAPE   # reach and work alias
+    assert call(1024, 64, 8, 8, 10, c=ctypes.c_void_p(4098)) == en.ESA_ERR_ALIGN
+
+
+def test_hole_checker_validates_before_the_gpu():
+    import check_attn_hole as ch
+    with pytest.raises(ValueError, match="position_id must be between 0 and 99"):
+        ch.attention_reachability(100, 8, 8, 64, position_id=100)
+    with pytest.raises(ValueError, match="attn_length must be positive"):
+        ch.attention_reachability(100, 8, 8, 0)
