@@ -3,14 +3,16 @@
 // Replaces the forward branch of the reference's per-token Triton kernel
 // (elastic_sparse_attention.py:117-166) for prefill.  One workgroup (4 waves,
 // 256 lanes) owns one (batch, head, 128-row query block) work item and visits
-// only the 128-key tiles the block layout lists as active for it.  The
-// executed tile is the layout tile: every active tile's K and V are staged
-// whole and its mask is built whole; inside it, each wave issues MFMAs only
-// for the 32 x 32 (rows x keys) blocks where one of its rows has a valid key
-// (about 36% of them at dilated layers), since the others contribute exactly
+// only the key blocks the block layout lists as active for it.  Inside a
+// staged block each wave issues MFMAs only for the 32 x 32 (rows x keys)
+// blocks where one of its rows has a valid key (about 36% of those in active
+// 128 x 128 tiles at dilated layers), since the others contribute exactly
 // zero.
 //
-// K/V staging: a tile is consumed in two 64-key stages.  Each stage's K and V
+// K/V staging: keys are consumed in 64-key stages.  With a layout built at
+// 64-key blocks (the 128-key tiles split in halves, a half listed only when a
+// row of the query block has a valid key in it) each listed block is one
+// stage; a 128-key layout gives two stages per tile.  Each stage's K and V
 // rows are copied HBM -> LDS by buffer_load_dwordx4 ... lds (no registers),
 // one stage ahead, into two stage buffers (64 KB per workgroup at D = 128, so
 // two workgroups share a CU).  Rows past kv_len fall outside the buffer
@@ -19,13 +21,13 @@
 // 16-byte MFMA operand reads; V: the 4 rows of a ds_read_b64_tr_b16 group hit
 // distinct bank groups), since the direct loads write whole rows unpadded.
 //
-// Per tile and wave (32 query rows):
+// Per stage and wave (32 query rows):
 //   mask           each lane owns one query row; rows whose index list is a
 //                  contiguous run (the sliding window of layer 0, and the
 //                  first w - 1 rows of every layer) set a bit range, the
 //                  others walk their elastic indices (the same float32
-//                  sequence as the layout builder) through the tile
-// then for each 32-key block of the tile:
+//                  sequence as the layout builder) through the stage
+// then for each 32-key block of the stage:
 //   S^T = K Q^T    NS x v_mfma_f32_32x32x16_bf16 (A = K rows from LDS,
 //                  B = Q kept in registers for the whole item)
 //   softmax        online, in registers, log2 domain.  The S^T accumulator
@@ -56,7 +58,6 @@ namespace esa {
 template <int D>
 struct TileCfg {
   static constexpr int BM = 128;
-  static constexpr int BN = 128;
   static constexpr int HALF = 64;                 // keys per stage
   static constexpr int CPR = D / 8;               // 16-byte chunks per row
   static constexpr int STAGE = HALF * D;          // elements per stage buffer (one matrix)
@@ -65,16 +66,12 @@ struct TileCfg {
   static constexpr int ND = D / 32;               // 32-wide d blocks of PV
 };
 
-template <int D>
+// RING = false: a layout of 128- or 64-key blocks, staged in 64-key stages
+// with a workgroup barrier per stage; RING = true: a layout of 32-key blocks,
+// staged through a ring of slots that each wave consumes at its own pace.
+template <int D, bool RING>
 __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   using C = TileCfg<D>;
-  // stage buffers (HALF rows x D, rows unpadded, chunks swizzled); separate
-  // objects, so the compiler can tell reads of one buffer from the direct
-  // loads into the other
-  __shared__ __attribute__((aligned(1024))) uint16_t k_st0[C::STAGE];
-  __shared__ __attribute__((aligned(1024))) uint16_t v_st0[C::STAGE];
-  __shared__ __attribute__((aligned(1024))) uint16_t k_st1[C::STAGE];
-  __shared__ __attribute__((aligned(1024))) uint16_t v_st1[C::STAGE];
   // the layout and the work list are read-only here: scalar loads
   const cptr_i32 items = (cptr_i32)A.items;
   const cptr_i32 row_ptr = (cptr_i32)A.row_ptr;
@@ -120,9 +117,6 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
 #pragma unroll
   for (int d = 0; d < C::ND; ++d) oacc[d] = f32x16{};
 
-  const int64_t lrow = (int64_t)h * A.nqb + qb;
-  const int t0 = row_ptr[lrow], t1 = row_ptr[lrow + 1];
-
   // ---- staging: buffer resources over this (batch, kv head)'s rows; keys at
   // or past kv_len are outside num_records and load as zeros (the host keeps
   // kv_len * row stride * 2 below 2^31)
@@ -132,28 +126,6 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh), (short)0,
       (int)((int64_t)A.kv_len * A.vss * 2), 0x00020000);
-  // load j of this lane fills chunk slot (LOADS wave + j) * 64 + lane of a
-  // stage buffer: row slot / CPR, physical chunk slot % CPR
-  int koff[C::LOADS], voff[C::LOADS];
-#pragma unroll
-  for (int j = 0; j < C::LOADS; ++j) {
-    const int slot = (C::LOADS * wave + j) * 64 + lane;
-    const int row = slot / C::CPR, pc = slot % C::CPR;
-    koff[j] = (row * (int)A.kss + 8 * (pc ^ swz_k<D>(row))) * 2;
-    voff[j] = (row * (int)A.vss + 8 * (pc ^ swz_v<D>(row))) * 2;
-  }
-  // stage hh (keys 64 hh .. 64 hh + 63) of tile kt -> buffers (kd, vd)
-  auto issue = [&](int kt, int hh, uint16_t* kd, uint16_t* vd) {
-    const int key0 = col_idx[kt] * C::BN + C::HALF * hh;
-    const int ks = key0 * (int)A.kss * 2, vs = key0 * (int)A.vss * 2;
-#pragma unroll
-    for (int j = 0; j < C::LOADS; ++j) {
-      // each load writes 64 lanes x 16 bytes = 512 elements
-      load_lds16(krs, kd + (C::LOADS * wave + j) * 512, koff[j], ks);
-      load_lds16(vrs, vd + (C::LOADS * wave + j) * 512, voff[j], vs);
-    }
-  };
-
   // ---- LDS read addresses (elements), fixed for the whole item: K rows
   // 32 kbl + l32 at chunk 2 s + hf; V rows 4 hf + lam / 4 (+ 32 kbl + 16 u,
   // + 8) at column 32 d + 16 (g4 & 1) + 4 (lam & 3)
@@ -189,11 +161,7 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
     // the mask enters as the accumulator's initial value: 0 for a valid key,
     // -inf for a masked one
     f32x16 sacc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const uint32_t on = (uint32_t)__builtin_amdgcn_sbfe((int)mk, 8 * (r / 4) + r % 4, 1);
-      sacc[r] = __uint_as_float(~on & 0xff800000u);
-    }
+    mask_init<0>(sacc, ~mk);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < C::NS; ++s) sacc = mfma32(ka[s], qop[s], sacc);
@@ -260,30 +228,178 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
     }
   };
 
-  if (t0 < t1) issue(t0, 0, k_st0, v_st0);
+  const int64_t lrow = (int64_t)h * A.nqb + qb;
+  if constexpr (!RING) {
+    // stage buffers (HALF rows x D, rows unpadded, chunks swizzled); separate
+    // objects, so the compiler can tell reads of one buffer from the direct
+    // loads into the other
+    __shared__ __attribute__((aligned(1024))) uint16_t k_st0[C::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint16_t v_st0[C::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint16_t k_st1[C::STAGE];
+    __shared__ __attribute__((aligned(1024))) uint16_t v_st1[C::STAGE];
+    // ---- the item's 64-key stages: layout key blocks of 64 keys are one stage
+    // each; 128-key blocks are two (stage s is half s & 1 of block s >> 1)
+    const int sh = A.stage_shift;
+    const int s0 = row_ptr[lrow] << sh, s1 = row_ptr[lrow + 1] << sh;
 
-  for (int t = t0; t < t1; ++t) {
-    const int k0 = col_idx[t] * C::BN;
+    // load j of this lane fills chunk slot (LOADS wave + j) * 64 + lane of a
+    // stage buffer: row slot / CPR, physical chunk slot % CPR
+    int koff[C::LOADS], voff[C::LOADS];
+  #pragma unroll
+    for (int j = 0; j < C::LOADS; ++j) {
+      const int slot = (C::LOADS * wave + j) * 64 + lane;
+      const int row = slot / C::CPR, pc = slot % C::CPR;
+      koff[j] = (row * (int)A.kss + 8 * (pc ^ swz_k<D>(row))) * 2;
+      voff[j] = (row * (int)A.vss + 8 * (pc ^ swz_v<D>(row))) * 2;
+    }
+    auto stage_key0 = [&](int st) { return (col_idx[st >> sh] << (6 + sh)) + ((st & sh) << 6); };
+    // the 64 keys from key0 -> buffers (kd, vd)
+    auto issue = [&](int key0, uint16_t* kd, uint16_t* vd) {
+      const int ks = key0 * (int)A.kss * 2, vs = key0 * (int)A.vss * 2;
+  #pragma unroll
+      for (int j = 0; j < C::LOADS; ++j) {
+        // each load writes 64 lanes x 16 bytes = 512 elements
+        load_lds16(krs, kd + (C::LOADS * wave + j) * 512, koff[j], ks);
+        load_lds16(vrs, vd + (C::LOADS * wave + j) * 512, voff[j], vs);
+      }
+    };
 
-    // ---- this row's valid keys inside [k0, k0 + 128) as a 128-bit mask
-    uint32_t mb[4];
-    walk.tile(k0, mb);
+    // ---- two stage buffers, one stage ahead: each barrier retires every
+    // wave's reads of the other buffer before the next stage is loaded into it.
+    // Stages go in pairs (buffer 0, buffer 1); this row's valid keys of both
+    // are walked first.  The next two stage keys are read together at the top
+    // of a pair (clamped indices: unconditional scalar loads, one wait).
+    int ka = s0 < s1 ? stage_key0(s0) : 0;
+    if (s0 < s1) issue(ka, k_st0, v_st0);
+    for (int st = s0; st < s1; st += 2) {
+      const bool has_b = st + 1 < s1, has_c = st + 2 < s1;
+      const int kb = stage_key0(min(st + 1, s1 - 1));
+      const int kc = stage_key0(min(st + 2, s1 - 1));
+      uint32_t mb[4];
+      walk.stage_pair(ka, kb, has_b, mb);
 
-    // ---- stage 0: keys k0 .. k0 + 63 (buffer 0); stage 1 loads meanwhile.
-    // The barrier also retires every wave's reads of buffer 1.
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __syncthreads();
+      if (has_b) issue(kb, k_st1, v_st1);
+      block(k_st0, v_st0, 0, mb[0]);
+      block(k_st0, v_st0, 1, mb[1]);
+      if (!has_b) break;
+
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      __syncthreads();
+      if (has_c) issue(kc, k_st0, v_st0);
+      block(k_st1, v_st1, 0, mb[2]);
+      block(k_st1, v_st1, 1, mb[3]);
+      ka = kc;
+    }
+  } else {
+    // ---- a ring of NB slots of 32-key stages and no workgroup barrier in the
+    // loop: each wave walks the item's stages at its own pace.
+    //   wait     until the stage's slot is marked ready (ready[slot] == stage)
+    //   compute  its 32 x 32 block of the stage
+    //   release  done[slot] += 1; the wave that brings the count to 4 uses
+    //            (the last to leave the slot) loads stage + NB into it, all
+    //            of it, alone
+    //   publish  a wave marks a stage it loaded ready one stage later, after
+    //            waiting for its own loads (s_waitcnt vmcnt), so the wave that
+    //            loads (often the slowest) never waits for load latency
+    // A wave can so run up to NB - 2 stages ahead of the slowest instead of
+    // meeting it at every stage.  A wave waits only for a stage loaded by a
+    // wave that has left an earlier stage, and every wave publishes before it
+    // waits, so each wait ends; each spin is also capped.  The stage loads
+    // are inline asm (stage_load_asm), so the compiler adds no waits for them
+    // before the reads of other slots.
+    constexpr int SK = 32;                     // keys per stage
+    constexpr int NB = D == 128 ? 4 : 8;       // slots: 64 KB at D = 128 and 64
+    constexpr int SEL = SK * D;                // elements per slot and matrix
+    constexpr int J = SK * C::CPR / 64;        // 16-byte loads per lane and matrix
+    constexpr int ROWS4 = 256 / C::CPR;        // rows filled by 4 loads
+    constexpr int kSpinCap = 1 << 22;
+    __shared__ __attribute__((aligned(1024))) uint16_t k_ring[NB * SEL];
+    __shared__ __attribute__((aligned(1024))) uint16_t v_ring[NB * SEL];
+    __shared__ int ready[NB], done[NB];
+    // the flags stay in the LDS address space (a generic pointer would make
+    // flat accesses, which also wait on the vector-memory counter)
+    typedef __attribute__((address_space(3))) volatile int lds_vint;
+    lds_vint* vready = (lds_vint*)ready;
+    const int s0 = row_ptr[lrow], n = row_ptr[lrow + 1] - s0;
+
+    // a stage loaded by one wave: load j fills chunk j * 64 + lane, row
+    // (j * 64 + lane) / CPR; the chunk swizzles repeat every 4 loads
+    int rkoff[4], rvoff[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int slot = jj * 64 + lane;
+      const int row = slot / C::CPR, pc = slot % C::CPR;
+      rkoff[jj] = (row * (int)A.kss + 8 * (pc ^ swz_k<D>(row))) * 2;
+      rvoff[jj] = (row * (int)A.vss + 8 * (pc ^ swz_v<D>(row))) * 2;
+    }
+    const u32x4 krw = rsrc_words(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh,
+                                 (int)((int64_t)A.kv_len * A.kss * 2));
+    const u32x4 vrw = rsrc_words(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh,
+                                 (int)((int64_t)A.kv_len * A.vss * 2));
+    const uint32_t k_lds = (uint32_t)(uintptr_t)(lds_void*)k_ring;
+    const uint32_t v_lds = (uint32_t)(uintptr_t)(lds_void*)v_ring;
+    auto load_stage = [&](int k) {
+      const int key0 = col_idx[s0 + k] * SK;
+      const uint32_t off = (uint32_t)((k % NB) * SEL * 2);
+      stage_load_asm<J>(krw, k_lds + off, rkoff, key0 * (int)A.kss * 2,
+                        (key0 + ROWS4) * (int)A.kss * 2);
+      stage_load_asm<J>(vrw, v_lds + off, rvoff, key0 * (int)A.vss * 2,
+                        (key0 + ROWS4) * (int)A.vss * 2);
+    };
+
+    // prologue: the first NB stages, loaded by the four waves together
+    const int pre = min(NB, n);
+    for (int k = wave; k < pre; k += 4) load_stage(k);
+    if (tid < NB) {
+      ready[tid] = tid < pre ? tid : -1;
+      done[tid] = 0;
+    }
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
-    issue(t, 1, k_st1, v_st1);
-    block(k_st0, v_st0, 0, mb[0]);
-    block(k_st0, v_st0, 1, mb[1]);
 
-    // ---- stage 1: keys k0 + 64 .. k0 + 127 (buffer 1); the next tile's
-    // stage 0 loads meanwhile
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    __syncthreads();
-    if (t + 1 < t1) issue(t + 1, 0, k_st0, v_st0);
-    block(k_st1, v_st1, 0, mb[2]);
-    block(k_st1, v_st1, 1, mb[3]);
+    int older = -1, newer = -1;  // stages this wave loaded at its last two stage ends
+    for (int k = 0; k < n; ++k) {
+      // publish the older load: at most the newer one's 2 J loads remain in flight
+      if (older >= 0) {
+        if (newer >= 0)
+          __builtin_amdgcn_s_waitcnt(kWaitVmcntRing<2 * J>());
+        else
+          __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        asm volatile("" ::: "memory");
+        if (lane == 0) vready[older % NB] = older;
+      }
+      older = newer;
+      newer = -1;
+
+      uint32_t mb[1];
+      walk.span<1>(col_idx[s0 + k] * SK, mb);
+      for (int guard = 0;
+           __builtin_amdgcn_readfirstlane(vready[k % NB]) != k && guard < kSpinCap; ++guard)
+        __builtin_amdgcn_s_sleep(1);
+      asm volatile("" ::: "memory");
+      block(k_ring + (k % NB) * SEL, v_ring + (k % NB) * SEL, 0, mb[0]);
+
+      // release: this wave's reads of the slot have completed
+      __builtin_amdgcn_s_waitcnt(kWaitLgkmcnt0);
+      asm volatile("" ::: "memory");
+      int prev = 0;
+      if (lane == 0) prev = atomicAdd(&done[k % NB], 1);
+      prev = __builtin_amdgcn_readlane(prev, 0);
+      if (prev == 4 * (k / NB) + 3 && k + NB < n) {
+        load_stage(k + NB);
+        newer = k + NB;
+      }
+    }
+    if (older >= 0 || newer >= 0) {
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      asm volatile("" ::: "memory");
+      if (lane == 0) {
+        if (older >= 0) vready[older % NB] = older;
+        if (newer >= 0) vready[newer % NB] = newer;
+      }
+    }
   }
 
   // ---- epilogue: normalise and store O rows and the log-sum-exp
@@ -314,10 +430,17 @@ hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
                            hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
   dim3 grid((unsigned)num_items);
-  if (head_dim == 128)
-    tile_fwd_kernel<128><<<grid, 256, 0, stream>>>(a);
-  else
-    tile_fwd_kernel<64><<<grid, 256, 0, stream>>>(a);
+  if (a.ring) {
+    if (head_dim == 128)
+      tile_fwd_kernel<128, true><<<grid, 256, 0, stream>>>(a);
+    else
+      tile_fwd_kernel<64, true><<<grid, 256, 0, stream>>>(a);
+  } else {
+    if (head_dim == 128)
+      tile_fwd_kernel<128, false><<<grid, 256, 0, stream>>>(a);
+    else
+      tile_fwd_kernel<64, false><<<grid, 256, 0, stream>>>(a);
+  }
   return hipGetLastError();
 }
 

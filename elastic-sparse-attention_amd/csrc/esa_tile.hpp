@@ -25,8 +25,15 @@ constexpr int kContigLimit = 1 << 21;
 // Lazy rescale threshold (log2 units): the running max moves only when a
 // block raises a row's max by more than this, so probabilities stay <= 2^8.
 constexpr float kRescaleSlack = 8.0f;
-// s_waitcnt with vmcnt(0) and the other counters left alone (gfx9 encoding)
-constexpr int kWaitVmcnt0 = 0x0F70;
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt
+// 6:4, lgkmcnt 11:8; a field at its maximum leaves that counter alone)
+constexpr int kWaitVmcnt0 = 0x0F70;    // vmcnt(0)
+constexpr int kWaitLgkmcnt0 = 0xC07F;  // lgkmcnt(0)
+template <int N>
+constexpr int kWaitVmcntRing() {       // vmcnt(N), N < 64
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  return (N & 15) | ((N >> 4) << 14) | 0x0F70;
+}
 
 __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -61,6 +68,99 @@ __device__ __forceinline__ uint32_t range_word(int a, int b, int w) {
   const int n = hi - lo;
   const uint32_t bits = (0xffffffffu >> ((31 - n) & 31)) << (lo & 31);
   return n >= 0 ? bits : 0u;
+}
+
+// S^T accumulator initial values from a lane's masked-key bits nmk (bit
+// 8 (r / 4) + r % 4 for register r): -inf where set, else 0.  One v_bfe_i32
+// (0 or -1) and one v_and per register; written as inline asm because the
+// compiler turns a one-bit sign extract into a test, compare and select.
+template <int R>
+__device__ __forceinline__ void mask_init(f32x16& s, uint32_t nmk) {
+  if constexpr (R < 16) {
+    uint32_t v;
+    asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(v) : "v"(nmk), "i"(8 * (R / 4) + R % 4));
+    s[R] = __uint_as_float(v & 0xff800000u);
+    mask_init<R + 1>(s, nmk);
+  }
+}
+
+// Buffer resource words (base, stride 0, num_records, the raw-buffer flags
+// the kernels pass to __builtin_amdgcn_make_buffer_rsrc) for inline asm.
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, int num_records) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  u32x4 r;
+  r[0] = (uint32_t)a;
+  r[1] = (uint32_t)(a >> 32) & 0xffffu;
+  r[2] = (uint32_t)num_records;
+  r[3] = 0x00020000u;
+  return r;
+}
+
+// One wave copies a 32-row stage of one matrix HBM -> LDS: J (4 or 8)
+// buffer_load_dwordx4 ... lds per lane, load j reading voffset vo[j & 3] +
+// soffset (so0 for j < 4, so1 for j >= 4) into LDS bytes lds + 1024 j +
+// 16 lane.  Written as inline asm so that the compiler does not track these
+// LDS writes: it would otherwise wait for them (s_waitcnt vmcnt) before
+// every later access of the same LDS object; the caller orders them with
+// explicit s_waitcnt.  M0 is saved and restored; each write of M0 is
+// followed by one wait state before the load that reads it.
+template <int J>
+__device__ __forceinline__ void stage_load_asm(u32x4 rsrc, uint32_t lds, const int (&vo)[4], int so0,
+                                               int so1) {
+  uint32_t sav;
+  if constexpr (J == 8) {
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %6, %7 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %3, %6, %7 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %4, %6, %7 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %5, %6, %7 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %6, %8 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %3, %6, %8 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %4, %6, %8 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %5, %6, %8 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(sav)
+        : "s"(lds), "v"(vo[0]), "v"(vo[1]), "v"(vo[2]), "v"(vo[3]), "s"(rsrc), "s"(so0), "s"(so1)
+        : "memory", "scc");
+  } else {
+    static_assert(J == 4, "4 or 8 loads per stage");
+    (void)so1;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %6, %7 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %3, %6, %7 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %4, %6, %7 offen lds\n\t"
+        "s_add_u32 m0, m0, 0x400\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %5, %6, %7 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(sav)
+        : "s"(lds), "v"(vo[0]), "v"(vo[1]), "v"(vo[2]), "v"(vo[3]), "s"(rsrc), "s"(so0)
+        : "memory", "scc");
+  }
 }
 
 __device__ __forceinline__ bool wave_any(bool p) {
@@ -112,25 +212,26 @@ struct RowWalker {
     }
   }
 
-  // Valid keys of this row inside [k0, k0 + 128); tiles must come in
-  // ascending order and include every tile holding a valid entry.
-  __device__ __forceinline__ void tile(int k0, uint32_t (&mb)[4]) {
-    mb[0] = mb[1] = mb[2] = mb[3] = 0u;
+  // Valid keys of this row inside [k0, k0 + 32 NW) as NW mask words; spans
+  // must come in ascending, non-overlapping order and include every span
+  // holding a valid entry of the row.
+  template <int NW>
+  __device__ __forceinline__ void span(int k0, uint32_t* mb) {
+#pragma unroll
+    for (int q = 0; q < NW; ++q) mb[q] = 0u;
     if (contig) {
-      const int a = max(c_lo, k0) - k0, e = min(c_hi, k0 + 127) - k0;
+      const int a = max(c_lo, k0) - k0, e = min(c_hi, k0 + 32 * NW - 1) - k0;
       if (a <= e) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) mb[q] = range_word(a, e, q);
+        for (int q = 0; q < NW; ++q) mb[q] = range_word(a, e, q);
       }
     }
-    while (pend < k0 + 128) {
+    while (pend < k0 + 32 * NW) {
       const int rel = pend - k0;
       const uint32_t bit = 1u << (rel & 31);
       const int wsel = rel >> 5;
-      mb[0] |= wsel == 0 ? bit : 0u;
-      mb[1] |= wsel == 1 ? bit : 0u;
-      mb[2] |= wsel == 2 ? bit : 0u;
-      mb[3] |= wsel == 3 ? bit : 0u;
+#pragma unroll
+      for (int q = 0; q < NW; ++q) mb[q] |= wsel == q ? bit : 0u;
       if (++jp == w) {
         pend = kNone;
       } else {
@@ -138,6 +239,24 @@ struct RowWalker {
         o_next = oversized(rp, jp + 1);
         pend = interp_index(o_cur, o_next, hw);
         if (pend > row) pend = kNone;  // indices rise with j: the rest are masked
+      }
+    }
+  }
+
+  // Valid keys of this row inside the 128-key tile [k0, k0 + 128).
+  __device__ __forceinline__ void tile(int k0, uint32_t (&mb)[4]) { span<4>(k0, mb); }
+
+  // Two 64-key stages at ka and kb (kb > ka, or no second stage): mb[0..1]
+  // for ka, mb[2..3] for kb; adjacent stages are walked as one 128-key span.
+  __device__ __forceinline__ void stage_pair(int ka, int kb, bool has_b, uint32_t (&mb)[4]) {
+    if (has_b && kb == ka + 64) {
+      span<4>(ka, mb);
+    } else {
+      span<2>(ka, mb);
+      if (has_b) {
+        span<2>(kb, mb + 2);
+      } else {
+        mb[2] = mb[3] = 0u;
       }
     }
   }
