@@ -66,12 +66,16 @@ struct TileCfg {
   static constexpr int ND = D / 32;               // 32-wide d blocks of PV
 };
 
-// RING = false: a layout of 128- or 64-key blocks, staged in 64-key stages
-// with a workgroup barrier per stage; RING = true: a layout of 32-key blocks,
-// staged through a ring of slots that each wave consumes at its own pace.
-template <int D, bool RING>
+template <int D>
 __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   using C = TileCfg<D>;
+  // stage buffers (HALF rows x D, rows unpadded, chunks swizzled); separate
+  // objects, so the compiler can tell reads of one buffer from the direct
+  // loads into the other
+  __shared__ __attribute__((aligned(1024))) uint16_t k_st0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_st0[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t k_st1[C::STAGE];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_st1[C::STAGE];
   // the layout and the work list are read-only here: scalar loads
   const cptr_i32 items = (cptr_i32)A.items;
   const cptr_i32 row_ptr = (cptr_i32)A.row_ptr;
@@ -229,177 +233,60 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
   };
 
   const int64_t lrow = (int64_t)h * A.nqb + qb;
-  if constexpr (!RING) {
-    // stage buffers (HALF rows x D, rows unpadded, chunks swizzled); separate
-    // objects, so the compiler can tell reads of one buffer from the direct
-    // loads into the other
-    __shared__ __attribute__((aligned(1024))) uint16_t k_st0[C::STAGE];
-    __shared__ __attribute__((aligned(1024))) uint16_t v_st0[C::STAGE];
-    __shared__ __attribute__((aligned(1024))) uint16_t k_st1[C::STAGE];
-    __shared__ __attribute__((aligned(1024))) uint16_t v_st1[C::STAGE];
-    // ---- the item's 64-key stages: layout key blocks of 64 keys are one stage
-    // each; 128-key blocks are two (stage s is half s & 1 of block s >> 1)
-    const int sh = A.stage_shift;
-    const int s0 = row_ptr[lrow] << sh, s1 = row_ptr[lrow + 1] << sh;
+  // ---- the item's 64-key stages: layout key blocks of 64 keys are one stage
+  // each; 128-key blocks are two (stage s is half s & 1 of block s >> 1)
+  const int sh = A.stage_shift;
+  const int s0 = row_ptr[lrow] << sh, s1 = row_ptr[lrow + 1] << sh;
 
-    // load j of this lane fills chunk slot (LOADS wave + j) * 64 + lane of a
-    // stage buffer: row slot / CPR, physical chunk slot % CPR
-    int koff[C::LOADS], voff[C::LOADS];
-  #pragma unroll
-    for (int j = 0; j < C::LOADS; ++j) {
-      const int slot = (C::LOADS * wave + j) * 64 + lane;
-      const int row = slot / C::CPR, pc = slot % C::CPR;
-      koff[j] = (row * (int)A.kss + 8 * (pc ^ swz_k<D>(row))) * 2;
-      voff[j] = (row * (int)A.vss + 8 * (pc ^ swz_v<D>(row))) * 2;
-    }
-    auto stage_key0 = [&](int st) { return (col_idx[st >> sh] << (6 + sh)) + ((st & sh) << 6); };
-    // the 64 keys from key0 -> buffers (kd, vd)
-    auto issue = [&](int key0, uint16_t* kd, uint16_t* vd) {
-      const int ks = key0 * (int)A.kss * 2, vs = key0 * (int)A.vss * 2;
-  #pragma unroll
-      for (int j = 0; j < C::LOADS; ++j) {
-        // each load writes 64 lanes x 16 bytes = 512 elements
-        load_lds16(krs, kd + (C::LOADS * wave + j) * 512, koff[j], ks);
-        load_lds16(vrs, vd + (C::LOADS * wave + j) * 512, voff[j], vs);
-      }
-    };
-
-    // ---- two stage buffers, one stage ahead: each barrier retires every
-    // wave's reads of the other buffer before the next stage is loaded into it.
-    // Stages go in pairs (buffer 0, buffer 1); this row's valid keys of both
-    // are walked first.  The next two stage keys are read together at the top
-    // of a pair (clamped indices: unconditional scalar loads, one wait).
-    int ka = s0 < s1 ? stage_key0(s0) : 0;
-    if (s0 < s1) issue(ka, k_st0, v_st0);
-    for (int st = s0; st < s1; st += 2) {
-      const bool has_b = st + 1 < s1, has_c = st + 2 < s1;
-      const int kb = stage_key0(min(st + 1, s1 - 1));
-      const int kc = stage_key0(min(st + 2, s1 - 1));
-      uint32_t mb[4];
-      walk.stage_pair(ka, kb, has_b, mb);
-
-      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-      __syncthreads();
-      if (has_b) issue(kb, k_st1, v_st1);
-      block(k_st0, v_st0, 0, mb[0]);
-      block(k_st0, v_st0, 1, mb[1]);
-      if (!has_b) break;
-
-      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-      __syncthreads();
-      if (has_c) issue(kc, k_st0, v_st0);
-      block(k_st1, v_st1, 0, mb[2]);
-      block(k_st1, v_st1, 1, mb[3]);
-      ka = kc;
-    }
-  } else {
-    // ---- a ring of NB slots of 32-key stages and no workgroup barrier in the
-    // loop: each wave walks the item's stages at its own pace.
-    //   wait     until the stage's slot is marked ready (ready[slot] == stage)
-    //   compute  its 32 x 32 block of the stage
-    //   release  done[slot] += 1; the wave that brings the count to 4 uses
-    //            (the last to leave the slot) loads stage + NB into it, all
-    //            of it, alone
-    //   publish  a wave marks a stage it loaded ready one stage later, after
-    //            waiting for its own loads (s_waitcnt vmcnt), so the wave that
-    //            loads (often the slowest) never waits for load latency
-    // A wave can so run up to NB - 2 stages ahead of the slowest instead of
-    // meeting it at every stage.  A wave waits only for a stage loaded by a
-    // wave that has left an earlier stage, and every wave publishes before it
-    // waits, so each wait ends; each spin is also capped.  The stage loads
-    // are inline asm (stage_load_asm), so the compiler adds no waits for them
-    // before the reads of other slots.
-    constexpr int SK = 32;                     // keys per stage
-    constexpr int NB = D == 128 ? 4 : 8;       // slots: 64 KB at D = 128 and 64
-    constexpr int SEL = SK * D;                // elements per slot and matrix
-    constexpr int J = SK * C::CPR / 64;        // 16-byte loads per lane and matrix
-    constexpr int ROWS4 = 256 / C::CPR;        // rows filled by 4 loads
-    constexpr int kSpinCap = 1 << 22;
-    __shared__ __attribute__((aligned(1024))) uint16_t k_ring[NB * SEL];
-    __shared__ __attribute__((aligned(1024))) uint16_t v_ring[NB * SEL];
-    __shared__ int ready[NB], done[NB];
-    // the flags stay in the LDS address space (a generic pointer would make
-    // flat accesses, which also wait on the vector-memory counter)
-    typedef __attribute__((address_space(3))) volatile int lds_vint;
-    lds_vint* vready = (lds_vint*)ready;
-    const int s0 = row_ptr[lrow], n = row_ptr[lrow + 1] - s0;
-
-    // a stage loaded by one wave: load j fills chunk j * 64 + lane, row
-    // (j * 64 + lane) / CPR; the chunk swizzles repeat every 4 loads
-    int rkoff[4], rvoff[4];
+  // load j of this lane fills chunk slot (LOADS wave + j) * 64 + lane of a
+  // stage buffer: row slot / CPR, physical chunk slot % CPR
+  int koff[C::LOADS], voff[C::LOADS];
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int slot = jj * 64 + lane;
-      const int row = slot / C::CPR, pc = slot % C::CPR;
-      rkoff[jj] = (row * (int)A.kss + 8 * (pc ^ swz_k<D>(row))) * 2;
-      rvoff[jj] = (row * (int)A.vss + 8 * (pc ^ swz_v<D>(row))) * 2;
+  for (int j = 0; j < C::LOADS; ++j) {
+    const int slot = (C::LOADS * wave + j) * 64 + lane;
+    const int row = slot / C::CPR, pc = slot % C::CPR;
+    koff[j] = (row * (int)A.kss + 8 * (pc ^ swz_k<D>(row))) * 2;
+    voff[j] = (row * (int)A.vss + 8 * (pc ^ swz_v<D>(row))) * 2;
+  }
+  auto stage_key0 = [&](int st) { return (col_idx[st >> sh] << (6 + sh)) + ((st & sh) << 6); };
+  // the 64 keys from key0 -> buffers (kd, vd)
+  auto issue = [&](int key0, uint16_t* kd, uint16_t* vd) {
+    const int ks = key0 * (int)A.kss * 2, vs = key0 * (int)A.vss * 2;
+#pragma unroll
+    for (int j = 0; j < C::LOADS; ++j) {
+      // each load writes 64 lanes x 16 bytes = 512 elements
+      load_lds16(krs, kd + (C::LOADS * wave + j) * 512, koff[j], ks);
+      load_lds16(vrs, vd + (C::LOADS * wave + j) * 512, voff[j], vs);
     }
-    const u32x4 krw = rsrc_words(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh,
-                                 (int)((int64_t)A.kv_len * A.kss * 2));
-    const u32x4 vrw = rsrc_words(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh,
-                                 (int)((int64_t)A.kv_len * A.vss * 2));
-    const uint32_t k_lds = (uint32_t)(uintptr_t)(lds_void*)k_ring;
-    const uint32_t v_lds = (uint32_t)(uintptr_t)(lds_void*)v_ring;
-    auto load_stage = [&](int k) {
-      const int key0 = col_idx[s0 + k] * SK;
-      const uint32_t off = (uint32_t)((k % NB) * SEL * 2);
-      stage_load_asm<J>(krw, k_lds + off, rkoff, key0 * (int)A.kss * 2,
-                        (key0 + ROWS4) * (int)A.kss * 2);
-      stage_load_asm<J>(vrw, v_lds + off, rvoff, key0 * (int)A.vss * 2,
-                        (key0 + ROWS4) * (int)A.vss * 2);
-    };
+  };
 
-    // prologue: the first NB stages, loaded by the four waves together
-    const int pre = min(NB, n);
-    for (int k = wave; k < pre; k += 4) load_stage(k);
-    if (tid < NB) {
-      ready[tid] = tid < pre ? tid : -1;
-      done[tid] = 0;
-    }
+  // ---- two stage buffers, one stage ahead: each barrier retires every
+  // wave's reads of the other buffer before the next stage is loaded into it.
+  // Stages go in pairs (buffer 0, buffer 1); this row's valid keys of both
+  // are walked first.  The next two stage keys are read together at the top
+  // of a pair (clamped indices: unconditional scalar loads, one wait).
+  int ka = s0 < s1 ? stage_key0(s0) : 0;
+  if (s0 < s1) issue(ka, k_st0, v_st0);
+  for (int st = s0; st < s1; st += 2) {
+    const bool has_b = st + 1 < s1, has_c = st + 2 < s1;
+    const int kb = stage_key0(min(st + 1, s1 - 1));
+    const int kc = stage_key0(min(st + 2, s1 - 1));
+    uint32_t mb[4];
+    walk.stage_pair(ka, kb, has_b, mb);
+
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
+    if (has_b) issue(kb, k_st1, v_st1);
+    block(k_st0, v_st0, 0, mb[0]);
+    block(k_st0, v_st0, 1, mb[1]);
+    if (!has_b) break;
 
-    int older = -1, newer = -1;  // stages this wave loaded at its last two stage ends
-    for (int k = 0; k < n; ++k) {
-      // publish the older load: at most the newer one's 2 J loads remain in flight
-      if (older >= 0) {
-        if (newer >= 0)
-          __builtin_amdgcn_s_waitcnt(kWaitVmcntRing<2 * J>());
-        else
-          __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-        asm volatile("" ::: "memory");
-        if (lane == 0) vready[older % NB] = older;
-      }
-      older = newer;
-      newer = -1;
-
-      uint32_t mb[1];
-      walk.span<1>(col_idx[s0 + k] * SK, mb);
-      for (int guard = 0;
-           __builtin_amdgcn_readfirstlane(vready[k % NB]) != k && guard < kSpinCap; ++guard)
-        __builtin_amdgcn_s_sleep(1);
-      asm volatile("" ::: "memory");
-      block(k_ring + (k % NB) * SEL, v_ring + (k % NB) * SEL, 0, mb[0]);
-
-      // release: this wave's reads of the slot have completed
-      __builtin_amdgcn_s_waitcnt(kWaitLgkmcnt0);
-      asm volatile("" ::: "memory");
-      int prev = 0;
-      if (lane == 0) prev = atomicAdd(&done[k % NB], 1);
-      prev = __builtin_amdgcn_readlane(prev, 0);
-      if (prev == 4 * (k / NB) + 3 && k + NB < n) {
-        load_stage(k + NB);
-        newer = k + NB;
-      }
-    }
-    if (older >= 0 || newer >= 0) {
-      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-      asm volatile("" ::: "memory");
-      if (lane == 0) {
-        if (older >= 0) vready[older % NB] = older;
-        if (newer >= 0) vready[newer % NB] = newer;
-      }
-    }
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    if (has_c) issue(kc, k_st0, v_st0);
+    block(k_st1, v_st1, 0, mb[2]);
+    block(k_st1, v_st1, 1, mb[3]);
+    ka = kc;
   }
 
   // ---- epilogue: normalise and store O rows and the log-sum-exp
@@ -430,17 +317,10 @@ hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
                            hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
   dim3 grid((unsigned)num_items);
-  if (a.ring) {
-    if (head_dim == 128)
-      tile_fwd_kernel<128, true><<<grid, 256, 0, stream>>>(a);
-    else
-      tile_fwd_kernel<64, true><<<grid, 256, 0, stream>>>(a);
-  } else {
-    if (head_dim == 128)
-      tile_fwd_kernel<128, false><<<grid, 256, 0, stream>>>(a);
-    else
-      tile_fwd_kernel<64, false><<<grid, 256, 0, stream>>>(a);
-  }
+  if (head_dim == 128)
+    tile_fwd_kernel<128><<<grid, 256, 0, stream>>>(a);
+  else
+    tile_fwd_kernel<64><<<grid, 256, 0, stream>>>(a);
   return hipGetLastError();
 }
 

@@ -28,7 +28,6 @@ struct TileArgs {
   int nq;      // query blocks a q_len-row forward visits (<= nqb)
   int num_bh;  // batch * H
   int stage_shift;  // layout key blocks are 64 << stage_shift keys (64 or 128)
-  int ring;         // 1: layout key blocks of 32 keys, staged through the slot ring
   float scale_log2;  // sm_scale * log2(e)
   PatternConsts pc;
   const int32_t* row_ptr;

@@ -25,15 +25,8 @@ constexpr int kContigLimit = 1 << 21;
 // Lazy rescale threshold (log2 units): the running max moves only when a
 // block raises a row's max by more than this, so probabilities stay <= 2^8.
 constexpr float kRescaleSlack = 8.0f;
-// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt
-// 6:4, lgkmcnt 11:8; a field at its maximum leaves that counter alone)
-constexpr int kWaitVmcnt0 = 0x0F70;    // vmcnt(0)
-constexpr int kWaitLgkmcnt0 = 0xC07F;  // lgkmcnt(0)
-template <int N>
-constexpr int kWaitVmcntRing() {       // vmcnt(N), N < 64
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  return (N & 15) | ((N >> 4) << 14) | 0x0F70;
-}
+// s_waitcnt with vmcnt(0) and the other counters left alone (gfx9 encoding)
+constexpr int kWaitVmcnt0 = 0x0F70;
 
 __device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -81,85 +74,6 @@ __device__ __forceinline__ void mask_init(f32x16& s, uint32_t nmk) {
     asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(v) : "v"(nmk), "i"(8 * (R / 4) + R % 4));
     s[R] = __uint_as_float(v & 0xff800000u);
     mask_init<R + 1>(s, nmk);
-  }
-}
-
-// Buffer resource words (base, stride 0, num_records, the raw-buffer flags
-// the kernels pass to __builtin_amdgcn_make_buffer_rsrc) for inline asm.
-__device__ __forceinline__ u32x4 rsrc_words(const void* base, int num_records) {
-  const uint64_t a = (uint64_t)(uintptr_t)base;
-  u32x4 r;
-  r[0] = (uint32_t)a;
-  r[1] = (uint32_t)(a >> 32) & 0xffffu;
-  r[2] = (uint32_t)num_records;
-  r[3] = 0x00020000u;
-  return r;
-}
-
-// One wave copies a 32-row stage of one matrix HBM -> LDS: J (4 or 8)
-// buffer_load_dwordx4 ... lds per lane, load j reading voffset vo[j & 3] +
-// soffset (so0 for j < 4, so1 for j >= 4) into LDS bytes lds + 1024 j +
-// 16 lane.  Written as inline asm so that the compiler does not track these
-// LDS writes: it would otherwise wait for them (s_waitcnt vmcnt) before
-// every later access of the same LDS object; the caller orders them with
-// explicit s_waitcnt.  M0 is saved and restored; each write of M0 is
-// followed by one wait state before the load that reads it.
-template <int J>
-__device__ __forceinline__ void stage_load_asm(u32x4 rsrc, uint32_t lds, const int (&vo)[4], int so0,
-                                               int so1) {
-  uint32_t sav;
-  if constexpr (J == 8) {
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %6, %7 offen lds\n\t"
-        "s_add_u32 m0, m0, 0x400\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %3, %6, %7 offen lds\n\t"
-        "s_add_u32 m0, m0, 0x400\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %4, %6, %7 offen lds\n\t"
-        "s_add_u32 m0, m0, 0x400\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %5, %6, %7 offen lds\n\t"
-        "s_add_u32 m0, m0, 0x400\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %6, %8 offen lds\n\t"
-        "s_add_u32 m0, m0, 0x400\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %3, %6, %8 offen lds\n\t"
-        "s_add_u32 m0, m0, 0x400\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %4, %6, %8 offen lds\n\t"
-        "s_add_u32 m0, m0, 0x400\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %5, %6, %8 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(sav)
-        : "s"(lds), "v"(vo[0]), "v"(vo[1]), "v"(vo[2]), "v"(vo[3]), "s"(rsrc), "s"(so0), "s"(so1)
-        : "memory", "scc");
-  } else {
-    static_assert(J == 4, "4 or 8 loads per stage");
-    (void)so1;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %1\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %2, %6, %7 offen lds\n\t"
-        "s_add_u32 m0, m0, 0x400\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %3, %6, %7 offen lds\n\t"
-        "s_add_u32 m0, m0, 0x400\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %4, %6, %7 offen lds\n\t"
-        "s_add_u32 m0, m0, 0x400\n\t"
-        "s_nop 0\n\t"
-        "buffer_load_dwordx4 %5, %6, %7 offen lds\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(sav)
-        : "s"(lds), "v"(vo[0]), "v"(vo[1]), "v"(vo[2]), "v"(vo[3]), "s"(rsrc), "s"(so0)
-        : "memory", "scc");
   }
 }
 

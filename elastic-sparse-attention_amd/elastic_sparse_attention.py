@@ -169,23 +169,24 @@ class ElasticLayout:
         self._col_idx_host: Optional[torch.Tensor] = None
         self._bwd_plans: Dict[Tuple[int, int, int], Tuple[torch.Tensor, ...]] = {}
         self._masks: Dict[int, torch.Tensor] = {}
-        self._stages: Dict[int, "ElasticLayout"] = {}
+        self._stages: Dict[Tuple[int, int], "ElasticLayout"] = {}
 
-    def stages(self, block_n: int = 64) -> "ElasticLayout":
-        """The same pattern's layout at ``block_n``-key blocks (64 or 32), the
-        forward's staging unit: a part of a 128-key tile that no row of the
-        query block needs is not listed, so the forward never loads it.
-        Built once per width, cached; the 128 x 128 layout itself stays the
-        declared tile (counted flops, the backward)."""
-        if self.pattern.block_n == block_n:
+    def stages(self, block_n: int = 64, block_m: Optional[int] = None) -> "ElasticLayout":
+        """The same pattern's layout at ``block_m`` x ``block_n`` blocks
+        (128 x 64 for the forward's staging unit: a half of a 128-key tile
+        that no row of the query block needs is not listed, so the forward
+        never loads it).  Built once per shape, cached; the 128 x 128 layout
+        itself stays the declared tile (counted flops, the backward)."""
+        block_m = self.pattern.block_m if block_m is None else block_m
+        if self.pattern.block_n == block_n and self.pattern.block_m == block_m:
             return self
-        got = self._stages.get(block_n)
+        got = self._stages.get((block_m, block_n))
         if got is None:
             p = self.pattern
             got = ElasticLayout(
                 make_pattern(p.seq_len, p.attention_length, p.layer_idx, p.num_hidden_layers,
-                             p.num_heads, p.block_m, block_n), self.device)
-            self._stages[block_n] = got
+                             p.num_heads, block_m, block_n), self.device)
+            self._stages[(block_m, block_n)] = got
         return got
 
     def tiles_for(self, q_len: int) -> int:
@@ -315,20 +316,18 @@ def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
     Returns ``o`` as ``[B, Lq, H, D]`` (so ``o.view(B, Lq, H * D)`` is the
     module output, :761-763) and, if asked, ``lse`` float32 ``[B, H, Lq]``.
-    ``key_block`` selects the staging unit: 32 streams the layout's 32-key
-    blocks through a ring of LDS slots that each wave consumes at its own
-    pace; 64 stages 64-key blocks (skipping tile halves no row needs) with a
-    workgroup barrier per stage; 128 stages whole 128-key tiles of
-    ``layout``.  All give the same output bit for bit.
+    ``key_block`` 64 stages K/V from the layout's 64-key blocks (skipping
+    tile halves no row needs); 128 stages whole 128-key tiles of ``layout``.
+    Both give the same output bit for bit.
     """
     _check_qkv(q, k, v)
     B, H, Lq, D = q.shape
     q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
     o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
-    if key_block not in (32, 64, 128):
-        raise ValueError(f"key_block must be 32, 64 or 128, got {key_block}")
-    st = layout if key_block == 128 else layout.stages(key_block)
+    if key_block not in (64, 128):
+        raise ValueError(f"key_block must be 64 or 128, got {key_block}")
+    st = layout if key_block == 128 else layout.stages(64)
     items, n = st.schedule(Lq, B)
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
     check(load().esa_elastic_fwd(ctypes.byref(a), ctypes.byref(st.pattern),

@@ -131,12 +131,11 @@ esa_status esa_plan_schedule(const esa_pattern* p, const int32_t* row_ptr_host,
  * .forward (elastic_sparse_attention.py:592-622, 241-297) for prefill.
  * Visits only the active key blocks of the layout, runs QK^T and PV on bf16
  * MFMA with float32 accumulation and online softmax.  The layout may be
- * built at block_n = 128, 64 or 32 (block_m = 128): at 64 a 128-key tile's
- * half that no row of the query block needs is never staged (the fastest
- * choice here); at 32 the key blocks stream through a ring of LDS slots that
- * each wave consumes at its own pace.  All give the same output bit for bit.
- * Requires dtype ESA_BF16, head_dim 64 or 128, block_m = 128 and block_n in
- * {32, 64, 128}, a finite sm_scale > 0
+ * built at block_n = 128 or 64 (block_m = 128): at 64 a 128-key tile's half
+ * that no row of the query block needs is never staged, so the forward runs
+ * faster on the same output (bit for bit).  Requires dtype ESA_BF16,
+ * head_dim 64 or 128, block_m = 128 and block_n in {64, 128}, a finite
+ * sm_scale > 0
  * (ESA_ERR_UNSUPPORTED otherwise; esa_elastic_fwd_rows takes any), K and V
  * row strides >= head_dim with kv_len * row stride * 2 < 2^31 (one head's
  * rows within a 2 GiB window), q_len <= kv_len,
