@@ -115,13 +115,23 @@ __global__ __launch_bounds__(256) void tile_mask_kernel(PatternConsts pc, const 
 }
 
 // ---------------------------------------------------------------------------
-// At D = 128 one workgroup per CU: the K and V operands (64 VGPRs) and the
-// dK^T, dV^T accumulators (128) stay resident, which leaves no room for the
-// per-block operands at two workgroups per CU (the compiler spills there).
-// D = 64 needs half of that and keeps two.
+// dK, dV of one (batch, kv head, 128-key block): 8 waves, one workgroup per
+// CU.  The block's K and V rows are staged into LDS once (64 KB at D = 128)
+// and read as MFMA operands from there, so each wave keeps only its dK^T and
+// dV^T accumulators resident and two waves share each SIMD.  Wave w owns
+// keys 32 (w % 4) .. + 31 of the block and the 32-row half w / 4 of every
+// 64-row Q / dO stage; the two halves' partial sums are added through LDS at
+// the end, in a fixed order.
 template <int D>
-__global__ __launch_bounds__(256, D == 128 ? 1 : 2) void dkdv_kernel(BwdArgs A, const float* lse2) {
+__global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs A, const float* lse2) {
   using C = BwdCfg<D>;
+  constexpr int KB = 128;                           // keys per item
+  constexpr int KLOADS = KB * C::CPR / 512;         // 16-byte loads per lane per matrix (block)
+  constexpr int QLOADS = C::HALF * C::CPR / 512;    // 16-byte loads per lane per matrix (stage)
+  static_assert(KLOADS >= 1 && QLOADS >= 1, "at least one load per lane");
+  // K rows at kv_blk[0, KB D), V rows at kv_blk[KB D, 2 KB D); the same
+  // space holds the partial-sum exchange at the end
+  __shared__ __attribute__((aligned(1024))) uint16_t kv_blk[2 * KB * D];
   __shared__ __attribute__((aligned(1024))) uint16_t q_st0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint16_t o_st0[C::STAGE];  // dO rows
   __shared__ __attribute__((aligned(1024))) uint16_t q_st1[C::STAGE];
@@ -141,26 +151,29 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void dkdv_kernel(BwdArgs A, 
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kw = wave & 3, qh = wave >> 2;  // key sub-block, query half
   const int hf = lane >> 5, l32 = lane & 31, g4 = lane >> 4, lam = lane & 15;
-  const int key = kb * 128 + wave * 32 + l32;
+  const int key = kb * KB + kw * 32 + l32;
   const bool key_ok = key < A.kv_len;
 
-  // this wave's 32 keys: K and V rows as B operands (8 consecutive d per lane)
-  bf16x8 kop[C::NS], vop[C::NS];
-  {
-    const uint16_t* kr = A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh + (int64_t)key * A.kss;
-    const uint16_t* vr = A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh + (int64_t)key * A.vss;
+  // ---- the key block's K and V rows -> LDS (rows past kv_len read as zeros)
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh), (short)0,
+      (int)((int64_t)A.kv_len * A.kss * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh), (short)0,
+      (int)((int64_t)A.kv_len * A.vss * 2), 0x00020000);
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) {
-      u32x4 kraw = {0u, 0u, 0u, 0u}, vraw = {0u, 0u, 0u, 0u};
-      if (key_ok) {
-        kraw = *(const u32x4*)(kr + 16 * s + 8 * hf);
-        vraw = *(const u32x4*)(vr + 16 * s + 8 * hf);
-      }
-      kop[s] = __builtin_bit_cast(bf16x8, kraw);
-      vop[s] = __builtin_bit_cast(bf16x8, vraw);
-    }
+  for (int j = 0; j < KLOADS; ++j) {
+    const int slot = (KLOADS * wave + j) * 64 + lane;
+    const int row = slot / C::CPR, pc = slot % C::CPR;
+    const int chunk = 8 * (pc ^ swz_k<D>(row));
+    load_lds16(krs, kv_blk + (KLOADS * wave + j) * 512, (row * (int)A.kss + chunk) * 2,
+               kb * KB * (int)A.kss * 2);
+    load_lds16(vrs, kv_blk + KB * D + (KLOADS * wave + j) * 512, (row * (int)A.vss + chunk) * 2,
+               kb * KB * (int)A.vss * 2);
   }
+
   f32x16 dkacc[C::ND], dvacc[C::ND];
 #pragma unroll
   for (int d = 0; d < C::ND; ++d) {
@@ -169,10 +182,10 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void dkdv_kernel(BwdArgs A, 
   }
 
   // staging: Q and dO rows of one 64-row half of a (head, query block) tile
-  int qoff[C::LOADS], ooff[C::LOADS];
+  int qoff[QLOADS], ooff[QLOADS];
 #pragma unroll
-  for (int j = 0; j < C::LOADS; ++j) {
-    const int slot = (C::LOADS * wave + j) * 64 + lane;
+  for (int j = 0; j < QLOADS; ++j) {
+    const int slot = (QLOADS * wave + j) * 64 + lane;
     const int row = slot / C::CPR, pc = slot % C::CPR;
     qoff[j] = (row * (int)A.qss + 8 * (pc ^ swz_k<D>(row))) * 2;
     ooff[j] = (row * (int)A.doss + 8 * (pc ^ swz_k<D>(row))) * 2;
@@ -191,9 +204,9 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void dkdv_kernel(BwdArgs A, 
         (int)((int64_t)A.q_len * A.doss * 2), 0x00020000);
     const int qs_ = r0 * (int)A.qss * 2, os_ = r0 * (int)A.doss * 2;
 #pragma unroll
-    for (int j = 0; j < C::LOADS; ++j) {
-      load_lds16(qrs, qd + (C::LOADS * wave + j) * 512, qoff[j], qs_);
-      load_lds16(ors, od + (C::LOADS * wave + j) * 512, ooff[j], os_);
+    for (int j = 0; j < QLOADS; ++j) {
+      load_lds16(qrs, qd + (QLOADS * wave + j) * 512, qoff[j], qs_);
+      load_lds16(ors, od + (QLOADS * wave + j) * 512, ooff[j], os_);
     }
     if (wave < 2) {
       const float* src = (wave == 0 ? lse2 : A.delta) + ((int64_t)b * A.H + h) * A.q_len;
@@ -203,43 +216,60 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void dkdv_kernel(BwdArgs A, 
     }
   };
 
-  // LDS read addresses (elements): 16-byte row reads (rows 32 s2 + l32,
-  // chunk 2 s + hf) and transposed reads (rows 4 hf + lam / 4 + 16 u (+ 8),
-  // column 32 d + 16 (g4 & 1) + 4 (lam & 3)), both under the K swizzle
-  int raddr[C::NS], taddr0[C::ND], taddr8[C::ND];
-#pragma unroll
-  for (int s = 0; s < C::NS; ++s) raddr[s] = l32 * D + 8 * ((2 * s + hf) ^ swz_k<D>(l32));
+  // LDS read addresses (elements): 16-byte row reads (rows 32 s2 + l32 of a
+  // stage, rows 32 kw + l32 of the key block; chunk 2 s + hf) and transposed
+  // reads (rows 4 hf + lam / 4 + 16 u (+ 8), column 32 d + 16 (g4 & 1) +
+  // 4 (lam & 3)), all under the K swizzle
+  //   chunk (2 s + hf) ^ x = 2 (s ^ (x >> 1)) + (hf ^ (x & 1)), and the row
+  //   base leaves bits 4.. of the element offset free below the row, so
+  //   raddr(s) = rb ^ 16 s and, likewise, taddr(d) = tb ^ 32 d (one register
+  //   each instead of one per s or d)
+  const int rx = swz_k<D>(l32);
+  const int rb = (l32 * D + 8 * (hf ^ (rx & 1))) | (16 * (rx >> 1));
+  int tb0, tb8;
   {
     const int tr = 4 * hf + (lam >> 2);
-#pragma unroll
-    for (int d = 0; d < C::ND; ++d) {
-      const int col = 32 * d + 16 * (g4 & 1) + 4 * (lam & 3);
-      taddr0[d] = tr * D + 8 * ((col >> 3) ^ swz_k<D>(tr)) + (col & 7);
-      taddr8[d] = (tr + 8) * D + 8 * ((col >> 3) ^ swz_k<D>(tr + 8)) + (col & 7);
-    }
+    const int low = 2 * (g4 & 1) + ((lam >> 1) & 1);  // (col >> 3) & 3
+    const int x0 = swz_k<D>(tr), x8 = swz_k<D>(tr + 8);
+    tb0 = (tr * D + 8 * (low ^ (x0 & 3)) + 4 * (lam & 1)) | (32 * (x0 >> 2));
+    tb8 = ((tr + 8) * D + 8 * (low ^ (x8 & 3)) + 4 * (lam & 1)) | (32 * (x8 >> 2));
   }
+
+  const uint16_t* kblk = kv_blk + kw * 32 * D;       // this wave's K rows
+  const uint16_t* vblk = kv_blk + (KB + kw * 32) * D;  // and V rows
   const float scale2 = A.scale_log2;
 
-  // one 32-row query sub-block s2 (0, 1) of a stage held in (qb_, ob_, lb_, db_)
+  // this wave's 32-row query half of a stage held in (qb_, ob_, lb_, db_)
   auto sub = [&](const uint16_t* qb_, const uint16_t* ob_, const float* lb_, const float* db_,
-                 int s2, uint32_t mw) {
-    // rows 8 (r / 4) + 4 hf + r % 4 of the sub-block, key l32 of the wave
+                 uint32_t mw) {
+    // rows 8 (r / 4) + 4 hf + r % 4 of the half, key l32 of the wave
     if (!wave_any(mw != 0u)) return;
-    bf16x8 ra[C::NS];
+    // the address bases pass through an empty asm, so the compiler forms
+    // each XORed address where it is used instead of keeping one register
+    // per address live across the loop
+    int rbl = rb, t0l = tb0, t8l = tb8;
+    asm volatile("" : "+v"(rbl), "+v"(t0l), "+v"(t8l));
+    auto raddr = [&](int s) { return rbl ^ (16 * s); };
+    auto taddr0 = [&](int d) { return t0l ^ (32 * d); };
+    auto taddr8 = [&](int d) { return t8l ^ (32 * d); };
+    const int qrow = 32 * qh * D;
+    f32x16 sacc = f32x16{}, dp = f32x16{};
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) ra[s] = *(const bf16x8*)(qb_ + raddr[s] + 32 * s2 * D);
-    f32x16 sacc = f32x16{};
+    for (int s = 0; s < C::NS; ++s) {
+      const bf16x8 qa = *(const bf16x8*)(qb_ + raddr(s) + qrow);
+      const bf16x8 kbv = *(const bf16x8*)(kblk + raddr(s));
+      sacc = mfma32(qa, kbv, sacc);
+    }
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) sacc = mfma32(ra[s], kop[s], sacc);
-#pragma unroll
-    for (int s = 0; s < C::NS; ++s) ra[s] = *(const bf16x8*)(ob_ + raddr[s] + 32 * s2 * D);
-    f32x16 dp = f32x16{};
-#pragma unroll
-    for (int s = 0; s < C::NS; ++s) dp = mfma32(ra[s], vop[s], dp);
+    for (int s = 0; s < C::NS; ++s) {
+      const bf16x8 oa = *(const bf16x8*)(ob_ + raddr(s) + qrow);
+      const bf16x8 vbv = *(const bf16x8*)(vblk + raddr(s));
+      dp = mfma32(oa, vbv, dp);
+    }
     uint32_t pw[8], sw[8];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int rbase = 32 * s2 + 8 * g + 4 * hf;
+      const int rbase = 32 * qh + 8 * g + 4 * hf;
       const f32x4 lv = *(const f32x4*)(lb_ + rbase);
       const f32x4 dv = *(const f32x4*)(db_ + rbase);
       float p[4], ds[4];
@@ -259,11 +289,11 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void dkdv_kernel(BwdArgs A, 
     for (int d = 0; d < C::ND; ++d) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int ro = (32 * s2 + 16 * u) * D;
-        const s16x4 o1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(ob_ + taddr0[d] + ro));
-        const s16x4 o2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(ob_ + taddr8[d] + ro));
-        const s16x4 q1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(qb_ + taddr0[d] + ro));
-        const s16x4 q2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(qb_ + taddr8[d] + ro));
+        const int ro = (32 * qh + 16 * u) * D;
+        const s16x4 o1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(ob_ + taddr0(d) + ro));
+        const s16x4 o2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(ob_ + taddr8(d) + ro));
+        const s16x4 q1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(qb_ + taddr0(d) + ro));
+        const s16x4 q2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(qb_ + taddr8(d) + ro));
         const s16x4 oo[2] = {o1, o2}, qq[2] = {q1, q2};
         const u32x4 pq = {pw[4 * u], pw[4 * u + 1], pw[4 * u + 2], pw[4 * u + 3]};
         const u32x4 sq = {sw[4 * u], sw[4 * u + 1], sw[4 * u + 2], sw[4 * u + 3]};
@@ -277,25 +307,53 @@ __global__ __launch_bounds__(256, D == 128 ? 1 : 2) void dkdv_kernel(BwdArgs A, 
   if (e0 < e1) issue(e0, 0, q_st0, o_st0, l_st0, d_st0);
   for (int e = e0; e < e1; ++e) {
     const int64_t t = kv_tiles[e];
-    const uint32_t* tm = mt + t * 512 + wave * 32 + l32;
-    const uint32_t m0 = tm[0], m1 = tm[128], m2 = tm[256], m3 = tm[384];
+    // this wave's query sub-blocks of the tile: qh (stage 0) and 2 + qh (stage 1)
+    const uint32_t* tm = mt + t * 512 + kw * 32 + l32;
+    const uint32_t ma = tm[qh * 128], mb = tm[(2 + qh) * 128];
 
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
     issue(e, 1, q_st1, o_st1, l_st1, d_st1);
-    sub(q_st0, o_st0, l_st0, d_st0, 0, m0);
-    sub(q_st0, o_st0, l_st0, d_st0, 1, m1);
+    sub(q_st0, o_st0, l_st0, d_st0, ma);
 
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
     if (e + 1 < e1) issue(e + 1, 0, q_st0, o_st0, l_st0, d_st0);
-    sub(q_st1, o_st1, l_st1, d_st1, 0, m2);
-    sub(q_st1, o_st1, l_st1, d_st1, 1, m3);
+    sub(q_st1, o_st1, l_st1, d_st1, mb);
   }
+
+  // ---- the second query half's partial sums -> the first half's waves,
+  // through the K/V block space (4 key sub-blocks x 16 regs x 64 lanes)
+  f32x4* red = (f32x4*)kv_blk;
+  auto exchange = [&](f32x16 (&acc)[C::ND]) {
+    __syncthreads();
+    if (qh == 1) {
+#pragma unroll
+      for (int d = 0; d < C::ND; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 v4 = {acc[d][4 * g], acc[d][4 * g + 1], acc[d][4 * g + 2], acc[d][4 * g + 3]};
+          red[((kw * C::ND + d) * 4 + g) * 64 + lane] = v4;
+        }
+    }
+    __syncthreads();
+    if (qh == 0) {
+#pragma unroll
+      for (int d = 0; d < C::ND; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 v4 = red[((kw * C::ND + d) * 4 + g) * 64 + lane];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[d][4 * g + e] += v4[e];
+        }
+    }
+  };
+  exchange(dvacc);
+  exchange(dkacc);
 
   // dK = scale * (dK^T)^T, dV = (dV^T)^T: lane holds key l32, d = 32 d' +
   // 8 (r / 4) + 4 hf + r % 4
-  if (key_ok) {
+  if (qh == 0 && key_ok) {
     uint16_t* dkr = A.dk + (int64_t)b * A.dksb + (int64_t)kvh * A.dksh + (int64_t)key * A.dkss;
     uint16_t* dvr = A.dv + (int64_t)b * A.dvsb + (int64_t)kvh * A.dvsh + (int64_t)key * A.dvss;
 #pragma unroll
@@ -507,9 +565,9 @@ hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,
   if (e != hipSuccess) return e;
   if (num_kv_items > 0) {
     if (head_dim == 128)
-      dkdv_kernel<128><<<dim3((unsigned)num_kv_items), 256, 0, stream>>>(a, lse2);
+      dkdv_kernel<128><<<dim3((unsigned)num_kv_items), 512, 0, stream>>>(a, lse2);
     else
-      dkdv_kernel<64><<<dim3((unsigned)num_kv_items), 256, 0, stream>>>(a, lse2);
+      dkdv_kernel<64><<<dim3((unsigned)num_kv_items), 512, 0, stream>>>(a, lse2);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
