@@ -84,7 +84,9 @@ __global__ __launch_bounds__(256) void prep_kernel(BwdArgs A, float* lse2) {
   if (row < A.q_len && g == 0) {
     const int64_t at = ((int64_t)b * A.H + h) * A.q_len + row;
     A.delta[at] = acc;
-    lse2[at] = A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + row] * 1.4426950408889634f;
+    // kept finite: masked scores enter as -inf, and -inf - (-inf) would be NaN
+    lse2[at] = fmaxf(A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + row] * 1.4426950408889634f,
+                     -3.0e38f);
   }
 }
 
@@ -253,7 +255,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs A, const float* ls
     auto taddr0 = [&](int d) { return t0l ^ (32 * d); };
     auto taddr8 = [&](int d) { return t8l ^ (32 * d); };
     const int qrow = 32 * qh * D;
-    f32x16 sacc = f32x16{}, dp = f32x16{};
+    // the mask enters as S's initial value (0 or -inf), so p = exp2(...) is 0
+    // for a masked entry without a select
+    f32x16 sacc, dp = f32x16{};
+    mask_init<0>(sacc, ~(mw >> (4 * hf)));
 #pragma unroll
     for (int s = 0; s < C::NS; ++s) {
       const bf16x8 qa = *(const bf16x8*)(qb_ + raddr(s) + qrow);
@@ -275,8 +280,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs A, const float* ls
       float p[4], ds[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const bool on = (mw >> (8 * g + 4 * hf + e)) & 1u;
-        p[e] = on ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[4 * g + e], scale2, -lv[e])) : 0.f;
+        p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[4 * g + e], scale2, -lv[e]));
         ds[e] = p[e] * (dp[4 * g + e] - dv[e]);
       }
       pw[2 * g] = pack_bf16x2(p[0], p[1]);
@@ -474,7 +478,9 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2
     bf16x8 ra[C::NS];
 #pragma unroll
     for (int s = 0; s < C::NS; ++s) ra[s] = *(const bf16x8*)(Kb + raddr[s] + 32 * kbl * D);
-    f32x16 sacc = f32x16{};
+    // the mask enters as S's initial value (0 or -inf): p = 0 without a select
+    f32x16 sacc;
+    mask_init<0>(sacc, ~mk);
 #pragma unroll
     for (int s = 0; s < C::NS; ++s) sacc = mfma32(ra[s], qop[s], sacc);
 #pragma unroll
@@ -489,8 +495,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int r = 2 * q + e;
-        const bool on = (mk >> (8 * (r / 4) + r % 4)) & 1u;
-        const float p = on ? __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], scale2, -l2)) : 0.f;
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], scale2, -l2));
         ds[e] = p * (dp[r] - dl);
       }
       sw[q] = pack_bf16x2(ds[0], ds[1]);
