@@ -101,3 +101,39 @@ def test_backward_full_size_8k_layer4():
         e = (rel_err(dq[:, h:h + 1], rq), rel_err(dk[:, h:h + 1], rk), rel_err(dv[:, h:h + 1], rv))
         print(f"  head {h} rel err dq {e[0]:.3e} dk {e[1]:.3e} dv {e[2]:.3e}", flush=True)
         assert max(e) <= REL
+
+
+@pytest.mark.parametrize("B,H,Hkv,L,D,layer", [
+    (1, 32, 32, 32768, 128, 4),   # the headline shape
+    (1, 32, 32, 32768, 128, 7),
+    (2, 8, 2, 8192, 64, 5),       # GQA, D = 64
+])
+def test_backward_identities_full_size(B, H, Hkv, L, D, layer):
+    """Size-independent checks at full size.  Every row of P sums to one, so
+    the sum of dV over a kv head's keys equals the sum of dO over the rows of
+    its query heads; every row of dS = P (dP - delta) sums to zero, so the sum
+    of dK over a kv head's keys is zero.  Both are compared against the sum
+    of absolute values; without the identities the ratio would be about
+    1 / sqrt(L) (random signs), here only rounding is left (P and dS enter
+    the MFMAs in bf16, dK and dV are stored in bf16)."""
+    print(f"bwd identities B={B} H={H} Hkv={Hkv} L={L} D={D} layer={layer}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=90 + layer, scale=D ** -0.25)
+    sc = scaling_for(D)
+    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc)
+    g = torch.Generator().manual_seed(layer)
+    do = torch.randn(B, L, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    dq, dk, dv = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc)
+    assert all(bool(torch.isfinite(t.float()).all()) for t in (dq, dk, dv))
+    groups = H // Hkv
+    sum_do = do.float().sum(dim=1).view(B, Hkv, groups, D).sum(dim=2)      # [B, Hkv, D]
+    sum_dv = dv.float().sum(dim=2)
+    abs_dv = dv.float().abs().sum(dim=2)
+    r_v = ((sum_dv - sum_do).abs() / abs_dv).max().item()
+    r_k = (dk.float().sum(dim=2).abs() / dk.float().abs().sum(dim=2)).max().item()
+    print(f"  |sum dV - sum dO| / sum|dV| {r_v:.3e}   |sum dK| / sum|dK| {r_k:.3e}   "
+          f"(random signs: ~{L ** -0.5:.1e})", flush=True)
+    # measured about 1e-4 at these shapes; a dropped delta term, a wrong lse
+    # or a wrong scale gives ratios of order one
+    assert r_v <= 1e-3 and r_k <= 1e-3
