@@ -198,7 +198,7 @@ def main() -> None:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     lay = m.layout(dev)           # 128 x 128 tiles: the declared (counted) tile
-    lay.stages().schedule(L, B)   # 128 x 64 blocks: the forward's staging unit
+    lay.stages().schedule(L, B)   # 64 x 32 blocks: the forward's staging unit
     torch.cuda.synchronize()
     layout_ms = (time.perf_counter() - t0) * 1e3
 
@@ -261,7 +261,7 @@ def main() -> None:
                    "batch": B, "heads": H, "seq_len": L, "head_dim": D,
                    "attention_length": W, "layer_idx": args.layer, "num_hidden_layers": NL,
                    "block": [128, 128], "active_tiles": tiles,
-                   "staged_64key_blocks": lay.stages().num_tiles * B},
+                   "staging_block": [64, 32], "staged_blocks": lay.stages().num_tiles * B},
         "pct_of_bf16_mfma_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
         "kernel_ms": round(kern_ms, 4),
         "executed_flop_fraction": round(executed / counted, 4),

@@ -252,8 +252,11 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
   if (!row_ptr || !col_idx || !items) return ESA_ERR_NULL;
   if (a->dtype != ESA_BF16) return ESA_ERR_DTYPE;
   if (a->head_dim != 64 && a->head_dim != 128) return ESA_ERR_UNSUPPORTED;
-  // 128-row query blocks; key blocks of 128 (two stages each) or 64 keys
-  if (p->block_m != 128 || (p->block_n != 128 && p->block_n != 64)) return ESA_ERR_UNSUPPORTED;
+  // 128-row query blocks with key blocks of 128 (two 64-key stages each) or
+  // 64 keys; or 64-row query blocks with 32-key blocks
+  const bool rows64 = p->block_m == 64 && p->block_n == 32;
+  if (!rows64 && (p->block_m != 128 || (p->block_n != 128 && p->block_n != 64)))
+    return ESA_ERR_UNSUPPORTED;
   // The per-tile key masks assume strictly rising indices, which holds for
   // 0 <= alpha <= 1.
   if (p->layer_idx < 0 || p->layer_idx > std::max(p->num_hidden_layers - 1, 0))
@@ -297,6 +300,7 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
   t.q_len = a->q_len; t.kv_len = a->kv_len; t.nqb = d.nqb; t.nq = nq;
   t.num_bh = a->batch * a->num_heads;
   t.stage_shift = p->block_n == 128 ? 1 : 0;
+  t.rows64 = rows64 ? 1 : 0;
   t.scale_log2 = a->sm_scale * 1.4426950408889634f;
   t.pc = make_consts(*p);
   t.row_ptr = row_ptr; t.col_idx = col_idx; t.items = items;

@@ -55,20 +55,30 @@
 
 namespace esa {
 
-template <int D>
+// BMQ query rows per work item: 128 (4 waves, 64-key stages, two
+// workgroups per CU) or 64 (2 waves, 32-key stages, four workgroups per CU:
+// fewer waves meet at each barrier)
+template <int D, int BMQ>
 struct TileCfg {
-  static constexpr int BM = 128;
-  static constexpr int HALF = 64;                 // keys per stage
+  static constexpr int BM = BMQ;
+  static constexpr int W = BMQ / 32;              // waves
+  static constexpr int HALF = BMQ == 128 ? 64 : 32;  // keys per stage
+  static constexpr int LOG_HALF = BMQ == 128 ? 6 : 5;
+  static constexpr int NB = HALF / 32;            // 32-key blocks per stage
   static constexpr int CPR = D / 8;               // 16-byte chunks per row
   static constexpr int STAGE = HALF * D;          // elements per stage buffer (one matrix)
-  static constexpr int LOADS = HALF * CPR / 256;  // 16-byte loads per lane per matrix per stage
+  static constexpr int LOADS = HALF * CPR / (64 * W);  // 16-byte loads per lane per matrix per stage
   static constexpr int NS = D / 16;               // k-steps of QK^T
   static constexpr int ND = D / 32;               // 32-wide d blocks of PV
+  static_assert(LOADS >= 1 && LOADS * 64 * W == HALF * CPR, "whole stage per load round");
 };
 
-template <int D>
-__global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
-  using C = TileCfg<D>;
+// (the second launch bound is the minimum number of waves per SIMD: two,
+// so at most 256 VGPRs; LDS then allows two 128-row or four 64-row
+// workgroups per CU)
+template <int D, int BMQ>
+__global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
+  using C = TileCfg<D, BMQ>;
   // stage buffers (HALF rows x D, rows unpadded, chunks swizzled); separate
   // objects, so the compiler can tell reads of one buffer from the direct
   // loads into the other
@@ -248,8 +258,10 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
     koff[j] = (row * (int)A.kss + 8 * (pc ^ swz_k<D>(row))) * 2;
     voff[j] = (row * (int)A.vss + 8 * (pc ^ swz_v<D>(row))) * 2;
   }
-  auto stage_key0 = [&](int st) { return (col_idx[st >> sh] << (6 + sh)) + ((st & sh) << 6); };
-  // the 64 keys from key0 -> buffers (kd, vd)
+  auto stage_key0 = [&](int st) {
+    return (col_idx[st >> sh] << (C::LOG_HALF + sh)) + ((st & sh) << C::LOG_HALF);
+  };
+  // the HALF keys from key0 -> buffers (kd, vd)
   auto issue = [&](int key0, uint16_t* kd, uint16_t* vd) {
     const int ks = key0 * (int)A.kss * 2, vs = key0 * (int)A.vss * 2;
 #pragma unroll
@@ -271,21 +283,21 @@ __global__ __launch_bounds__(256, 2) void tile_fwd_kernel(TileArgs A) {
     const bool has_b = st + 1 < s1, has_c = st + 2 < s1;
     const int kb = stage_key0(min(st + 1, s1 - 1));
     const int kc = stage_key0(min(st + 2, s1 - 1));
-    uint32_t mb[4];
-    walk.stage_pair(ka, kb, has_b, mb);
+    uint32_t mb[2 * C::NB];
+    walk.stage_pair<C::NB>(ka, kb, has_b, mb);
 
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
     if (has_b) issue(kb, k_st1, v_st1);
-    block(k_st0, v_st0, 0, mb[0]);
-    block(k_st0, v_st0, 1, mb[1]);
+#pragma unroll
+    for (int j = 0; j < C::NB; ++j) block(k_st0, v_st0, j, mb[j]);
     if (!has_b) break;
 
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
     if (has_c) issue(kc, k_st0, v_st0);
-    block(k_st1, v_st1, 0, mb[2]);
-    block(k_st1, v_st1, 1, mb[3]);
+#pragma unroll
+    for (int j = 0; j < C::NB; ++j) block(k_st1, v_st1, j, mb[C::NB + j]);
     ka = kc;
   }
 
@@ -317,10 +329,17 @@ hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
                            hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
   dim3 grid((unsigned)num_items);
-  if (head_dim == 128)
-    tile_fwd_kernel<128><<<grid, 256, 0, stream>>>(a);
-  else
-    tile_fwd_kernel<64><<<grid, 256, 0, stream>>>(a);
+  if (a.rows64) {
+    if (head_dim == 128)
+      tile_fwd_kernel<128, 64><<<grid, 128, 0, stream>>>(a);
+    else
+      tile_fwd_kernel<64, 64><<<grid, 128, 0, stream>>>(a);
+  } else {
+    if (head_dim == 128)
+      tile_fwd_kernel<128, 128><<<grid, 256, 0, stream>>>(a);
+    else
+      tile_fwd_kernel<64, 128><<<grid, 256, 0, stream>>>(a);
+  }
   return hipGetLastError();
 }
 

@@ -27,7 +27,8 @@ struct TileArgs {
   int nqb;     // query blocks per head in the layout
   int nq;      // query blocks a q_len-row forward visits (<= nqb)
   int num_bh;  // batch * H
-  int stage_shift;  // layout key blocks are 64 << stage_shift keys (64 or 128)
+  int stage_shift;  // layout key blocks are (stage keys) << stage_shift keys
+  int rows64;       // 1: 64-row items (2 waves) over a 64 x 32 layout
   float scale_log2;  // sm_scale * log2(e)
   PatternConsts pc;
   const int32_t* row_ptr;

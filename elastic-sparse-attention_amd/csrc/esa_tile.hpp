@@ -160,17 +160,20 @@ struct RowWalker {
   // Valid keys of this row inside the 128-key tile [k0, k0 + 128).
   __device__ __forceinline__ void tile(int k0, uint32_t (&mb)[4]) { span<4>(k0, mb); }
 
-  // Two 64-key stages at ka and kb (kb > ka, or no second stage): mb[0..1]
-  // for ka, mb[2..3] for kb; adjacent stages are walked as one 128-key span.
-  __device__ __forceinline__ void stage_pair(int ka, int kb, bool has_b, uint32_t (&mb)[4]) {
-    if (has_b && kb == ka + 64) {
-      span<4>(ka, mb);
+  // Two stages of 32 NW keys at ka and kb (kb > ka, or no second stage):
+  // mb[0 .. NW) for ka, mb[NW .. 2 NW) for kb; adjacent stages are walked as
+  // one span.
+  template <int NW>
+  __device__ __forceinline__ void stage_pair(int ka, int kb, bool has_b, uint32_t (&mb)[2 * NW]) {
+    if (has_b && kb == ka + 32 * NW) {
+      span<2 * NW>(ka, mb);
     } else {
-      span<2>(ka, mb);
+      span<NW>(ka, mb);
       if (has_b) {
-        span<2>(kb, mb + 2);
+        span<NW>(kb, mb + NW);
       } else {
-        mb[2] = mb[3] = 0u;
+#pragma unroll
+        for (int q = NW; q < 2 * NW; ++q) mb[q] = 0u;
       }
     }
   }

@@ -171,12 +171,13 @@ class ElasticLayout:
         self._masks: Dict[int, torch.Tensor] = {}
         self._stages: Dict[Tuple[int, int], "ElasticLayout"] = {}
 
-    def stages(self, block_n: int = 64, block_m: Optional[int] = None) -> "ElasticLayout":
-        """The same pattern's layout at ``block_m`` x ``block_n`` blocks
-        (128 x 64 for the forward's staging unit: a half of a 128-key tile
-        that no row of the query block needs is not listed, so the forward
-        never loads it).  Built once per shape, cached; the 128 x 128 layout
-        itself stays the declared tile (counted flops, the backward)."""
+    def stages(self, block_n: int = 32, block_m: Optional[int] = 64) -> "ElasticLayout":
+        """The same pattern's layout at ``block_m`` x ``block_n`` blocks, the
+        forward's staging unit (64 x 32 by default, or 128 x 64): a part of a
+        128 x 128 tile that no row of the query block needs is not listed, so
+        the forward never loads it.  Built once per shape, cached; the
+        128 x 128 layout itself stays the declared tile (counted flops, the
+        backward)."""
         block_m = self.pattern.block_m if block_m is None else block_m
         if self.pattern.block_n == block_n and self.pattern.block_m == block_m:
             return self
@@ -310,24 +311,31 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
 
 def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           layout: ElasticLayout, scaling: float, return_lse: bool = True,
-                          out: Optional[torch.Tensor] = None, key_block: int = 64
+                          out: Optional[torch.Tensor] = None, key_block: int = 32,
+                          query_block: int = 64
                           ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Block-sparse MFMA forward (prefill: query row r is position r).
 
     Returns ``o`` as ``[B, Lq, H, D]`` (so ``o.view(B, Lq, H * D)`` is the
     module output, :761-763) and, if asked, ``lse`` float32 ``[B, H, Lq]``.
-    ``key_block`` 64 stages K/V from the layout's 64-key blocks (skipping
-    tile halves no row needs); 128 stages whole 128-key tiles of ``layout``.
-    Both give the same output bit for bit.
+    The staging unit is ``query_block`` x ``key_block``: by default each
+    workgroup of two waves takes 64 query rows and stages K/V in 32-key
+    blocks from the pattern's 64 x 32 layout (the fastest choice measured at
+    every shape but one); (128, 64) gives four waves 128 rows and 64-key
+    stages (halves of 128-key tiles no row needs are skipped); (128, 128)
+    stages whole 128-key tiles of ``layout``.  All give the same output bit
+    for bit.
     """
     _check_qkv(q, k, v)
     B, H, Lq, D = q.shape
     q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
     o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
-    if key_block not in (64, 128):
-        raise ValueError(f"key_block must be 64 or 128, got {key_block}")
-    st = layout if key_block == 128 else layout.stages(64)
+    if (query_block, key_block) not in ((128, 64), (128, 128), (64, 32)):
+        raise ValueError(f"(query_block, key_block) must be (128, 64), (128, 128) or (64, 32), "
+                         f"got ({query_block}, {key_block})")
+    st = layout if (query_block, key_block) == (128, 128) else layout.stages(key_block,
+                                                                             query_block)
     items, n = st.schedule(Lq, B)
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
     check(load().esa_elastic_fwd(ctypes.byref(a), ctypes.byref(st.pattern),

@@ -130,12 +130,14 @@ esa_status esa_plan_schedule(const esa_pattern* p, const int32_t* row_ptr_host,
  * 0..q_len-1.  Replaces _triton_forward + ElasticSparseAttentionFunction
  * .forward (elastic_sparse_attention.py:592-622, 241-297) for prefill.
  * Visits only the active key blocks of the layout, runs QK^T and PV on bf16
- * MFMA with float32 accumulation and online softmax.  The layout may be
- * built at block_n = 128 or 64 (block_m = 128): at 64 a 128-key tile's half
- * that no row of the query block needs is never staged, so the forward runs
- * faster on the same output (bit for bit).  Requires dtype ESA_BF16,
- * head_dim 64 or 128, block_m = 128 and block_n in {64, 128}, a finite
- * sm_scale > 0
+ * MFMA with float32 accumulation and online softmax.  The layout's block
+ * shape is the staging unit: 128 x 128 (whole tiles), 128 x 64 (four waves
+ * per 128 query rows, 64-key stages) or 64 x 32 (two waves per 64 query
+ * rows, 32-key stages, the fastest in general); in the finer layouts the
+ * parts of a 128-key tile that no row of the query block needs are never
+ * staged.  All give the same output bit for bit.  Requires dtype ESA_BF16,
+ * head_dim 64 or 128, (block_m, block_n) in {(128, 128), (128, 64),
+ * (64, 32)}, a finite sm_scale > 0
  * (ESA_ERR_UNSUPPORTED otherwise; esa_elastic_fwd_rows takes any), K and V
  * row strides >= head_dim with kv_len * row stride * 2 < 2^31 (one head's
  * rows within a 2 GiB window), q_len <= kv_len,

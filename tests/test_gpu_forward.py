@@ -132,11 +132,17 @@ def test_stage_layout_matches_tile_layout(B, H, Hkv, L, Lq, D, layer):
     print(f"stages vs tiles B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} layer={layer}", flush=True)
     q, k, v, _, _ = case(B, H, Hkv, L, D, torch.bfloat16, layer, seed=layer + 11, Lq=Lq)
     lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
-    assert lay.stages().num_tiles <= 2 * lay.num_tiles
+    assert lay.stages(64, 128).num_tiles <= 2 * lay.num_tiles
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
-    o64, l64 = elastic_attention_fwd(qd, kd, vd, lay, scaling_for(D), key_block=64)
-    o128, l128 = elastic_attention_fwd(qd, kd, vd, lay, scaling_for(D), key_block=128)
+    o64, l64 = elastic_attention_fwd(qd, kd, vd, lay, scaling_for(D), key_block=64,
+                                     query_block=128)
+    o128, l128 = elastic_attention_fwd(qd, kd, vd, lay, scaling_for(D), key_block=128,
+                                       query_block=128)
     assert torch.equal(o64, o128) and torch.equal(l64, l128)
+    # 64-row items of two waves over 32-key stages
+    o32, l32 = elastic_attention_fwd(qd, kd, vd, lay, scaling_for(D), key_block=32,
+                                     query_block=64)
+    assert torch.equal(o32, o128) and torch.equal(l32, l128)
 
 
 
