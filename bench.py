@@ -4,17 +4,21 @@
                     [--layer N] [--no-cpu]
 
 A step is one ElasticSparseAttention.forward over one batch of synthetic
-input already resident in HBM (the module's drop-in HIP path: one
-block-sparse MFMA launch).  The block layout is built before the timed
-region, as the reference builds its index cache at construction; its build
-time is reported separately.
+input already resident in HBM (the module's drop-in HIP path: one kernel
+launch, the band-gathered kernel or the block-sparse tile kernel, whichever
+is faster for the shape; config.kernel names it).  The block layout is built
+before the timed region, as the reference builds its index cache at
+construction; its build time is reported separately.
 
 Prints ONE JSON line.  value = counted active-tile flops / wall time per
-step, where counted flops = active 128x128 tiles x 4 * 128 * 128 * D.
-roofline.achieved uses the same flops over the kernel's own average duration
-(HIP events on the launch stream).  Inside an active tile the kernel issues
-MFMAs only for the 32 x 32 blocks that hold a valid key for one of a wave's
-rows; executed_flop_fraction and executed_mfma_tflops report that work.  cpu_baseline times the reference's
+step, where counted flops = active 128x128 tiles x 4 * 128 * 128 * D (the
+metric's unit of work, whatever the kernel executes).  roofline.achieved
+uses the same flops over the kernel's own average duration (HIP events on the
+launch stream).  The kernels issue far fewer MFMA flops than that: the tile
+kernel only the 32 x 32 blocks of an active tile that hold a valid key for
+one of a wave's rows, the band kernel 16 keys x 16 rows per entry of the
+rows' index lists; executed_flop_fraction and executed_mfma_tflops report
+that work.  cpu_baseline times the reference's
 PyTorch fallback (_naive_forward, restated in oracle/) on the host cores on a
 bounded sample of query rows of the same workload, extrapolated linearly
 (every row costs the same w-key gather there).
@@ -138,6 +142,19 @@ def executed_blocks(torch, lay, L: int) -> int:
     return int(masks[:n * 512].view(n, 4, 4, 32).ne(0).any(-1).sum().item())
 
 
+def band_executed_flops(B: int, H: int, L: int, D: int, w: int) -> float:
+    """MFMA flops the band kernel issues in its main loop: per 16-row group
+    and pair of index-list entries with a valid key in the group, D/32 QK^T
+    and D/16 PV 16x16x32 MFMAs per entry pair (2 D/32 + D/16 in all), 16384
+    flops each.  Entries j > i are masked for rows i < w - 1, so group g
+    holds min(w, 16 g + 16) live entries."""
+    pairs = 0
+    for g in range((L + 15) // 16):
+        live = min(w, 16 * g + 16)
+        pairs += (live + 1) // 2
+    return float(B * H * pairs * (2 * (D // 32) + D // 16) * 16384)
+
+
 def traffic_from_profile(name: str):
     """HBM bytes per launch of the forward kernel, from the committed rocprofv3
     --pmc summary for this workload (profiles/<name>), or None."""
@@ -159,6 +176,8 @@ def main() -> None:
     ap.add_argument("--config", default="32k", choices=sorted(CONFIGS))
     ap.add_argument("--layer", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel", default="auto", choices=["auto", "band", "tile"],
+                    help="prefill kernel the module runs (default: the faster for the shape)")
     ap.add_argument("--backward", action="store_true",
                     help="also time the block-sparse backward (reported beside the forward)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -174,7 +193,7 @@ def main() -> None:
     if args.copy_calibration:
         copy_calibration(torch)
         return
-    from elastic_sparse_attention import ElasticSparseAttention
+    from elastic_sparse_attention import ElasticSparseAttention, prefill_kernel
 
     B, H, L, D, scale, outl = CONFIGS[args.config]
     dev = torch.device("cuda", 0)
@@ -198,7 +217,9 @@ def main() -> None:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     lay = m.layout(dev)           # 128 x 128 tiles: the declared (counted) tile
-    lay.stages().schedule(L, B)   # 64 x 32 blocks: the forward's staging unit
+    lay.stages().schedule(L, B)   # 64 x 32 blocks: the tile kernel's staging unit
+    kernel = prefill_kernel(lay, L, B, D) if args.kernel == "auto" else args.kernel
+    m.prefill_kernel = kernel
     torch.cuda.synchronize()
     layout_ms = (time.perf_counter() - t0) * 1e3
 
@@ -228,11 +249,14 @@ def main() -> None:
 
     achieved = counted / (kern_ms * 1e-3) / 1e12
     value = counted / wall / 1e12
-    # MFMA work actually issued: inside each active tile a wave skips the
-    # 32 x 32 (rows x keys) blocks where none of its rows has a valid key
-    executed = B * executed_blocks(torch, lay, L) * 4.0 * 32 * 32 * D
+    if kernel == "tile":
+        # MFMA work actually issued: inside each active tile a wave skips the
+        # 32 x 32 (rows x keys) blocks where none of its rows has a valid key
+        executed = B * executed_blocks(torch, lay, L) * 4.0 * 32 * 32 * D
+    else:
+        executed = band_executed_flops(B, H, L, D, W)
     traffic = traffic_from_profile(
-        f"tile_fwd_kernel_bf16_B{B}_H{H}_L{L}_D{D}_layer{args.layer}_pmc.md")
+        f"{kernel}_fwd_kernel_bf16_B{B}_H{H}_L{L}_D{D}_layer{args.layer}_pmc.md")
     if args.layer == 0:
         # a plain sliding window: ~127 flop/B, below the MFMA ridge -> HBM-bound
         gbs = alg_bytes / (kern_ms * 1e-3) / 1e9
@@ -260,8 +284,8 @@ def main() -> None:
                                 f"128x128 tiles"),
                    "batch": B, "heads": H, "seq_len": L, "head_dim": D,
                    "attention_length": W, "layer_idx": args.layer, "num_hidden_layers": NL,
-                   "block": [128, 128], "active_tiles": tiles,
-                   "staging_block": [64, 32], "staged_blocks": lay.stages().num_tiles * B},
+                   "block": [128, 128], "active_tiles": tiles, "kernel": kernel,
+                   "staged_blocks_64x32": lay.stages().num_tiles * B},
         "pct_of_bf16_mfma_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
         "kernel_ms": round(kern_ms, 4),
         "executed_flop_fraction": round(executed / counted, 4),

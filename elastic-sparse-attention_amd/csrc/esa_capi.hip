@@ -307,6 +307,60 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
   return hip_status(launch_tile_fwd(t, a->head_dim, num_items, (hipStream_t)stream));
 }
 
+esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, void* stream) {
+  esa_status s = check_fwd_common(a);
+  if (s != ESA_OK) return s;
+  s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  if (a->dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (a->head_dim != 64 && a->head_dim != 128) return ESA_ERR_UNSUPPORTED;
+  // one wave holds a row's band descriptors for at most 64 bands; indices
+  // rise with the band (0 <= alpha <= 1)
+  if (p->attention_length > 64) return ESA_ERR_UNSUPPORTED;
+  if (p->layer_idx < 0 || p->layer_idx > std::max(p->num_hidden_layers - 1, 0))
+    return ESA_ERR_UNSUPPORTED;
+  if (p->num_heads != a->num_heads) return ESA_ERR_SHAPE;
+  if (a->q_len > a->kv_len || a->q_len > p->seq_len) return ESA_ERR_SHAPE;
+  if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale)) return ESA_ERR_UNSUPPORTED;
+  // band descriptors pack the first key in 24 bits; K/V rows are addressed
+  // through 32-bit buffer offsets per (batch, kv head)
+  if (a->kv_len >= (1 << 24)) return ESA_ERR_UNSUPPORTED;
+  if ((int64_t)(a->kv_len + 16) * a->k_stride_s * 2 >= (int64_t(1) << 31) ||
+      (int64_t)(a->kv_len + 16) * a->v_stride_s * 2 >= (int64_t(1) << 31) ||
+      a->k_stride_s < a->head_dim || a->v_stride_s < a->head_dim)
+    return ESA_ERR_UNSUPPORTED;
+  // 16-byte row loads and stores
+  if (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16) || !aligned(a->o, 16))
+    return ESA_ERR_ALIGN;
+  const int64_t st[] = {a->q_stride_b, a->q_stride_h, a->q_stride_s, a->k_stride_b,
+                        a->k_stride_h, a->k_stride_s, a->v_stride_b, a->v_stride_h,
+                        a->v_stride_s, a->o_stride_b, a->o_stride_h, a->o_stride_s};
+  for (int64_t x : st)
+    if (x % 8 != 0) return ESA_ERR_ALIGN;
+  if (a->batch == 0 || a->q_len == 0) return ESA_OK;
+  const int ng = (a->q_len + 15) / 16;
+  const int64_t n_groups = (int64_t)a->batch * a->num_heads * ng;
+  if (n_groups > INT32_MAX / 2) return ESA_ERR_SHAPE;
+
+  BandArgs t{};
+  t.q = (const uint16_t*)a->q; t.k = (const uint16_t*)a->k; t.v = (const uint16_t*)a->v;
+  t.o = (uint16_t*)a->o; t.lse = a->lse;
+  t.qsb = a->q_stride_b; t.qsh = a->q_stride_h; t.qss = a->q_stride_s;
+  t.ksb = a->k_stride_b; t.ksh = a->k_stride_h; t.kss = a->k_stride_s;
+  t.vsb = a->v_stride_b; t.vsh = a->v_stride_h; t.vss = a->v_stride_s;
+  t.osb = a->o_stride_b; t.osh = a->o_stride_h; t.oss = a->o_stride_s;
+  t.lsb = a->lse_stride_b; t.lsh = a->lse_stride_h;
+  t.H = a->num_heads; t.groups = a->num_heads / a->num_kv_heads; t.q_len = a->q_len;
+  t.ng = ng;
+  t.n_groups = (int)n_groups;
+  t.per_xcd = (int)((n_groups + 7) / 8);
+  t.nrec_k = (int)((int64_t)a->kv_len * a->k_stride_s * 2);
+  t.nrec_v = (int)((int64_t)a->kv_len * a->v_stride_s * 2);
+  t.scale_log2 = a->sm_scale * 1.4426950408889634f;
+  t.pc = make_consts(*p);
+  return hip_status(launch_band_fwd(t, a->head_dim, (hipStream_t)stream));
+}
+
 esa_status esa_elastic_fwd_rows(const esa_fwd_args* a, const esa_pattern* p,
                                 const int64_t* positions, void* stream) {
   esa_status s = check_fwd_common(a);

@@ -1,0 +1,441 @@
+// Band-gathered forward over the elastic pattern (gfx950), prefill rows.
+//
+// Replaces the forward branch of the reference's per-token Triton kernel
+// (elastic_sparse_attention.py:117-166) for query positions 0 .. q_len - 1,
+// with the index list of every row regenerated on the device (the recipe of
+// elastic_sparse_attention.py:482-535).
+//
+// Structure the kernel relies on: entry j of a row's index list (its "band")
+// moves by 0 or 1 key from one row to the next (by 2 at a few rows of a head
+// whose interpolation weight is 1/2), so across 16 consecutive rows band j
+// spans at most 16 consecutive keys, rarely 17.  One wave owns
+// 16 query rows (a group).  For each band it gathers the keys [lo_j, lo_j+16)
+// (lo_j = the band's smallest valid key over the group; keys past the band's
+// largest one read as zero and cost no traffic), computes the 16 x 16 scores
+// with MFMA, keeps for each row only its own key of the band (exactly one
+// per row and band, so no key is counted twice even where bands overlap),
+// and accumulates P V with MFMA.  A band wider than 16 keys (not produced by
+// the shapes measured, but allowed) gets its extra keys in a tail pass.
+// Every group does the same number of bands, and waves share nothing: no
+// barriers, no LDS shared between waves.
+//
+// Per band and wave:
+//   S^T = K Q^T     D/32 x v_mfma_f32_16x16x32_bf16; A = K rows read from
+//                   LDS (lane m: key lo + m%16), B = Q held in registers for
+//                   the whole group
+//   select          each lane owns one row and 4 of the 16 keys; the lane
+//                   holding the row's key of this band keeps its score, the
+//                   row's 4 lanes share it with two lane swaps
+//   softmax         online, log2 domain, one running-max update per band
+//                   pair, lazy rescale (the running max moves only when a
+//                   score exceeds it by more than 8)
+//   O^T += V^T P^T  bands go in pairs (32 keys = one MFMA k-step): D/16 x
+//                   v_mfma_f32_16x16x32_bf16, A = V^T read with
+//                   ds_read_b64_tr_b16 from row-major V rows in LDS, B = P
+//                   straight from the select step
+// K and V rows reach LDS by buffer_load ... lds, whole rows per 16 lanes:
+// the L1 spends about a clock per (16-lane pass, cache line), so loading the
+// MFMA operand straight into registers (16 key rows per pass) would cost 8x
+// the L1 time.  Two K and two V slots per wave: the next pair's K is
+// requested once this pair's K operands are in registers, its V once this
+// pair's PV has read V.
+//
+// MFMA 16x16x32 register layouts (gfx950):
+//   A[i][k]: lane l holds i = l%16, k = 8*(l/16) + e, e = 0..7
+//   B[k][j]: lane l holds k = 8*(l/16) + e, j = l%16
+//   C[i][j]: lane l, reg r holds i = 4*(l/16) + r, j = l%16
+// ds_read_b64_tr_b16 in each 16-lane group: lane g receives element r from
+// lane 4r + g/4's 8-byte chunk, element g%4.
+#include "esa_tile.hpp"
+
+namespace esa {
+
+namespace {
+
+template <int D>
+struct BandCfg {
+  static constexpr int NS = D / 32;       // QK^T k-steps (32 dims each)
+  static constexpr int NV = D / 16;       // 16-dim slices of O^T
+  static constexpr int CW = D / 4;        // dims per lane group of an O row
+  static constexpr int CPR = D / 8;       // 16-byte chunks per K/V row
+  static constexpr int ROWB = 2 * D;      // bytes per row
+  static constexpr int SLOT = 16 * D;     // elements per V ring slot (16 rows)
+  static constexpr int VLOADS = 16 * CPR / 64;  // DMA instructions per band
+};
+
+// physical 16-byte chunk of logical chunk lc in row r of a V slot: the 16
+// lanes of a transposed read hit 16 distinct bank groups
+template <int D>
+__device__ __forceinline__ int vswz(int r, int lc) {
+  return D == 128 ? lc ^ (r & 3) : lc ^ ((r >> 1) & 1);
+}
+// the same for a K slot: 16 lanes reading one chunk of rows 0..15 hit 16
+// distinct bank groups
+template <int D>
+__device__ __forceinline__ int kswz(int r, int lc) {
+  return D == 128 ? lc ^ (r & 15) : lc ^ ((r >> 1) & 7);
+}
+
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// max over the 4 lanes l, l^16, l^32, l^48 (one row's lanes)
+__device__ __forceinline__ float row4_max(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  const float m1 = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m1), __float_as_uint(m1),
+                                                  false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// min / max over the 16 lanes of a lane group (DPP row rotations)
+__device__ __forceinline__ int row16_min(int v) {
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x122, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x121, 0xf, 0xf, false));
+  return v;
+}
+__device__ __forceinline__ int row16_max(int v) {
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x122, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x121, 0xf, 0xf, false));
+  return v;
+}
+
+}  // namespace
+
+// Band descriptor word: lo | W << 24 (W = keys from lo to the band's largest
+// valid key, 0 for a band no row of the group uses); lo < 2^24 (host check).
+template <int D>
+__global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
+  using C = BandCfg<D>;
+  // K and V slots of the pair's two bands (separate objects, so the compiler
+  // can tell reads of one slot from the direct loads into another)
+  __shared__ __attribute__((aligned(1024))) uint16_t ks0[C::SLOT];
+  __shared__ __attribute__((aligned(1024))) uint16_t ks1[C::SLOT];
+  __shared__ __attribute__((aligned(1024))) uint16_t vs0[C::SLOT];
+  __shared__ __attribute__((aligned(1024))) uint16_t vs1[C::SLOT];
+  uint16_t* const slot[4] = {ks0, ks1, vs0, vs1};
+
+  // ---- group: XCD x takes the contiguous range [x per, (x + 1) per)
+  const int bid = blockIdx.x;
+  const int g = (bid & 7) * A.per_xcd + (bid >> 3);
+  if (g >= A.n_groups) return;
+  const int bh = g / A.ng, gq = g % A.ng;
+  const int h = bh % A.H, b = bh / A.H;
+  const int kvh = h / A.groups;
+
+  const int lane = threadIdx.x;
+  const int n = lane & 15, q = lane >> 4;
+  const int i = gq * 16 + n;  // this lane's query row
+  const bool row_ok = i < A.q_len;
+
+  // ---- slots to zeros once: rows a band does not fill keep finite values
+  {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int c = 0; c < C::SLOT / 512; ++c) *(u32x4*)(slot[s] + (c * 64 + lane) * 8) = z;
+  }
+
+  // ---- Q as the B operand: row n, dims 32 s + 8 q .. + 8 for k-step s
+  bf16x8 qop[C::NS];
+  {
+    const uint16_t* qrow = A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)i * A.qss;
+#pragma unroll
+    for (int s = 0; s < C::NS; ++s) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (row_ok) raw = *(const u32x4*)(qrow + 32 * s + 8 * q);
+      qop[s] = __builtin_bit_cast(bf16x8, raw);
+    }
+  }
+
+  // ---- this row's keys of bands 16 q .. 16 q + 15 (-1: no key), and the
+  // group's band descriptors for the same bands (every lane of group q)
+  int kreg[16], info[16];
+  {
+    const HeadWeights hw = head_weights(A.pc, h);
+    const RowParams rp = row_params(A.pc, i);
+    int o_cur = oversized(rp, 16 * q);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int j = 16 * q + r;
+      const int o_next = oversized(rp, j + 1);
+      const int idx = interp_index(o_cur, o_next, hw);
+      o_cur = o_next;
+      kreg[r] = (row_ok && j < A.pc.w && idx <= i) ? idx : -1;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int lo = row16_min(kreg[r] < 0 ? 0x7fffffff : kreg[r]);
+      const int hi = row16_max(kreg[r]);
+      const int wdt = hi >= 0 ? min(hi - lo + 1, 255) : 0;
+      info[r] = hi >= 0 ? (lo | (wdt << 24)) : 0;
+    }
+  }
+
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh), (short)0, A.nrec_k, 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh), (short)0, A.nrec_v, 0x00020000);
+  const int kss2 = (int)A.kss * 2, vss2 = (int)A.vss * 2;
+
+  // K or V rows of band info word `bi` -> slot dst: DMA t, lane l fills row
+  // R = (64 t + l) / CPR, physical chunk l % CPR; rows past the band read as
+  // zeros (offset past num_records).  A fixed number of loads per band keeps
+  // the vmcnt waits below exact.
+  auto load_rows = [&](__amdgpu_buffer_rsrc_t rs, int ss2, int nrec, bool is_k, int bi,
+                       uint16_t* dst) {
+    const int lo = bi & 0xffffff, wdt = (int)((uint32_t)bi >> 24);
+#pragma unroll
+    for (int t = 0; t < C::VLOADS; ++t) {
+      const int R = (64 * t + lane) / C::CPR, pc = lane % C::CPR;
+      const int lc = is_k ? kswz<D>(R, pc) : vswz<D>(R, pc);
+      load_lds16(rs, dst + 512 * t, R < wdt ? (lo + R) * ss2 + 16 * lc : nrec, 0);
+    }
+  };
+  auto load_k = [&](int bi, uint16_t* dst) { load_rows(krs, kss2, A.nrec_k, true, bi, dst); };
+  auto load_v = [&](int bi, uint16_t* dst) { load_rows(vrs, vss2, A.nrec_v, false, bi, dst); };
+
+  // K operand read addresses (bytes within a slot) for k-step s: lane
+  // (m = n, q) reads key row n, dims 32 s + 8 q .. + 8
+  int krd[C::NS];
+#pragma unroll
+  for (int s = 0; s < C::NS; ++s) krd[s] = n * C::ROWB + 16 * kswz<D>(n, 4 * s + q);
+  auto read_k = [&](const uint16_t* src, bf16x8 (&kb)[C::NS]) {
+#pragma unroll
+    for (int s = 0; s < C::NS; ++s) kb[s] = *(const bf16x8*)((const char*)src + krd[s]);
+  };
+
+  // V^T operand read addresses (bytes within a slot) for slice s: lane x of
+  // its 16-lane group reads ring row 4 q + x/4, dims CW (x%4) + 4 s .. + 3
+  int vrd[C::NV];
+#pragma unroll
+  for (int s = 0; s < C::NV; ++s) {
+    const int x = n, R = 4 * q + (x >> 2);
+    const int dim0 = C::CW * (x & 3) + 4 * s;
+    vrd[s] = R * C::ROWB + 16 * vswz<D>(R, dim0 >> 3) + 2 * (dim0 & 7);
+  }
+
+  const float scale = A.scale_log2;
+  float m_run = -INFINITY, l_run = 0.f, n_run = 0.f;
+  f32x4 oacc[C::NV];
+#pragma unroll
+  for (int s = 0; s < C::NV; ++s) oacc[s] = f32x4{};
+
+  // This row's scaled score (log2 units) in chunk [c0, c0 + 16) of a band
+  // (key = the row's key of the band, -1 for none), the same in the row's 4
+  // lanes; -inf when the row has no key there.  has / e: this lane holds the
+  // key, at register e.
+  auto pick = [&](const f32x4& sacc, int key, int c0, bool& has, int& e) -> float {
+    const int d = key - c0;
+    has = key >= 0 && (uint32_t)d < 16u && (d >> 2) == q;
+    e = d & 3;
+    const float s01 = (e & 1) ? sacc[1] : sacc[0];
+    const float s23 = (e & 1) ? sacc[3] : sacc[2];
+    const float s = (e & 2) ? s23 : s01;
+    return row4_max(has ? s * scale : -INFINITY);
+  };
+  // Online softmax over two bands' scores xa, xb (one running-max update per
+  // pair, so both probabilities share one scale) -> P words (bf16 at
+  // register e of the lane holding the key, else 0)
+  auto pair_softmax = [&](float xa, bool ha, int ea, float xb, bool hb, int eb, uint64_t& pa,
+                          uint64_t& pb) {
+    const float xm = fmaxf(xa, xb);
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float ra = xa - m_use, rb = xb - m_use;
+    const float rm = xm - m_use;
+    const bool grow = m_run == -INFINITY ? xm != -INFINITY : rm > kRescaleSlack;
+    if (wave_any(grow)) {
+      const float delta = grow ? rm : 0.f;
+      // rows that do not grow keep alpha = 1 (m_run may still be -inf there)
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - (m_use + delta)) : 1.0f;
+      l_run *= alpha;
+      n_run *= alpha;
+#pragma unroll
+      for (int v = 0; v < C::NV; ++v) oacc[v] *= alpha;
+      m_run = grow ? m_use + delta : m_run;
+      ra -= delta;
+      rb -= delta;
+    }
+    const float p0 = __builtin_amdgcn_exp2f(ra);
+    const float p1 = __builtin_amdgcn_exp2f(rb);
+    l_run += p0;
+    l_run += p1;
+    const uint32_t b0 = (uint32_t)f32_to_bf16_bits(p0);
+    const uint32_t b1 = (uint32_t)f32_to_bf16_bits(p1);
+    // O is normalised by the probabilities PV used (rounded to bf16)
+    n_run += __uint_as_float(b0 << 16);
+    n_run += __uint_as_float(b1 << 16);
+    pa = ha ? ((uint64_t)b0 << (16 * ea)) : 0ull;
+    pb = hb ? ((uint64_t)b1 << (16 * eb)) : 0ull;
+  };
+
+  auto scores = [&](const bf16x8 (&kb)[C::NS]) {
+    f32x4 sacc = mfma16(kb[0], qop[0], f32x4{});
+#pragma unroll
+    for (int s = 1; s < C::NS; ++s) sacc = mfma16(kb[s], qop[s], sacc);
+    return sacc;
+  };
+
+  // O^T += V^T P^T over two bands held in ring slots va, vb with P words
+  // pa, pb (k-slots 8 q .. 8 q + 3: band a keys 4 q .. 4 q + 3; 8 q + 4 ..
+  // 8 q + 7: band b's)
+  auto pv = [&](const uint16_t* va, const uint16_t* vb, uint64_t pa, uint64_t pb) {
+    s16x4 ta[C::NV], tb[C::NV];
+#pragma unroll
+    for (int s = 0; s < C::NV; ++s) {
+      ta[s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s16x4*)((const char*)va + vrd[s]));
+      tb[s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s16x4*)((const char*)vb + vrd[s]));
+    }
+    const u32x4 pq = {(uint32_t)pa, (uint32_t)(pa >> 32), (uint32_t)pb, (uint32_t)(pb >> 32)};
+    const bf16x8 pop = __builtin_bit_cast(bf16x8, pq);
+#pragma unroll
+    for (int s = 0; s < C::NV; ++s) {
+      const s16x4 vv[2] = {ta[s], tb[s]};
+      oacc[s] = mfma16(__builtin_bit_cast(bf16x8, vv), pop, oacc[s]);
+    }
+  };
+
+  // ---- main loop: band pairs (2 p, 2 p + 1).  Load order per pair: K of
+  // the next pair (after this pair's K reads), then V of the next pair (after
+  // this pair's PV), so before either wait exactly 2 VLOADS newer loads may
+  // be in flight.
+  constexpr int kWaitPair = (0xF70 & ~0xF) | ((2 * C::VLOADS) & 0xF) |
+                            (((2 * C::VLOADS) >> 4) << 14);  // vmcnt(2 VLOADS)
+  constexpr int kWaitLds = 0xC07F;                           // lgkmcnt(0)
+  const int lane_key = 4 * n;  // ds_bpermute byte address of row n in group 0
+  {
+    const int i0 = __builtin_amdgcn_readlane(info[0], 0);
+    const int i1 = __builtin_amdgcn_readlane(info[1], 0);
+    __builtin_amdgcn_s_waitcnt(kWaitLds);  // the slot zeros are in LDS
+    load_k(i0, ks0);
+    load_k(i1, ks1);
+    load_v(i0, vs0);
+    load_v(i1, vs1);
+  }
+  for (int qj = 0; qj < 4; ++qj) {
+    const bool more = qj < 3;
+#pragma unroll
+    for (int rp = 0; rp < 8; ++rp) {
+      const int ra = 2 * rp, rb = 2 * rp + 1;
+      const int ia = __builtin_amdgcn_readlane(info[ra], 16 * qj);
+      const int ib = __builtin_amdgcn_readlane(info[rb], 16 * qj);
+      // next pair's descriptors
+      int na, nb;
+      if (rp < 7) {
+        na = __builtin_amdgcn_readlane(info[ra + 2], 16 * qj);
+        nb = __builtin_amdgcn_readlane(info[rb + 2], 16 * qj);
+      } else {
+        na = more ? __builtin_amdgcn_readlane(info[0], 16 * qj + 16) : 0;
+        nb = more ? __builtin_amdgcn_readlane(info[1], 16 * qj + 16) : 0;
+      }
+      const bool live = (ia | ib) != 0;  // some row of the group uses a band
+      __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's K is in LDS
+      bf16x8 kopa[C::NS], kopb[C::NS];
+      if (live) {
+        read_k(ks0, kopa);
+        read_k(ks1, kopb);
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitLds);  // K slots read: refill them
+      load_k(na, ks0);
+      load_k(nb, ks1);
+      if (live) {
+        const int addr = lane_key + 64 * qj;
+        const int keya = __builtin_amdgcn_ds_bpermute(addr, kreg[ra]);
+        const int keyb = __builtin_amdgcn_ds_bpermute(addr, kreg[rb]);
+        const f32x4 sa = scores(kopa);
+        const f32x4 sb = scores(kopb);
+        bool ha, hb;
+        int ea, eb;
+        const float xa = pick(sa, keya, ia & 0xffffff, ha, ea);
+        const float xb = pick(sb, keyb, ib & 0xffffff, hb, eb);
+        uint64_t pa, pbw;
+        pair_softmax(xa, ha, ea, xb, hb, eb, pa, pbw);
+        __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's V is in LDS
+        pv(vs0, vs1, pa, pbw);
+      }
+      // this pair's V has landed (and been read): refill the V slots
+      __builtin_amdgcn_s_waitcnt(kWaitPair & kWaitLds);
+      load_v(na, vs0);
+      load_v(nb, vs1);
+    }
+  }
+
+  // ---- tail: keys of bands wider than 16, one 16-key chunk at a time
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  int wmax = 0;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) wmax = max(wmax, (int)((uint32_t)info[r] >> 24));
+  for (int j = 0; j < 64 && wave_any(wmax > 16); ++j) {
+    const int qj = j >> 4;
+    int bi = 0, key = -1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if ((j & 15) == r) {
+        bi = __builtin_amdgcn_readlane(info[r], 16 * qj);
+        key = __builtin_amdgcn_ds_bpermute(lane_key + 64 * qj, kreg[r]);
+      }
+    }
+    const int lo = bi & 0xffffff, wdt = (int)((uint32_t)bi >> 24);
+    for (int c0 = lo + 16; c0 < lo + wdt; c0 += 16) {
+      const int rem = lo + wdt - c0;
+      const int ci = c0 | (min(rem, 16) << 24);
+      __builtin_amdgcn_s_waitcnt(kWaitLds);  // earlier reads of slots 0 done
+      load_k(ci, ks0);
+      load_v(ci, vs0);
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      bf16x8 kt[C::NS];
+      read_k(ks0, kt);
+      const f32x4 st = scores(kt);
+      bool ht;
+      int et;
+      const float xt = pick(st, key, c0, ht, et);
+      uint64_t pt, pz;
+      pair_softmax(xt, ht, et, -INFINITY, false, 0, pt, pz);
+      // the second band of the pair contributes p = 0 (vs1 holds finite rows)
+      pv(vs0, vs1, pt, 0ull);
+    }
+  }
+
+  // ---- epilogue: lane (n, q) holds O^T[dim][row n] for dims CW q .. CW q + CW
+  // (slice s, reg e: dim CW q + 4 s + e)
+  if (row_ok) {
+    const float inv = n_run > 0.f ? 1.f / n_run : 0.f;
+    uint16_t* orow = A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)i * A.oss;
+#pragma unroll
+    for (int t = 0; t < C::NV / 2; ++t) {
+      bf16x8 ov;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ov[e] = (__bf16)(oacc[2 * t][e] * inv);
+        ov[4 + e] = (__bf16)(oacc[2 * t + 1][e] * inv);
+      }
+      *(bf16x8*)(orow + C::CW * q + 8 * t) = ov;
+    }
+    if (A.lse && q == 0) {
+      const float lse = l_run > 0.f ? (m_run + __log2f(l_run)) * 0.69314718055994530942f
+                                    : -INFINITY;
+      A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + i] = lse;
+    }
+  }
+}
+
+hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) {
+  if (a.n_groups <= 0) return hipSuccess;
+  dim3 grid((unsigned)(8 * a.per_xcd));
+  if (head_dim == 128)
+    band_fwd_kernel<128><<<grid, 64, 0, stream>>>(a);
+  else
+    band_fwd_kernel<64><<<grid, 64, 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+}  // namespace esa

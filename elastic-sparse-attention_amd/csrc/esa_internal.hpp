@@ -36,6 +36,27 @@ struct TileArgs {
   const int32_t* items;
 };
 
+// Arguments of the band-gathered forward (prefill rows 0 .. q_len - 1).
+struct BandArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  float* lse;
+  int64_t qsb, qsh, qss;
+  int64_t ksb, ksh, kss;
+  int64_t vsb, vsh, vss;
+  int64_t osb, osh, oss;
+  int64_t lsb, lsh;
+  int H, groups, q_len;
+  int ng;        // 16-row groups per (batch, head)
+  int n_groups;  // batch * H * ng
+  int per_xcd;   // groups per XCD range
+  int nrec_k, nrec_v;  // bytes of one (batch, kv head)'s kv_len K / V rows
+  float scale_log2;    // sm_scale * log2(e)
+  PatternConsts pc;
+};
+
 // Arguments of the per-row gather forward.
 struct GatherArgs {
   const void* q;
@@ -102,6 +123,7 @@ hipError_t launch_layout(const PatternConsts& pc, const LayoutDims& ld, int32_t*
                          int32_t* col_idx, void* workspace, hipStream_t stream);
 hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
                            hipStream_t stream);
+hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream);
 hipError_t launch_gather_fwd(const GatherArgs& a, bool f32, bool pattern, hipStream_t stream);
 hipError_t launch_tile_masks(const PatternConsts& pc, const int32_t* row_ptr, const int32_t* col_idx,
                              int nqb, int q_len, uint32_t* mask_t, hipStream_t stream);

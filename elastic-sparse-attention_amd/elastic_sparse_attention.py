@@ -309,25 +309,54 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
                          f"({k.shape[1]})")
 
 
+# Measured crossover (MI355X) between the two prefill kernels: the band
+# kernel costs about the same per 16-row group at every layer, the tile
+# kernel about the same per staged 64 x 32 block, and the band kernel is the
+# faster one once a group's rows stage more than this many blocks.
+BAND_CROSSOVER = {128: 19.0, 64: 13.0}
+
+
+def prefill_kernel(layout: ElasticLayout, q_len: int, batch: int, head_dim: int) -> str:
+    """"band" or "tile": the faster prefill kernel for this pattern and shape
+    (the band kernel needs attention_length <= 64 and kv_len < 2^24)."""
+    p = layout.pattern
+    if p.attention_length > 64 or head_dim not in BAND_CROSSOVER or p.seq_len >= (1 << 24):
+        return "tile"
+    groups = batch * p.num_heads * ((q_len + 15) // 16)
+    staged = batch * layout.stages().tiles_for(q_len)
+    return "band" if staged > BAND_CROSSOVER[head_dim] * groups else "tile"
+
+
 def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           layout: ElasticLayout, scaling: float, return_lse: bool = True,
                           out: Optional[torch.Tensor] = None, key_block: int = 32,
-                          query_block: int = 64
+                          query_block: int = 64, kernel: str = "auto"
                           ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
-    """Block-sparse MFMA forward (prefill: query row r is position r).
+    """Prefill forward over the elastic pattern (query row r is position r).
 
     Returns ``o`` as ``[B, Lq, H, D]`` (so ``o.view(B, Lq, H * D)`` is the
     module output, :761-763) and, if asked, ``lse`` float32 ``[B, H, Lq]``.
-    The staging unit is ``query_block`` x ``key_block``: by default each
-    workgroup of two waves takes 64 query rows and stages K/V in 32-key
-    blocks from the pattern's 64 x 32 layout (the fastest choice measured at
-    every shape but one); (128, 64) gives four waves 128 rows and 64-key
-    stages (halves of 128-key tiles no row needs are skipped); (128, 128)
-    stages whole 128-key tiles of ``layout``.  All give the same output bit
-    for bit.
+
+    ``kernel``: "tile" is the block-sparse MFMA kernel over ``layout``;
+    "band" the band-gathered kernel (:func:`elastic_attention_band`); "auto"
+    takes the faster for the shape (:func:`prefill_kernel`).  Both agree to
+    bf16 rounding.  For the tile kernel the staging unit is ``query_block``
+    x ``key_block``: by default each workgroup of two waves takes 64 query
+    rows and stages K/V in 32-key blocks from the pattern's 64 x 32 layout;
+    (128, 64) gives four waves 128 rows and 64-key stages (halves of 128-key
+    tiles no row needs are skipped); (128, 128) stages whole 128-key tiles of
+    ``layout``.  All tile variants give the same output bit for bit.
     """
     _check_qkv(q, k, v)
     B, H, Lq, D = q.shape
+    if kernel not in ("auto", "tile", "band"):
+        raise ValueError(f"kernel must be 'auto', 'tile' or 'band', got {kernel!r}")
+    if kernel == "auto":
+        kernel = prefill_kernel(layout, Lq, B, D)
+        if out is not None and out.data_ptr() % 16 != 0:
+            kernel = "tile"
+    if kernel == "band":
+        return elastic_attention_band(q, k, v, layout.pattern, scaling, return_lse, out)
     q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
     o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
@@ -343,6 +372,26 @@ def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                  ctypes.c_void_p(st.col_idx.data_ptr()),
                                  ctypes.c_void_p(items.data_ptr()), n, _stream(q.device)),
           "esa_elastic_fwd")
+    return o, lse
+
+
+def elastic_attention_band(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                           pattern: EsaPattern, scaling: float, return_lse: bool = True,
+                           out: Optional[torch.Tensor] = None
+                           ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Band-gathered MFMA forward (prefill: query row r is position r), no
+    layout needed: each wave takes 16 query rows and, for every entry j of
+    their index lists, gathers the at most 16 consecutive keys those rows use
+    at entry j.  Returns ``o`` ``[B, Lq, H, D]`` and, if asked, ``lse``
+    float32 ``[B, H, Lq]``, as :func:`elastic_attention_fwd`."""
+    _check_qkv(q, k, v)
+    B, H, Lq, D = q.shape
+    q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
+    o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
+    lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
+    a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
+    check(load().esa_elastic_fwd_band(ctypes.byref(a), ctypes.byref(pattern), _stream(q.device)),
+          "esa_elastic_fwd_band")
     return o, lse
 
 
@@ -463,12 +512,12 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
 
 
 class _ElasticTileAttention(torch.autograd.Function):
-    """Prefill forward (block-sparse MFMA) with its block-sparse backward:
-    ``apply(q, k, v, layout, scaling) -> o [B, Lq, H, D]``."""
+    """Prefill forward (either kernel) with the block-sparse backward:
+    ``apply(q, k, v, layout, scaling, kernel) -> o [B, Lq, H, D]``."""
 
     @staticmethod
-    def forward(ctx, q, k, v, layout, scaling):
-        o, lse = elastic_attention_fwd(q, k, v, layout, scaling, return_lse=True)
+    def forward(ctx, q, k, v, layout, scaling, kernel="auto"):
+        o, lse = elastic_attention_fwd(q, k, v, layout, scaling, return_lse=True, kernel=kernel)
         ctx.save_for_backward(q, k, v, o, lse)
         ctx.layout = layout
         ctx.scaling = scaling
@@ -478,7 +527,7 @@ class _ElasticTileAttention(torch.autograd.Function):
     def backward(ctx, do):
         q, k, v, o, lse = ctx.saved_tensors
         dq, dk, dv = elastic_attention_bwd(q, k, v, o, lse, do, ctx.layout, ctx.scaling)
-        return dq, dk, dv, None, None
+        return dq, dk, dv, None, None, None
 
 
 class ElasticSparseAttentionFunction(torch.autograd.Function):
@@ -549,6 +598,8 @@ class ElasticSparseAttention(nn.Module):
         self._index_cache: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
         self._last_device: Optional[torch.device] = None
         self.full_attention_mask = None
+        # bf16 prefill kernel: "auto" (the faster for the shape), "band" or "tile"
+        self.prefill_kernel = "auto"
 
     # -- the reference's cached buffers, built on the GPU on first access --
     def _indices(self) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -609,10 +660,11 @@ class ElasticSparseAttention(nn.Module):
             if q.dtype == torch.bfloat16 and D in (64, 128):
                 if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or
                                                 v.requires_grad):
-                    o = _ElasticTileAttention.apply(q, k, v, self.layout(q.device), self.scaling)
+                    o = _ElasticTileAttention.apply(q, k, v, self.layout(q.device), self.scaling,
+                                                    self.prefill_kernel)
                     return o.reshape(B, Lq, H * D), None
                 o, _ = elastic_attention_fwd(q, k, v, self.layout(q.device), self.scaling,
-                                             return_lse=False)
+                                             return_lse=False, kernel=self.prefill_kernel)
             else:
                 o, _ = elastic_attention_rows(q, k, v, self.pattern, self.scaling, None,
                                               return_lse=False)

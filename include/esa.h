@@ -149,6 +149,23 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p,
                            const int32_t* items, int64_t num_items,
                            void* stream);
 
+/* Band-gathered forward over the elastic pattern, prefill rows 0 .. q_len-1
+ * (no layout needed).  Replaces the forward branch of the Triton kernel
+ * (elastic_sparse_attention.py:117-166) as _triton_forward launches it for
+ * prefill (:592-622), with each row's index list regenerated on the device
+ * (bit-exact with :470-535).  Entry j of the rows' index lists (a band)
+ * moves by at most one key per row (two at a few rows of some heads), so 16
+ * consecutive rows mostly use at most 16 consecutive keys of each band
+ * (wider bands are handled, more slowly):
+ * one wave gathers each band's keys once for its 16 rows and runs QK^T and
+ * PV on bf16 MFMA with float32 accumulation and online softmax.  Same
+ * outputs as esa_elastic_fwd within bf16 rounding.  Requires dtype
+ * ESA_BF16, head_dim 64 or 128, attention_length <= 64, kv_len < 2^24,
+ * (kv_len + 16) * K/V row stride * 2 < 2^31, row strides >= head_dim,
+ * q_len <= kv_len, q_len <= p->seq_len, finite sm_scale > 0, 16-byte
+ * aligned q, k, v, o and strides (elements) that are multiples of 8. */
+esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, void* stream);
+
 /* Per-row gather forward over the elastic pattern for arbitrary query
  * positions: row r of q is position positions[r] (int64 device array, as
  * cache_position, :602-608), or r when positions is NULL.  Replaces the

@@ -15,7 +15,8 @@ import torch
 from esa_oracle import (elastic_indices, forward_fp32, prepared_rows, scaling_for,
                         seeded_inputs)
 from elastic_sparse_attention import (ElasticLayout, ElasticSparseAttention,
-                                      ElasticSparseAttentionFunction, elastic_attention_fwd,
+                                      ElasticSparseAttentionFunction, elastic_attention_band,
+                                      elastic_attention_fwd, prefill_kernel,
                                       elastic_attention_rows, make_pattern,
                                       sparse_attention_fwd)
 
@@ -56,7 +57,7 @@ def test_tile_all_layers(D):
         q, k, v, idx, msk = case(B, H, H, L, D, torch.bfloat16, layer, seed=layer)
         sc = scaling_for(D)
         lay = ElasticLayout(make_pattern(L, w, layer, nl, H), DEV)
-        o, lse = elastic_attention_fwd(q.to(DEV), k.to(DEV), v.to(DEV), lay, sc)
+        o, lse = elastic_attention_fwd(q.to(DEV), k.to(DEV), v.to(DEV), lay, sc, kernel="tile")
         ro, rl = oracle(q, k, v, idx, msk, sc, 1)
         assert (to_bhsd(o).float().cpu() - ro).abs().max().item() <= BF16_TOL
         assert (lse.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
@@ -74,7 +75,7 @@ def test_tile_shapes(B, H, Hkv, L, Lq, D, layer):
     q, k, v, idx, msk = case(B, H, Hkv, L, D, torch.bfloat16, layer, seed=11, Lq=Lq)
     sc = scaling_for(D)
     lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
-    o, lse = elastic_attention_fwd(q.to(DEV), k.to(DEV), v.to(DEV), lay, sc)
+    o, lse = elastic_attention_fwd(q.to(DEV), k.to(DEV), v.to(DEV), lay, sc, kernel="tile")
     pi, pm = prepared_rows(idx, msk, Lq, L, L)
     ro, rl = oracle(q, k, v, pi, pm, sc, H // Hkv)
     assert (to_bhsd(o).float().cpu() - ro).abs().max().item() <= BF16_TOL
@@ -86,21 +87,24 @@ def test_tile_unit_variance_logits():
     q, k, v, idx, msk = case(1, 4, 4, 2048, 128, torch.bfloat16, 4, seed=5, scale=1.0)
     sc = scaling_for(128)
     lay = ElasticLayout(make_pattern(2048, 64, 4, 8, 4), DEV)
-    o, lse = elastic_attention_fwd(q.to(DEV), k.to(DEV), v.to(DEV), lay, sc)
+    o, lse = elastic_attention_fwd(q.to(DEV), k.to(DEV), v.to(DEV), lay, sc, kernel="tile")
     ro, rl = oracle(q, k, v, idx, msk, sc, 1)
     assert (to_bhsd(o).float().cpu() - ro).abs().max().item() <= BF16_TOL
     assert (lse.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
 
 
-def full_size_check(B, H, L, D, layer, scale, outlier, seed, n_rows=384):
-    print(f"full size B={B} H={H} L={L} D={D} layer={layer}", flush=True)
+def full_size_check(B, H, L, D, layer, scale, outlier, seed, n_rows=384, band=False):
+    print(f"full size B={B} H={H} L={L} D={D} layer={layer} band={band}", flush=True)
     q, k, v = seeded_inputs(B, H, H, L, D, torch.bfloat16, seed=seed, scale=scale,
                             outlier_frac=outlier)
     idx, msk = elastic_indices(L, layer, 8, H, 64)
     sc = scaling_for(D)
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
-    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
-    o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc)
+    if band:
+        o, lse = elastic_attention_band(qd, kd, vd, make_pattern(L, 64, layer, 8, H), sc)
+    else:
+        lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+        o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc, kernel="tile")
     g = torch.Generator().manual_seed(seed)
     rows = torch.cat([torch.tensor([0, 63, 64, 127, 128, L - 129, L - 1]),
                       torch.randint(0, L, (n_rows,), generator=g)]).unique()
@@ -135,13 +139,13 @@ def test_stage_layout_matches_tile_layout(B, H, Hkv, L, Lq, D, layer):
     assert lay.stages(64, 128).num_tiles <= 2 * lay.num_tiles
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
     o64, l64 = elastic_attention_fwd(qd, kd, vd, lay, scaling_for(D), key_block=64,
-                                     query_block=128)
+                                     query_block=128, kernel="tile")
     o128, l128 = elastic_attention_fwd(qd, kd, vd, lay, scaling_for(D), key_block=128,
-                                       query_block=128)
+                                       query_block=128, kernel="tile")
     assert torch.equal(o64, o128) and torch.equal(l64, l128)
     # 64-row items of two waves over 32-key stages
     o32, l32 = elastic_attention_fwd(qd, kd, vd, lay, scaling_for(D), key_block=32,
-                                     query_block=64)
+                                     query_block=64, kernel="tile")
     assert torch.equal(o32, o128) and torch.equal(l32, l128)
 
 
@@ -164,6 +168,99 @@ def test_full_size_batched_4k(layer):
 @pytest.mark.parametrize("layer", [0, 4, 7])
 def test_full_size_long_outliers_128k(layer):
     full_size_check(1, 8, 131072, 128, layer, 1.0, 0.01, seed=50 + layer, n_rows=128)
+
+
+# ---------------------------------------------------------------- band-gathered kernel
+@pytest.mark.parametrize("D", [128, 64])
+def test_band_all_layers(D):
+    B, H, L, w, nl = 1, 4, 1024, 64, 8
+    for layer in range(nl):
+        print(f"band D={D} layer={layer}", flush=True)
+        q, k, v, idx, msk = case(B, H, H, L, D, torch.bfloat16, layer, seed=layer + 3)
+        sc = scaling_for(D)
+        o, lse = elastic_attention_band(q.to(DEV), k.to(DEV), v.to(DEV),
+                                        make_pattern(L, w, layer, nl, H), sc)
+        ro, rl = oracle(q, k, v, idx, msk, sc, 1)
+        assert (to_bhsd(o).float().cpu() - ro).abs().max().item() <= BF16_TOL
+        assert (lse.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
+
+
+@pytest.mark.parametrize("B,H,Hkv,L,Lq,D,layer,w,nl", [
+    (2, 4, 2, 1000, 1000, 64, 3, 64, 8),    # GQA, partial last group
+    (1, 4, 4, 1024, 700, 128, 5, 64, 8),    # q_len < kv_len
+    (3, 2, 1, 777, 777, 128, 6, 64, 8),     # batch, MQA, ragged length
+    (1, 2, 2, 17, 17, 128, 4, 64, 8),       # one row past a group
+    (1, 2, 2, 5, 5, 64, 7, 64, 8),          # shorter than one group
+    (1, 3, 3, 1024, 1024, 128, 1, 64, 8),   # odd head count: bands of 17 keys
+    (1, 5, 5, 2048, 2048, 64, 4, 64, 8),    # odd head count, D = 64
+    (1, 3, 3, 1024, 1024, 128, 4, 48, 6),   # w = 48, wide bands
+    (1, 4, 4, 1024, 1024, 128, 2, 17, 4),   # w = 17
+    (1, 1, 1, 1024, 1024, 128, 5, 32, 8),   # one head (t = 0)
+])
+def test_band_shapes(B, H, Hkv, L, Lq, D, layer, w, nl):
+    print(f"band shape B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} layer={layer} w={w} nl={nl}",
+          flush=True)
+    q, k, v, idx, msk = case(B, H, Hkv, L, D, torch.bfloat16, layer, nl=nl, w=w, seed=13, Lq=Lq)
+    sc = scaling_for(D)
+    o, lse = elastic_attention_band(q.to(DEV), k.to(DEV), v.to(DEV),
+                                    make_pattern(L, w, layer, nl, H), sc)
+    pi, pm = prepared_rows(idx, msk, Lq, L, L)
+    ro, rl = oracle(q, k, v, pi, pm, sc, H // Hkv)
+    assert (to_bhsd(o).float().cpu() - ro).abs().max().item() <= BF16_TOL
+    assert (lse.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
+
+
+def test_band_sharp_softmax_outliers():
+    """N(0,1) inputs with x20 outlier channels: logits of std ~50 move the
+    running max often (the rescale path)."""
+    q, k, v, idx, msk = case(1, 4, 4, 2048, 128, torch.bfloat16, 4, seed=7, scale=1.0,
+                             outlier=0.01)
+    sc = scaling_for(128)
+    o, lse = elastic_attention_band(q.to(DEV), k.to(DEV), v.to(DEV),
+                                    make_pattern(2048, 64, 4, 8, 4), sc)
+    ro, rl = oracle(q, k, v, idx, msk, sc, 1)
+    assert (to_bhsd(o).float().cpu() - ro).abs().max().item() <= BF16_TOL
+    assert (lse.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
+
+
+@pytest.mark.parametrize("L,H,B,D,layer,want", [
+    (32768, 32, 1, 128, 4, "band"), (32768, 32, 1, 128, 0, "tile"), (8192, 32, 1, 128, 1, "tile"),
+    (8192, 32, 1, 128, 7, "band"), (4096, 16, 8, 64, 4, "tile"), (4096, 16, 8, 64, 7, "band"),
+])
+def test_prefill_kernel_choice(L, H, B, D, layer, want):
+    # the measured crossover: the band kernel where a group's rows stage many
+    # 64 x 32 blocks, the tile kernel where they stage few
+    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+    assert prefill_kernel(lay, L, B, D) == want
+
+
+def test_band_rejects_unsupported():
+    q = torch.zeros(1, 2, 64, 128, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError):
+        elastic_attention_band(q, q, q, make_pattern(64, 65, 3, 8, 2), 0.1)  # w > 64
+    with pytest.raises(ValueError):
+        elastic_attention_band(q.float(), q.float(), q.float(), make_pattern(64, 64, 3, 8, 2), 0.1)
+    qd = torch.zeros(1, 2, 64, 96, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError):
+        elastic_attention_band(qd, qd, qd, make_pattern(64, 64, 3, 8, 2), 0.1)
+
+
+@pytest.mark.parametrize("layer", [4, 7])
+def test_band_full_size_headline_32k(layer):
+    full_size_check(1, 32, 32768, 128, layer, 128 ** -0.25, 0.0, seed=60 + layer, n_rows=256,
+                    band=True)
+
+
+def test_band_full_size_8k():
+    full_size_check(1, 32, 8192, 128, 4, 128 ** -0.25, 0.0, seed=70, band=True)
+
+
+def test_band_full_size_batched_4k():
+    full_size_check(8, 16, 4096, 64, 7, 1.0, 0.0, seed=71, n_rows=128, band=True)
+
+
+def test_band_full_size_long_outliers_128k():
+    full_size_check(1, 8, 131072, 128, 4, 1.0, 0.01, seed=72, n_rows=128, band=True)
 
 
 # ---------------------------------------------------------------- per-row gather kernel
