@@ -1,0 +1,101 @@
+// Device helpers shared by the band-gathered kernels (gfx950): slot
+// layouts and swizzles, 16x16x32 MFMA, lane-group reductions, and each
+// row's index list as per-entry ("band") keys with the group's band
+// descriptors.
+//
+// MFMA 16x16x32 register layouts (gfx950):
+//   A[i][k]: lane l holds i = l%16, k = 8*(l/16) + e, e = 0..7
+//   B[k][j]: lane l holds k = 8*(l/16) + e, j = l%16
+//   C[i][j]: lane l, reg r holds i = 4*(l/16) + r, j = l%16
+// ds_read_b64_tr_b16 in each 16-lane group: lane g receives element r from
+// lane 4r + g/4's 8-byte chunk, element g%4.
+#pragma once
+#include "esa_tile.hpp"
+
+namespace esa {
+
+template <int D>
+struct BandCfg {
+  static constexpr int NS = D / 32;       // QK^T k-steps (32 dims each)
+  static constexpr int NV = D / 16;       // 16-dim slices of O^T
+  static constexpr int CW = D / 4;        // dims per lane group of an O row
+  static constexpr int CPR = D / 8;       // 16-byte chunks per K/V row
+  static constexpr int ROWB = 2 * D;      // bytes per row
+  static constexpr int SLOT = 16 * D;     // elements per V ring slot (16 rows)
+  static constexpr int VLOADS = 16 * CPR / 64;  // DMA instructions per band
+};
+
+// physical 16-byte chunk of logical chunk lc in row r of a V slot: the 16
+// lanes of a transposed read hit 16 distinct bank groups
+template <int D>
+__device__ __forceinline__ int vswz(int r, int lc) {
+  return D == 128 ? lc ^ (r & 3) : lc ^ ((r >> 1) & 1);
+}
+// the same for a K slot: 16 lanes reading one chunk of rows 0..15 hit 16
+// distinct bank groups
+template <int D>
+__device__ __forceinline__ int kswz(int r, int lc) {
+  return D == 128 ? lc ^ (r & 15) : lc ^ ((r >> 1) & 7);
+}
+
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// max over the 4 lanes l, l^16, l^32, l^48 (one row's lanes)
+__device__ __forceinline__ float row4_max(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  const float m1 = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m1), __float_as_uint(m1),
+                                                  false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// min / max over the 16 lanes of a lane group (DPP row rotations)
+__device__ __forceinline__ int row16_min(int v) {
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x122, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x121, 0xf, 0xf, false));
+  return v;
+}
+__device__ __forceinline__ int row16_max(int v) {
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x122, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x121, 0xf, 0xf, false));
+  return v;
+}
+
+
+// This lane's row i (of a 16-row group; lane group q holds entries
+// 16 q .. 16 q + 15): kreg[r] = the row's key of entry 16 q + r, or -1 when
+// the entry is masked (j >= w, idx > i) or the row is past q_len; and, the
+// same in every lane of group q, the group's band descriptors
+// info[r] = lo | W << 24, with lo / lo + W - 1 the smallest / largest valid
+// key of entry 16 q + r over the group's rows (W = 0: no row uses it).
+// lo < 2^24 (host check).
+__device__ __forceinline__ void band_rows(const PatternConsts& pc, int h, int i, bool row_ok,
+                                          int q, int (&kreg)[16], int (&info)[16]) {
+  const HeadWeights hw = head_weights(pc, h);
+  const RowParams rp = row_params(pc, i);
+  int o_cur = oversized(rp, 16 * q);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int j = 16 * q + r;
+    const int o_next = oversized(rp, j + 1);
+    const int idx = interp_index(o_cur, o_next, hw);
+    o_cur = o_next;
+    kreg[r] = (row_ok && j < pc.w && idx <= i) ? idx : -1;
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int lo = row16_min(kreg[r] < 0 ? 0x7fffffff : kreg[r]);
+    const int hi = row16_max(kreg[r]);
+    const int wdt = hi >= 0 ? min(hi - lo + 1, 255) : 0;
+    info[r] = hi >= 0 ? (lo | (wdt << 24)) : 0;
+  }
+}
+
+}  // namespace esa

@@ -576,6 +576,7 @@ hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
+  if (num_q_items < 0) return launch_band_dq(a, head_dim, lse2, stream);  // no work list
   if (num_q_items > 0) {
     if (head_dim == 128)
       dq_kernel<128><<<dim3((unsigned)num_q_items), 256, 0, stream>>>(a, lse2);

@@ -482,9 +482,12 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
     return ESA_ERR_NULL;
   esa_status s = check_pattern(p);
   if (s != ESA_OK) return s;
-  if (!row_ptr || !col_idx || !q_items || !tile_row || !kv_ptr || !kv_tiles || !kv_items ||
-      !mask_t || !workspace)
+  if (!row_ptr || !col_idx || !tile_row || !kv_ptr || !kv_tiles || !kv_items || !mask_t ||
+      !workspace)
     return ESA_ERR_NULL;
+  // q_items NULL: dQ by the band-gathered kernel (no work list)
+  const bool band_dq = q_items == nullptr;
+  if (band_dq && (p->attention_length > 64 || a->kv_len >= (1 << 24))) return ESA_ERR_UNSUPPORTED;
   if (a->dtype != ESA_BF16) return ESA_ERR_DTYPE;
   if (a->batch < 0 || a->num_heads < 1 || a->num_kv_heads < 1 || a->q_len < 0 || a->kv_len < 1 ||
       a->num_heads % a->num_kv_heads != 0 || a->num_heads != p->num_heads)
@@ -521,7 +524,8 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
   const LayoutDims d = dims_of(*p);
   const int nq = (a->q_len + 127) / 128;
   const int64_t n_real = (int64_t)a->batch * a->num_heads * nq;
-  if (num_q_items < n_real || num_q_items > 8 * std::max<int64_t>(n_real, 1)) return ESA_ERR_SHAPE;
+  if (!band_dq && (num_q_items < n_real || num_q_items > 8 * std::max<int64_t>(n_real, 1)))
+    return ESA_ERR_SHAPE;
   const int64_t kv_real = (int64_t)a->batch * a->num_kv_heads * d.nkb;
   if (num_kv_items < kv_real || num_kv_items > 8 * std::max<int64_t>(kv_real, 1))
     return ESA_ERR_SHAPE;
@@ -549,7 +553,15 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
   t.pc = make_consts(*p);
   t.row_ptr = row_ptr; t.col_idx = col_idx; t.q_items = q_items;
   t.tile_row = tile_row; t.kv_ptr = kv_ptr; t.kv_tiles = kv_tiles; t.kv_items = kv_items;
-  return hip_status(launch_tile_bwd(t, a->head_dim, num_q_items, num_kv_items, (hipStream_t)stream));
+  t.ng = (a->q_len + 15) / 16;
+  const int64_t n_groups = (int64_t)a->batch * a->num_heads * t.ng;
+  if (band_dq && n_groups > INT32_MAX / 2) return ESA_ERR_SHAPE;
+  t.n_groups = (int)n_groups;
+  t.per_xcd = (int)((n_groups + 7) / 8);
+  t.nrec_k = (int)((int64_t)a->kv_len * a->k_stride_s * 2);
+  t.nrec_v = (int)((int64_t)a->kv_len * a->v_stride_s * 2);
+  return hip_status(launch_tile_bwd(t, a->head_dim, band_dq ? -1 : num_q_items, num_kv_items,
+                                    (hipStream_t)stream));
 }
 
 esa_status esa_reachability(int32_t seq_len, int32_t attention_length,

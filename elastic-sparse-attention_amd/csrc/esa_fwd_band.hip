@@ -40,73 +40,10 @@
 // requested once this pair's K operands are in registers, its V once this
 // pair's PV has read V.
 //
-// MFMA 16x16x32 register layouts (gfx950):
-//   A[i][k]: lane l holds i = l%16, k = 8*(l/16) + e, e = 0..7
-//   B[k][j]: lane l holds k = 8*(l/16) + e, j = l%16
-//   C[i][j]: lane l, reg r holds i = 4*(l/16) + r, j = l%16
-// ds_read_b64_tr_b16 in each 16-lane group: lane g receives element r from
-// lane 4r + g/4's 8-byte chunk, element g%4.
-#include "esa_tile.hpp"
+// Operand layouts: esa_band.hpp.
+#include "esa_band.hpp"
 
 namespace esa {
-
-namespace {
-
-template <int D>
-struct BandCfg {
-  static constexpr int NS = D / 32;       // QK^T k-steps (32 dims each)
-  static constexpr int NV = D / 16;       // 16-dim slices of O^T
-  static constexpr int CW = D / 4;        // dims per lane group of an O row
-  static constexpr int CPR = D / 8;       // 16-byte chunks per K/V row
-  static constexpr int ROWB = 2 * D;      // bytes per row
-  static constexpr int SLOT = 16 * D;     // elements per V ring slot (16 rows)
-  static constexpr int VLOADS = 16 * CPR / 64;  // DMA instructions per band
-};
-
-// physical 16-byte chunk of logical chunk lc in row r of a V slot: the 16
-// lanes of a transposed read hit 16 distinct bank groups
-template <int D>
-__device__ __forceinline__ int vswz(int r, int lc) {
-  return D == 128 ? lc ^ (r & 3) : lc ^ ((r >> 1) & 1);
-}
-// the same for a K slot: 16 lanes reading one chunk of rows 0..15 hit 16
-// distinct bank groups
-template <int D>
-__device__ __forceinline__ int kswz(int r, int lc) {
-  return D == 128 ? lc ^ (r & 15) : lc ^ ((r >> 1) & 7);
-}
-
-__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// max over the 4 lanes l, l^16, l^32, l^48 (one row's lanes)
-__device__ __forceinline__ float row4_max(float v) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
-                                                  false);
-  const float m1 = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m1), __float_as_uint(m1),
-                                                  false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-
-// min / max over the 16 lanes of a lane group (DPP row rotations)
-__device__ __forceinline__ int row16_min(int v) {
-  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));
-  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xf, 0xf, false));
-  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x122, 0xf, 0xf, false));
-  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x121, 0xf, 0xf, false));
-  return v;
-}
-__device__ __forceinline__ int row16_max(int v) {
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x122, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x121, 0xf, 0xf, false));
-  return v;
-}
-
-}  // namespace
 
 // Band descriptor word: lo | W << 24 (W = keys from lo to the band's largest
 // valid key, 0 for a band no row of the group uses); lo < 2^24 (host check).
@@ -158,26 +95,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   // ---- this row's keys of bands 16 q .. 16 q + 15 (-1: no key), and the
   // group's band descriptors for the same bands (every lane of group q)
   int kreg[16], info[16];
-  {
-    const HeadWeights hw = head_weights(A.pc, h);
-    const RowParams rp = row_params(A.pc, i);
-    int o_cur = oversized(rp, 16 * q);
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int j = 16 * q + r;
-      const int o_next = oversized(rp, j + 1);
-      const int idx = interp_index(o_cur, o_next, hw);
-      o_cur = o_next;
-      kreg[r] = (row_ok && j < A.pc.w && idx <= i) ? idx : -1;
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int lo = row16_min(kreg[r] < 0 ? 0x7fffffff : kreg[r]);
-      const int hi = row16_max(kreg[r]);
-      const int wdt = hi >= 0 ? min(hi - lo + 1, 255) : 0;
-      info[r] = hi >= 0 ? (lo | (wdt << 24)) : 0;
-    }
-  }
+  band_rows(A.pc, h, i, row_ok, q, kreg, info);
 
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh), (short)0, A.nrec_k, 0x00020000);

@@ -115,6 +115,9 @@ struct BwdArgs {
   const int32_t* kv_ptr;    // [Hkv * nkb + 1]: tiles of each (kv head, key block)
   const int32_t* kv_tiles;  // layout tile ids, grouped by (kv head, key block)
   const int32_t* kv_items;  // dK/dV work list: (b * Hkv + kvh) * nkb + kb, -1 = idle
+  // band-gathered dQ (when q_items is NULL): 16-row groups per (b, h), all
+  // groups, groups per XCD range, bytes of one (b, kv head)'s K / V rows
+  int ng, n_groups, per_xcd, nrec_k, nrec_v;
 };
 
 hipError_t launch_indices(const PatternConsts& pc, int row0, int nrows, void* indices, void* mask,
@@ -124,6 +127,7 @@ hipError_t launch_layout(const PatternConsts& pc, const LayoutDims& ld, int32_t*
 hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
                            hipStream_t stream);
 hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream);
+hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2, hipStream_t stream);
 hipError_t launch_gather_fwd(const GatherArgs& a, bool f32, bool pattern, hipStream_t stream);
 hipError_t launch_tile_masks(const PatternConsts& pc, const int32_t* row_ptr, const int32_t* col_idx,
                              int nqb, int q_len, uint32_t* mask_t, hipStream_t stream);

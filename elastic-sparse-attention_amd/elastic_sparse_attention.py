@@ -458,14 +458,17 @@ def sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
 def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
                           lse: torch.Tensor, dout: torch.Tensor, layout: ElasticLayout,
-                          scaling: float) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Block-sparse MFMA backward of ``elastic_attention_fwd`` (prefill, bf16).
+                          scaling: float, dq_kernel: str = "auto"
+                          ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """MFMA backward of ``elastic_attention_fwd`` (prefill, bf16).
 
     ``o`` and ``dout`` are ``[B, Lq, H, D]`` (the forward's output layout),
     ``lse`` float32 ``[B, H, Lq]``.  Returns ``dq`` ``[B, H, Lq, D]`` and
     ``dk``, ``dv`` ``[B, Hkv, Lk, D]``: the gradients the reference's
     ElasticSparseAttentionFunction.backward returns (:299-339), computed
-    without atomics.
+    without atomics.  dK/dV run block-sparse over the layout; ``dq_kernel``
+    "band" computes dQ with the band-gathered kernel, "tile" block-sparse,
+    "auto" as the forward's kernel choice (:func:`prefill_kernel`).
     """
     _check_qkv(q, k, v)
     B, H, Lq, D = q.shape
@@ -497,13 +500,21 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
     ws = ctypes.c_size_t()
     check(lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(ws)), "esa_bwd_workspace_size")
     work = torch.empty(max(ws.value // 4, 4), dtype=torch.float32, device=q.device)
-    items, n_items = layout.schedule(Lq, B)
+    if dq_kernel not in ("auto", "tile", "band"):
+        raise ValueError(f"dq_kernel must be 'auto', 'tile' or 'band', got {dq_kernel!r}")
+    if dq_kernel == "auto":
+        dq_kernel = prefill_kernel(layout, Lq, B, D)
+    if dq_kernel == "band":
+        items, n_items = None, 0   # no work list: the band kernel covers every row group
+    else:
+        items, n_items = layout.schedule(Lq, B)
     tile_row, kv_ptr, kv_tiles, kv_items, n_kv = layout.bwd_plan(Lq, B, Hkv)
     masks = layout.tile_masks(Lq)
     vp = ctypes.c_void_p
     check(lib.esa_elastic_bwd(ctypes.byref(a), ctypes.byref(layout.pattern),
                               vp(layout.row_ptr.data_ptr()), vp(layout.col_idx.data_ptr()),
-                              vp(items.data_ptr()), n_items, vp(tile_row.data_ptr()),
+                              vp(items.data_ptr() if items is not None else None), n_items,
+                              vp(tile_row.data_ptr()),
                               vp(kv_ptr.data_ptr()), vp(kv_tiles.data_ptr()),
                               vp(kv_items.data_ptr()), n_kv, vp(masks.data_ptr()),
                               vp(work.data_ptr()), work.numel() * 4, _stream(q.device)),

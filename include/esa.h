@@ -259,13 +259,16 @@ esa_status esa_build_tile_masks(const esa_pattern* p, const int32_t* row_ptr,
  * (2 * batch * num_heads * q_len floats). */
 esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes);
 
-/* Block-sparse backward over the elastic pattern: replaces the backward
- * branch of the Triton kernel (elastic_sparse_attention.py:168-233) and
+/* Backward over the elastic pattern: replaces the backward branch of the
+ * Triton kernel (elastic_sparse_attention.py:168-233) and
  * ElasticSparseAttentionFunction.backward (:299-339) for the prefill
- * forward of esa_elastic_fwd.  Writes dq, dk and dv (every element; no
+ * forward (esa_elastic_fwd or esa_elastic_fwd_band: any O and LSE of it).  Writes dq, dk and dv (every element; no
  * zero-initialisation needed, no atomics: each gradient row is accumulated
  * by one workgroup in a fixed order, so results are deterministic).
- * q_items/num_q_items: esa_plan_schedule's list for (q_len, batch);
+ * q_items/num_q_items: esa_plan_schedule's list for (q_len, batch), for a
+ * block-sparse dQ; q_items NULL computes dQ with the band-gathered kernel
+ * instead (as esa_elastic_fwd_band gathers: attention_length <= 64,
+ * kv_len < 2^24; num_q_items is ignored);
  * tile_row, kv_ptr, kv_tiles, kv_items/num_kv_items: esa_plan_bwd's;
  * mask_t: esa_build_tile_masks' for this q_len (all device memory).
  * Requires dtype ESA_BF16, head_dim 64 or 128, block 128 x 128, a finite

@@ -32,6 +32,7 @@ def rel_err(got, ref):
     return ((got.float().cpu() - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
 
 
+@pytest.mark.parametrize("dq_kernel", ["tile", "band"])
 @pytest.mark.parametrize("B,H,Hkv,L,Lq,D,layer", [
     (1, 4, 4, 1024, 1024, 128, 4),
     (1, 4, 4, 1024, 1024, 128, 0),
@@ -40,9 +41,11 @@ def rel_err(got, ref):
     (2, 8, 2, 640, 640, 128, 5),     # GQA, batch
     (1, 4, 4, 1000, 700, 128, 6),    # q_len < kv_len, ragged blocks
     (1, 2, 1, 200, 200, 64, 2),      # MQA, short
+    (1, 3, 3, 1024, 1024, 128, 1),   # odd head count: bands of 17 keys (band dQ tail)
 ])
-def test_backward_matches_autograd(B, H, Hkv, L, Lq, D, layer):
-    print(f"bwd B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} layer={layer}", flush=True)
+def test_backward_matches_autograd(B, H, Hkv, L, Lq, D, layer, dq_kernel):
+    print(f"bwd B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} layer={layer} dq={dq_kernel}",
+          flush=True)
     q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=layer + 3, scale=1.0, Lq=Lq)
     idx, msk = elastic_indices(L, layer, 8, H, 64)
     pi, pm = prepared_rows(idx, msk, Lq, L, L)
@@ -54,13 +57,13 @@ def test_backward_matches_autograd(B, H, Hkv, L, Lq, D, layer):
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
     o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc)
     do = g.to(DEV).permute(0, 2, 1, 3).contiguous()  # [B, Lq, H, D] like o
-    dq, dk, dv = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc)
+    dq, dk, dv = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel=dq_kernel)
     e = (rel_err(dq, rq), rel_err(dk, rk), rel_err(dv, rv))
     print(f"  rel err dq {e[0]:.3e} dk {e[1]:.3e} dv {e[2]:.3e}", flush=True)
     assert all(torch.isfinite(t.float()).all() for t in (dq, dk, dv))
     assert max(e) <= REL
     # deterministic: a second run is bit-identical
-    dq2, dk2, dv2 = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc)
+    dq2, dk2, dv2 = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel=dq_kernel)
     assert torch.equal(dq, dq2) and torch.equal(dk, dk2) and torch.equal(dv, dv2)
 
 
@@ -137,3 +140,26 @@ def test_backward_identities_full_size(B, H, Hkv, L, D, layer):
     # measured about 1e-4 at these shapes; a dropped delta term, a wrong lse
     # or a wrong scale gives ratios of order one
     assert r_v <= 1e-3 and r_k <= 1e-3
+
+
+@pytest.mark.parametrize("layer", [4, 7])
+def test_band_dq_matches_tile_dq_full_size(layer):
+    """The headline shape: dQ from the band kernel against dQ from the
+    block-sparse kernel (two independent paths over the same O and LSE),
+    max |difference| <= 2e-2 * max |dQ|."""
+    B, H, L, D = 1, 32, 32768, 128
+    print(f"band dq vs tile dq B={B} H={H} L={L} D={D} layer={layer}", flush=True)
+    q, k, v = seeded_inputs(B, H, H, L, D, torch.bfloat16, seed=110 + layer, scale=D ** -0.25)
+    sc = scaling_for(D)
+    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc)
+    do = torch.randn(B, L, H, D, generator=torch.Generator().manual_seed(layer))
+    do = do.to(torch.bfloat16).to(DEV)
+    dq_t, dk_t, dv_t = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="tile")
+    dq_b, dk_b, dv_b = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="band")
+    assert bool(torch.isfinite(dq_b.float()).all())
+    r = ((dq_b.float() - dq_t.float()).abs().max() / dq_t.float().abs().max()).item()
+    print(f"  max|dq band - dq tile| / max|dq| {r:.3e}", flush=True)
+    assert r <= REL
+    assert torch.equal(dk_t, dk_b) and torch.equal(dv_t, dv_b)
