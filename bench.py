@@ -18,7 +18,9 @@ launch stream).  The kernels issue far fewer MFMA flops than that: the tile
 kernel only the 32 x 32 blocks of an active tile that hold a valid key for
 one of a wave's rows, the band kernel 16 keys x 16 rows per entry of the
 rows' index lists; executed_flop_fraction and executed_mfma_tflops report
-that work.  cpu_baseline times the reference's
+that work.  What bounds both at dilated layers is the K/V they gather from
+L2: l2_to_cu gives those bytes (from the committed rocprofv3 summary) over
+the kernel's time, against the L2 -> CU rate a copy kernel reaches.  cpu_baseline times the reference's
 PyTorch fallback (_naive_forward, restated in oracle/) on the host cores on a
 bounded sample of query rows of the same workload, extrapolated linearly
 (every row costs the same w-key gather there).
@@ -155,17 +157,24 @@ def band_executed_flops(B: int, H: int, L: int, D: int, w: int) -> float:
     return float(B * H * pairs * (2 * (D // 32) + D // 16) * 16384)
 
 
-def traffic_from_profile(name: str):
-    """HBM bytes per launch of the forward kernel, from the committed rocprofv3
-    --pmc summary for this workload (profiles/<name>), or None."""
+def figure_from_profile(name: str, key: str = "traffic_bytes_per_launch"):
+    """A per-launch figure of the forward kernel (HBM bytes by default) from
+    the committed rocprofv3 --pmc summary for this workload
+    (profiles/<name>), or None."""
     path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     with open(path) as f:
         for line in f:
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith(key + ":"):
                 return int(float(line.split(":", 1)[1].strip()))
     return None
+
+
+# L2 -> CU streaming rate of MI355X measured with a copy kernel reading 4 KB
+# row blocks from an L2-resident buffer (buffer_load ... lds or into
+# registers, 4-10 waves per CU): the ceiling of the gather-bound forwards
+L2_TO_CU_TBS = 36.0
 
 
 def main() -> None:
@@ -255,8 +264,9 @@ def main() -> None:
         executed = B * executed_blocks(torch, lay, L) * 4.0 * 32 * 32 * D
     else:
         executed = band_executed_flops(B, H, L, D, W)
-    traffic = traffic_from_profile(
-        f"{kernel}_fwd_kernel_bf16_B{B}_H{H}_L{L}_D{D}_layer{args.layer}_pmc.md")
+    prof = f"{kernel}_fwd_kernel_bf16_B{B}_H{H}_L{L}_D{D}_layer{args.layer}_pmc.md"
+    traffic = figure_from_profile(prof)
+    l2_bytes = figure_from_profile(prof, "l2_to_cu_bytes_per_launch")
     if args.layer == 0:
         # a plain sliding window: ~127 flop/B, below the MFMA ridge -> HBM-bound
         gbs = alg_bytes / (kern_ms * 1e-3) / 1e9
@@ -296,6 +306,12 @@ def main() -> None:
         "roofline": roofline,
         "cpu_baseline": None,
     }
+    if l2_bytes is not None:
+        # what bounds the kernel at dilated layers: bytes it gathers from L2
+        # (profiled) over its measured time, against the probe's ceiling
+        tbs = l2_bytes / (kern_ms * 1e-3) / 1e12
+        out["l2_to_cu"] = {"achieved": round(tbs, 2), "ceiling": L2_TO_CU_TBS, "unit": "TB/s",
+                           "frac": round(tbs / L2_TO_CU_TBS, 4), "bytes": l2_bytes}
     if args.backward:
         out["backward"] = time_backward(torch, m, q, k, v, lay, counted, args.steps, args.warmup)
     if not args.no_cpu:
