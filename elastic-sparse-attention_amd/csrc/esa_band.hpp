@@ -14,6 +14,8 @@
 
 namespace esa {
 
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+
 template <int D>
 struct BandCfg {
   static constexpr int NS = D / 32;       // QK^T k-steps (32 dims each)

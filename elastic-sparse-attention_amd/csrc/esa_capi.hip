@@ -354,8 +354,6 @@ esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, voi
   t.ng = ng;
   t.n_groups = (int)n_groups;
   t.per_xcd = (int)((n_groups + 7) / 8);
-  t.nrec_k = (int)((int64_t)a->kv_len * a->k_stride_s * 2);
-  t.nrec_v = (int)((int64_t)a->kv_len * a->v_stride_s * 2);
   t.scale_log2 = a->sm_scale * 1.4426950408889634f;
   t.pc = make_consts(*p);
   return hip_status(launch_band_fwd(t, a->head_dim, (hipStream_t)stream));
@@ -558,8 +556,6 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
   if (band_dq && n_groups > INT32_MAX / 2) return ESA_ERR_SHAPE;
   t.n_groups = (int)n_groups;
   t.per_xcd = (int)((n_groups + 7) / 8);
-  t.nrec_k = (int)((int64_t)a->kv_len * a->k_stride_s * 2);
-  t.nrec_v = (int)((int64_t)a->kv_len * a->v_stride_s * 2);
   return hip_status(launch_tile_bwd(t, a->head_dim, band_dq ? -1 : num_q_items, num_kv_items,
                                     (hipStream_t)stream));
 }

@@ -97,28 +97,40 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   int kreg[16], info[16];
   band_rows(A.pc, h, i, row_ok, q, kreg, info);
 
-  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh), (short)0, A.nrec_k, 0x00020000);
-  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh), (short)0, A.nrec_v, 0x00020000);
+  const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
+  const char* const vbase = (const char*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh);
   const int kss2 = (int)A.kss * 2, vss2 = (int)A.vss * 2;
+  // LDS pointers of the slots, formed once (the DMA takes LDS addresses)
+  lds_u16* const lk0 = (lds_u16*)ks0;
+  lds_u16* const lk1 = (lds_u16*)ks1;
+  lds_u16* const lv0 = (lds_u16*)vs0;
+  lds_u16* const lv1 = (lds_u16*)vs1;
 
-  // K or V rows of band info word `bi` -> slot dst: DMA t, lane l fills row
-  // R = (64 t + l) / CPR, physical chunk l % CPR; rows past the band read as
-  // zeros (offset past num_records).  A fixed number of loads per band keeps
-  // the vmcnt waits below exact.
-  auto load_rows = [&](__amdgpu_buffer_rsrc_t rs, int ss2, int nrec, bool is_k, int bi,
-                       uint16_t* dst) {
-    const int lo = bi & 0xffffff, wdt = (int)((uint32_t)bi >> 24);
+  // DMA t, lane l fills slot row R = (64 t + l) / CPR, physical chunk
+  // l % CPR: its byte offset from the band's first row, fixed per lane
+  int kofs[C::VLOADS], vofs[C::VLOADS];
 #pragma unroll
-    for (int t = 0; t < C::VLOADS; ++t) {
-      const int R = (64 * t + lane) / C::CPR, pc = lane % C::CPR;
-      const int lc = is_k ? kswz<D>(R, pc) : vswz<D>(R, pc);
-      load_lds16(rs, dst + 512 * t, R < wdt ? (lo + R) * ss2 + 16 * lc : nrec, 0);
-    }
+  for (int t = 0; t < C::VLOADS; ++t) {
+    const int R = (64 * t + lane) / C::CPR, pc = lane % C::CPR;
+    kofs[t] = R * kss2 + 16 * kswz<D>(R, pc);
+    vofs[t] = R * vss2 + 16 * vswz<D>(R, pc);
+  }
+  // K or V rows of band info word `bi` -> slot dst, through a buffer resource
+  // that starts at the band's first row and holds its W rows: rows past the
+  // band fall outside num_records and read as zeros without a fetch.  A
+  // fixed number of loads per band keeps the vmcnt waits below exact.
+  auto load_rows = [&](const char* base, int ss2, const int* ofs, int bi,
+                       lds_u16* dst) {
+    const int lo = bi & 0xffffff, wdt = (int)((uint32_t)bi >> 24);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(base + (int64_t)lo * ss2), (short)0, min(wdt, 16) * ss2, 0x00020000);
+#pragma unroll
+    for (int t = 0; t < C::VLOADS; ++t)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + 512 * t), 16, ofs[t], 0, 0,
+                                               0);
   };
-  auto load_k = [&](int bi, uint16_t* dst) { load_rows(krs, kss2, A.nrec_k, true, bi, dst); };
-  auto load_v = [&](int bi, uint16_t* dst) { load_rows(vrs, vss2, A.nrec_v, false, bi, dst); };
+  auto load_k = [&](int bi, lds_u16* dst) { load_rows(kbase, kss2, kofs, bi, dst); };
+  auto load_v = [&](int bi, lds_u16* dst) { load_rows(vbase, vss2, vofs, bi, dst); };
 
   // K operand read addresses (bytes within a slot) for k-step s: lane
   // (m = n, q) reads key row n, dims 32 s + 8 q .. + 8
@@ -234,10 +246,10 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     const int i0 = __builtin_amdgcn_readlane(info[0], 0);
     const int i1 = __builtin_amdgcn_readlane(info[1], 0);
     __builtin_amdgcn_s_waitcnt(kWaitLds);  // the slot zeros are in LDS
-    load_k(i0, ks0);
-    load_k(i1, ks1);
-    load_v(i0, vs0);
-    load_v(i1, vs1);
+    load_k(i0, lk0);
+    load_k(i1, lk1);
+    load_v(i0, lv0);
+    load_v(i1, lv1);
   }
   for (int qj = 0; qj < 4; ++qj) {
     const bool more = qj < 3;
@@ -263,8 +275,8 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
         read_k(ks1, kopb);
       }
       __builtin_amdgcn_s_waitcnt(kWaitLds);  // K slots read: refill them
-      load_k(na, ks0);
-      load_k(nb, ks1);
+      load_k(na, lk0);
+      load_k(nb, lk1);
       if (live) {
         const int addr = lane_key + 64 * qj;
         const int keya = __builtin_amdgcn_ds_bpermute(addr, kreg[ra]);
@@ -282,8 +294,8 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
       }
       // this pair's V has landed (and been read): refill the V slots
       __builtin_amdgcn_s_waitcnt(kWaitPair & kWaitLds);
-      load_v(na, vs0);
-      load_v(nb, vs1);
+      load_v(na, lv0);
+      load_v(nb, lv1);
     }
   }
 
@@ -307,8 +319,8 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
       const int rem = lo + wdt - c0;
       const int ci = c0 | (min(rem, 16) << 24);
       __builtin_amdgcn_s_waitcnt(kWaitLds);  // earlier reads of slots 0 done
-      load_k(ci, ks0);
-      load_v(ci, vs0);
+      load_k(ci, lk0);
+      load_v(ci, lv0);
       __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
       bf16x8 kt[C::NS];
       read_k(ks0, kt);

@@ -52,8 +52,7 @@ struct BandArgs {
   int ng;        // 16-row groups per (batch, head)
   int n_groups;  // batch * H * ng
   int per_xcd;   // groups per XCD range
-  int nrec_k, nrec_v;  // bytes of one (batch, kv head)'s kv_len K / V rows
-  float scale_log2;    // sm_scale * log2(e)
+  float scale_log2;  // sm_scale * log2(e)
   PatternConsts pc;
 };
 
@@ -116,8 +115,8 @@ struct BwdArgs {
   const int32_t* kv_tiles;  // layout tile ids, grouped by (kv head, key block)
   const int32_t* kv_items;  // dK/dV work list: (b * Hkv + kvh) * nkb + kb, -1 = idle
   // band-gathered dQ (when q_items is NULL): 16-row groups per (b, h), all
-  // groups, groups per XCD range, bytes of one (b, kv head)'s K / V rows
-  int ng, n_groups, per_xcd, nrec_k, nrec_v;
+  // groups, groups per XCD range
+  int ng, n_groups, per_xcd;
 };
 
 hipError_t launch_indices(const PatternConsts& pc, int row0, int nrows, void* indices, void* mask,
