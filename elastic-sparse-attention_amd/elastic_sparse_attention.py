@@ -313,7 +313,7 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
 # kernel costs about the same per 16-row group at every layer, the tile
 # kernel about the same per staged 64 x 32 block, and the band kernel is the
 # faster one once a group's rows stage more than this many blocks.
-BAND_CROSSOVER = {128: 19.0, 64: 13.0}
+BAND_CROSSOVER = {128: 16.5, 64: 12.5}
 
 
 def prefill_kernel(layout: ElasticLayout, q_len: int, batch: int, head_dim: int) -> str:

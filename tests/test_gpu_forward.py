@@ -224,8 +224,8 @@ def test_band_sharp_softmax_outliers():
 
 
 @pytest.mark.parametrize("L,H,B,D,layer,want", [
-    (32768, 32, 1, 128, 4, "band"), (32768, 32, 1, 128, 0, "tile"), (8192, 32, 1, 128, 1, "tile"),
-    (8192, 32, 1, 128, 7, "band"), (4096, 16, 8, 64, 4, "tile"), (4096, 16, 8, 64, 7, "band"),
+    (32768, 32, 1, 128, 4, "band"), (32768, 32, 1, 128, 0, "tile"), (8192, 32, 1, 128, 3, "tile"),
+    (8192, 32, 1, 128, 4, "band"), (4096, 16, 8, 64, 5, "tile"), (4096, 16, 8, 64, 6, "band"),
 ])
 def test_prefill_kernel_choice(L, H, B, D, layer, want):
     # the measured crossover: the band kernel where a group's rows stage many
