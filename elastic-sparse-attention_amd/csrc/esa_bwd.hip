@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void prep_kernel(BwdArgs A, float* lse2) {
 #pragma unroll
   for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
   if (row < A.q_len && g == 0) {
-    const int64_t at = ((int64_t)b * A.H + h) * A.q_len + row;
+    const int64_t at = ((int64_t)b * A.H + h) * A.qpad + row;
     A.delta[at] = acc;
     // kept finite: masked scores enter as -inf, and -inf - (-inf) would be NaN
     lse2[at] = fmaxf(A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + row] * 1.4426950408889634f,
@@ -211,7 +211,7 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs A, const float* ls
       load_lds16(ors, od + (QLOADS * wave + j) * 512, ooff[j], os_);
     }
     if (wave < 2) {
-      const float* src = (wave == 0 ? lse2 : A.delta) + ((int64_t)b * A.H + h) * A.q_len;
+      const float* src = (wave == 0 ? lse2 : A.delta) + ((int64_t)b * A.H + h) * A.qpad;
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           (void*)src, (short)0, A.q_len * 4, 0x00020000);
       load_lds4(rs, wave == 0 ? ld : dd, lane * 4, r0 * 4);
@@ -421,7 +421,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2
   }
   float l2 = 0.f, dl = 0.f;
   if (row_ok) {
-    const int64_t at = ((int64_t)b * A.H + h) * A.q_len + i;
+    const int64_t at = ((int64_t)b * A.H + h) * A.qpad + i;
     l2 = lse2[at];
     dl = A.delta[at];
   }
@@ -560,7 +560,7 @@ hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,
                            int64_t num_kv_items, hipStream_t stream) {
   if (a.q_len <= 0 || a.B <= 0) return hipSuccess;
   // lse in log2 units goes in the second half of the delta workspace
-  float* lse2 = a.delta + (int64_t)a.B * a.H * a.q_len;
+  float* lse2 = a.delta + (int64_t)a.B * a.H * a.qpad;
   dim3 pg((unsigned)((a.q_len + 15) / 16), (unsigned)a.H, (unsigned)a.B);
   if (head_dim == 128)
     prep_kernel<128><<<pg, 256, 0, stream>>>(a, lse2);
@@ -568,7 +568,10 @@ hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,
     prep_kernel<64><<<pg, 256, 0, stream>>>(a, lse2);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (num_kv_items > 0) {
+  if (num_kv_items < 0) {  // no work list: band-gathered dK / dV
+    e = launch_band_dkdv(a, head_dim, lse2, stream);
+    if (e != hipSuccess) return e;
+  } else if (num_kv_items > 0) {
     if (head_dim == 128)
       dkdv_kernel<128><<<dim3((unsigned)num_kv_items), 512, 0, stream>>>(a, lse2);
     else

@@ -1,6 +1,6 @@
-// Band-gathered dQ of the elastic prefill backward (gfx950).
+// Band-gathered dQ and dK / dV of the elastic prefill backward (gfx950).
 //
-// Replaces the dQ half of the reference's Triton backward
+// band_dq_kernel replaces the dQ half of the reference's Triton backward
 // (elastic_sparse_attention.py:168-233) the way band_fwd_kernel replaces the
 // forward: one wave per 16 query rows (a group); for each entry j of the
 // rows' index lists (a band) the keys [lo_j, lo_j + 16) are staged in LDS
@@ -18,8 +18,9 @@
 //
 // dQ = scale * dQ^T^T.  Each row's key of a band is selected in exactly one
 // chunk (bands wider than 16 keys get a tail pass), so every valid (row,
-// key) pair contributes once, as in :191-228; dK and dV come from
-// dkdv_kernel (esa_bwd.hip).  Operand layouts: esa_band.hpp.
+// key) pair contributes once, as in :191-228.  band_dkdv_kernel (below) is
+// the key-major counterpart for dK and dV; dkdv_kernel (esa_bwd.hip) is the
+// block-sparse one.  Operand layouts: esa_band.hpp.
 #include "esa_band.hpp"
 
 namespace esa {
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   }
   float l2 = 0.f, dl = 0.f;
   if (row_ok) {
-    const int64_t at = ((int64_t)b * A.H + h) * A.q_len + i;
+    const int64_t at = ((int64_t)b * A.H + h) * A.qpad + i;
     l2 = lse2[at];
     dl = A.delta[at];
   }
@@ -294,6 +295,308 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
       *(bf16x8*)(dqr + C::CW * q + 8 * t) = ov;
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// Band-gathered dK / dV: one wave per (batch, kv head, 16-key block
+// [u0, u0 + 16)).  Entry j's key is nondecreasing in the row (the window
+// start, the spacing and both interpolated terms of the recipe never
+// decrease), so for each query head of the kv group and each entry j the
+// rows whose key of entry j lies in the block form one range; lane j finds
+// it by binary search.  The ranges are walked 32 rows at a time (starts
+// rounded down to a multiple of 4; the extra rows are masked): Q and dO rows
+// staged in LDS (buffer_load ... lds, rows past the range read as zeros),
+// then
+//   S = Q K^T, dP = dO V^T   2 x D/32 MFMAs each (A = Q / dO rows from LDS,
+//                            B = the block's K / V in registers)
+//   P = exp2(S scale log2e - lse2), dS = P (dP - delta) on the (row, key)
+//   pairs where the key is the row's entry j and not past the row (one key
+//   per row)
+//   dV^T += dO^T P, dK^T += Q^T dS   D/16 MFMAs each over the 32 rows (A =
+//                            dO^T / Q^T read transposed from the same slots)
+// dK = scale dK^T^T.  Each (row, entry) pair lands in exactly one block and
+// one step, as in the reference's dK/dV loop (:168-233 accumulates the same
+// pairs); every gradient row is accumulated by one wave in a fixed order:
+// deterministic, no atomics.  A block's work is the number of rows using its
+// keys: low blocks of late layers are the heaviest, so blocks go to the
+// eight XCDs in chunks of kBlkChunk consecutive blocks, round robin (each
+// XCD starts with its heaviest chunk and keeps neighbouring blocks, which
+// share rows, in one L2).
+constexpr int kBlkChunk = 8;
+
+template <int D>
+__global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float* lse2) {
+  using C = BandCfg<D>;
+  constexpr int ROWS = 32;                // query rows per step
+  constexpr int SLOT2 = ROWS * D;         // elements per Q or dO slot
+  constexpr int SL = ROWS * C::CPR / 64;  // DMA instructions per slot
+  __shared__ __attribute__((aligned(1024))) uint16_t qsl[SLOT2];
+  __shared__ __attribute__((aligned(1024))) uint16_t osl[SLOT2];
+  lds_u16* const lq = (lds_u16*)qsl;
+  lds_u16* const lo = (lds_u16*)osl;
+
+  // ---- block: slot k of XCD x takes block (k / chunk * 8 + x) * chunk + k % chunk
+  const int bid = blockIdx.x;
+  const int kx = bid >> 3;
+  const int g = ((kx / kBlkChunk) * 8 + (bid & 7)) * kBlkChunk + kx % kBlkChunk;
+  if (g >= A.n_kblk) return;
+  const int bkv = g / A.nkb16, kb = g % A.nkb16;
+  const int kvh = bkv % A.Hkv, b = bkv / A.Hkv;
+  const int u0 = 16 * kb;
+
+  const int lane = threadIdx.x;
+  const int n = lane & 15, q = lane >> 4;
+  const int key = u0 + n;
+  const bool key_ok = key < A.kv_len;
+
+  // the block's K and V as B operands: key n, dims 32 s + 8 q .. + 8
+  bf16x8 kop[C::NS], vop[C::NS];
+  {
+    const uint16_t* kr = A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh + (int64_t)key * A.kss;
+    const uint16_t* vr = A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh + (int64_t)key * A.vss;
+#pragma unroll
+    for (int s = 0; s < C::NS; ++s) {
+      u32x4 kraw = {0u, 0u, 0u, 0u}, vraw = {0u, 0u, 0u, 0u};
+      if (key_ok) {
+        kraw = *(const u32x4*)(kr + 32 * s + 8 * q);
+        vraw = *(const u32x4*)(vr + 32 * s + 8 * q);
+      }
+      kop[s] = __builtin_bit_cast(bf16x8, kraw);
+      vop[s] = __builtin_bit_cast(bf16x8, vraw);
+    }
+  }
+
+  const int qss2 = (int)A.qss * 2, oss2 = (int)A.doss * 2;
+  // DMA t, lane l fills slot row R = (64 t + l) / CPR, physical chunk l % CPR
+  int qofs[SL], oofs[SL];
+#pragma unroll
+  for (int t = 0; t < SL; ++t) {
+    const int R = (64 * t + lane) / C::CPR, pc = lane % C::CPR;
+    qofs[t] = R * qss2 + 16 * kswz<D>(R, pc);
+    oofs[t] = R * oss2 + 16 * kswz<D>(R, pc);
+  }
+  // row reads (A operand of S and dP) of chunk c (slot rows 16 c .. + 15):
+  // lane (m = n, q) reads slot row 16 c + n, dims 32 s + 8 q .. + 8
+  int rrd[C::NS];
+#pragma unroll
+  for (int s = 0; s < C::NS; ++s) rrd[s] = n * C::ROWB + 16 * kswz<D>(n, 4 * s + q);
+  // transposed reads (A operand of dV^T, dK^T) for slice s of chunk c: lane
+  // x of its 16-lane group reads slot row 16 c + 4 q + x/4, dims
+  // CW (x%4) + 4 s .. + 3 (the swizzle of row 16 c + r is that of row r)
+  int trd[C::NV];
+#pragma unroll
+  for (int s = 0; s < C::NV; ++s) {
+    const int R = 4 * q + (n >> 2), dim0 = C::CW * (n & 3) + 4 * s;
+    trd[s] = R * C::ROWB + 16 * kswz<D>(R, dim0 >> 3) + 2 * (dim0 & 7);
+  }
+  constexpr int CHB = 16 * C::ROWB;  // bytes of one 16-row chunk
+
+  f32x4 dkacc[C::NV], dvacc[C::NV];
+#pragma unroll
+  for (int s = 0; s < C::NV; ++s) dkacc[s] = dvacc[s] = f32x4{};
+  const float scale2 = A.scale_log2;
+  constexpr int kWaitLds = 0xC07F;  // lgkmcnt(0)
+  // vmcnt(SL): before a slot's reads at most one slot's DMA (and the step's
+  // lse2 / delta loads, issued before it or not at all) is newer; loads
+  // complete in order, so at most SL outstanding leaves the slot filled
+  constexpr int kWaitSlot = (0xF70 & ~0xF) | (SL & 0xF) | ((SL >> 4) << 14);
+
+  for (int hg = 0; hg < A.groups; ++hg) {
+    const int h = kvh * A.groups + hg;
+    const HeadWeights hw = head_weights(A.pc, h);
+    auto key_at = [&](int i, int j) {
+      const RowParams rp = row_params(A.pc, i);
+      return interp_index(oversized(rp, j), oversized(rp, j + 1), hw);
+    };
+    // lane j: rows [r0, r1] whose key of entry j lies in the block (rows
+    // before u0 cannot use a key >= u0)
+    int r0 = 0, r1 = -1;
+    if (lane < A.pc.w) {
+      int a0 = u0, a1 = A.q_len;  // first row >= u0 with key >= u0
+      while (a0 < a1) {
+        const int mid = (a0 + a1) >> 1;
+        if (key_at(mid, lane) >= u0) a1 = mid; else a0 = mid + 1;
+      }
+      int c0 = a0, c1 = A.q_len;  // first row with key >= u0 + 16
+      while (c0 < c1) {
+        const int mid = (c0 + c1) >> 1;
+        if (key_at(mid, lane) >= u0 + 16) c1 = mid; else c0 = mid + 1;
+      }
+      if (a0 < c0) {
+        r0 = a0 & ~3;
+        r1 = c0 - 1;
+      }
+    }
+    const uint64_t live = __builtin_amdgcn_ballot_w64(r0 <= r1);
+    if (live == 0ull) continue;
+
+    const char* const qbase = (const char*)(A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh);
+    const char* const obase = (const char*)(A.dout + (int64_t)b * A.dosb + (int64_t)h * A.dosh);
+    const float* const l2row = lse2 + ((int64_t)b * A.H + h) * A.qpad;
+    const float* const dlrow = A.delta + ((int64_t)b * A.H + h) * A.qpad;
+    // rows [r, min(r + 32, rl + 1)) of Q or dO -> slot, through a buffer
+    // resource over those rows (slot rows past rl read as zeros without a
+    // fetch); a fixed number of DMAs per slot keeps the waits exact
+    auto load_step = [&](const char* base, int ss2, const int* ofs, int r, int rl,
+                         lds_u16* dst) {
+      const int nrow = max(0, min(rl - r + 1, ROWS));
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(base + (int64_t)r * ss2), (short)0, nrow * ss2, 0x00020000);
+#pragma unroll
+      for (int t = 0; t < SL; ++t)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + 512 * t), 16, ofs[t], 0,
+                                                 0, 0);
+    };
+
+    int jc = (int)__builtin_ctzll(live);
+    int rc = __builtin_amdgcn_readlane(r0, jc), rlc = __builtin_amdgcn_readlane(r1, jc);
+    __builtin_amdgcn_s_waitcnt(kWaitLds);  // the last head's slot reads are done
+    load_step(qbase, qss2, qofs, rc, rlc, lq);
+    load_step(obase, oss2, oofs, rc, rlc, lo);
+    while (jc < 64) {
+      // the next step: the rest of this range, else the next live entry's
+      int jn = jc, rn = rc + ROWS, rln = rlc;
+      if (rn > rlc) {
+        const uint64_t rest = jc >= 63 ? 0ull : (live & (~0ull << (jc + 1)));
+        jn = rest ? (int)__builtin_ctzll(rest) : 64;
+        rn = jn < 64 ? __builtin_amdgcn_readlane(r0, jn) : 0;
+        rln = jn < 64 ? __builtin_amdgcn_readlane(r1, jn) : -1;
+      }
+      // lse2 and delta of rows rc + 16 c + 4 q .. + 3 (rc is a multiple of 4;
+      // rows up to rc + 31 < qpad lie in the padded workspace)
+      f32x4 l2v[2], dlv[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        l2v[c] = *(const f32x4*)(l2row + rc + 16 * c + 4 * q);
+        dlv[c] = *(const f32x4*)(dlrow + rc + 16 * c + 4 * q);
+      }
+      // entry jc's key of row rc + (lane % 32), -1 when masked or past the range
+      int rkey = -1;
+      {
+        const int row = rc + (lane & 31);
+        if (row <= rlc) {
+          const int kk = key_at(row, jc);
+          rkey = kk <= row ? kk : -1;
+        }
+      }
+
+      __builtin_amdgcn_s_waitcnt(kWaitSlot);  // this step's Q is in LDS
+      f32x4 sacc[2];
+      s16x4 qt[2][C::NV];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        bf16x8 qa[C::NS];
+#pragma unroll
+        for (int s = 0; s < C::NS; ++s)
+          qa[s] = *(const bf16x8*)((const char*)qsl + c * CHB + rrd[s]);
+        sacc[c] = mfma16(qa[0], kop[0], f32x4{});
+#pragma unroll
+        for (int s = 1; s < C::NS; ++s) sacc[c] = mfma16(qa[s], kop[s], sacc[c]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int s = 0; s < C::NV; ++s)
+          qt[c][s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4*)((const char*)qsl + c * CHB + trd[s]));
+      __builtin_amdgcn_s_waitcnt(kWaitLds);  // Q slot read: refill it
+      load_step(qbase, qss2, qofs, rn, rln, lq);
+
+      __builtin_amdgcn_s_waitcnt(kWaitSlot);  // this step's dO is in LDS
+      f32x4 pacc[2];
+      s16x4 ot[2][C::NV];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        bf16x8 oa[C::NS];
+#pragma unroll
+        for (int s = 0; s < C::NS; ++s)
+          oa[s] = *(const bf16x8*)((const char*)osl + c * CHB + rrd[s]);
+        pacc[c] = mfma16(oa[0], vop[0], f32x4{});
+#pragma unroll
+        for (int s = 1; s < C::NS; ++s) pacc[c] = mfma16(oa[s], vop[s], pacc[c]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int s = 0; s < C::NV; ++s)
+          ot[c][s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4*)((const char*)osl + c * CHB + trd[s]));
+      __builtin_amdgcn_s_waitcnt(kWaitLds);  // dO slot read: refill it
+      load_step(obase, oss2, oofs, rn, rln, lo);
+
+      // P and dS where the row's key of entry jc is this lane's key: lane
+      // (key n, q) holds rows 16 c + 4 q + e, which are k-slots 8 q + 4 c + e
+      // of the products over rows
+      uint32_t pw[4], sw[4];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float pv[4], dv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int rk = __builtin_amdgcn_ds_bpermute(4 * (16 * c + 4 * q + e), rkey);
+          const bool has = rk == key;
+          const float p =
+              __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[c][e], scale2, -l2v[c][e]));
+          pv[e] = has ? p : 0.f;
+          dv[e] = has ? p * (pacc[c][e] - dlv[c][e]) : 0.f;
+        }
+        pw[2 * c] = pack_bf16x2(pv[0], pv[1]);
+        pw[2 * c + 1] = pack_bf16x2(pv[2], pv[3]);
+        sw[2 * c] = pack_bf16x2(dv[0], dv[1]);
+        sw[2 * c + 1] = pack_bf16x2(dv[2], dv[3]);
+      }
+      const u32x4 pq = {pw[0], pw[1], pw[2], pw[3]};
+      const u32x4 sq = {sw[0], sw[1], sw[2], sw[3]};
+#pragma unroll
+      for (int s = 0; s < C::NV; ++s) {
+        const s16x4 oo[2] = {ot[0][s], ot[1][s]};
+        dvacc[s] =
+            mfma16(__builtin_bit_cast(bf16x8, oo), __builtin_bit_cast(bf16x8, pq), dvacc[s]);
+        const s16x4 qq[2] = {qt[0][s], qt[1][s]};
+        dkacc[s] =
+            mfma16(__builtin_bit_cast(bf16x8, qq), __builtin_bit_cast(bf16x8, sq), dkacc[s]);
+      }
+      jc = jn;
+      rc = rn;
+      rlc = rln;
+    }
+    // the last step's (empty) refills have landed before the next head's
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  }
+
+  // ---- dK = scale dK^T^T, dV = dV^T^T: lane (key n, q) holds dims
+  // CW q + 4 s + e of key u0 + n
+  if (key_ok) {
+    uint16_t* dkr = A.dk + (int64_t)b * A.dksb + (int64_t)kvh * A.dksh + (int64_t)key * A.dkss;
+    uint16_t* dvr = A.dv + (int64_t)b * A.dvsb + (int64_t)kvh * A.dvsh + (int64_t)key * A.dvss;
+#pragma unroll
+    for (int t = 0; t < C::NV / 2; ++t) {
+      bf16x8 kv, vv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kv[e] = (__bf16)(dkacc[2 * t][e] * A.sm_scale);
+        kv[4 + e] = (__bf16)(dkacc[2 * t + 1][e] * A.sm_scale);
+        vv[e] = (__bf16)dvacc[2 * t][e];
+        vv[4 + e] = (__bf16)dvacc[2 * t + 1][e];
+      }
+      *(bf16x8*)(dkr + C::CW * q + 8 * t) = kv;
+      *(bf16x8*)(dvr + C::CW * q + 8 * t) = vv;
+    }
+  }
+}
+
+hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,
+                            hipStream_t stream) {
+  if (a.n_kblk <= 0) return hipSuccess;
+  const int64_t chunks = (a.n_kblk + 8 * kBlkChunk - 1) / (8 * kBlkChunk);
+  const dim3 grid((unsigned)(chunks * 8 * kBlkChunk));
+  if (head_dim == 128)
+    band_dkdv_kernel<128><<<grid, 64, 0, stream>>>(a, lse2);
+  else
+    band_dkdv_kernel<64><<<grid, 64, 0, stream>>>(a, lse2);
+  return hipGetLastError();
 }
 
 hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2,

@@ -160,6 +160,11 @@ void plan_xcd_grid(const int32_t* row_ptr, int nqb, int nq, int batch, int H,
 
 esa_status hip_status(hipError_t e) { return e == hipSuccess ? ESA_OK : ESA_ERR_HIP; }
 
+// Row stride of the backward's per-row workspace (delta, lse2): q_len rounded
+// up to 32, plus 32, so a 32-row step that starts on a valid row reads inside
+// its (b, h) rows
+int bwd_qpad(int q_len) { return (q_len + 31) / 32 * 32 + 32; }
+
 }  // namespace
 
 extern "C" {
@@ -466,7 +471,8 @@ esa_status esa_build_tile_masks(const esa_pattern* p, const int32_t* row_ptr,
 esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes) {
   if (!a || !workspace_bytes) return ESA_ERR_NULL;
   if (a->batch < 0 || a->num_heads < 1 || a->q_len < 0) return ESA_ERR_SHAPE;
-  *workspace_bytes = (size_t)2 * a->batch * a->num_heads * a->q_len * sizeof(float);
+  // delta and lse2 per row, rows of each (b, h) padded to qpad (bwd_qpad)
+  *workspace_bytes = (size_t)2 * a->batch * a->num_heads * bwd_qpad(a->q_len) * sizeof(float);
   return ESA_OK;
 }
 
@@ -480,12 +486,15 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
     return ESA_ERR_NULL;
   esa_status s = check_pattern(p);
   if (s != ESA_OK) return s;
-  if (!row_ptr || !col_idx || !tile_row || !kv_ptr || !kv_tiles || !kv_items || !mask_t ||
-      !workspace)
+  // q_items NULL: dQ by the band-gathered kernel (no work list or layout);
+  // kv_items NULL: dK / dV by the band-gathered kernel (no work list, tile
+  // lists or masks)
+  const bool band_dq = q_items == nullptr, band_dkdv = kv_items == nullptr;
+  if (!workspace || (!band_dq && (!row_ptr || !col_idx)) ||
+      (!band_dkdv && (!tile_row || !kv_ptr || !kv_tiles || !mask_t)))
     return ESA_ERR_NULL;
-  // q_items NULL: dQ by the band-gathered kernel (no work list)
-  const bool band_dq = q_items == nullptr;
-  if (band_dq && (p->attention_length > 64 || a->kv_len >= (1 << 24))) return ESA_ERR_UNSUPPORTED;
+  if ((band_dq || band_dkdv) && (p->attention_length > 64 || a->kv_len >= (1 << 24)))
+    return ESA_ERR_UNSUPPORTED;
   if (a->dtype != ESA_BF16) return ESA_ERR_DTYPE;
   if (a->batch < 0 || a->num_heads < 1 || a->num_kv_heads < 1 || a->q_len < 0 || a->kv_len < 1 ||
       a->num_heads % a->num_kv_heads != 0 || a->num_heads != p->num_heads)
@@ -525,7 +534,8 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
   if (!band_dq && (num_q_items < n_real || num_q_items > 8 * std::max<int64_t>(n_real, 1)))
     return ESA_ERR_SHAPE;
   const int64_t kv_real = (int64_t)a->batch * a->num_kv_heads * d.nkb;
-  if (num_kv_items < kv_real || num_kv_items > 8 * std::max<int64_t>(kv_real, 1))
+  if (!band_dkdv &&
+      (num_kv_items < kv_real || num_kv_items > 8 * std::max<int64_t>(kv_real, 1)))
     return ESA_ERR_SHAPE;
   if (a->batch == 0 || a->q_len == 0) return ESA_OK;
 
@@ -546,6 +556,7 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
   t.B = a->batch; t.H = a->num_heads; t.Hkv = a->num_kv_heads;
   t.groups = a->num_heads / a->num_kv_heads;
   t.q_len = a->q_len; t.kv_len = a->kv_len;
+  t.qpad = bwd_qpad(a->q_len);
   t.nqb = d.nqb; t.nq = nq; t.nkb = d.nkb;
   t.sm_scale = a->sm_scale; t.scale_log2 = a->sm_scale * 1.4426950408889634f;
   t.pc = make_consts(*p);
@@ -556,8 +567,12 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
   if (band_dq && n_groups > INT32_MAX / 2) return ESA_ERR_SHAPE;
   t.n_groups = (int)n_groups;
   t.per_xcd = (int)((n_groups + 7) / 8);
-  return hip_status(launch_tile_bwd(t, a->head_dim, band_dq ? -1 : num_q_items, num_kv_items,
-                                    (hipStream_t)stream));
+  t.nkb16 = (a->kv_len + 15) / 16;
+  const int64_t n_kblk = (int64_t)a->batch * a->num_kv_heads * t.nkb16;
+  if (band_dkdv && n_kblk > INT32_MAX / 2) return ESA_ERR_SHAPE;
+  t.n_kblk = (int)n_kblk;
+  return hip_status(launch_tile_bwd(t, a->head_dim, band_dq ? -1 : num_q_items,
+                                    band_dkdv ? -1 : num_kv_items, (hipStream_t)stream));
 }
 
 esa_status esa_reachability(int32_t seq_len, int32_t attention_length,

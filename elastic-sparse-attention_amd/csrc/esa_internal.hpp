@@ -92,7 +92,7 @@ struct BwdArgs {
   uint16_t* dk;
   uint16_t* dv;
   const float* lse;      // forward log-sum-exp, natural log, [B, H, q_len]
-  float* delta;          // workspace [B, H, q_len]: rowsum(dO * O)
+  float* delta;          // workspace [B, H, qpad]: rowsum(dO * O) (then lse2)
   const uint32_t* mask_t;  // [tiles][4 query sub-blocks][128 keys] key-major tile masks
   int64_t qsb, qsh, qss;
   int64_t ksb, ksh, kss;
@@ -104,6 +104,7 @@ struct BwdArgs {
   int64_t dvsb, dvsh, dvss;
   int64_t lsb, lsh;
   int B, H, Hkv, groups, q_len, kv_len;
+  int qpad;  // row stride of delta and lse2 per (b, h): q_len rounded up to 32, + 32
   int nqb, nq, nkb;
   float sm_scale, scale_log2;
   PatternConsts pc;
@@ -117,6 +118,9 @@ struct BwdArgs {
   // band-gathered dQ (when q_items is NULL): 16-row groups per (b, h), all
   // groups, groups per XCD range
   int ng, n_groups, per_xcd;
+  // band-gathered dK / dV (when kv_items is NULL): 16-key blocks per
+  // (b, kv head), all blocks
+  int nkb16, n_kblk;
 };
 
 hipError_t launch_indices(const PatternConsts& pc, int row0, int nrows, void* indices, void* mask,
@@ -127,6 +131,8 @@ hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
                            hipStream_t stream);
 hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream);
 hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2, hipStream_t stream);
+hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,
+                            hipStream_t stream);
 hipError_t launch_gather_fwd(const GatherArgs& a, bool f32, bool pattern, hipStream_t stream);
 hipError_t launch_tile_masks(const PatternConsts& pc, const int32_t* row_ptr, const int32_t* col_idx,
                              int nqb, int q_len, uint32_t* mask_t, hipStream_t stream);

@@ -327,6 +327,14 @@ def prefill_kernel(layout: ElasticLayout, q_len: int, batch: int, head_dim: int)
     return "band" if staged > BAND_CROSSOVER[head_dim] * groups else "tile"
 
 
+def bwd_kernels(layout: ElasticLayout, q_len: int, batch: int, head_dim: int
+                ) -> Tuple[str, str]:
+    """("band" | "tile", "band" | "tile"): the faster dQ and dK/dV kernels for
+    this pattern and shape; both follow the forward's choice."""
+    kind = prefill_kernel(layout, q_len, batch, head_dim)
+    return kind, kind
+
+
 def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           layout: ElasticLayout, scaling: float, return_lse: bool = True,
                           out: Optional[torch.Tensor] = None, key_block: int = 32,
@@ -458,7 +466,7 @@ def sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
 def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
                           lse: torch.Tensor, dout: torch.Tensor, layout: ElasticLayout,
-                          scaling: float, dq_kernel: str = "auto"
+                          scaling: float, dq_kernel: str = "auto", dkdv_kernel: str = "auto"
                           ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """MFMA backward of ``elastic_attention_fwd`` (prefill, bf16).
 
@@ -466,9 +474,9 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
     ``lse`` float32 ``[B, H, Lq]``.  Returns ``dq`` ``[B, H, Lq, D]`` and
     ``dk``, ``dv`` ``[B, Hkv, Lk, D]``: the gradients the reference's
     ElasticSparseAttentionFunction.backward returns (:299-339), computed
-    without atomics.  dK/dV run block-sparse over the layout; ``dq_kernel``
-    "band" computes dQ with the band-gathered kernel, "tile" block-sparse,
-    "auto" as the forward's kernel choice (:func:`prefill_kernel`).
+    without atomics.  ``dq_kernel`` and ``dkdv_kernel``: "band" computes that
+    half with a band-gathered kernel (dQ row-major, dK/dV key-major), "tile"
+    block-sparse over the layout, "auto" as :func:`bwd_kernels` picks.
     """
     _check_qkv(q, k, v)
     B, H, Lq, D = q.shape
@@ -500,24 +508,30 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
     ws = ctypes.c_size_t()
     check(lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(ws)), "esa_bwd_workspace_size")
     work = torch.empty(max(ws.value // 4, 4), dtype=torch.float32, device=q.device)
-    if dq_kernel not in ("auto", "tile", "band"):
-        raise ValueError(f"dq_kernel must be 'auto', 'tile' or 'band', got {dq_kernel!r}")
-    if dq_kernel == "auto":
-        dq_kernel = prefill_kernel(layout, Lq, B, D)
-    if dq_kernel == "band":
-        items, n_items = None, 0   # no work list: the band kernel covers every row group
-    else:
-        items, n_items = layout.schedule(Lq, B)
-    tile_row, kv_ptr, kv_tiles, kv_items, n_kv = layout.bwd_plan(Lq, B, Hkv)
-    masks = layout.tile_masks(Lq)
+    for name, val in (("dq_kernel", dq_kernel), ("dkdv_kernel", dkdv_kernel)):
+        if val not in ("auto", "tile", "band"):
+            raise ValueError(f"{name} must be 'auto', 'tile' or 'band', got {val!r}")
+    auto_dq, auto_dkdv = bwd_kernels(layout, Lq, B, D)
+    dq_kernel = auto_dq if dq_kernel == "auto" else dq_kernel
+    dkdv_kernel = auto_dkdv if dkdv_kernel == "auto" else dkdv_kernel
     vp = ctypes.c_void_p
+
+    def ptr(t):
+        return vp(t.data_ptr() if t is not None else None)
+
+    # a band half takes no work list (its kernel covers every row group or
+    # key block), and no layout arrays when both halves are band-gathered
+    items, n_items = (None, 0) if dq_kernel == "band" else layout.schedule(Lq, B)
+    if dkdv_kernel == "band":
+        tile_row = kv_ptr = kv_tiles = kv_items = masks = None
+        n_kv = 0
+    else:
+        tile_row, kv_ptr, kv_tiles, kv_items, n_kv = layout.bwd_plan(Lq, B, Hkv)
+        masks = layout.tile_masks(Lq)
     check(lib.esa_elastic_bwd(ctypes.byref(a), ctypes.byref(layout.pattern),
-                              vp(layout.row_ptr.data_ptr()), vp(layout.col_idx.data_ptr()),
-                              vp(items.data_ptr() if items is not None else None), n_items,
-                              vp(tile_row.data_ptr()),
-                              vp(kv_ptr.data_ptr()), vp(kv_tiles.data_ptr()),
-                              vp(kv_items.data_ptr()), n_kv, vp(masks.data_ptr()),
-                              vp(work.data_ptr()), work.numel() * 4, _stream(q.device)),
+                              ptr(layout.row_ptr), ptr(layout.col_idx), ptr(items), n_items,
+                              ptr(tile_row), ptr(kv_ptr), ptr(kv_tiles), ptr(kv_items), n_kv,
+                              ptr(masks), ptr(work), work.numel() * 4, _stream(q.device)),
           "esa_elastic_bwd")
     return dq, dk, dv
 

@@ -255,8 +255,9 @@ esa_status esa_build_tile_masks(const esa_pattern* p, const int32_t* row_ptr,
                                 uint32_t* mask_t, int64_t mask_capacity,
                                 void* stream);
 
-/* Host only.  Bytes of float32 workspace esa_elastic_bwd needs
- * (2 * batch * num_heads * q_len floats). */
+/* Host only.  Bytes of float32 workspace esa_elastic_bwd needs:
+ * 2 * batch * num_heads * qpad floats, qpad = q_len rounded up to 32, plus
+ * 32 (per-row delta and log2 LSE). */
 esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes);
 
 /* Backward over the elastic pattern: replaces the backward branch of the
@@ -266,11 +267,15 @@ esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes
  * zero-initialisation needed, no atomics: each gradient row is accumulated
  * by one workgroup in a fixed order, so results are deterministic).
  * q_items/num_q_items: esa_plan_schedule's list for (q_len, batch), for a
- * block-sparse dQ; q_items NULL computes dQ with the band-gathered kernel
- * instead (as esa_elastic_fwd_band gathers: attention_length <= 64,
- * kv_len < 2^24; num_q_items is ignored);
- * tile_row, kv_ptr, kv_tiles, kv_items/num_kv_items: esa_plan_bwd's;
- * mask_t: esa_build_tile_masks' for this q_len (all device memory).
+ * block-sparse dQ over the layout row_ptr/col_idx; q_items NULL computes dQ
+ * with the band-gathered kernel instead (as esa_elastic_fwd_band gathers:
+ * attention_length <= 64, kv_len < 2^24; num_q_items is ignored).
+ * tile_row, kv_ptr, kv_tiles, kv_items/num_kv_items: esa_plan_bwd's, and
+ * mask_t: esa_build_tile_masks' for this q_len, for a block-sparse dK/dV;
+ * kv_items NULL computes dK and dV with the band-gathered key-major kernel
+ * instead (same limits; tile_row, kv_ptr, kv_tiles, mask_t and num_kv_items
+ * are ignored).  With both NULL no layout is read (row_ptr, col_idx may be
+ * NULL).  All lists and masks are device memory.
  * Requires dtype ESA_BF16, head_dim 64 or 128, block 128 x 128, a finite
  * sm_scale > 0, q_len <= kv_len, 16-byte aligned rows. */
 esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p,

@@ -276,11 +276,24 @@ def test_bwd_entry_points_reject_bad_arguments():
     a.sm_scale = 128 ** -0.5
     ws = ctypes.c_size_t()
     assert lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(ws)) == en.ESA_OK
-    assert ws.value == 2 * 1 * 4 * 256 * 4
+    assert ws.value == 2 * 1 * 4 * (256 + 32) * 4   # rows padded to 32, + 32
 
-    def call(args, items=8, kv_items=64, wsb=ws.value):
-        return lib.esa_elastic_bwd(ctypes.byref(args), ctypes.byref(p), fake, fake, fake, items,
-                                   fake, fake, fake, fake, kv_items, fake, fake, wsb, None)
+    def call(args, items=8, kv_items=64, wsb=ws.value, pat_=p, layout=fake, q_list=fake,
+             kv_lists=fake, kv_list=fake, masks=fake):
+        return lib.esa_elastic_bwd(ctypes.byref(args), ctypes.byref(pat_), layout, layout, q_list,
+                                   items, kv_lists, kv_lists, kv_lists, kv_list, kv_items, masks,
+                                   fake, wsb, None)
+
+    # the block-sparse halves need their layout, lists and masks; the band
+    # halves need none of them, and attention_length <= 64
+    assert call(a, layout=None) == en.ESA_ERR_NULL
+    assert call(a, masks=None) == en.ESA_ERR_NULL
+    assert call(a, kv_lists=None) == en.ESA_ERR_NULL
+    assert call(a, q_list=None, kv_list=None, layout=None, kv_lists=None, masks=None,
+                wsb=16) == en.ESA_ERR_CAPACITY
+    assert call(a, q_list=None, kv_list=None, pat_=pat(L=1024, H=4, w=65)) \
+        == en.ESA_ERR_UNSUPPORTED
+    assert call(a, kv_list=None, kv_items=31, wsb=16) == en.ESA_ERR_CAPACITY  # count ignored
 
     assert call(a, wsb=16) == en.ESA_ERR_CAPACITY
     assert call(a, items=7) == en.ESA_ERR_SHAPE

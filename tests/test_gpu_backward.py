@@ -32,7 +32,7 @@ def rel_err(got, ref):
     return ((got.float().cpu() - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
 
 
-@pytest.mark.parametrize("dq_kernel", ["tile", "band"])
+@pytest.mark.parametrize("kernels", ["tile/tile", "band/tile", "band/band", "tile/band"])
 @pytest.mark.parametrize("B,H,Hkv,L,Lq,D,layer", [
     (1, 4, 4, 1024, 1024, 128, 4),
     (1, 4, 4, 1024, 1024, 128, 0),
@@ -42,10 +42,14 @@ def rel_err(got, ref):
     (1, 4, 4, 1000, 700, 128, 6),    # q_len < kv_len, ragged blocks
     (1, 2, 1, 200, 200, 64, 2),      # MQA, short
     (1, 3, 3, 1024, 1024, 128, 1),   # odd head count: bands of 17 keys (band dQ tail)
+    (1, 6, 2, 777, 777, 64, 7),      # last layer: key 0 in every row of head 0
+    (1, 2, 2, 64, 64, 128, 3),       # one row block, rows 0 .. w - 1 only
 ])
-def test_backward_matches_autograd(B, H, Hkv, L, Lq, D, layer, dq_kernel):
-    print(f"bwd B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} layer={layer} dq={dq_kernel}",
-          flush=True)
+def test_backward_matches_autograd(B, H, Hkv, L, Lq, D, layer, kernels):
+    """kernels: dQ kernel / dK-dV kernel."""
+    dq_kernel, dkdv_kernel = kernels.split("/")
+    print(f"bwd B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} layer={layer} dq={dq_kernel} "
+          f"dkdv={dkdv_kernel}", flush=True)
     q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=layer + 3, scale=1.0, Lq=Lq)
     idx, msk = elastic_indices(L, layer, 8, H, 64)
     pi, pm = prepared_rows(idx, msk, Lq, L, L)
@@ -57,13 +61,15 @@ def test_backward_matches_autograd(B, H, Hkv, L, Lq, D, layer, dq_kernel):
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
     o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc)
     do = g.to(DEV).permute(0, 2, 1, 3).contiguous()  # [B, Lq, H, D] like o
-    dq, dk, dv = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel=dq_kernel)
+    dq, dk, dv = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel=dq_kernel,
+                                       dkdv_kernel=dkdv_kernel)
     e = (rel_err(dq, rq), rel_err(dk, rk), rel_err(dv, rv))
     print(f"  rel err dq {e[0]:.3e} dk {e[1]:.3e} dv {e[2]:.3e}", flush=True)
     assert all(torch.isfinite(t.float()).all() for t in (dq, dk, dv))
     assert max(e) <= REL
     # deterministic: a second run is bit-identical
-    dq2, dk2, dv2 = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel=dq_kernel)
+    dq2, dk2, dv2 = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel=dq_kernel,
+                                          dkdv_kernel=dkdv_kernel)
     assert torch.equal(dq, dq2) and torch.equal(dk, dk2) and torch.equal(dv, dv2)
 
 
@@ -106,12 +112,13 @@ def test_backward_full_size_8k_layer4():
         assert max(e) <= REL
 
 
+@pytest.mark.parametrize("kernels", ["tile/tile", "band/band"])
 @pytest.mark.parametrize("B,H,Hkv,L,D,layer", [
     (1, 32, 32, 32768, 128, 4),   # the headline shape
     (1, 32, 32, 32768, 128, 7),
     (2, 8, 2, 8192, 64, 5),       # GQA, D = 64
 ])
-def test_backward_identities_full_size(B, H, Hkv, L, D, layer):
+def test_backward_identities_full_size(B, H, Hkv, L, D, layer, kernels):
     """Size-independent checks at full size.  Every row of P sums to one, so
     the sum of dV over a kv head's keys equals the sum of dO over the rows of
     its query heads; every row of dS = P (dP - delta) sums to zero, so the sum
@@ -119,7 +126,9 @@ def test_backward_identities_full_size(B, H, Hkv, L, D, layer):
     of absolute values; without the identities the ratio would be about
     1 / sqrt(L) (random signs), here only rounding is left (P and dS enter
     the MFMAs in bf16, dK and dV are stored in bf16)."""
-    print(f"bwd identities B={B} H={H} Hkv={Hkv} L={L} D={D} layer={layer}", flush=True)
+    dq_kernel, dkdv_kernel = kernels.split("/")
+    print(f"bwd identities B={B} H={H} Hkv={Hkv} L={L} D={D} layer={layer} {kernels}",
+          flush=True)
     q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=90 + layer, scale=D ** -0.25)
     sc = scaling_for(D)
     lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
@@ -127,7 +136,8 @@ def test_backward_identities_full_size(B, H, Hkv, L, D, layer):
     o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc)
     g = torch.Generator().manual_seed(layer)
     do = torch.randn(B, L, H, D, generator=g).to(torch.bfloat16).to(DEV)
-    dq, dk, dv = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc)
+    dq, dk, dv = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel=dq_kernel,
+                                       dkdv_kernel=dkdv_kernel)
     assert all(bool(torch.isfinite(t.float()).all()) for t in (dq, dk, dv))
     groups = H // Hkv
     sum_do = do.float().sum(dim=1).view(B, Hkv, groups, D).sum(dim=2)      # [B, Hkv, D]
@@ -142,13 +152,14 @@ def test_backward_identities_full_size(B, H, Hkv, L, D, layer):
     assert r_v <= 1e-3 and r_k <= 1e-3
 
 
-@pytest.mark.parametrize("layer", [4, 7])
-def test_band_dq_matches_tile_dq_full_size(layer):
-    """The headline shape: dQ from the band kernel against dQ from the
-    block-sparse kernel (two independent paths over the same O and LSE),
-    max |difference| <= 2e-2 * max |dQ|."""
+@pytest.mark.parametrize("layer", [0, 4, 7])
+def test_band_matches_tile_full_size(layer):
+    """The headline shape: dQ, dK and dV from the band kernels against the
+    block-sparse kernels (independent paths over the same O and LSE), max
+    |difference| <= 2e-2 * max |tile gradient| per tensor; each half of one
+    kind leaves the other half bit-identical."""
     B, H, L, D = 1, 32, 32768, 128
-    print(f"band dq vs tile dq B={B} H={H} L={L} D={D} layer={layer}", flush=True)
+    print(f"band vs tile backward B={B} H={H} L={L} D={D} layer={layer}", flush=True)
     q, k, v = seeded_inputs(B, H, H, L, D, torch.bfloat16, seed=110 + layer, scale=D ** -0.25)
     sc = scaling_for(D)
     lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
@@ -156,10 +167,16 @@ def test_band_dq_matches_tile_dq_full_size(layer):
     o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc)
     do = torch.randn(B, L, H, D, generator=torch.Generator().manual_seed(layer))
     do = do.to(torch.bfloat16).to(DEV)
-    dq_t, dk_t, dv_t = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="tile")
-    dq_b, dk_b, dv_b = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="band")
-    assert bool(torch.isfinite(dq_b.float()).all())
-    r = ((dq_b.float() - dq_t.float()).abs().max() / dq_t.float().abs().max()).item()
-    print(f"  max|dq band - dq tile| / max|dq| {r:.3e}", flush=True)
-    assert r <= REL
-    assert torch.equal(dk_t, dk_b) and torch.equal(dv_t, dv_b)
+    tt = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="tile",
+                               dkdv_kernel="tile")
+    bt = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="band",
+                               dkdv_kernel="tile")
+    bb = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="band",
+                               dkdv_kernel="band")
+    for name, x, y in zip(("dq", "dk", "dv"), tt, bb):
+        assert bool(torch.isfinite(y.float()).all())
+        r = ((y.float() - x.float()).abs().max() / x.float().abs().max()).item()
+        print(f"  max|{name} band - {name} tile| / max|{name}| {r:.3e}", flush=True)
+        assert r <= REL
+    assert torch.equal(tt[1], bt[1]) and torch.equal(tt[2], bt[2])
+    assert torch.equal(bt[0], bb[0])
