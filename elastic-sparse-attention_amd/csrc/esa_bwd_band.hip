@@ -318,11 +318,13 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
 // one step, as in the reference's dK/dV loop (:168-233 accumulates the same
 // pairs); every gradient row is accumulated by one wave in a fixed order:
 // deterministic, no atomics.  A block's work is the number of rows using its
-// keys: low blocks of late layers are the heaviest, so blocks go to the
-// eight XCDs in chunks of kBlkChunk consecutive blocks, round robin (each
-// XCD starts with its heaviest chunk and keeps neighbouring blocks, which
-// share rows, in one L2).
-constexpr int kBlkChunk = 8;
+// keys (the low blocks of late layers are the heaviest), and a row's Q and
+// dO serve every block holding one of its keys, so the blocks one XCD runs
+// at a time should be neighbours (one L2).  Blocks go to the eight XCDs in
+// chunks of A.kchunk consecutive blocks, round robin: with whole kv heads
+// per XCD (batch * kv heads a multiple of 8) one chunk per XCD, each a
+// contiguous range; otherwise chunks of 8 blocks, which balance the heavy
+// low blocks over the XCDs.
 
 template <int D>
 __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float* lse2) {
@@ -338,7 +340,7 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
   // ---- block: slot k of XCD x takes block (k / chunk * 8 + x) * chunk + k % chunk
   const int bid = blockIdx.x;
   const int kx = bid >> 3;
-  const int g = ((kx / kBlkChunk) * 8 + (bid & 7)) * kBlkChunk + kx % kBlkChunk;
+  const int g = ((kx / A.kchunk) * 8 + (bid & 7)) * A.kchunk + kx % A.kchunk;
   if (g >= A.n_kblk) return;
   const int bkv = g / A.nkb16, kb = g % A.nkb16;
   const int kvh = bkv % A.Hkv, b = bkv / A.Hkv;
@@ -439,7 +441,9 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
     // fetch); a fixed number of DMAs per slot keeps the waits exact
     auto load_step = [&](const char* base, int ss2, const int* ofs, int r, int rl,
                          lds_u16* dst) {
-      const int nrow = max(0, min(rl - r + 1, ROWS));
+      // (readfirstlane: a value the compiler computes in VGPRs would put the
+      // resource in VGPRs and each DMA in a waterfall loop)
+      const int nrow = __builtin_amdgcn_readfirstlane(max(0, min(rl - r + 1, ROWS)));
       const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
           (void*)(base + (int64_t)r * ss2), (short)0, nrow * ss2, 0x00020000);
 #pragma unroll
@@ -589,9 +593,9 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
 
 hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,
                             hipStream_t stream) {
-  if (a.n_kblk <= 0) return hipSuccess;
-  const int64_t chunks = (a.n_kblk + 8 * kBlkChunk - 1) / (8 * kBlkChunk);
-  const dim3 grid((unsigned)(chunks * 8 * kBlkChunk));
+  if (a.n_kblk <= 0 || a.kchunk <= 0) return hipSuccess;
+  const int64_t chunks = (a.n_kblk + 8 * (int64_t)a.kchunk - 1) / (8 * (int64_t)a.kchunk);
+  const dim3 grid((unsigned)(chunks * 8 * a.kchunk));
   if (head_dim == 128)
     band_dkdv_kernel<128><<<grid, 64, 0, stream>>>(a, lse2);
   else

@@ -119,8 +119,8 @@ struct BwdArgs {
   // groups, groups per XCD range
   int ng, n_groups, per_xcd;
   // band-gathered dK / dV (when kv_items is NULL): 16-key blocks per
-  // (b, kv head), all blocks
-  int nkb16, n_kblk;
+  // (b, kv head), all blocks, consecutive blocks per XCD chunk
+  int nkb16, n_kblk, kchunk;
 };
 
 hipError_t launch_indices(const PatternConsts& pc, int row0, int nrows, void* indices, void* mask,
