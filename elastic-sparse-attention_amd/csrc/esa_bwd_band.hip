@@ -303,10 +303,11 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
 // start, the spacing and both interpolated terms of the recipe never
 // decrease), so for each query head of the kv group and each entry j the
 // rows whose key of entry j lies in the block form one range; lane j finds
-// it by binary search.  The ranges are walked 32 rows at a time (starts
-// rounded down to a multiple of 4; the extra rows are masked): Q and dO rows
-// staged in LDS (buffer_load ... lds, rows past the range read as zeros),
-// then
+// it by binary search.  The ranges are packed back to back and walked 32
+// rows at a time (a step may hold rows of several entries): each slot row's
+// Q and dO row is staged in LDS by buffer_load ... lds with per-lane row
+// offsets (empty slot rows read as zeros), its delta and lse2 by a one-dword
+// DMA, then
 //   S = Q K^T, dP = dO V^T   2 x D/32 MFMAs each (A = Q / dO rows from LDS,
 //                            B = the block's K / V in registers)
 //   P = exp2(S scale log2e - lse2), dS = P (dP - delta) on the (row, key)
@@ -334,6 +335,7 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
   constexpr int SL = ROWS * C::CPR / 64;  // DMA instructions per slot
   __shared__ __attribute__((aligned(1024))) uint16_t qsl[SLOT2];
   __shared__ __attribute__((aligned(1024))) uint16_t osl[SLOT2];
+  __shared__ __attribute__((aligned(256))) float lsl[64];  // delta, lse2 of the slot rows
   lds_u16* const lq = (lds_u16*)qsl;
   lds_u16* const lo = (lds_u16*)osl;
 
@@ -369,13 +371,15 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
   }
 
   const int qss2 = (int)A.qss * 2, oss2 = (int)A.doss * 2;
-  // DMA t, lane l fills slot row R = (64 t + l) / CPR, physical chunk l % CPR
-  int qofs[SL], oofs[SL];
+  // DMA t, lane l fills slot row R_t = (64 t + l) / CPR at physical chunk
+  // l % CPR, from logical chunk kswz(R_t, l % CPR) of the row the step puts
+  // there (fetched from the lane holding slot row R_t)
+  int dmar[SL], cofs[SL];
 #pragma unroll
   for (int t = 0; t < SL; ++t) {
-    const int R = (64 * t + lane) / C::CPR, pc = lane % C::CPR;
-    qofs[t] = R * qss2 + 16 * kswz<D>(R, pc);
-    oofs[t] = R * oss2 + 16 * kswz<D>(R, pc);
+    const int R = (64 * t + lane) / C::CPR;
+    dmar[t] = 4 * R;
+    cofs[t] = 16 * kswz<D>(R, lane % C::CPR);
   }
   // row reads (A operand of S and dP) of chunk c (slot rows 16 c .. + 15):
   // lane (m = n, q) reads slot row 16 c + n, dims 32 s + 8 q .. + 8
@@ -398,10 +402,18 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
   for (int s = 0; s < C::NV; ++s) dkacc[s] = dvacc[s] = f32x4{};
   const float scale2 = A.scale_log2;
   constexpr int kWaitLds = 0xC07F;  // lgkmcnt(0)
-  // vmcnt(SL): before a slot's reads at most one slot's DMA (and the step's
-  // lse2 / delta loads, issued before it or not at all) is newer; loads
-  // complete in order, so at most SL outstanding leaves the slot filled
-  constexpr int kWaitSlot = (0xF70 & ~0xF) | (SL & 0xF) | ((SL >> 4) << 14);
+  // Each step issues, in order, its successor's Q DMAs (SL), dO DMAs (SL)
+  // and delta / lse2 DMA (1), each after the step's reads of that buffer.
+  // Loads complete in order, so: Q of this step is in LDS once at most
+  // SL + 1 loads (its dO and delta / lse2) are outstanding; dO once at most
+  // SL + 1 (its delta / lse2, the next Q); delta / lse2 once at most 2 SL.
+  constexpr int kWaitRows = (0xF70 & ~0xF) | ((SL + 1) & 0xF) | (((SL + 1) >> 4) << 14);
+  constexpr int kWaitStats = (0xF70 & ~0xF) | ((2 * SL) & 0xF) | (((2 * SL) >> 4) << 14);
+  // a buffer offset past every resource used here (num_records < 2^31 - 16),
+  // so a DMA lane without a row reads zeros and fetches nothing
+  constexpr int kOob = 0x7ffffff0;
+  const int slot_row = lane & 31;
+  const int lse_off = (int)((const char*)lse2 - (const char*)A.delta);
 
   for (int hg = 0; hg < A.groups; ++hg) {
     const int h = kvh * A.groups + hg;
@@ -410,9 +422,9 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
       const RowParams rp = row_params(A.pc, i);
       return interp_index(oversized(rp, j), oversized(rp, j + 1), hw);
     };
-    // lane j: rows [r0, r1] whose key of entry j lies in the block (rows
-    // before u0 cannot use a key >= u0)
-    int r0 = 0, r1 = -1;
+    // lane j: rows [r0, r0 + len) whose key of entry j lies in the block
+    // (rows before u0 cannot use a key >= u0)
+    int r0 = 0, len = 0;
     if (lane < A.pc.w) {
       int a0 = u0, a1 = A.q_len;  // first row >= u0 with key >= u0
       while (a0 < a1) {
@@ -424,67 +436,95 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
         const int mid = (c0 + c1) >> 1;
         if (key_at(mid, lane) >= u0 + 16) c1 = mid; else c0 = mid + 1;
       }
-      if (a0 < c0) {
-        r0 = a0 & ~3;
-        r1 = c0 - 1;
-      }
+      r0 = a0;
+      len = c0 - a0;
     }
-    const uint64_t live = __builtin_amdgcn_ballot_w64(r0 <= r1);
-    if (live == 0ull) continue;
+    // the ranges are packed back to back: entry j's rows are positions
+    // [cum, cum + len) of one sequence, walked 32 positions per step
+    int cum = len;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(cum, off, 64);
+      if (lane >= off) cum += t;
+    }
+    const int total = __builtin_amdgcn_readlane(cum, 63);
+    cum -= len;
+    if (total == 0) continue;
+    const uint64_t live = __builtin_amdgcn_ballot_w64(len > 0);
+    // row and entry of slot row (lane % 32) in the step at position P (row
+    // -1: none); e is the first live entry reaching past P on entry, the
+    // first reaching past P + 32 on return
+    auto map_step = [&](int P, int& e, int& row, int& ent) {
+      row = -1;
+      ent = 0;
+      while (e < 64) {
+        const int ce = __builtin_amdgcn_readlane(cum, e);
+        if (ce >= P + ROWS) break;
+        const int le = __builtin_amdgcn_readlane(len, e);
+        const int re = __builtin_amdgcn_readlane(r0, e);
+        const int d = P + slot_row - ce;
+        if ((uint32_t)d < (uint32_t)le) {
+          row = re + d;
+          ent = e;
+        }
+        if (ce + le > P + ROWS) break;
+        const uint64_t rest = e >= 63 ? 0ull : (live & (~0ull << (e + 1)));
+        e = rest ? (int)__builtin_ctzll(rest) : 64;
+      }
+    };
 
     const char* const qbase = (const char*)(A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh);
     const char* const obase = (const char*)(A.dout + (int64_t)b * A.dosb + (int64_t)h * A.dosh);
-    const float* const l2row = lse2 + ((int64_t)b * A.H + h) * A.qpad;
-    const float* const dlrow = A.delta + ((int64_t)b * A.H + h) * A.qpad;
-    // rows [r, min(r + 32, rl + 1)) of Q or dO -> slot, through a buffer
-    // resource over those rows (slot rows past rl read as zeros without a
-    // fetch); a fixed number of DMAs per slot keeps the waits exact
-    auto load_step = [&](const char* base, int ss2, const int* ofs, int r, int rl,
-                         lds_u16* dst) {
-      // (readfirstlane: a value the compiler computes in VGPRs would put the
-      // resource in VGPRs and each DMA in a waterfall loop)
-      const int nrow = __builtin_amdgcn_readfirstlane(max(0, min(rl - r + 1, ROWS)));
-      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)(base + (int64_t)r * ss2), (short)0, nrow * ss2, 0x00020000);
+    const char* const sbase = (const char*)(A.delta + ((int64_t)b * A.H + h) * A.qpad);
+    const __amdgpu_buffer_rsrc_t qrs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)qbase, (short)0, A.q_len * qss2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ors =
+        __builtin_amdgcn_make_buffer_rsrc((void*)obase, (short)0, A.q_len * oss2, 0x00020000);
+    // delta row of (b, h) and, lse_off bytes further, its lse2 row
+    const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)sbase, (short)0, lse_off + 4 * A.qpad, 0x00020000);
+    // Q or dO rows of the step whose slot rows hold `row` -> slot dst (after
+    // the step's reads of dst)
+    auto issue_rows = [&](__amdgpu_buffer_rsrc_t rs, int ss2, int row, lds_u16* dst) {
+      // (a fixed size: hipcc drops the kernel's host stub when a lambda here
+      // declares an array whose size depends on D)
+      static_assert(SL <= 8, "at most 8 DMAs per slot");
+      int ofs[8];
+#pragma unroll
+      for (int t = 0; t < SL; ++t) {
+        const int rr = __builtin_amdgcn_ds_bpermute(dmar[t], row);
+        ofs[t] = rr >= 0 ? rr * ss2 + cofs[t] : kOob;
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitLds);  // the slot's reads are done
 #pragma unroll
       for (int t = 0; t < SL; ++t)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + 512 * t), 16, ofs[t], 0,
                                                  0, 0);
     };
+    // delta (lanes 0..31) and lse2 (lanes 32..63) of the step's rows -> lsl
+    auto issue_stats = [&](int row) {
+      const int ofs = row >= 0 ? 4 * row + (lane >= 32 ? lse_off : 0) : kOob;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_void*)lsl, 4, ofs, 0, 0, 0);
+    };
 
-    int jc = (int)__builtin_ctzll(live);
-    int rc = __builtin_amdgcn_readlane(r0, jc), rlc = __builtin_amdgcn_readlane(r1, jc);
-    __builtin_amdgcn_s_waitcnt(kWaitLds);  // the last head's slot reads are done
-    load_step(qbase, qss2, qofs, rc, rlc, lq);
-    load_step(obase, oss2, oofs, rc, rlc, lo);
-    while (jc < 64) {
-      // the next step: the rest of this range, else the next live entry's
-      int jn = jc, rn = rc + ROWS, rln = rlc;
-      if (rn > rlc) {
-        const uint64_t rest = jc >= 63 ? 0ull : (live & (~0ull << (jc + 1)));
-        jn = rest ? (int)__builtin_ctzll(rest) : 64;
-        rn = jn < 64 ? __builtin_amdgcn_readlane(r0, jn) : 0;
-        rln = jn < 64 ? __builtin_amdgcn_readlane(r1, jn) : -1;
-      }
-      // lse2 and delta of rows rc + 16 c + 4 q .. + 3 (rc is a multiple of 4;
-      // rows up to rc + 31 < qpad lie in the padded workspace)
-      f32x4 l2v[2], dlv[2];
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        l2v[c] = *(const f32x4*)(l2row + rc + 16 * c + 4 * q);
-        dlv[c] = *(const f32x4*)(dlrow + rc + 16 * c + 4 * q);
-      }
-      // entry jc's key of row rc + (lane % 32), -1 when masked or past the range
+    int e = (int)__builtin_ctzll(live);
+    int row_c, ent_c;
+    map_step(0, e, row_c, ent_c);
+    issue_rows(qrs, qss2, row_c, lq);
+    issue_rows(ors, oss2, row_c, lo);
+    __builtin_amdgcn_s_waitcnt(kWaitLds);  // the last head's stats reads are done
+    issue_stats(row_c);
+    for (int P = 0; P < total; P += ROWS) {
+      int row_n = -1, ent_n = 0;
+      if (P + ROWS < total) map_step(P + ROWS, e, row_n, ent_n);
+      // the key of slot row (lane % 32), -1 when masked or empty
       int rkey = -1;
-      {
-        const int row = rc + (lane & 31);
-        if (row <= rlc) {
-          const int kk = key_at(row, jc);
-          rkey = kk <= row ? kk : -1;
-        }
+      if (row_c >= 0) {
+        const int kk = key_at(row_c, ent_c);
+        rkey = kk <= row_c ? kk : -1;
       }
 
-      __builtin_amdgcn_s_waitcnt(kWaitSlot);  // this step's Q is in LDS
+      __builtin_amdgcn_s_waitcnt(kWaitRows);  // this step's Q is in LDS
       f32x4 sacc[2];
       s16x4 qt[2][C::NV];
 #pragma unroll
@@ -504,10 +544,9 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
         for (int s = 0; s < C::NV; ++s)
           qt[c][s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (lds_s16x4*)((const char*)qsl + c * CHB + trd[s]));
-      __builtin_amdgcn_s_waitcnt(kWaitLds);  // Q slot read: refill it
-      load_step(qbase, qss2, qofs, rn, rln, lq);
+      issue_rows(qrs, qss2, row_n, lq);
 
-      __builtin_amdgcn_s_waitcnt(kWaitSlot);  // this step's dO is in LDS
+      __builtin_amdgcn_s_waitcnt(kWaitRows);  // this step's dO is in LDS
       f32x4 pacc[2];
       s16x4 ot[2][C::NV];
 #pragma unroll
@@ -527,24 +566,33 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
         for (int s = 0; s < C::NV; ++s)
           ot[c][s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (lds_s16x4*)((const char*)osl + c * CHB + trd[s]));
-      __builtin_amdgcn_s_waitcnt(kWaitLds);  // dO slot read: refill it
-      load_step(obase, oss2, oofs, rn, rln, lo);
+      issue_rows(ors, oss2, row_n, lo);
 
-      // P and dS where the row's key of entry jc is this lane's key: lane
-      // (key n, q) holds rows 16 c + 4 q + e, which are k-slots 8 q + 4 c + e
-      // of the products over rows
+      __builtin_amdgcn_s_waitcnt(kWaitStats);  // this step's delta / lse2 are in LDS
+      f32x4 l2v[2], dlv[2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        dlv[c] = *(const f32x4*)(lsl + 16 * c + 4 * q);
+        l2v[c] = *(const f32x4*)(lsl + 32 + 16 * c + 4 * q);
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitLds);  // stats read: refill them
+      issue_stats(row_n);
+
+      // P and dS where the row's key is this lane's key: lane (key n, q)
+      // holds slot rows 16 c + 4 q + e, which are k-slots 8 q + 4 c + e of
+      // the products over rows
       uint32_t pw[4], sw[4];
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         float pv[4], dv[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int rk = __builtin_amdgcn_ds_bpermute(4 * (16 * c + 4 * q + e), rkey);
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const int rk = __builtin_amdgcn_ds_bpermute(4 * (16 * c + 4 * q + e2), rkey);
           const bool has = rk == key;
           const float p =
-              __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[c][e], scale2, -l2v[c][e]));
-          pv[e] = has ? p : 0.f;
-          dv[e] = has ? p * (pacc[c][e] - dlv[c][e]) : 0.f;
+              __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[c][e2], scale2, -l2v[c][e2]));
+          pv[e2] = has ? p : 0.f;
+          dv[e2] = has ? p * (pacc[c][e2] - dlv[c][e2]) : 0.f;
         }
         pw[2 * c] = pack_bf16x2(pv[0], pv[1]);
         pw[2 * c + 1] = pack_bf16x2(pv[2], pv[3]);
@@ -562,9 +610,8 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
         dkacc[s] =
             mfma16(__builtin_bit_cast(bf16x8, qq), __builtin_bit_cast(bf16x8, sq), dkacc[s]);
       }
-      jc = jn;
-      rc = rn;
-      rlc = rln;
+      row_c = row_n;
+      ent_c = ent_n;
     }
     // the last step's (empty) refills have landed before the next head's
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);

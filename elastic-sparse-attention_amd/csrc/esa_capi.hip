@@ -570,6 +570,8 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
   t.nkb16 = (a->kv_len + 15) / 16;
   const int64_t n_kblk = (int64_t)a->batch * a->num_kv_heads * t.nkb16;
   if (band_dkdv && n_kblk > INT32_MAX / 2) return ESA_ERR_SHAPE;
+  // (the band dK/dV reaches lse2 from a delta row by a 32-bit buffer offset)
+  if (band_dkdv && (int64_t)a->batch * a->num_heads * t.qpad * 8 >= lim) return ESA_ERR_UNSUPPORTED;
   t.n_kblk = (int)n_kblk;
   t.kchunk = ((int64_t)a->batch * a->num_kv_heads) % 8 == 0 ? (int)(n_kblk / 8) : 8;
   return hip_status(launch_tile_bwd(t, a->head_dim, band_dq ? -1 : num_q_items,
