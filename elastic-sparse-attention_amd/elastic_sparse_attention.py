@@ -330,7 +330,9 @@ def prefill_kernel(layout: ElasticLayout, q_len: int, batch: int, head_dim: int)
 def bwd_kernels(layout: ElasticLayout, q_len: int, batch: int, head_dim: int
                 ) -> Tuple[str, str]:
     """("band" | "tile", "band" | "tile"): the faster dQ and dK/dV kernels for
-    this pattern and shape; both follow the forward's choice."""
+    this pattern and shape.  Both follow the forward's choice: over every
+    layer of six shapes (D = 64 and 128, GQA included) the fastest pair was
+    the forward's kind for both halves or within 1% of it."""
     kind = prefill_kernel(layout, q_len, batch, head_dim)
     return kind, kind
 
