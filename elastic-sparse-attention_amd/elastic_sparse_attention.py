@@ -16,8 +16,10 @@ Underneath, every call goes through libesa.so's C ABI (include/esa.h) to
 hand-written gfx950 HIP kernels:
 
 * prefill (``cache_position is None``), bf16, head_dim 64 or 128: the
-  block-sparse MFMA kernel over the block layout (CSR of active 128x128
-  tiles) built once per device by the HIP layout builder;
+  band-gathered MFMA kernel (each row's index-list entries as 16-key bands)
+  or the block-sparse MFMA kernel over the block layout (CSR of active
+  128x128 tiles, built once per device by the HIP layout builder),
+  whichever is faster for the shape (``prefill_kernel``);
 * decode (``cache_position`` given), float32, or other head dims: the
   per-row gather kernel that regenerates each row's elastic indices on the
   device.
@@ -34,9 +36,9 @@ Differences from the reference, all deliberate:
   ``None`` attention weights.  There is no CPU path: CPU tensors raise.
 * ``attention_dropout`` is ignored, as the reference's Triton path ignores it.
 * Backward: the prefill bf16 path (head_dim 64 or 128) backpropagates
-  through hand-written block-sparse MFMA kernels (deterministic, no
-  atomics); the other paths (decode rows, float32, explicit index lists)
-  raise NotImplementedError in backward.
+  through hand-written MFMA kernels, band-gathered or block-sparse like the
+  forward (deterministic, no atomics); the other paths (decode rows,
+  float32, explicit index lists) raise NotImplementedError in backward.
 * A query row with no valid entry (impossible for the elastic pattern, only
   reachable through explicit masks) gives output 0 rather than NaN.
 """
