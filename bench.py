@@ -102,19 +102,24 @@ def copy_calibration(torch) -> None:
 
 
 def time_backward(torch, m, q, k, v, lay, counted_fwd, steps, warmup) -> dict:
-    """The block-sparse backward (dQ, dK, dV from the forward's O and LSE) on
-    the same inputs: mean of `steps` launches (HIP events on the launch
-    stream) after `warmup`; the tile masks and work lists are built (and
-    cached) before timing, as the layout is.  TFLOP/s counts 2.5x the
-    forward's active-tile flops (QK^T, dP, dV, dK, dQ)."""
-    from elastic_sparse_attention import elastic_attention_bwd, elastic_attention_fwd
+    """The backward (dQ, dK, dV from the forward's O and LSE, with the
+    kernels `bwd_kernels` picks) on the same inputs: mean of `steps` launches
+    (HIP events on the launch stream) after `warmup`; for a block-sparse
+    half the tile masks and work lists are built (and cached) before timing,
+    as the layout is.  TFLOP/s counts 2.5x the forward's active-tile flops
+    (QK^T, dP, dV, dK, dQ)."""
+    from elastic_sparse_attention import bwd_kernels, elastic_attention_bwd, elastic_attention_fwd
     B, H, L, D = q.shape
     o, lse = elastic_attention_fwd(q, k, v, lay, m.scaling)
     g = torch.Generator(device="cpu").manual_seed(1)
     do = torch.randn(B, L, H, D, generator=g).to(q.dtype).to(q.device)
+    kinds = bwd_kernels(lay, L, B, D)
     t0 = time.perf_counter()
-    lay.tile_masks(L)
-    lay.bwd_plan(L, B, k.shape[1])
+    if kinds[1] == "tile":
+        lay.tile_masks(L)
+        lay.bwd_plan(L, B, k.shape[1])
+    if kinds[0] == "tile":
+        lay.schedule(L, B)
     torch.cuda.synchronize()
     setup_ms = (time.perf_counter() - t0) * 1e3
     for _ in range(warmup):
@@ -131,6 +136,7 @@ def time_backward(torch, m, q, k, v, lay, counted_fwd, steps, warmup) -> dict:
     ms = statistics.mean(a.elapsed_time(b) for a, b in evs)
     return {"ms": round(ms, 4), "tflops": round(2.5 * counted_fwd / (ms * 1e-3) / 1e12, 3),
             "flops_convention": "2.5 x forward active-tile flops",
+            "kernels": {"dq": kinds[0], "dkdv": kinds[1]},
             "mask_and_plan_setup_ms": round(setup_ms, 2)}
 
 
@@ -188,7 +194,7 @@ def main() -> None:
     ap.add_argument("--kernel", default="auto", choices=["auto", "band", "tile"],
                     help="prefill kernel the module runs (default: the faster for the shape)")
     ap.add_argument("--backward", action="store_true",
-                    help="also time the block-sparse backward (reported beside the forward)")
+                    help="also time the backward (reported beside the forward)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of known size (HBM counter scale)")
     args = ap.parse_args()
