@@ -140,6 +140,59 @@ def time_backward(torch, m, q, k, v, lay, counted_fwd, steps, warmup) -> dict:
             "mask_and_plan_setup_ms": round(setup_ms, 2)}
 
 
+DECODE = (128, 32, 8, 32768, 128)  # batch, query heads, kv heads, cache length, head dim
+
+
+def time_decode(torch, layer: int, steps: int, warmup: int) -> dict:
+    """One decode step of a serving batch: B sequences, one new query row
+    each at position L - 1 of a cache of L keys (GQA 32 / 8, bf16), through
+    esa_elastic_fwd_rows (the path the module's cache_position branch takes).
+    The C entry point is called directly with prebuilt arguments, `steps`
+    times back to back between two HIP events on the launch stream, so the
+    host's per-call cost (a few us) stays below the kernel's.  Bytes: the
+    w K rows and w V rows each (batch, head) gathers, plus Q and O."""
+    import ctypes
+    from elastic_sparse_attention import _fwd_args, _stream, make_pattern
+    from esa_native import check, load
+    B, H, Hkv, L, D = DECODE
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(3)
+    k = torch.randn(B, Hkv, L, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, L, D, device=dev, generator=g).to(torch.bfloat16)
+    q = (torch.randn(B, H, 1, D, device=dev, generator=g) * D ** -0.25).to(torch.bfloat16)
+    o = torch.empty(B, 1, H, D, dtype=torch.bfloat16, device=dev)
+    pat = make_pattern(L, W, layer, NL, H)
+    pos = torch.tensor([L - 1], dtype=torch.int64, device=dev)
+    a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), None, D ** -0.5)
+    lib = load()
+    st = _stream(dev)
+    pp = ctypes.c_void_p(pos.data_ptr())
+
+    def call():
+        check(lib.esa_elastic_fwd_rows(ctypes.byref(a), ctypes.byref(pat), pp, st),
+              "esa_elastic_fwd_rows")
+
+    for _ in range(warmup):
+        call()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        call()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    nbytes = B * H * W * D * 2 * 2 + 2 * B * H * D * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"workload": (f"decode step, bf16, B={B} sequences x 1 row, H={H} Hkv={Hkv}, "
+                         f"cache L={L}, D={D}, w={W}, layer {layer} of {NL}"),
+            "us_per_step": round(us, 2), "rows_per_s": round(B / (us * 1e-6)),
+            "gathered_bytes": nbytes,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}}
+
+
 def executed_blocks(torch, lay, L: int) -> int:
     """Number of (active tile, 32-row block, 32-key block) triples in which
     some row has a valid key, per batch element: the blocks the forward
@@ -195,6 +248,8 @@ def main() -> None:
                     help="prefill kernel the module runs (default: the faster for the shape)")
     ap.add_argument("--backward", action="store_true",
                     help="also time the backward (reported beside the forward)")
+    ap.add_argument("--decode", action="store_true",
+                    help="also time one decode step of a serving batch (reported beside)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of known size (HBM counter scale)")
     args = ap.parse_args()
@@ -320,6 +375,10 @@ def main() -> None:
                            "frac": round(tbs / L2_TO_CU_TBS, 4), "bytes": l2_bytes}
     if args.backward:
         out["backward"] = time_backward(torch, m, q, k, v, lay, counted, args.steps, args.warmup)
+    if args.decode:
+        del q, k, v
+        torch.cuda.empty_cache()
+        out["decode"] = time_decode(torch, args.layer, max(args.steps, 50), args.warmup)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.config, args.layer, counted)
     print(json.dumps(out), flush=True)
