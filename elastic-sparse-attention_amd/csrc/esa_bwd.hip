@@ -72,6 +72,9 @@ __global__ __launch_bounds__(256) void prep_kernel(BwdArgs A, float* lse2) {
   const int h = blockIdx.y, b = blockIdx.z;
   const int g = threadIdx.x & 15;
   constexpr int PER = D / 16;  // elements per lane
+  if (A.split_parts > 1 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
+    for (int i = threadIdx.x; i < A.n_bkv * A.split_blocks; i += 256)
+      A.part_cnt[i] = 0;  // split arrivals
   float acc = 0.f;
   if (row < A.q_len) {
     const uint16_t* o = A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)row * A.oss;

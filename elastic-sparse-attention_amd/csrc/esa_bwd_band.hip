@@ -317,11 +317,18 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
 //                            dO^T / Q^T read transposed from the same slots)
 // dK = scale dK^T^T.  Each (row, entry) pair lands in exactly one block and
 // one step, as in the reference's dK/dV loop (:168-233 accumulates the same
-// pairs); every gradient row is accumulated by one wave in a fixed order:
-// deterministic, no atomics.  A block's work is the number of rows using its
-// keys (the low blocks of late layers are the heaviest), and a row's Q and
-// dO serve every block holding one of its keys, so the blocks one XCD runs
-// at a time should be neighbours (one L2).  Blocks go to the eight XCDs in
+// pairs); every gradient row is accumulated in a fixed order (by one wave,
+// or by the parts of a split block added in part order): deterministic, no
+// atomics on gradients.  A block's work is the number of
+// rows using its keys, and a row's Q and dO serve every block holding one of
+// its keys, so the blocks one XCD runs at a time should be neighbours (one
+// L2).  At the last layer of a pattern key block 0 takes far more rows than
+// the rest (entry 0 of the heads with small interpolation weight stays in it
+// for thousands of rows), so the host splits blocks 0 .. split_blocks - 1
+// (block 0) over split_parts waves each: each part walks a fixed range of
+// the block's steps, stores float32 sums, and the part that arrives last (an
+// atomic counter) adds the parts in part order and writes the block, so
+// results do not depend on which wave is last.  Blocks go to the eight XCDs in
 // chunks of A.kchunk consecutive blocks, round robin: with whole kv heads
 // per XCD (batch * kv heads a multiple of 8) one chunk per XCD, each a
 // contiguous range; otherwise chunks of 8 blocks, which balance the heavy
@@ -339,12 +346,25 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
   lds_u16* const lq = (lds_u16*)qsl;
   lds_u16* const lo = (lds_u16*)osl;
 
-  // ---- block: slot k of XCD x takes block (k / chunk * 8 + x) * chunk + k % chunk
+  // ---- work item: the first n_extra workgroups take parts 1 .. split_parts
+  // - 1 of the split blocks; then slot k of XCD x takes block
+  // (k / chunk * 8 + x) * chunk + k % chunk (part 0 if split)
   const int bid = blockIdx.x;
-  const int kx = bid >> 3;
-  const int g = ((kx / A.kchunk) * 8 + (bid & 7)) * A.kchunk + kx % A.kchunk;
-  if (g >= A.n_kblk) return;
+  int g, part = 0;
+  if (bid < A.n_extra) {
+    const int n_split = A.n_bkv * A.split_blocks;
+    if (bid >= n_split * (A.split_parts - 1)) return;
+    part = 1 + bid / n_split;
+    const int sb = bid % n_split;  // (split block, b kv head), blocks outermost
+    g = (sb % A.n_bkv) * A.nkb16 + sb / A.n_bkv;
+  } else {
+    const int bj = bid - A.n_extra;  // n_extra is a multiple of 8: same XCD
+    const int kx = bj >> 3;
+    g = ((kx / A.kchunk) * 8 + (bj & 7)) * A.kchunk + kx % A.kchunk;
+    if (g >= A.n_kblk) return;
+  }
   const int bkv = g / A.nkb16, kb = g % A.nkb16;
+  const bool split = A.split_parts > 1 && kb < A.split_blocks;
   const int kvh = bkv % A.Hkv, b = bkv / A.Hkv;
   const int u0 = 16 * kb;
 
@@ -415,16 +435,18 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
   const int slot_row = lane & 31;
   const int lse_off = (int)((const char*)lse2 - (const char*)A.delta);
 
-  for (int hg = 0; hg < A.groups; ++hg) {
-    const int h = kvh * A.groups + hg;
+  // lane j of head h: rows [r0, r0 + len) whose key of entry j lies in the
+  // block (rows before u0 cannot use a key >= u0); the ranges are packed back
+  // to back: entry j's rows are positions [cum, cum + len) of one sequence,
+  // walked 32 positions per step; returns the sequence length
+  auto head_ranges = [&](int h, int& r0, int& len, int& cum) {
     const HeadWeights hw = head_weights(A.pc, h);
     auto key_at = [&](int i, int j) {
       const RowParams rp = row_params(A.pc, i);
       return interp_index(oversized(rp, j), oversized(rp, j + 1), hw);
     };
-    // lane j: rows [r0, r0 + len) whose key of entry j lies in the block
-    // (rows before u0 cannot use a key >= u0)
-    int r0 = 0, len = 0;
+    r0 = 0;
+    len = 0;
     if (lane < A.pc.w) {
       int a0 = u0, a1 = A.q_len;  // first row >= u0 with key >= u0
       while (a0 < a1) {
@@ -439,9 +461,7 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
       r0 = a0;
       len = c0 - a0;
     }
-    // the ranges are packed back to back: entry j's rows are positions
-    // [cum, cum + len) of one sequence, walked 32 positions per step
-    int cum = len;
+    cum = len;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const int t = __shfl_up(cum, off, 64);
@@ -449,7 +469,36 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
     }
     const int total = __builtin_amdgcn_readlane(cum, 63);
     cum -= len;
-    if (total == 0) continue;
+    return total;
+  };
+  // a split block's part takes steps [s_lo, s_hi) of the group's heads' step
+  // sequences laid end to end
+  int s_lo = 0, s_hi = 0x7fffffff;
+  if (split) {
+    int64_t steps = 0;
+    for (int hg = 0; hg < A.groups; ++hg) {
+      int r0, len, cum;
+      steps += (head_ranges(kvh * A.groups + hg, r0, len, cum) + ROWS - 1) / ROWS;
+    }
+    s_lo = (int)(steps * part / A.split_parts);
+    s_hi = (int)(steps * (part + 1) / A.split_parts);
+  }
+
+  int s_base = 0;  // steps of the earlier heads
+  for (int hg = 0; hg < A.groups; ++hg) {
+    const int h = kvh * A.groups + hg;
+    const HeadWeights hw = head_weights(A.pc, h);
+    auto key_at = [&](int i, int j) {
+      const RowParams rp = row_params(A.pc, i);
+      return interp_index(oversized(rp, j), oversized(rp, j + 1), hw);
+    };
+    int r0, len, cum;
+    const int total = head_ranges(h, r0, len, cum);
+    const int steps_h = (total + ROWS - 1) / ROWS;
+    const int ls0 = min(max(s_lo - s_base, 0), steps_h), ls1 = min(max(s_hi - s_base, 0), steps_h);
+    s_base += steps_h;
+    if (ls0 >= ls1) continue;
+    const int p_first = ROWS * ls0, p_end = min(total, ROWS * ls1);
     const uint64_t live = __builtin_amdgcn_ballot_w64(len > 0);
     // row and entry of slot row (lane % 32) in the step at position P (row
     // -1: none); e is the first live entry reaching past P on entry, the
@@ -507,16 +556,17 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
       __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (lds_void*)lsl, 4, ofs, 0, 0, 0);
     };
 
-    int e = (int)__builtin_ctzll(live);
+    // the first live entry reaching past the part's first position
+    int e = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(len > 0 && cum + len > p_first));
     int row_c, ent_c;
-    map_step(0, e, row_c, ent_c);
+    map_step(p_first, e, row_c, ent_c);
     issue_rows(qrs, qss2, row_c, lq);
     issue_rows(ors, oss2, row_c, lo);
     __builtin_amdgcn_s_waitcnt(kWaitLds);  // the last head's stats reads are done
     issue_stats(row_c);
-    for (int P = 0; P < total; P += ROWS) {
+    for (int P = p_first; P < p_end; P += ROWS) {
       int row_n = -1, ent_n = 0;
-      if (P + ROWS < total) map_step(P + ROWS, e, row_n, ent_n);
+      if (P + ROWS < p_end) map_step(P + ROWS, e, row_n, ent_n);
       // the key of slot row (lane % 32), -1 when masked or empty
       int rkey = -1;
       if (row_c >= 0) {
@@ -617,6 +667,41 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   }
 
+  // ---- a split block: every part stores its float32 sums; the part that
+  // arrives last adds the parts in part order (a fixed order whichever wave
+  // is last) and writes the block
+  if (split) {
+    constexpr int PART = 2 * C::NV * 4 * 64;  // floats per part
+    const int sb = bkv * A.split_blocks + kb;
+    float* const pb = A.part_buf + (int64_t)sb * A.split_parts * PART;
+    float* const mine = pb + (int64_t)part * PART;
+#pragma unroll
+    for (int s = 0; s < C::NV; ++s)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        mine[((0 * C::NV + s) * 4 + e) * 64 + lane] = dkacc[s][e];
+        mine[((1 * C::NV + s) * 4 + e) * 64 + lane] = dvacc[s][e];
+      }
+    __threadfence();  // the sums are visible to the other XCDs before arriving
+    int arrived = 0;
+    if (lane == 0) arrived = atomicAdd(&A.part_cnt[sb], 1);
+    arrived = __shfl(arrived, 0, 64);
+    if (arrived != A.split_parts - 1) return;
+    __threadfence();  // the other parts' sums, not stale copies
+#pragma unroll
+    for (int s = 0; s < C::NV; ++s) dkacc[s] = dvacc[s] = f32x4{};
+    for (int pp = 0; pp < A.split_parts; ++pp) {
+      const float* src = pb + (int64_t)pp * PART;
+#pragma unroll
+      for (int s = 0; s < C::NV; ++s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          dkacc[s][e] += src[((0 * C::NV + s) * 4 + e) * 64 + lane];
+          dvacc[s][e] += src[((1 * C::NV + s) * 4 + e) * 64 + lane];
+        }
+    }
+  }
+
   // ---- dK = scale dK^T^T, dV = dV^T^T: lane (key n, q) holds dims
   // CW q + 4 s + e of key u0 + n
   if (key_ok) {
@@ -642,7 +727,7 @@ hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,
                             hipStream_t stream) {
   if (a.n_kblk <= 0 || a.kchunk <= 0) return hipSuccess;
   const int64_t chunks = (a.n_kblk + 8 * (int64_t)a.kchunk - 1) / (8 * (int64_t)a.kchunk);
-  const dim3 grid((unsigned)(chunks * 8 * a.kchunk));
+  const dim3 grid((unsigned)(a.n_extra + chunks * 8 * a.kchunk));
   if (head_dim == 128)
     band_dkdv_kernel<128><<<grid, 64, 0, stream>>>(a, lse2);
   else

@@ -468,11 +468,37 @@ esa_status esa_build_tile_masks(const esa_pattern* p, const int32_t* row_ptr,
                                       (hipStream_t)stream));
 }
 
+// The band dK/dV's split at the last layer of a pattern (alpha = 1): entry 0
+// of a query head with interpolation weight t has key ~ t (i + 1) / w, so the
+// heads with small t put a key of each of the first blocks into about
+// 16 w / t rows, and every row's entry 0 into block 0 for t = 0.  Key block
+// 0 of every (b, kv head) (about groups * q_len / 32 steps against a mean of
+// about groups * w steps) is split over split_parts waves of about 200
+// steps each.  Measured at B=1 H=32 L=32768 D=128: with 8 kv heads the last
+// layer's backward takes 7.64 ms unsplit, 5.30 ms with block 0 split and
+// 5.47 ms with blocks 0 .. 7 split (the other heavy blocks stay under a
+// slot's share); with 32 kv heads all three are within 1.5%.
+int bwd_split_parts(const esa_bwd_args* a) {
+  const int groups = a->num_kv_heads > 0 ? a->num_heads / a->num_kv_heads : 1;
+  const int64_t p = ((int64_t)groups * a->q_len + 6143) / 6144;
+  return (int)std::min<int64_t>(std::max<int64_t>(p, 1), 32);
+}
+int bwd_split_blocks(const esa_bwd_args*) { return 1; }
+
 esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes) {
   if (!a || !workspace_bytes) return ESA_ERR_NULL;
-  if (a->batch < 0 || a->num_heads < 1 || a->q_len < 0) return ESA_ERR_SHAPE;
+  if (a->batch < 0 || a->num_heads < 1 || a->num_kv_heads < 1 || a->q_len < 0 ||
+      a->head_dim < 1)
+    return ESA_ERR_SHAPE;
   // delta and lse2 per row, rows of each (b, h) padded to qpad (bwd_qpad)
-  *workspace_bytes = (size_t)2 * a->batch * a->num_heads * bwd_qpad(a->q_len) * sizeof(float);
+  size_t bytes = (size_t)2 * a->batch * a->num_heads * bwd_qpad(a->q_len) * sizeof(float);
+  const int parts = bwd_split_parts(a);
+  if (parts > 1) {  // split partial sums and arrival counters
+    const size_t n_split = (size_t)a->batch * a->num_kv_heads * bwd_split_blocks(a);
+    bytes += n_split * parts * 2 * 16 * a->head_dim * sizeof(float);
+    bytes += (n_split * sizeof(int) + 15) / 16 * 16;
+  }
+  *workspace_bytes = bytes;
   return ESA_OK;
 }
 
@@ -574,6 +600,18 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
   if (band_dkdv && (int64_t)a->batch * a->num_heads * t.qpad * 8 >= lim) return ESA_ERR_UNSUPPORTED;
   t.n_kblk = (int)n_kblk;
   t.kchunk = ((int64_t)a->batch * a->num_kv_heads) % 8 == 0 ? (int)(n_kblk / 8) : 8;
+  t.split_parts = 1;
+  t.split_blocks = 0;
+  t.n_bkv = a->batch * a->num_kv_heads;
+  if (band_dkdv && t.pc.a == 1.0f && bwd_split_parts(a) > 1) {
+    t.split_parts = bwd_split_parts(a);
+    t.split_blocks = bwd_split_blocks(a);
+    const int64_t n_split = (int64_t)t.n_bkv * t.split_blocks;
+    if (n_split * (t.split_parts - 1) > INT32_MAX / 2) return ESA_ERR_SHAPE;
+    t.n_extra = (int)((n_split * (t.split_parts - 1) + 7) / 8 * 8);
+    t.part_buf = (float*)workspace + (int64_t)2 * a->batch * a->num_heads * t.qpad;
+    t.part_cnt = (int*)(t.part_buf + n_split * t.split_parts * 2 * 16 * a->head_dim);
+  }
   return hip_status(launch_tile_bwd(t, a->head_dim, band_dq ? -1 : num_q_items,
                                     band_dkdv ? -1 : num_kv_items, (hipStream_t)stream));
 }

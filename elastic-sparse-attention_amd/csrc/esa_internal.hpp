@@ -121,6 +121,14 @@ struct BwdArgs {
   // band-gathered dK / dV (when kv_items is NULL): 16-key blocks per
   // (b, kv head), all blocks, consecutive blocks per XCD chunk
   int nkb16, n_kblk, kchunk;
+  // key blocks 0 .. split_blocks - 1 of each (b, kv head) split over
+  // split_parts waves (1: not split); n_bkv = B * Hkv; n_extra workgroups (a
+  // multiple of 8) run the parts after the first; part_buf: float32 partial
+  // sums [n_bkv][split_blocks][split_parts][2][D / 16][4][64]; part_cnt:
+  // arrivals [n_bkv][split_blocks]
+  int split_parts, split_blocks, n_bkv, n_extra;
+  float* part_buf;
+  int* part_cnt;
 };
 
 hipError_t launch_indices(const PatternConsts& pc, int row0, int nrows, void* indices, void* mask,

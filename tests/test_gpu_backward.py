@@ -44,6 +44,8 @@ def rel_err(got, ref):
     (1, 3, 3, 1024, 1024, 128, 1),   # odd head count: bands of 17 keys (band dQ tail)
     (1, 6, 2, 777, 777, 64, 7),      # last layer: key 0 in every row of head 0
     (1, 2, 2, 64, 64, 128, 3),       # one row block, rows 0 .. w - 1 only
+    (1, 8, 2, 2048, 2048, 128, 7),   # last layer, GQA: band dK/dV splits key block 0 (2 parts)
+    (2, 4, 1, 3000, 3000, 64, 7),    # the same with batch 2, MQA, D = 64, ragged rows
 ])
 def test_backward_matches_autograd(B, H, Hkv, L, Lq, D, layer, kernels):
     """kernels: dQ kernel / dK-dV kernel."""
@@ -112,10 +114,42 @@ def test_backward_full_size_8k_layer4():
         assert max(e) <= REL
 
 
+def test_backward_last_layer_split_8k():
+    """Last layer, GQA 8 / 2, L = 8192: the band dK/dV splits key block 0 of
+    each kv head over 6 waves and adds their float32 partial sums in part
+    order.  Each kv head's gradients against autograd through
+    the oracle (the kv head's four query heads), and two runs bit-identical."""
+    B, H, Hkv, L, D, layer = 1, 8, 2, 8192, 128, 7
+    print(f"bwd last-layer split B={B} H={H} Hkv={Hkv} L={L} D={D}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=41, scale=D ** -0.25)
+    sc = scaling_for(D)
+    g = torch.randn(B, H, L, D, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc)
+    do = g.to(DEV).permute(0, 2, 1, 3).contiguous()
+    got = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="band",
+                                dkdv_kernel="band")
+    again = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="band",
+                                  dkdv_kernel="band")
+    assert all(torch.equal(x, y) for x, y in zip(got, again))
+    dq, dk, dv = got
+    idx, msk = elastic_indices(L, layer, 8, H, 64)
+    for kvh in range(Hkv):
+        hs = slice(4 * kvh, 4 * kvh + 4)
+        rq, rk, rv = reference_grads(q[:, hs], k[:, kvh:kvh + 1], v[:, kvh:kvh + 1], idx[hs],
+                                     msk[hs], sc, 4, g[:, hs].float())
+        e = (rel_err(dq[:, hs], rq), rel_err(dk[:, kvh:kvh + 1], rk),
+             rel_err(dv[:, kvh:kvh + 1], rv))
+        print(f"  kv head {kvh} rel err dq {e[0]:.3e} dk {e[1]:.3e} dv {e[2]:.3e}", flush=True)
+        assert max(e) <= REL
+
+
 @pytest.mark.parametrize("kernels", ["tile/tile", "band/band"])
 @pytest.mark.parametrize("B,H,Hkv,L,D,layer", [
     (1, 32, 32, 32768, 128, 4),   # the headline shape
-    (1, 32, 32, 32768, 128, 7),
+    (1, 32, 32, 32768, 128, 7),   # last layer: band dK/dV splits key block 0 (6 parts)
+    (1, 32, 8, 32768, 128, 7),    # GQA last layer (22 parts)
     (2, 8, 2, 8192, 64, 5),       # GQA, D = 64
 ])
 def test_backward_identities_full_size(B, H, Hkv, L, D, layer, kernels):
@@ -152,15 +186,15 @@ def test_backward_identities_full_size(B, H, Hkv, L, D, layer, kernels):
     assert r_v <= 1e-3 and r_k <= 1e-3
 
 
-@pytest.mark.parametrize("layer", [0, 4, 7])
-def test_band_matches_tile_full_size(layer):
+@pytest.mark.parametrize("layer,Hkv", [(0, 32), (4, 32), (7, 32), (7, 8)])
+def test_band_matches_tile_full_size(layer, Hkv):
     """The headline shape: dQ, dK and dV from the band kernels against the
     block-sparse kernels (independent paths over the same O and LSE), max
     |difference| <= 2e-2 * max |tile gradient| per tensor; each half of one
     kind leaves the other half bit-identical."""
     B, H, L, D = 1, 32, 32768, 128
-    print(f"band vs tile backward B={B} H={H} L={L} D={D} layer={layer}", flush=True)
-    q, k, v = seeded_inputs(B, H, H, L, D, torch.bfloat16, seed=110 + layer, scale=D ** -0.25)
+    print(f"band vs tile backward B={B} H={H} Hkv={Hkv} L={L} D={D} layer={layer}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=110 + layer, scale=D ** -0.25)
     sc = scaling_for(D)
     lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
     qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
