@@ -255,17 +255,24 @@ esa_status esa_build_tile_masks(const esa_pattern* p, const int32_t* row_ptr,
                                 uint32_t* mask_t, int64_t mask_capacity,
                                 void* stream);
 
-/* Host only.  Bytes of float32 workspace esa_elastic_bwd needs:
+/* Host only.  Bytes of workspace esa_elastic_bwd needs:
  * 2 * batch * num_heads * qpad floats, qpad = q_len rounded up to 32, plus
- * 32 (per-row delta and log2 LSE). */
+ * 32 (per-row delta and log2 LSE), and, when the band dK/dV may split key
+ * block 0 (num_heads / num_kv_heads * q_len > 6144), P float32 partial
+ * sums of 2 * 16 * head_dim floats and one counter per (batch, kv head),
+ * P = that product / 6144 rounded up, at most 32.  Requires num_kv_heads
+ * and head_dim >= 1. */
 esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes);
 
 /* Backward over the elastic pattern: replaces the backward branch of the
  * Triton kernel (elastic_sparse_attention.py:168-233) and
  * ElasticSparseAttentionFunction.backward (:299-339) for the prefill
  * forward (esa_elastic_fwd or esa_elastic_fwd_band: any O and LSE of it).  Writes dq, dk and dv (every element; no
- * zero-initialisation needed, no atomics: each gradient row is accumulated
- * by one workgroup in a fixed order, so results are deterministic).
+ * zero-initialisation needed, and deterministic: each gradient row is
+ * accumulated by one workgroup in a fixed order, except that at the last
+ * layer (alpha = 1) the band dK/dV splits key block 0 over several waves
+ * whose float32 sums the last to arrive (an atomic counter in the
+ * workspace) adds in part order; no atomics on the gradients).
  * q_items/num_q_items: esa_plan_schedule's list for (q_len, batch), for a
  * block-sparse dQ over the layout row_ptr/col_idx; q_items NULL computes dQ
  * with the band-gathered kernel instead (as esa_elastic_fwd_band gathers:
