@@ -75,6 +75,33 @@ def test_backward_matches_autograd(B, H, Hkv, L, Lq, D, layer, kernels):
     assert torch.equal(dq, dq2) and torch.equal(dk, dk2) and torch.equal(dv, dv2)
 
 
+@pytest.mark.parametrize("kernels", ["tile/tile", "band/band"])
+@pytest.mark.parametrize("B,H,Hkv,L,D,layer,w", [
+    (1, 4, 2, 1000, 128, 5, 33),   # odd index-list length: lanes 33 .. 63 idle
+    (1, 3, 1, 700, 64, 7, 16),     # short lists, last layer, MQA
+    (2, 1, 1, 513, 128, 3, 64),    # one head (interpolation weight 0), ragged
+])
+def test_backward_attention_lengths(B, H, Hkv, L, D, layer, w, kernels):
+    """Index lists shorter than 64 entries and a single head, both halves of
+    either kind, against autograd through the oracle."""
+    dq_kernel, dkdv_kernel = kernels.split("/")
+    print(f"bwd B={B} H={H} Hkv={Hkv} L={L} D={D} layer={layer} w={w} {kernels}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=layer + w, scale=1.0)
+    idx, msk = elastic_indices(L, layer, 8, H, w)
+    sc = scaling_for(D)
+    g = torch.randn(B, H, L, D, generator=torch.Generator().manual_seed(w)).to(torch.bfloat16)
+    rq, rk, rv = reference_grads(q, k, v, idx, msk, sc, H // Hkv, g.float())
+    lay = ElasticLayout(make_pattern(L, w, layer, 8, H), DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc)
+    do = g.to(DEV).permute(0, 2, 1, 3).contiguous()
+    dq, dk, dv = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel=dq_kernel,
+                                       dkdv_kernel=dkdv_kernel)
+    e = (rel_err(dq, rq), rel_err(dk, rk), rel_err(dv, rv))
+    print(f"  rel err dq {e[0]:.3e} dk {e[1]:.3e} dv {e[2]:.3e}", flush=True)
+    assert max(e) <= REL
+
+
 def test_module_autograd():
     """The drop-in module's output backpropagates through the HIP backward."""
     B, H, L, D, layer = 1, 4, 768, 128, 4
