@@ -80,7 +80,8 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   }
 
   int kreg[16], info[16];
-  band_rows(A.pc, h, i, row_ok, q, kreg, info);
+  // entry rotation: 64 / 256 resident waves per XCD per dispatched group
+  band_rows(A.pc, h, i, row_ok, q, ((bid >> 3) / 4) & 63, kreg, info);
 
   const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
   const char* const vbase = (const char*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh);

@@ -95,7 +95,9 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   // ---- this row's keys of bands 16 q .. 16 q + 15 (-1: no key), and the
   // group's band descriptors for the same bands (every lane of group q)
   int kreg[16], info[16];
-  band_rows(A.pc, h, i, row_ok, q, kreg, info);
+  // entry rotation: about 64 / 320 resident waves per XCD (LDS holds ten
+  // waves per CU) per dispatched group, 3/16
+  band_rows(A.pc, h, i, row_ok, q, ((bid >> 3) * 3 / 16) & 63, kreg, info);
 
   const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
   const char* const vbase = (const char*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh);
