@@ -293,6 +293,70 @@ def test_rows_decode_positions():
     assert (lse.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
 
 
+@pytest.mark.parametrize("dtype,D,w,layer", [
+    (torch.float32, 128, 64, 4),    # 32-key chunks: two per row
+    (torch.float32, 128, 100, 6),   # four chunks, the last partial
+    (torch.bfloat16, 256, 64, 5),   # 32 lanes per row, 32-key chunks
+    (torch.bfloat16, 128, 100, 7),  # 64-key chunks: two, the second partial
+    (torch.float32, 256, 48, 2),    # 64 lanes per row, 16-key chunks
+])
+def test_rows_chunks_and_head_dims(dtype, D, w, layer):
+    """The cooperative-row gather at every chunk split it uses (rows of D
+    elements read by D * size / 16 lanes, chunks of 64 / 32 / 16 keys) and
+    index lists longer than one chunk, against the float32 oracle."""
+    B, H, Hkv, L = 1, 4, 2, 700
+    print(f"rows {dtype} D={D} w={w} layer={layer}", flush=True)
+    q, k, v, idx, msk = case(B, H, Hkv, L, D, dtype, layer, w=w, seed=w + D, scale=1.0)
+    sc = scaling_for(D)
+    o, lse = elastic_attention_rows(q.to(DEV), k.to(DEV), v.to(DEV),
+                                    make_pattern(L, w, layer, 8, H), sc)
+    ro, rl = oracle(q, k, v, idx, msk, sc, H // Hkv)
+    tol, ltol = (F32_TOL, F32_TOL) if dtype == torch.float32 else (BF16_TOL, BF16_LSE_TOL)
+    assert (to_bhsd(o).float().cpu() - ro).abs().max().item() <= tol
+    assert (lse.cpu() - rl).abs().max().item() <= ltol
+
+
+def test_rows_unaligned_rows_take_the_per_lane_gather():
+    """bf16 K rows 132 elements apart (264 bytes: not a 16-byte multiple)
+    take the per-lane gather; both kernels meet the bar against the oracle."""
+    B, H, L, D, layer = 1, 2, 600, 128, 3
+    q, k, v, idx, msk = case(B, H, H, L, D, torch.bfloat16, layer, seed=9, scale=1.0)
+    kw = torch.zeros(B, H, L, 132, dtype=torch.bfloat16)
+    kw[..., :D] = k
+    sc = scaling_for(D)
+    pat = make_pattern(L, 64, layer, 8, H)
+    o1, l1 = elastic_attention_rows(q.to(DEV), kw.to(DEV)[..., :D], v.to(DEV), pat, sc)
+    o2, l2 = elastic_attention_rows(q.to(DEV), k.to(DEV), v.to(DEV), pat, sc)
+    ro, rl = oracle(q, k, v, idx, msk, sc, 1)
+    for o, lse in ((o1, l1), (o2, l2)):
+        assert (to_bhsd(o).float().cpu() - ro).abs().max().item() <= BF16_TOL
+        assert (lse.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
+
+
+def test_operator_out_of_range_cooperative_rows():
+    """Explicit indices with duplicates, out-of-range entries and an empty row
+    at D = 128 (the cooperative-row gather): a valid out-of-range index scores
+    0 against a zero key / value."""
+    B, H, L, D, w = 1, 2, 300, 128, 80
+    g = torch.Generator().manual_seed(5)
+    q, k, v = seeded_inputs(B, H, H, L, D, torch.float32, seed=11)
+    idx = torch.randint(-5, L + 5, (H, L, w), generator=g)
+    idx[:, :, 3] = idx[:, :, 2]
+    msk = (torch.rand(H, L, w, generator=g) > 0.2).long()
+    msk[:, 11] = 0
+    sc = 0.15
+    o, lse = sparse_attention_fwd(q.to(DEV), k.to(DEV), v.to(DEV), idx.to(DEV), msk.to(DEV), sc, 1)
+    oor = (idx < 0) | (idx >= L)
+    k2 = torch.cat([k, torch.zeros(B, H, 1, D)], dim=2)
+    v2 = torch.cat([v, torch.zeros(B, H, 1, D)], dim=2)
+    idx2 = torch.where(oor, torch.full_like(idx, L), idx)
+    ro, rl = forward_fp32(q, k2, v2, idx2, msk, sc, 1)
+    assert (o.cpu() - ro).abs().max().item() <= F32_TOL
+    finite = torch.isfinite(rl)
+    assert (lse.cpu()[finite] - rl[finite]).abs().max().item() <= F32_TOL
+    assert torch.equal(o.cpu()[:, :, 11], torch.zeros(B, H, D))
+
+
 # ---------------------------------------------------------------- explicit-index operator
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, F32_TOL), (torch.bfloat16, BF16_TOL)])
 def test_operator_with_reference_indices(dtype, tol):
