@@ -366,6 +366,12 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
   }
   const int bkv = g / A.nkb16, kb = g % A.nkb16;
   const bool split = A.split_parts > 1 && kb < A.split_blocks;
+  // entry rotation (as in band_rows): lane r of the walk holds entry
+  // (r + rot) mod 64, rot growing by 1/4 entry per block dispatched on the
+  // XCD (256 resident waves), so the blocks resident at once walk
+  // neighbouring entries and share Q / dO rows in L2.  The parts of a split
+  // block walk one sequence: no rotation there.
+  const int rot = split ? 0 : (((bid - A.n_extra) >> 3) / 4) & 63;
   const int kvh = bkv % A.Hkv, b = bkv / A.Hkv;
   const int u0 = 16 * kb;
 
@@ -436,10 +442,11 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
   const int slot_row = lane & 31;
   const int lse_off = (int)((const char*)lse2 - (const char*)A.delta);
 
-  // lane j of head h: rows [r0, r0 + len) whose key of entry j lies in the
-  // block (rows before u0 cannot use a key >= u0); the ranges are packed back
-  // to back: entry j's rows are positions [cum, cum + len) of one sequence,
-  // walked 32 positions per step; returns the sequence length
+  // lane r of head h, entry j = (r + rot) mod 64: rows [r0, r0 + len) whose
+  // key of entry j lies in the block (rows before u0 cannot use a key >= u0);
+  // the ranges are packed back to back in lane order: lane r's rows are
+  // positions [cum, cum + len) of one sequence, walked 32 positions per step;
+  // returns the sequence length
   auto head_ranges = [&](int h, int& r0, int& len, int& cum) {
     const HeadWeights hw = head_weights(A.pc, h);
     auto key_at = [&](int i, int j) {
@@ -448,16 +455,17 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
     };
     r0 = 0;
     len = 0;
-    if (lane < A.pc.w) {
+    const int ej = (lane + rot) & 63;
+    if (ej < A.pc.w) {
       int a0 = u0, a1 = A.q_len;  // first row >= u0 with key >= u0
       while (a0 < a1) {
         const int mid = (a0 + a1) >> 1;
-        if (key_at(mid, lane) >= u0) a1 = mid; else a0 = mid + 1;
+        if (key_at(mid, ej) >= u0) a1 = mid; else a0 = mid + 1;
       }
       int c0 = a0, c1 = A.q_len;  // first row with key >= u0 + 16
       while (c0 < c1) {
         const int mid = (c0 + c1) >> 1;
-        if (key_at(mid, lane) >= u0 + 16) c1 = mid; else c0 = mid + 1;
+        if (key_at(mid, ej) >= u0 + 16) c1 = mid; else c0 = mid + 1;
       }
       r0 = a0;
       len = c0 - a0;
@@ -501,9 +509,10 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
     if (ls0 >= ls1) continue;
     const int p_first = ROWS * ls0, p_end = min(total, ROWS * ls1);
     const uint64_t live = __builtin_amdgcn_ballot_w64(len > 0);
-    // row and entry of slot row (lane % 32) in the step at position P (row
-    // -1: none); e is the first live entry reaching past P on entry, the
-    // first reaching past P + 32 on return
+    // row and walk lane of slot row (lane % 32) in the step at position P
+    // (row -1: none; the lane's entry is (lane + rot) mod 64); e is the first
+    // live lane reaching past P on entry, the first reaching past P + 32 on
+    // return
     auto map_step = [&](int P, int& e, int& row, int& ent) {
       row = -1;
       ent = 0;
@@ -571,7 +580,7 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
       // the key of slot row (lane % 32), -1 when masked or empty
       int rkey = -1;
       if (row_c >= 0) {
-        const int kk = key_at(row_c, ent_c);
+        const int kk = key_at(row_c, (ent_c + rot) & 63);
         rkey = kk <= row_c ? kk : -1;
       }
 
