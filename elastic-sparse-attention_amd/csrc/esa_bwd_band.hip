@@ -303,12 +303,13 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
 // [u0, u0 + 16)).  Entry j's key is nondecreasing in the row (the window
 // start, the spacing and both interpolated terms of the recipe never
 // decrease), so for each query head of the kv group and each entry j the
-// rows whose key of entry j lies in the block form one range; lane j finds
-// it by binary search.  The ranges are packed back to back and walked 32
-// rows at a time (a step may hold rows of several entries): each slot row's
-// Q and dO row is staged in LDS by buffer_load ... lds with per-lane row
-// offsets (empty slot rows read as zeros), its delta and lse2 by a one-dword
-// DMA, then
+// rows whose key of entry j lies in the block form one range, which one lane
+// finds by binary search (lane r takes entry (r + rot) mod 64, see below).
+// The ranges are packed back to back in lane order and walked 32 rows at a
+// time (a step may hold rows of several entries): each slot row's Q and dO
+// row is staged in LDS by buffer_load ... lds with per-lane row offsets
+// (empty slot rows read as zeros), its delta and lse2 by a one-dword DMA,
+// then
 //   S = Q K^T, dP = dO V^T   2 x D/32 MFMAs each (A = Q / dO rows from LDS,
 //                            B = the block's K / V in registers)
 //   P = exp2(S scale log2e - lse2), dS = P (dP - delta) on the (row, key)
@@ -320,20 +321,24 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
 // one step, as in the reference's dK/dV loop (:168-233 accumulates the same
 // pairs); every gradient row is accumulated in a fixed order (by one wave,
 // or by the parts of a split block added in part order): deterministic, no
-// atomics on gradients.  A block's work is the number of
-// rows using its keys, and a row's Q and dO serve every block holding one of
-// its keys, so the blocks one XCD runs at a time should be neighbours (one
-// L2).  At the last layer of a pattern key block 0 takes far more rows than
-// the rest (entry 0 of the heads with small interpolation weight stays in it
-// for thousands of rows), so the host splits blocks 0 .. split_blocks - 1
-// (block 0) over split_parts waves each: each part walks a fixed range of
-// the block's steps, stores float32 sums, and the part that arrives last (an
-// atomic counter) adds the parts in part order and writes the block, so
-// results do not depend on which wave is last.  Blocks go to the eight XCDs in
-// chunks of A.kchunk consecutive blocks, round robin: with whole kv heads
-// per XCD (batch * kv heads a multiple of 8) one chunk per XCD, each a
-// contiguous range; otherwise chunks of 8 blocks, which balance the heavy
-// low blocks over the XCDs.
+// atomics on gradients.
+//
+// Schedule.  A row's Q and dO serve every block holding one of its keys, so
+// the blocks one XCD runs at a time should be neighbours (one L2): blocks go
+// to the eight XCDs in chunks of A.kchunk consecutive blocks, round robin
+// (with whole kv heads per XCD, batch * kv heads a multiple of 8, one chunk
+// per XCD, each a contiguous range; otherwise chunks of 8 blocks, which
+// balance the heavy low blocks over the XCDs), and each block starts its
+// walk at entry rot, 1/4 entry further per block dispatched on the XCD, so
+// the resident blocks walk neighbouring entries (the rotation of
+// band_rows).  At the last layer of a pattern key block 0 takes far more
+// rows than the rest (entry 0 of the heads with small interpolation weight
+// stays in it for thousands of rows), so the host splits blocks
+// 0 .. split_blocks - 1 (block 0) over split_parts waves each: each part
+// walks a fixed range of the block's steps (unrotated), stores float32 sums,
+// and the part that arrives last (an atomic counter) adds the parts in part
+// order and writes the block, so results do not depend on which wave is
+// last.
 
 template <int D>
 __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float* lse2) {
