@@ -322,6 +322,38 @@ def test_bwd_entry_points_reject_bad_arguments():
         == en.ESA_ERR_SHAPE
 
 
+def test_bwd_workspace_size_with_split():
+    """Above groups * q_len = 6144 the workspace also holds the band dK/dV's
+    split of key block 0: P = ceil(groups * q_len / 6144) (at most 32)
+    float32 partial sums of 2 * 16 * D floats and one counter per (batch, kv
+    head), after the 2 * B * H * qpad floats of delta and lse2 (each part of
+    the workspace 16-byte aligned, the total rounded up to 256 bytes)."""
+    lib = en.load()
+
+    def size(B, H, Hkv, q_len, D):
+        a = en.EsaBwdArgs()
+        a.batch, a.num_heads, a.num_kv_heads, a.q_len, a.kv_len, a.head_dim = B, H, Hkv, q_len, \
+            q_len, D
+        a.dout_stride_s = D
+        ws = ctypes.c_size_t()
+        assert lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(ws)) == en.ESA_OK
+        return ws.value
+
+    def expect(B, H, Hkv, q_len, D):
+        qpad = (q_len + 31) // 32 * 32 + 32
+        n = 2 * B * H * qpad * 4
+        parts = min(max(-(-(H // Hkv) * q_len // 6144), 1), 32)
+        if parts > 1:
+            n += B * Hkv * parts * 2 * 16 * D * 4 + (B * Hkv * 4 + 15) // 16 * 16
+        return n
+
+    for shape in [(1, 8, 2, 8192, 128), (2, 4, 4, 6144, 64), (1, 4, 4, 6145, 64),
+                  (1, 32, 8, 32768, 128), (1, 64, 1, 131072, 128), (3, 6, 3, 100, 64)]:
+        assert size(*shape) == expect(*shape), shape
+    # 6144 rows of one group: no split; one more row: two parts
+    assert size(1, 1, 1, 6144, 64) == expect(1, 1, 1, 6144, 64) == 2 * (6144 + 32) * 4
+
+
 def test_reachability_rejects_bad_arguments():
     lib = en.load()
     f1, f2 = ctypes.c_void_p(4096), ctypes.c_void_p(8192)
