@@ -541,7 +541,8 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
 
 
 class _ElasticTileAttention(torch.autograd.Function):
-    """Prefill forward (either kernel) with the block-sparse backward:
+    """Prefill forward (either kernel) with the MFMA backward (kernels as
+    :func:`bwd_kernels` picks):
     ``apply(q, k, v, layout, scaling, kernel) -> o [B, Lq, H, D]``."""
 
     @staticmethod
