@@ -241,3 +241,29 @@ def test_band_matches_tile_full_size(layer, Hkv):
         assert r <= REL
     assert torch.equal(tt[1], bt[1]) and torch.equal(tt[2], bt[2])
     assert torch.equal(bt[0], bb[0])
+
+
+@pytest.mark.parametrize("kernels", ["tile/tile", "band/band"])
+def test_strided_views_match_contiguous(kernels):
+    """q, k, v as [B, H, L, D] views of [B, L, H, D] storage (a projection's
+    output transposed, the usual caller layout): the forward and both
+    backward halves read them through their strides, so O, LSE, dQ, dK and dV
+    equal the contiguous inputs' bit for bit."""
+    kind, dkdv_kind = kernels.split("/")
+    B, H, Hkv, L, D, layer = 2, 8, 2, 1536, 128, 6
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=17, scale=D ** -0.25)
+    sc = scaling_for(D)
+    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+    qc, kc, vc = q.to(DEV), k.to(DEV), v.to(DEV)
+    qs, ks, vs = (t.transpose(1, 2).contiguous().to(DEV).transpose(1, 2) for t in (q, k, v))
+    assert not qs.is_contiguous() and torch.equal(qs, qc)
+    g = torch.randn(B, L, H, D, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    do = g.to(DEV)
+    res = []
+    for qq, kk, vv in ((qc, kc, vc), (qs, ks, vs)):
+        o, lse = elastic_attention_fwd(qq, kk, vv, lay, sc, kernel=kind)
+        grads = elastic_attention_bwd(qq, kk, vv, o, lse, do, lay, sc, dq_kernel=kind,
+                                      dkdv_kernel=dkdv_kind)
+        res.append((o, lse) + tuple(grads))
+    for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), *res):
+        assert torch.equal(x, y), name
