@@ -178,6 +178,7 @@ def test_backward_last_layer_split_8k():
     (1, 32, 32, 32768, 128, 7),   # last layer: band dK/dV splits key block 0 (6 parts)
     (1, 32, 8, 32768, 128, 7),    # GQA last layer (22 parts)
     (2, 8, 2, 8192, 64, 5),       # GQA, D = 64
+    (1, 8, 8, 131072, 128, 4),    # the long-context configuration
 ])
 def test_backward_identities_full_size(B, H, Hkv, L, D, layer, kernels):
     """Size-independent checks at full size.  Every row of P sums to one, so
