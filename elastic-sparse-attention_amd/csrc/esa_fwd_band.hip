@@ -47,7 +47,12 @@ namespace esa {
 
 // Band descriptor word: lo | W << 24 (W = keys from lo to the band's largest
 // valid key, 0 for a band no row of the group uses); lo < 2^24 (host check).
-template <int D>
+//
+// KSKIP: issue only the K DMAs that reach a band row (see load_rows).  Pays
+// where many bands are narrower than 16 keys (the dilated, late layers);
+// where nearly every band is 16 keys wide the run-time waits cost more than
+// the DMAs saved, so the host picks it by the pattern's interpolation weight.
+template <int D, bool KSKIP>
 __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   using C = BandCfg<D>;
   // K and V slots of the pair's two bands (separate objects, so the compiler
@@ -119,20 +124,46 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   }
   // K or V rows of band info word `bi` -> slot dst, through a buffer resource
   // that starts at the band's first row and holds its W rows: rows past the
-  // band fall outside num_records and read as zeros without a fetch.  A
-  // fixed number of loads per band keeps the vmcnt waits below exact.
-  auto load_rows = [&](const char* base, int ss2, const int* ofs, int bi,
-                       lds_u16* dst) {
+  // band fall outside num_records and read as zeros without a fetch.  V
+  // always takes VLOADS DMAs, so its slot rows past the band are zeros (they
+  // meet p = 0 in PV, and 0 * Inf would be NaN).  K takes VLOADS too, or
+  // with KSKIP only the ceil(W / RPI) that reach a band row (each DMA costs
+  // the texture unit a full 64-lane transfer, rows past W included): K rows
+  // past the band then keep older finite contents, whose scores belong to
+  // keys no row picks.  The vmcnt waits below count the DMAs issued.
+  constexpr int RPI = 64 / C::CPR;  // slot rows per DMA
+  auto n_loads = [&](int bi) { return (min((int)((uint32_t)bi >> 24), 16) + RPI - 1) / RPI; };
+  auto load_rows = [&](const char* base, int ss2, const int* ofs, int bi, lds_u16* dst,
+                       bool all) {
     const int lo = bi & 0xffffff, wdt = (int)((uint32_t)bi >> 24);
+    const int nl = __builtin_amdgcn_readfirstlane(n_loads(bi));
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(base + (int64_t)lo * ss2), (short)0, min(wdt, 16) * ss2, 0x00020000);
+        (void*)(base + (int64_t)lo * ss2), (short)0,
+        __builtin_amdgcn_readfirstlane(min(wdt, 16) * ss2), 0x00020000);
 #pragma unroll
-    for (int t = 0; t < C::VLOADS; ++t)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + 512 * t), 16, ofs[t], 0, 0,
-                                               0);
+    for (int t = 0; t < C::VLOADS; ++t) {
+      if (all || t < nl)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + 512 * t), 16, ofs[t], 0,
+                                                 0, 0);
+    }
   };
-  auto load_k = [&](int bi, lds_u16* dst) { load_rows(kbase, kss2, kofs, bi, dst); };
-  auto load_v = [&](int bi, lds_u16* dst) { load_rows(vbase, vss2, vofs, bi, dst); };
+  auto load_k = [&](int bi, lds_u16* dst) { load_rows(kbase, kss2, kofs, bi, dst, !KSKIP); };
+  auto load_v = [&](int bi, lds_u16* dst) { load_rows(vbase, vss2, vofs, bi, dst, true); };
+  // s_waitcnt vmcnt(n) for a count known only at run time (0 .. 8)
+  auto wait_vm = [&](int n) {
+    switch (n) {
+      case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+      case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+      case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+      case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+      case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+      case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+      case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+      case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+      default: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    }
+  };
+  static_assert(2 * C::VLOADS <= 8, "wait_vm covers at most 8 DMAs in flight");
 
   // K operand read addresses (bytes within a slot) for k-step s: lane
   // (m = n, q) reads key row n, dims 32 s + 8 q .. + 8
@@ -238,8 +269,9 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
 
   // ---- main loop: band pairs (2 p, 2 p + 1).  Load order per pair: K of
   // the next pair (after this pair's K reads), then V of the next pair (after
-  // this pair's PV), so before either wait exactly 2 VLOADS newer loads may
-  // be in flight.
+  // this pair's PV).  So before the K wait exactly this pair's 2 VLOADS V
+  // DMAs may be newer, and before the V wait the next pair's K DMAs (2 VLOADS
+  // of them, or with KSKIP as many as load_k issued).
   constexpr int kWaitPair = (0xF70 & ~0xF) | ((2 * C::VLOADS) & 0xF) |
                             (((2 * C::VLOADS) >> 4) << 14);  // vmcnt(2 VLOADS)
   constexpr int kWaitLds = 0xC07F;                           // lgkmcnt(0)
@@ -270,6 +302,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
         nb = more ? __builtin_amdgcn_readlane(info[1], 16 * qj + 16) : 0;
       }
       const bool live = (ia | ib) != 0;  // some row of the group uses a band
+      const int n_nxt = KSKIP ? n_loads(na) + n_loads(nb) : 2 * C::VLOADS;  // next K DMAs
       __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's K is in LDS
       bf16x8 kopa[C::NS], kopb[C::NS];
       if (live) {
@@ -291,11 +324,20 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
         const float xb = pick(sb, keyb, ib & 0xffffff, hb, eb);
         uint64_t pa, pbw;
         pair_softmax(xa, ha, ea, xb, hb, eb, pa, pbw);
-        __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's V is in LDS
+        // this pair's V is in LDS
+        if constexpr (KSKIP)
+          wait_vm(n_nxt);
+        else
+          __builtin_amdgcn_s_waitcnt(kWaitPair);
         pv(vs0, vs1, pa, pbw);
       }
       // this pair's V has landed (and been read): refill the V slots
-      __builtin_amdgcn_s_waitcnt(kWaitPair & kWaitLds);
+      if constexpr (KSKIP) {
+        wait_vm(n_nxt);
+        __builtin_amdgcn_s_waitcnt(kWaitLds);
+      } else {
+        __builtin_amdgcn_s_waitcnt(kWaitPair & kWaitLds);
+      }
       load_v(na, lv0);
       load_v(nb, lv1);
     }
@@ -363,10 +405,21 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
 hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) {
   if (a.n_groups <= 0) return hipSuccess;
   dim3 grid((unsigned)(8 * a.per_xcd));
-  if (head_dim == 128)
-    band_fwd_kernel<128><<<grid, 64, 0, stream>>>(a);
-  else
-    band_fwd_kernel<64><<<grid, 64, 0, stream>>>(a);
+  // K DMA skipping from interpolation weight 1/2 on: measured at B=1, H=32,
+  // L=32768, D=128, w=64 over 8 layers: 1-7% faster at weights 4/7 .. 1,
+  // even at 3/7, 3-4% slower at 1/7 and 2/7
+  const bool kskip = a.pc.a >= 0.5f;
+  if (head_dim == 128) {
+    if (kskip)
+      band_fwd_kernel<128, true><<<grid, 64, 0, stream>>>(a);
+    else
+      band_fwd_kernel<128, false><<<grid, 64, 0, stream>>>(a);
+  } else {
+    if (kskip)
+      band_fwd_kernel<64, true><<<grid, 64, 0, stream>>>(a);
+    else
+      band_fwd_kernel<64, false><<<grid, 64, 0, stream>>>(a);
+  }
   return hipGetLastError();
 }
 
