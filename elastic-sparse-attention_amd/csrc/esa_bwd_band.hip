@@ -25,7 +25,10 @@
 
 namespace esa {
 
-template <int D>
+// VSKIP: issue only the V DMAs that reach a band row (see load_rows); the
+// host picks it where many bands are narrower than 16 keys, as for the
+// forward's K DMA skip.
+template <int D, bool VSKIP>
 __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* lse2) {
   using C = BandCfg<D>;
   __shared__ __attribute__((aligned(1024))) uint16_t ks0[C::SLOT];
@@ -101,18 +104,45 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
     vofs[t] = R * vss2 + 16 * kswz<D>(R, pc);
   }
   // K or V rows of band `bi` -> slot dst, through a buffer resource over the
-  // band's W rows (rows past the band read as zeros without a fetch)
-  auto load_rows = [&](const char* base, int ss2, const int* ofs, int bi, lds_u16* dst) {
+  // band's W rows (rows past the band read as zeros without a fetch).  K
+  // always takes VLOADS DMAs: its slot rows past the band meet dS = 0 in
+  // dQ^T += K^T dS^T and must be zeros (0 * Inf would be NaN).  V takes
+  // VLOADS too, or with VSKIP only the ceil(W / RPI) DMAs that reach a band
+  // row: V rows past the band then keep older slot contents, which only
+  // feed dP of keys no row picks.  The vmcnt waits count the DMAs issued.
+  constexpr int RPI = 64 / C::CPR;  // slot rows per DMA
+  auto n_loads = [&](int bi) { return (min((int)((uint32_t)bi >> 24), 16) + RPI - 1) / RPI; };
+  auto load_rows = [&](const char* base, int ss2, const int* ofs, int bi, lds_u16* dst,
+                       bool all) {
     const int lo = bi & 0xffffff, wdt = (int)((uint32_t)bi >> 24);
+    const int nl = __builtin_amdgcn_readfirstlane(n_loads(bi));
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(base + (int64_t)lo * ss2), (short)0, min(wdt, 16) * ss2, 0x00020000);
+        (void*)(base + (int64_t)lo * ss2), (short)0,
+        __builtin_amdgcn_readfirstlane(min(wdt, 16) * ss2), 0x00020000);
 #pragma unroll
-    for (int t = 0; t < C::VLOADS; ++t)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + 512 * t), 16, ofs[t], 0, 0,
-                                               0);
+    for (int t = 0; t < C::VLOADS; ++t) {
+      if (all || t < nl)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + 512 * t), 16, ofs[t], 0,
+                                                 0, 0);
+    }
   };
-  auto load_k = [&](int bi, lds_u16* dst) { load_rows(kbase, kss2, kofs, bi, dst); };
-  auto load_v = [&](int bi, lds_u16* dst) { load_rows(vbase, vss2, vofs, bi, dst); };
+  auto load_k = [&](int bi, lds_u16* dst) { load_rows(kbase, kss2, kofs, bi, dst, true); };
+  auto load_v = [&](int bi, lds_u16* dst) { load_rows(vbase, vss2, vofs, bi, dst, !VSKIP); };
+  // s_waitcnt vmcnt(n) for a count known only at run time (0 .. 8)
+  auto wait_vm = [&](int n) {
+    switch (n) {
+      case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+      case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+      case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+      case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+      case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+      case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+      case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+      case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+      default: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    }
+  };
+  static_assert(2 * C::VLOADS <= 8, "wait_vm covers at most 8 DMAs in flight");
 
   // row operand reads: lane (m = n, q) reads slot row n, dims 32 s + 8 q .. + 8
   int rrd[C::NS];
@@ -176,8 +206,9 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   };
 
   // ---- band pairs: per pair, K reads, then K of the next pair; V reads,
-  // then V of the next pair (so before each wait exactly 2 VLOADS newer
-  // loads may be in flight)
+  // then V of the next pair.  So before the V wait exactly the next pair's
+  // 2 VLOADS K DMAs may be newer, and before the K wait this pair's V DMAs
+  // (2 VLOADS of them, or with VSKIP as many as load_v issued).
   constexpr int kWaitPair = (0xF70 & ~0xF) | ((2 * C::VLOADS) & 0xF) |
                             (((2 * C::VLOADS) >> 4) << 14);  // vmcnt(2 VLOADS)
   constexpr int kWaitLds = 0xC07F;                           // lgkmcnt(0)
@@ -207,7 +238,11 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
         nb = more ? __builtin_amdgcn_readlane(info[1], 16 * qj + 16) : 0;
       }
       const bool live = (ia | ib) != 0;
-      __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's K is in LDS
+      // this pair's K is in LDS
+      if constexpr (VSKIP)
+        wait_vm(n_loads(ia) + n_loads(ib));
+      else
+        __builtin_amdgcn_s_waitcnt(kWaitPair);
       f32x4 sa, sb;
       s16x4 ta[C::NV], tb[C::NV];
       if (live) {
@@ -754,10 +789,19 @@ hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2,
                           hipStream_t stream) {
   if (a.n_groups <= 0) return hipSuccess;
   dim3 grid((unsigned)(8 * a.per_xcd));
-  if (head_dim == 128)
-    band_dq_kernel<128><<<grid, 64, 0, stream>>>(a, lse2);
-  else
-    band_dq_kernel<64><<<grid, 64, 0, stream>>>(a, lse2);
+  // V DMA skipping from interpolation weight 1/2 on, as for the forward's K
+  const bool vskip = a.pc.a >= 0.5f;
+  if (head_dim == 128) {
+    if (vskip)
+      band_dq_kernel<128, true><<<grid, 64, 0, stream>>>(a, lse2);
+    else
+      band_dq_kernel<128, false><<<grid, 64, 0, stream>>>(a, lse2);
+  } else {
+    if (vskip)
+      band_dq_kernel<64, true><<<grid, 64, 0, stream>>>(a, lse2);
+    else
+      band_dq_kernel<64, false><<<grid, 64, 0, stream>>>(a, lse2);
+  }
   return hipGetLastError();
 }
 
