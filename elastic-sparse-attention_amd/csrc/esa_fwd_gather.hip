@@ -199,7 +199,10 @@ __device__ __forceinline__ float group_sum(float v) {
 
 // ---------------------------------------------------------------------------
 // Cooperative-row variant for D = 64, 128, 256 with 16-byte aligned rows (the
-// decode shapes): one wave per (batch, head, query row) as above, but each
+// decode shapes): one wave per (batch, head, query row) as above, waves
+// numbered over (batch, head, row) with the row fastest (a one-row decode
+// step fills every wave of a block; a block per row would leave three of
+// its four waves idle), but each
 // K and V row is read by LPK = D * sizeof(T) / 16 lanes, 16 bytes each, so
 // one load instruction covers KPI = 64 / LPK rows in whole cache lines, and a
 // chunk's K and V rows (SK keys, NI = SK / KPI instructions each) are all in
@@ -219,9 +222,11 @@ __global__ __launch_bounds__(256, 2) void gather_rows_kernel(GatherArgs A) {
   static_assert(LPK <= 64 && 64 % LPK == 0 && NI <= 16, "row split");
   __shared__ float sc_all[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r = blockIdx.x * 4 + wave;
-  const int h = blockIdx.y, b = blockIdx.z;
-  if (r >= A.q_len) return;  // whole wave leaves; no block-level barrier below
+  const int64_t wv = (int64_t)blockIdx.x * 4 + wave;
+  // whole wave leaves; no block-level barrier below
+  if (wv >= (int64_t)A.B * A.H * A.q_len) return;
+  const int r = (int)(wv % A.q_len);
+  const int h = (int)((wv / A.q_len) % A.H), b = (int)(wv / ((int64_t)A.q_len * A.H));
   const int kvh = h / A.groups;
   float* sc = sc_all[wave];
   const int gk = lane / LPK;  // row of an instruction this lane loads
@@ -385,7 +390,11 @@ static void launch_rows(const GatherArgs& a, dim3 grid, hipStream_t stream) {
 hipError_t launch_gather_fwd(const GatherArgs& a, bool f32, bool pattern, hipStream_t stream) {
   if (a.q_len <= 0 || a.B <= 0 || a.H <= 0) return hipSuccess;
   dim3 grid((unsigned)((a.q_len + 3) / 4), (unsigned)a.H, (unsigned)a.B);
-  if (rows_aligned16(a, f32 ? 4 : 2)) {
+  // the cooperative kernel's one-dimensional grid: four waves per block,
+  // within the 2^32 work-items of a dispatch
+  const int64_t coop_blocks = ((int64_t)a.B * a.H * a.q_len + 3) / 4;
+  if (rows_aligned16(a, f32 ? 4 : 2) && coop_blocks * 256 <= (int64_t)UINT32_MAX) {
+    grid = dim3((unsigned)coop_blocks);
     if (f32) {
       if (pattern)
         launch_rows<float, true>(a, grid, stream);
