@@ -65,11 +65,16 @@ __device__ __forceinline__ uint32_t transpose32(uint32_t x, int lane) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// delta and lse in log2 units, one 16-lane group per query row
+// delta and lse in log2 units, one 16-lane group per query row.  heads_fast:
+// the grid's fastest axis is the head (blockIdx.x = h, blockIdx.y = 16-row
+// block), so where O's heads lie inside a row ([B, L, H, D], the forward's
+// output) neighbouring blocks read neighbouring bytes; otherwise the axes
+// swap.
 template <int D>
-__global__ __launch_bounds__(256) void prep_kernel(BwdArgs A, float* lse2) {
-  const int row = blockIdx.x * 16 + (threadIdx.x >> 4);
-  const int h = blockIdx.y, b = blockIdx.z;
+__global__ __launch_bounds__(256) void prep_kernel(BwdArgs A, float* lse2, int heads_fast) {
+  const int rb = heads_fast ? blockIdx.y : blockIdx.x;
+  const int row = rb * 16 + (threadIdx.x >> 4);
+  const int h = heads_fast ? blockIdx.x : blockIdx.y, b = blockIdx.z;
   const int g = threadIdx.x & 15;
   constexpr int PER = D / 16;  // elements per lane
   if (A.split_parts > 1 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
@@ -564,11 +569,16 @@ hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,
   if (a.q_len <= 0 || a.B <= 0) return hipSuccess;
   // lse in log2 units goes in the second half of the delta workspace
   float* lse2 = a.delta + (int64_t)a.B * a.H * a.qpad;
-  dim3 pg((unsigned)((a.q_len + 15) / 16), (unsigned)a.H, (unsigned)a.B);
+  const unsigned n_rb = (unsigned)((a.q_len + 15) / 16);
+  // heads fastest where O interleaves heads within a row and the row blocks
+  // fit the grid's second axis (65535)
+  const int heads_fast = a.osh < a.oss && n_rb <= 65535u;
+  const dim3 pg = heads_fast ? dim3((unsigned)a.H, n_rb, (unsigned)a.B)
+                             : dim3(n_rb, (unsigned)a.H, (unsigned)a.B);
   if (head_dim == 128)
-    prep_kernel<128><<<pg, 256, 0, stream>>>(a, lse2);
+    prep_kernel<128><<<pg, 256, 0, stream>>>(a, lse2, heads_fast);
   else
-    prep_kernel<64><<<pg, 256, 0, stream>>>(a, lse2);
+    prep_kernel<64><<<pg, 256, 0, stream>>>(a, lse2, heads_fast);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (num_kv_items < 0) {  // no work list: band-gathered dK / dV
