@@ -569,6 +569,13 @@ hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,
   if (a.q_len <= 0 || a.B <= 0) return hipSuccess;
   // lse in log2 units goes in the second half of the delta workspace
   float* lse2 = a.delta + (int64_t)a.B * a.H * a.qpad;
+  if (num_q_items < 0 && num_kv_items < 0) {
+    // both halves band-gathered: the dQ kernel forms delta / lse2 (and clears
+    // the split counters) on its way, then dK / dV reads them
+    hipError_t e0 = launch_band_dq(a, head_dim, lse2, true, stream);
+    if (e0 != hipSuccess) return e0;
+    return launch_band_dkdv(a, head_dim, lse2, stream);
+  }
   const unsigned n_rb = (unsigned)((a.q_len + 15) / 16);
   // heads fastest where O interleaves heads within a row and the row blocks
   // fit the grid's second axis (65535)
@@ -592,7 +599,7 @@ hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if (num_q_items < 0) return launch_band_dq(a, head_dim, lse2, stream);  // no work list
+  if (num_q_items < 0) return launch_band_dq(a, head_dim, lse2, false, stream);  // no work list
   if (num_q_items > 0) {
     if (head_dim == 128)
       dq_kernel<128><<<dim3((unsigned)num_q_items), 256, 0, stream>>>(a, lse2);

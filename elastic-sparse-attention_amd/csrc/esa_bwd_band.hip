@@ -28,9 +28,16 @@ namespace esa {
 // VSKIP: issue only the V DMAs that reach a band row (see load_rows); the
 // host picks it where many bands are narrower than 16 keys, as for the
 // forward's K DMA skip.
-template <int D, bool VSKIP>
+// PREP: the kernel forms its rows' delta = rowsum(dO * O) and lse2 = lse *
+// log2(e) itself (instead of reading them) and stores both for the band
+// dK/dV kernel, which then runs after it; block 0 also clears the split
+// arrival counters.  Used when both halves are band kernels, so no separate
+// pass re-reads O and dO.
+template <int D, bool VSKIP, bool PREP>
 __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* lse2) {
   using C = BandCfg<D>;
+  if (PREP && A.split_parts > 1 && blockIdx.x == 0)
+    for (int t = threadIdx.x; t < A.n_bkv * A.split_blocks; t += 64) A.part_cnt[t] = 0;
   __shared__ __attribute__((aligned(1024))) uint16_t ks0[C::SLOT];
   __shared__ __attribute__((aligned(1024))) uint16_t ks1[C::SLOT];
   __shared__ __attribute__((aligned(1024))) uint16_t vs0[C::SLOT];
@@ -76,10 +83,70 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
     }
   }
   float l2 = 0.f, dl = 0.f;
-  if (row_ok) {
-    const int64_t at = ((int64_t)b * A.H + h) * A.qpad + i;
-    l2 = lse2[at];
-    dl = A.delta[at];
+  if constexpr (PREP) {
+    // rowsum(dO * O) in prep_kernel's order, so both give the same bits:
+    // there, lane g of 16 sums dims D/16 g .. + D/16 in sequence and the 16
+    // sums meet in an xor butterfly (strides 8, 4, 2, 1).  Here lane (n, q)
+    // holds dims 32 s + 8 q .. + 8; each product of two bf16 values is exact
+    // in float32, so only the order of the additions matters.
+    float hs[C::NS][2];  // sequential sums of each D/16-dim piece
+    {
+      u32x4 raw[C::NS];
+      const uint16_t* orow =
+          A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)i * A.oss;
+#pragma unroll
+      for (int s = 0; s < C::NS; ++s) {
+        raw[s] = u32x4{0u, 0u, 0u, 0u};
+        if (row_ok) raw[s] = *(const u32x4*)(orow + 32 * s + 8 * q);
+      }
+      constexpr int PER = D / 16;
+#pragma unroll
+      for (int s = 0; s < C::NS; ++s)
+#pragma unroll
+        for (int k = 0; k < 8 / PER; ++k) {
+          float acc = 0.f;
+#pragma unroll
+          for (int e = PER * k; e < PER * k + PER; ++e) {
+            const uint32_t w = raw[s][e / 2];
+            const float ov = __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+            acc += ov * (float)dop[s][e];
+          }
+          hs[s][k] = acc;
+        }
+    }
+    if constexpr (D == 128) {
+      // piece 4 s + q: strides 8 and 4 stay in the lane (s ^ 2, s ^ 1),
+      // 2 and 1 cross to lanes ^ 32 and ^ 16
+      float t = (hs[0][0] + hs[2][0]) + (hs[1][0] + hs[3][0]);
+      t += __shfl_xor(t, 32, 64);
+      t += __shfl_xor(t, 16, 64);
+      dl = t;
+    } else {
+      // piece 8 s + 2 q + k: stride 8 is s ^ 1, 4 and 2 cross to lanes ^ 32
+      // and ^ 16, 1 is k ^ 1
+      float t0 = hs[0][0] + hs[1][0], t1 = hs[0][1] + hs[1][1];
+      t0 += __shfl_xor(t0, 32, 64);
+      t1 += __shfl_xor(t1, 32, 64);
+      t0 += __shfl_xor(t0, 16, 64);
+      t1 += __shfl_xor(t1, 16, 64);
+      dl = t0 + t1;
+    }
+    if (row_ok) {
+      // kept finite: masked scores enter as -inf, and -inf - (-inf) would be NaN
+      l2 = fmaxf(A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + i] * 1.4426950408889634f,
+                 -3.0e38f);
+      if (q == 0) {
+        const int64_t at = ((int64_t)b * A.H + h) * A.qpad + i;
+        A.delta[at] = dl;
+        A.delta[(int64_t)A.B * A.H * A.qpad + at] = l2;  // the lse2 half of the workspace
+      }
+    }
+  } else {
+    if (row_ok) {
+      const int64_t at = ((int64_t)b * A.H + h) * A.qpad + i;
+      l2 = lse2[at];
+      dl = A.delta[at];
+    }
   }
 
   int kreg[16], info[16];
@@ -785,22 +852,29 @@ hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,
   return hipGetLastError();
 }
 
-hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2,
+template <int D, bool PREP>
+static void launch_band_dq_d(const BwdArgs& a, dim3 grid, const float* lse2, hipStream_t stream) {
+  // V DMA skipping from interpolation weight 1/2 on, as for the forward's K
+  if (a.pc.a >= 0.5f)
+    band_dq_kernel<D, true, PREP><<<grid, 64, 0, stream>>>(a, lse2);
+  else
+    band_dq_kernel<D, false, PREP><<<grid, 64, 0, stream>>>(a, lse2);
+}
+
+hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2, bool prep,
                           hipStream_t stream) {
   if (a.n_groups <= 0) return hipSuccess;
   dim3 grid((unsigned)(8 * a.per_xcd));
-  // V DMA skipping from interpolation weight 1/2 on, as for the forward's K
-  const bool vskip = a.pc.a >= 0.5f;
   if (head_dim == 128) {
-    if (vskip)
-      band_dq_kernel<128, true><<<grid, 64, 0, stream>>>(a, lse2);
+    if (prep)
+      launch_band_dq_d<128, true>(a, grid, lse2, stream);
     else
-      band_dq_kernel<128, false><<<grid, 64, 0, stream>>>(a, lse2);
+      launch_band_dq_d<128, false>(a, grid, lse2, stream);
   } else {
-    if (vskip)
-      band_dq_kernel<64, true><<<grid, 64, 0, stream>>>(a, lse2);
+    if (prep)
+      launch_band_dq_d<64, true>(a, grid, lse2, stream);
     else
-      band_dq_kernel<64, false><<<grid, 64, 0, stream>>>(a, lse2);
+      launch_band_dq_d<64, false>(a, grid, lse2, stream);
   }
   return hipGetLastError();
 }
