@@ -268,3 +268,30 @@ def test_strided_views_match_contiguous(kernels):
         res.append((o, lse) + tuple(grads))
     for name, x, y in zip(("o", "lse", "dq", "dk", "dv"), *res):
         assert torch.equal(x, y), name
+
+
+@pytest.mark.parametrize("kernels", ["tile/tile", "band/tile", "band/band"])
+def test_head_major_o_and_dout(kernels):
+    """O and dO held head-major ([B, H, L, D] storage seen as [B, L, H, D])
+    give the same gradients bit for bit as the forward's [B, L, H, D]
+    layout: the delta pass (its own kernel beside a block-sparse half, the
+    band dQ for the band pair) walks either layout in the same order."""
+    dq_kind, dkdv_kind = kernels.split("/")
+    B, H, Hkv, L, D, layer = 2, 8, 2, 1536, 128, 6
+    print(f"head-major O/dO {kernels} B={B} H={H} Hkv={Hkv} L={L} D={D} layer={layer}",
+          flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=19, scale=D ** -0.25)
+    sc = scaling_for(D)
+    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc)
+    do = torch.randn(B, L, H, D, generator=torch.Generator().manual_seed(5))
+    do = do.to(torch.bfloat16).to(DEV)
+    ref = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel=dq_kind,
+                                dkdv_kernel=dkdv_kind)
+    oh, doh = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (o, do))
+    assert oh.stride(2) > oh.stride(1) and torch.equal(oh, o) and torch.equal(doh, do)
+    got = elastic_attention_bwd(qd, kd, vd, oh, lse, doh, lay, sc, dq_kernel=dq_kind,
+                                dkdv_kernel=dkdv_kind)
+    for name, x, y in zip(("dq", "dk", "dv"), ref, got):
+        assert torch.equal(x, y), name
