@@ -191,6 +191,8 @@ esa_status esa_layout_sizes(const esa_pattern* p, int32_t* num_qblocks, int32_t*
   if (s != ESA_OK) return s;
   const LayoutDims d = dims_of(*p);
   if ((int64_t)d.nwords * 4 > 65536) return ESA_ERR_SHAPE;  // LDS bitmap bound
+  // row_ptr, the builder's scan and every tile id are int32
+  if (max_tiles_of(*p, d) > INT32_MAX) return ESA_ERR_SHAPE;
   if (num_qblocks) *num_qblocks = d.nqb;
   if (num_kblocks) *num_kblocks = d.nkb;
   if (max_tiles) *max_tiles = max_tiles_of(*p, d);
@@ -219,6 +221,7 @@ esa_status esa_build_layout(const esa_pattern* p, int32_t* row_ptr, int32_t* col
   if (!row_ptr || !col_idx || !workspace) return ESA_ERR_NULL;
   const LayoutDims d = dims_of(*p);
   if ((int64_t)d.nwords * 4 > 65536) return ESA_ERR_SHAPE;
+  if (max_tiles_of(*p, d) > INT32_MAX) return ESA_ERR_SHAPE;
   if (col_capacity < max_tiles_of(*p, d)) return ESA_ERR_CAPACITY;
   if (workspace_bytes < workspace_of(*p, d)) return ESA_ERR_CAPACITY;
   if (!aligned(workspace, 4)) return ESA_ERR_ALIGN;
@@ -454,15 +457,21 @@ esa_status esa_plan_bwd(const esa_pattern* p, const int32_t* row_ptr_host,
 }
 
 esa_status esa_build_tile_masks(const esa_pattern* p, const int32_t* row_ptr,
-                                const int32_t* col_idx, int32_t q_len, uint32_t* mask_t,
-                                int64_t mask_capacity, void* stream) {
+                                const int32_t* col_idx, const int32_t* row_ptr_host,
+                                int32_t q_len, uint32_t* mask_t, int64_t mask_capacity,
+                                void* stream) {
   esa_status s = check_pattern(p);
   if (s != ESA_OK) return s;
-  if (!row_ptr || !col_idx || !mask_t) return ESA_ERR_NULL;
+  if (!row_ptr || !col_idx || !row_ptr_host || !mask_t) return ESA_ERR_NULL;
   if (p->block_m != 128 || p->block_n != 128) return ESA_ERR_UNSUPPORTED;
   if (q_len < 0 || q_len > p->seq_len) return ESA_ERR_SHAPE;
   const LayoutDims d = dims_of(*p);
-  if (mask_capacity < max_tiles_of(*p, d) * 512) return ESA_ERR_CAPACITY;
+  if (q_len == 0) return ESA_OK;
+  // the masks of the tiles of query blocks below ceil(q_len / 128) are
+  // written; the last head's end among them bounds every tile id written
+  const int nq = (q_len + p->block_m - 1) / p->block_m;
+  const int64_t need = (int64_t)row_ptr_host[(int64_t)(p->num_heads - 1) * d.nqb + nq];
+  if (need < 0 || mask_capacity < need * 512) return ESA_ERR_CAPACITY;
   if (!aligned(mask_t, 4)) return ESA_ERR_ALIGN;
   return hip_status(launch_tile_masks(make_consts(*p), row_ptr, col_idx, d.nqb, q_len, mask_t,
                                       (hipStream_t)stream));
@@ -530,6 +539,8 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
   if (p->layer_idx < 0 || p->layer_idx > std::max(p->num_hidden_layers - 1, 0))
     return ESA_ERR_UNSUPPORTED;
   if (a->q_len > a->kv_len || a->q_len > p->seq_len || a->kv_len > kMaxSeqLen) return ESA_ERR_SHAPE;
+  // the block-sparse dK/dV writes the key blocks of the pattern's seq_len only
+  if (!band_dkdv && a->kv_len > p->seq_len) return ESA_ERR_SHAPE;
   if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale)) return ESA_ERR_UNSUPPORTED;
   const int64_t lim = int64_t(1) << 31;
   // (rows up to one tile past the length are addressed, and read as zeros)

@@ -95,10 +95,17 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(GatherArgs A) {
   const T* vbase = (const T*)A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh;
 
   int pos = r;
+  bool bad_pos = false;  // a position outside [0, kv_len): the row reads NaN
   HeadWeights hw{};
   RowParams rp{};
   if (PATTERN) {
-    pos = A.positions ? (int)A.positions[r] : r;
+    if (A.positions) {
+      // negative positions count from the end, as torch indexing does
+      const int64_t p0 = A.positions[r];
+      const int64_t p64 = p0 < 0 ? p0 + A.kv_len : p0;
+      bad_pos = p64 < 0 || p64 >= A.kv_len;
+      pos = bad_pos ? 0 : (int)p64;
+    }
     hw = head_weights(A.pc, h);
     rp = row_params(A.pc, pos);
   }
@@ -155,7 +162,7 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(GatherArgs A) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const float inv = bad_pos ? __builtin_nanf("") : (l > 0.f ? 1.f / l : 0.f);
   T* orow = (T*)A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)r * A.oss;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -163,7 +170,8 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(GatherArgs A) {
     if (d < D) st<T>(orow + d, acc[e] * inv);
   }
   if (A.lse && lane == 0)
-    A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + r] = l > 0.f ? m + logf(l) : -INFINITY;
+    A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + r] =
+        bad_pos ? __builtin_nanf("") : (l > 0.f ? m + logf(l) : -INFINITY);
 }
 
 // Sum over aligned groups of N lanes (N = 8, 16, 32, 64), in every lane of
@@ -248,10 +256,17 @@ __global__ __launch_bounds__(256, 2) void gather_rows_kernel(GatherArgs A) {
   const T* vbase = (const T*)A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh + EPL * ln;
 
   int pos = r;
+  bool bad_pos = false;  // a position outside [0, kv_len): the row reads NaN
   HeadWeights hw{};
   RowParams rp{};
   if (PATTERN) {
-    pos = A.positions ? (int)A.positions[r] : r;
+    if (A.positions) {
+      // negative positions count from the end, as torch indexing does
+      const int64_t p0 = A.positions[r];
+      const int64_t p64 = p0 < 0 ? p0 + A.kv_len : p0;
+      bad_pos = p64 < 0 || p64 >= A.kv_len;
+      pos = bad_pos ? 0 : (int)p64;
+    }
     hw = head_weights(A.pc, h);
     rp = row_params(A.pc, pos);
   }
@@ -344,7 +359,7 @@ __global__ __launch_bounds__(256, 2) void gather_rows_kernel(GatherArgs A) {
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc[e] += __shfl_xor(acc[e], off, 64);
 
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const float inv = bad_pos ? __builtin_nanf("") : (l > 0.f ? 1.f / l : 0.f);
   if (gk == 0) {
     T* orow = (T*)A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)r * A.oss + EPL * ln;
     u32x4 w;
@@ -359,7 +374,8 @@ __global__ __launch_bounds__(256, 2) void gather_rows_kernel(GatherArgs A) {
     *(u32x4*)orow = w;
   }
   if (A.lse && lane == 0)
-    A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + r] = l > 0.f ? m + logf(l) : -INFINITY;
+    A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + r] =
+        bad_pos ? __builtin_nanf("") : (l > 0.f ? m + logf(l) : -INFINITY);
 }
 
 // The cooperative kernel takes D = 64, 128, 256 and needs every Q, K, V and

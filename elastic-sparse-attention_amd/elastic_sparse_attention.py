@@ -167,6 +167,9 @@ class ElasticLayout:
         self.row_ptr_host = self.row_ptr.cpu()  # one synchronisation per layout
         del work
         self.num_tiles = int(self.row_ptr_host[-1])
+        # col_idx was sized by the bound; keep only the tiles the layout holds
+        if self.col_idx.numel() > max(1, self.num_tiles):
+            self.col_idx = self.col_idx[:max(1, self.num_tiles)].clone()
         self._schedules: Dict[Tuple[int, int], Tuple[torch.Tensor, int]] = {}
         self._col_idx_host: Optional[torch.Tensor] = None
         self._bwd_plans: Dict[Tuple[int, int, int], Tuple[torch.Tensor, ...]] = {}
@@ -252,20 +255,32 @@ class ElasticLayout:
         self._bwd_plans[key] = got
         return got
 
+    # tile masks kept for this many distinct q_len values (oldest dropped)
+    MASK_CACHE = 2
+
+    def mask_tiles(self, q_len: int) -> int:
+        """Tiles whose masks a backward over q_len rows reads: the end of the
+        last head's tiles among the query blocks below ceil(q_len / 128)."""
+        nq = (int(q_len) + self.pattern.block_m - 1) // self.pattern.block_m
+        return int(self.row_ptr_host[(self.pattern.num_heads - 1) * self.num_qblocks + nq])
+
     def tile_masks(self, q_len: int) -> torch.Tensor:
-        """Key-major masks of every active tile for q_len query rows
-        (esa_build_tile_masks), built once per q_len and cached: 2 KB per
-        tile."""
+        """Key-major masks of the active tiles for q_len query rows
+        (esa_build_tile_masks), 2 KB per tile of the query blocks q_len
+        covers; cached for the last MASK_CACHE values of q_len."""
         got = self._masks.get(int(q_len))
         if got is not None:
             return got
-        n = max(self.col_idx.numel(), 1) * 512
+        n = max(self.mask_tiles(q_len), 1) * 512
         masks = torch.empty(n, dtype=torch.int32, device=self.device)
         check(load().esa_build_tile_masks(ctypes.byref(self.pattern),
                                           ctypes.c_void_p(self.row_ptr.data_ptr()),
-                                          ctypes.c_void_p(self.col_idx.data_ptr()), q_len,
+                                          ctypes.c_void_p(self.col_idx.data_ptr()),
+                                          ctypes.c_void_p(self.row_ptr_host.data_ptr()), q_len,
                                           ctypes.c_void_p(masks.data_ptr()), n,
                                           _stream(self.device)), "esa_build_tile_masks")
+        while len(self._masks) >= self.MASK_CACHE:
+            self._masks.pop(next(iter(self._masks)))
         self._masks[int(q_len)] = masks
         return masks
 
@@ -668,6 +683,30 @@ class ElasticSparseAttention(nn.Module):
         idx, msk = self._indices()
         return idx[:, :kv_seq_len, :], msk[:, :kv_seq_len, :]
 
+    @staticmethod
+    def _positions(cache_position, q_len: int, kv_len: int, device: torch.device) -> torch.Tensor:
+        """cache_position as int64 on ``device``.  Negative positions count
+        from kv_len, as the reference's indexing of rows ``[:kv_len]`` counts
+        them (:588, :602-608); the kernel applies that.  A host-side value is
+        range-checked here (IndexError, as the reference's indexing raises); a
+        device tensor is passed through unchecked, so a decode step never
+        waits on the GPU: the kernel writes NaN for a row whose position is
+        out of range."""
+        if isinstance(cache_position, torch.Tensor) and cache_position.is_cuda:
+            pos = cache_position.reshape(-1)
+            if pos.dtype != torch.int64 or not pos.is_contiguous():
+                pos = pos.to(torch.int64).contiguous()
+            if pos.numel() != q_len:
+                raise ValueError(f"cache_position has {pos.numel()} entries for {q_len} query "
+                                 "rows")
+            return pos if pos.device == device else pos.to(device)
+        pos = torch.as_tensor(cache_position).to(torch.int64).reshape(-1)
+        if pos.numel() != q_len:
+            raise ValueError(f"cache_position has {pos.numel()} entries for {q_len} query rows")
+        if bool(((pos < -kv_len) | (pos >= kv_len)).any()):
+            raise IndexError(f"cache_position out of range for kv_len {kv_len}")
+        return pos.to(device)
+
     def forward(self, query_states: torch.Tensor, key_states: torch.Tensor,
                 value_states: torch.Tensor, cache_position: Optional[torch.LongTensor] = None
                 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
@@ -699,12 +738,7 @@ class ElasticSparseAttention(nn.Module):
                 o, _ = elastic_attention_rows(q, k, v, self.pattern, self.scaling, None,
                                               return_lse=False)
         else:
-            pos = torch.as_tensor(cache_position, device=q.device).to(torch.int64).reshape(-1)
-            if pos.numel() != Lq:
-                raise ValueError(f"cache_position has {pos.numel()} entries for {Lq} query rows")
-            pos = torch.where(pos < 0, pos + kv_len, pos)
-            if bool(((pos < 0) | (pos >= kv_len)).any()):
-                raise IndexError(f"cache_position out of range for kv_len {kv_len}")
+            pos = self._positions(cache_position, Lq, kv_len, q.device)
             o, _ = elastic_attention_rows(q, k, v, self.pattern, self.scaling, pos,
                                           return_lse=False)
         out = o.view(B, Lq, H * D)                                         # :761-763

@@ -133,7 +133,7 @@ def load() -> ctypes.CDLL:
     lib.esa_plan_bwd.argtypes = [P(EsaPattern), vp, vp, i32, i32, i32, vp, vp, vp, i64, vp, i64,
                                  P(i64), P(i64)]
     lib.esa_build_tile_masks.restype = st
-    lib.esa_build_tile_masks.argtypes = [P(EsaPattern), vp, vp, i32, vp, i64, vp]
+    lib.esa_build_tile_masks.argtypes = [P(EsaPattern), vp, vp, vp, i32, vp, i64, vp]
     lib.esa_bwd_workspace_size.restype = st
     lib.esa_bwd_workspace_size.argtypes = [P(EsaBwdArgs), P(ctypes.c_size_t)]
     lib.esa_elastic_bwd.restype = st

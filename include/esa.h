@@ -85,8 +85,9 @@ const char* esa_version(void);
 /* Host only.  Checks an esa_pattern and reports the sizes of its block
  * layout: query blocks per head, key blocks, an upper bound on the number of
  * active tiles (the col_idx capacity esa_build_layout needs) and the
- * workspace esa_build_layout needs.  No reference counterpart: the reference
- * never forms a block layout. */
+ * workspace esa_build_layout needs.  A pattern whose bound exceeds INT32_MAX
+ * is rejected (ESA_ERR_SHAPE): tile ids and row_ptr are int32.  No reference
+ * counterpart: the reference never forms a block layout. */
 esa_status esa_layout_sizes(const esa_pattern* p, int32_t* num_qblocks,
                             int32_t* num_kblocks, int64_t* max_tiles,
                             size_t* workspace_bytes);
@@ -171,8 +172,12 @@ esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, voi
  * cache_position, :602-608), or r when positions is NULL.  Replaces the
  * decode branch of _triton_forward (:602-619).  Each row's w indices are
  * regenerated on the device (bit-exact with :470-535) and clamped to
- * [0, kv_len - 1] (:615).  Positions must lie in [0, kv_len); the caller
- * checks.  dtype ESA_F32 or ESA_BF16, head_dim a multiple of 4, <= 256. */
+ * [0, kv_len - 1] (:615).  Positions index rows [0, kv_len) of the index set
+ * (:588, :602-608), a negative position counting from kv_len as torch
+ * indexing counts it; a row whose position lies outside [-kv_len, kv_len)
+ * (the reference's indexing error) gets NaN output and NaN lse, so the call
+ * never synchronises to check positions.  dtype ESA_F32 or ESA_BF16, head_dim a
+ * multiple of 4, <= 256. */
 esa_status esa_elastic_fwd_rows(const esa_fwd_args* a, const esa_pattern* p,
                                 const int64_t* positions, void* stream);
 
@@ -244,16 +249,19 @@ esa_status esa_plan_bwd(const esa_pattern* p, const int32_t* row_ptr_host,
                         int32_t* kv_items, int64_t kv_items_capacity,
                         int64_t* num_kv_tiles, int64_t* num_kv_items);
 
-/* Key-major masks of every active layout tile for a backward over q_len
- * query rows: mask_t[t * 512 + qs * 128 + k] bit r is set when query row
+/* Key-major masks of the active layout tiles a backward over q_len query
+ * rows reads: mask_t[t * 512 + qs * 128 + k] bit r is set when query row
  * qb * 128 + 32 qs + r (< q_len) has key col_idx[t] * 128 + k among its
- * valid elastic entries (:470-535).  mask_t holds row_ptr[H * nqb] * 512
- * uint32 (mask_capacity).  Depends only on the pattern and q_len, so it can
- * be built once and reused. */
+ * valid elastic entries (:470-535), for every tile t of a query block
+ * qb < ceil(q_len / 128).  row_ptr_host is the host copy of row_ptr; mask_t
+ * must hold row_ptr_host[(H - 1) * nqb + ceil(q_len / 128)] * 512 uint32
+ * (mask_capacity), the end of the last head's tiles among those blocks.
+ * Depends only on the pattern and q_len, so it can be built once and
+ * reused. */
 esa_status esa_build_tile_masks(const esa_pattern* p, const int32_t* row_ptr,
-                                const int32_t* col_idx, int32_t q_len,
-                                uint32_t* mask_t, int64_t mask_capacity,
-                                void* stream);
+                                const int32_t* col_idx, const int32_t* row_ptr_host,
+                                int32_t q_len, uint32_t* mask_t,
+                                int64_t mask_capacity, void* stream);
 
 /* Host only.  Bytes of workspace esa_elastic_bwd needs:
  * 2 * batch * num_heads * qpad floats, qpad = q_len rounded up to 32, plus

@@ -316,10 +316,17 @@ def test_bwd_entry_points_reject_bad_arguments():
     b = en.EsaBwdArgs.from_buffer_copy(a)
     b.dq_stride_s = 130
     assert call(b) == en.ESA_ERR_ALIGN
-    assert lib.esa_build_tile_masks(ctypes.byref(p), fake, fake, 256, fake, 1, None) \
-        == en.ESA_ERR_CAPACITY
-    assert lib.esa_build_tile_masks(ctypes.byref(p), fake, fake, 2048, fake, 1 << 30, None) \
-        == en.ESA_ERR_SHAPE
+    # capacity is checked against the tiles of the query blocks q_len covers,
+    # read from the host copy of row_ptr
+    nqb = (p.seq_len + 127) // 128
+    rp_host = (ctypes.c_int32 * (p.num_heads * nqb + 1))(*range(p.num_heads * nqb + 1))
+    need = rp_host[(p.num_heads - 1) * nqb + 2]  # q_len = 256: two query blocks
+    assert lib.esa_build_tile_masks(ctypes.byref(p), fake, fake, rp_host, 256, fake,
+                                    need * 512 - 1, None) == en.ESA_ERR_CAPACITY
+    assert lib.esa_build_tile_masks(ctypes.byref(p), fake, fake, None, 256, fake,
+                                    need * 512, None) == en.ESA_ERR_NULL
+    assert lib.esa_build_tile_masks(ctypes.byref(p), fake, fake, rp_host, 2048, fake, 1 << 30,
+                                    None) == en.ESA_ERR_SHAPE
 
 
 def test_bwd_workspace_size_with_split():

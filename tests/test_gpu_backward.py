@@ -102,6 +102,51 @@ def test_backward_attention_lengths(B, H, Hkv, L, D, layer, w, kernels):
     assert max(e) <= REL
 
 
+@pytest.mark.parametrize("B,H,Hkv,L,D,layer,w", [
+    (1, 4, 2, 1100, 128, 4, 100),
+    (1, 4, 4, 1024, 64, 6, 128),
+    (2, 2, 1, 777, 128, 7, 128),
+    (1, 4, 4, 1024, 128, 0, 128),
+    (1, 4, 2, 900, 64, 2, 32),
+])
+def test_backward_tile_attention_lengths(B, H, Hkv, L, D, layer, w):
+    """Index lists other than 64 entries through the block-sparse dQ and
+    dK/dV (attention_length > 64 always takes them), against autograd."""
+    print(f"bwd tile B={B} H={H} Hkv={Hkv} L={L} D={D} layer={layer} w={w}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=layer + w, scale=1.0)
+    idx, msk = elastic_indices(L, layer, 8, H, w)
+    sc = scaling_for(D)
+    g = torch.randn(B, H, L, D, generator=torch.Generator().manual_seed(w)).to(torch.bfloat16)
+    rq, rk, rv = reference_grads(q, k, v, idx, msk, sc, H // Hkv, g.float())
+    lay = ElasticLayout(make_pattern(L, w, layer, 8, H), DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc, kernel="tile")
+    do = g.to(DEV).permute(0, 2, 1, 3).contiguous()
+    dq, dk, dv = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="tile",
+                                       dkdv_kernel="tile")
+    e = (rel_err(dq, rq), rel_err(dk, rk), rel_err(dv, rv))
+    print(f"  rel err dq {e[0]:.3e} dk {e[1]:.3e} dv {e[2]:.3e}", flush=True)
+    assert max(e) <= REL
+
+
+def test_module_autograd_attention_length_128():
+    """The module at attention_length = 128 backpropagates through the
+    block-sparse kernels."""
+    B, H, L, D, layer, w = 1, 4, 1024, 128, 5, 128
+    m = ElasticSparseAttention(layer, 8, H, D, w, L)
+    q, k, v = seeded_inputs(B, H, H, L, D, torch.bfloat16, seed=21, scale=1.0)
+    idx, msk = elastic_indices(L, layer, 8, H, w)
+    g = torch.randn(B, L, H * D, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    out, _ = m(qd, kd, vd)
+    (out.float() * g.to(DEV).float()).sum().backward()
+    gref = g.float().view(B, L, H, D).permute(0, 2, 1, 3)
+    rq, rk, rv = reference_grads(q, k, v, idx, msk, m.scaling, 1, gref)
+    e = (rel_err(qd.grad, rq), rel_err(kd.grad, rk), rel_err(vd.grad, rv))
+    print(f"  module w=128 rel err dq {e[0]:.3e} dk {e[1]:.3e} dv {e[2]:.3e}", flush=True)
+    assert max(e) <= REL
+
+
 def test_module_autograd():
     """The drop-in module's output backpropagates through the HIP backward."""
     B, H, L, D, layer = 1, 4, 768, 128, 4

@@ -82,6 +82,40 @@ def test_tile_shapes(B, H, Hkv, L, Lq, D, layer):
     assert (lse.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
 
 
+@pytest.mark.parametrize("w", [32, 100, 128])
+@pytest.mark.parametrize("D", [128, 64])
+def test_tile_attention_lengths(w, D):
+    """Index lists other than 64 entries: every bf16 prefill with
+    attention_length > 64 runs the tile kernel (the band kernels take at most
+    64), so it is checked at every layer, with GQA and a ragged q_len."""
+    B, H, Hkv, L, Lq, nl = 2, 4, 2, 1100, 1037, 8
+    for layer in range(nl):
+        print(f"tile w={w} D={D} layer={layer}", flush=True)
+        q, k, v, idx, msk = case(B, H, Hkv, L, D, torch.bfloat16, layer, w=w, seed=w + layer,
+                                 scale=1.0, Lq=Lq)
+        sc = scaling_for(D)
+        lay = ElasticLayout(make_pattern(L, w, layer, nl, H), DEV)
+        assert prefill_kernel(lay, Lq, B, D) == "tile" or w <= 64
+        o, lse = elastic_attention_fwd(q.to(DEV), k.to(DEV), v.to(DEV), lay, sc, kernel="tile")
+        pi, pm = prepared_rows(idx, msk, Lq, L, L)
+        ro, rl = oracle(q, k, v, pi, pm, sc, H // Hkv)
+        assert (to_bhsd(o).float().cpu() - ro).abs().max().item() <= BF16_TOL
+        assert (lse.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
+
+
+def test_module_attention_length_128():
+    """The drop-in module at attention_length = 128 (the tile kernel), bf16
+    D = 128, against the oracle at every layer."""
+    B, H, L, D, w = 1, 8, 2048, 128, 128
+    for layer in (0, 2, 5, 7):
+        m = ElasticSparseAttention(layer, 8, H, D, w, L)
+        q, k, v, idx, msk = case(B, H, H, L, D, torch.bfloat16, layer, w=w, seed=layer)
+        out, _ = m(q.to(DEV), k.to(DEV), v.to(DEV))
+        ro, _ = oracle(q, k, v, idx, msk, m.scaling, 1)
+        ref = ro.transpose(1, 2).reshape(B, L, H * D)
+        assert (out.float().cpu() - ref).abs().max().item() <= BF16_TOL
+
+
 def test_tile_unit_variance_logits():
     """N(0,1) inputs without the D^-0.25 scale (sharper softmax)."""
     q, k, v, idx, msk = case(1, 4, 4, 2048, 128, torch.bfloat16, 4, seed=5, scale=1.0)
@@ -426,6 +460,29 @@ def test_module_forward_decode_matches_prefill_rows():
     with pytest.raises(ValueError, match="exceeds the maximum length"):
         big = torch.zeros(1, H, 1025, D, dtype=torch.bfloat16, device=DEV)
         m(big, big, big)
+
+
+def test_module_decode_device_positions():
+    """cache_position on the device goes to the kernel unchecked (no host
+    synchronisation): negative positions count from kv_len as torch indexing
+    does, and an out-of-range position gives a NaN row instead of an error;
+    the other rows of the call are unaffected."""
+    B, H, L, D = 2, 4, 300, 128
+    m = ElasticSparseAttention(5, 8, H, D, 64, 512)
+    q, k, v, idx, msk = case(B, H, H, L, D, torch.bfloat16, 5, seed=4, scale=1.0)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    full, _ = m(qd, kd, vd)
+    rows = [7, 299, 150]
+    got, _ = m(qd[:, :, rows], kd, vd, cache_position=torch.tensor([7, -1, -150], device=DEV))
+    for n, r in enumerate(rows):
+        assert (got.float()[:, n] - full.float()[:, r]).abs().max().item() <= BF16_TOL
+    bad, _ = m(qd[:, :, [3, 4, 5]], kd, vd,
+               cache_position=torch.tensor([3, 300, -301], device=DEV))
+    assert (bad.float()[:, 0] - full.float()[:, 3]).abs().max().item() <= BF16_TOL
+    assert bool(torch.isnan(bad.float()[:, 1:]).all())
+    # the same positions from the host raise, as the reference's indexing does
+    with pytest.raises(IndexError):
+        m(qd[:, :, [3]], kd, vd, cache_position=torch.tensor([-301]))
 
 
 def test_module_index_buffers_on_gpu():
