@@ -1,12 +1,15 @@
 """Builds libesa.so (the HIP kernels and the C ABI) for gfx950 in place.
 
-    python elastic-sparse-attention_amd/build_lib.py
+    python elastic-sparse-attention_amd/build_lib.py [-v]
 
-hipcc cross-compiles without a GPU.  The library lands next to this file,
-where esa_native.py loads it from.
+hipcc cross-compiles without a GPU.  Each source is compiled to an object
+(in parallel) under _build/ next to this file, then the objects are linked
+into libesa.so, which lands next to this file, where esa_native.py loads it
+from.
 """
 from __future__ import annotations
 
+import concurrent.futures as cf
 import os
 import shutil
 import subprocess
@@ -14,9 +17,15 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
-SOURCES = ["esa_capi.hip", "esa_layout.hip", "esa_fwd_tile.hip", "esa_fwd_band.hip", "esa_bwd_band.hip", "esa_fwd_gather.hip",
-           "esa_bwd.hip", "esa_reach.hip"]
+BUILD = os.path.join(HERE, "_build")
+SOURCES = ["esa_capi.hip", "esa_layout.hip", "esa_fwd_tile.hip", "esa_fwd_band.hip",
+           "esa_bwd_band.hip", "esa_fwd_gather.hip", "esa_bwd_gather.hip", "esa_bwd.hip",
+           "esa_reach.hip"]
 LIB = os.path.join(HERE, "libesa.so")
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
+         # packed fp32 VALU forms are kept out of every kernel
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-Wno-unused-result"]
 
 
 def hipcc() -> str:
@@ -26,26 +35,40 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found: the ROCm toolchain is required to build libesa.so")
 
 
-def build(verbose: bool = False) -> str:
-    """Compiles every source and links libesa.so; returns its path."""
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
-           # packed fp32 VALU forms are kept out of every kernel
-           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-           "-Wno-unused-result",
-           "-I", os.path.join(HERE, "..", "include"),
-           *[os.path.join(CSRC, s) for s in SOURCES],
-           "-o", tmp]
+def _messages(res: subprocess.CompletedProcess) -> list:
+    # hipcc's host pass warns that it does not know the packed-fp32 feature
+    return [ln for ln in (res.stdout + res.stderr).splitlines()
+            if "packed-fp32-ops" not in ln and ln.strip()]
+
+
+def _compile(src: str, verbose: bool) -> str:
+    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+    cmd = [hipcc(), *FLAGS, "-I", os.path.join(HERE, "..", "include"), "-c",
+           os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    # hipcc's host pass warns that it does not know the packed-fp32 feature
-    msgs = [ln for ln in (res.stdout + res.stderr).splitlines()
-            if "packed-fp32-ops" not in ln and ln.strip()]
+    msgs = _messages(res)
     if res.returncode != 0:
-        raise RuntimeError("libesa.so build failed:\n" + "\n".join(msgs))
+        raise RuntimeError(f"compiling {src} failed:\n" + "\n".join(msgs))
     if verbose and msgs:
-        print("\n".join(msgs))
+        print("\n".join(msgs), flush=True)
+    return obj
+
+
+def build(verbose: bool = False) -> str:
+    """Compiles every source and links libesa.so; returns its path."""
+    os.makedirs(BUILD, exist_ok=True)
+    workers = min(len(SOURCES), max(1, min(os.cpu_count() or 1, 8)))
+    with cf.ThreadPoolExecutor(workers) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
+    tmp = LIB + ".tmp"
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("linking libesa.so failed:\n" + "\n".join(_messages(res)))
     os.replace(tmp, LIB)
     return LIB
 

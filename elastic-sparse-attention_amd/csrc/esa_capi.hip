@@ -2,6 +2,7 @@
 // Declarations and contracts: include/esa.h.
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <numeric>
 #include <vector>
 
@@ -71,9 +72,11 @@ size_t workspace_of(const esa_pattern& p, const LayoutDims& d) {
 
 bool aligned(const void* ptr, size_t a) { return ((uintptr_t)ptr % a) == 0; }
 
+size_t elem_bytes(esa_dtype t) { return t == ESA_F32 ? 4 : 2; }
+
 esa_status check_fwd_common(const esa_fwd_args* a) {
   if (!a || !a->q || !a->k || !a->v || !a->o) return ESA_ERR_NULL;
-  if (a->dtype != ESA_F32 && a->dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (a->dtype != ESA_F32 && a->dtype != ESA_BF16 && a->dtype != ESA_F16) return ESA_ERR_DTYPE;
   if (a->batch < 0 || a->num_heads < 1 || a->num_kv_heads < 1 || a->q_len < 0 || a->kv_len < 1 ||
       a->head_dim < 1)
     return ESA_ERR_SHAPE;
@@ -93,12 +96,14 @@ GatherArgs gather_args_of(const esa_fwd_args* a) {
   g.B = a->batch; g.H = a->num_heads; g.groups = a->num_heads / a->num_kv_heads;
   g.q_len = a->q_len; g.kv_len = a->kv_len; g.D = a->head_dim;
   g.sm_scale = a->sm_scale;
+  g.elem = a->dtype;  // ESA_F32 / ESA_BF16 / ESA_F16 are Elem's codes
+  g.src.kv_len = a->kv_len;
   return g;
 }
 
 esa_status check_gather_layout(const esa_fwd_args* a) {
   if (a->head_dim % 4 != 0 || a->head_dim > 256) return ESA_ERR_UNSUPPORTED;
-  const size_t es = a->dtype == ESA_F32 ? 4 : 2;
+  const size_t es = elem_bytes(a->dtype);
   // K rows are read 4 elements at a time.
   if (!aligned(a->k, 4 * es) || a->k_stride_s % 4 != 0 || a->k_stride_h % 4 != 0 ||
       a->k_stride_b % 4 != 0)
@@ -159,6 +164,115 @@ void plan_xcd_grid(const int32_t* row_ptr, int nqb, int nq, int batch, int H,
 }
 
 esa_status hip_status(hipError_t e) { return e == hipSuccess ? ESA_OK : ESA_ERR_HIP; }
+
+// Byte offsets of the gather backward's workspace regions (each 256-byte
+// aligned): per batch element and entry a dV and a dK coefficient, two
+// (key, entry id) pair buffers for the sort, the per-key segment starts and
+// the sort's digit histograms, their scan and its chunk sums.
+struct GatherBwdLayout {
+  int64_t E;  // entries per batch element: H * q_len * w
+  size_t cp, cs, ka, va, kb, vb, seg, hist, offs, parts, total;
+};
+
+esa_status gather_bwd_layout(const esa_bwd_args* a, int32_t w, GatherBwdLayout* L) {
+  if (a->batch < 0 || a->num_heads < 1 || a->num_kv_heads < 1 || a->q_len < 0 || a->kv_len < 1 ||
+      a->head_dim < 1 || w < 1 || w > kMaxW)
+    return ESA_ERR_SHAPE;
+  const int64_t E = (int64_t)a->num_heads * a->q_len * w;
+  // entry ids and sorted positions are 32-bit; the sort keys' sentinel is
+  // Hkv * kv_len
+  if (E >= INT32_MAX || (int64_t)a->num_kv_heads * a->kv_len >= INT32_MAX) return ESA_ERR_SHAPE;
+  int64_t hist_ints = 0, part_ints = 0;
+  gather_bwd_sort_sizes(E, &hist_ints, &part_ints);
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  size_t at = 0;
+  auto take = [&](size_t bytes) {
+    const size_t off = at;
+    at += up(bytes);
+    return off;
+  };
+  L->E = E;
+  L->cp = take((size_t)a->batch * E * 4);
+  L->cs = take((size_t)a->batch * E * 4);
+  L->ka = take((size_t)E * 4);
+  L->va = take((size_t)E * 4);
+  L->kb = take((size_t)E * 4);
+  L->vb = take((size_t)E * 4);
+  L->seg = take(((size_t)a->num_kv_heads * a->kv_len + 1) * 4);
+  L->hist = take((size_t)hist_ints * 4);
+  L->offs = take((size_t)hist_ints * 4);
+  L->parts = take((size_t)part_ints * 4);
+  L->total = at;
+  return ESA_OK;
+}
+
+// Checks shared by the gather backward entry points; fills g.
+esa_status gather_bwd_args(const esa_bwd_args* a, int32_t w, void* workspace,
+                           size_t workspace_bytes, GatherBwdArgs* g) {
+  if (!a || !a->q || !a->k || !a->v || !a->o || !a->dout || !a->dq || !a->dk || !a->dv || !a->lse)
+    return ESA_ERR_NULL;
+  if (a->dtype != ESA_F32 && a->dtype != ESA_BF16 && a->dtype != ESA_F16) return ESA_ERR_DTYPE;
+  if (a->num_heads < 1 || a->num_kv_heads < 1 || a->num_heads % a->num_kv_heads != 0)
+    return ESA_ERR_SHAPE;
+  if (a->kv_len > kMaxSeqLen || a->q_len > kMaxSeqLen) return ESA_ERR_SHAPE;
+  if (a->head_dim % 4 != 0 || a->head_dim > 256) return ESA_ERR_UNSUPPORTED;
+  GatherBwdLayout L;
+  esa_status s = gather_bwd_layout(a, w, &L);
+  if (s != ESA_OK) return s;
+  // K and V rows are read 4 elements at a time
+  const size_t es = elem_bytes(a->dtype);
+  if (!aligned(a->k, 4 * es) || !aligned(a->v, 4 * es)) return ESA_ERR_ALIGN;
+  const int64_t st[] = {a->k_stride_b, a->k_stride_h, a->k_stride_s,
+                        a->v_stride_b, a->v_stride_h, a->v_stride_s};
+  for (int64_t x : st)
+    if (x % 4 != 0) return ESA_ERR_ALIGN;
+  if (a->batch == 0) {  // nothing to write
+    g->B = 0;
+    return ESA_OK;
+  }
+  // (q_len = 0 still writes dK = dV = 0, as the reference's zeros_like does)
+  if (!workspace) return ESA_ERR_NULL;
+  if (workspace_bytes < L.total) return ESA_ERR_CAPACITY;
+  if (!aligned(workspace, 256)) return ESA_ERR_ALIGN;
+  GatherBwdArgs& t = *g;
+  t = GatherBwdArgs{};
+  t.q = a->q; t.k = a->k; t.v = a->v; t.o = a->o; t.dout = a->dout;
+  t.dq = a->dq; t.dk = a->dk; t.dv = a->dv; t.lse = a->lse;
+  t.qsb = a->q_stride_b; t.qsh = a->q_stride_h; t.qss = a->q_stride_s;
+  t.ksb = a->k_stride_b; t.ksh = a->k_stride_h; t.kss = a->k_stride_s;
+  t.vsb = a->v_stride_b; t.vsh = a->v_stride_h; t.vss = a->v_stride_s;
+  t.osb = a->o_stride_b; t.osh = a->o_stride_h; t.oss = a->o_stride_s;
+  t.dosb = a->dout_stride_b; t.dosh = a->dout_stride_h; t.doss = a->dout_stride_s;
+  t.dqsb = a->dq_stride_b; t.dqsh = a->dq_stride_h; t.dqss = a->dq_stride_s;
+  t.dksb = a->dk_stride_b; t.dksh = a->dk_stride_h; t.dkss = a->dk_stride_s;
+  t.dvsb = a->dv_stride_b; t.dvsh = a->dv_stride_h; t.dvss = a->dv_stride_s;
+  t.lsb = a->lse_stride_b; t.lsh = a->lse_stride_h;
+  t.B = a->batch; t.H = a->num_heads; t.Hkv = a->num_kv_heads;
+  t.groups = a->num_heads / a->num_kv_heads;
+  t.q_len = a->q_len; t.kv_len = a->kv_len; t.D = a->head_dim;
+  t.sm_scale = a->sm_scale;
+  t.elem = a->dtype;
+  t.src.w = w;
+  t.src.kv_len = a->kv_len;
+  t.drop.p = 0.f;
+  t.drop.scale = 1.f;
+  t.E = L.E;
+  char* ws = (char*)workspace;
+  t.cp = (float*)(ws + L.cp);
+  t.cs = (float*)(ws + L.cs);
+  t.keys_in = (uint32_t*)(ws + L.ka);
+  t.vals_in = (uint32_t*)(ws + L.va);
+  t.keys_out = (uint32_t*)(ws + L.kb);
+  t.vals_out = (uint32_t*)(ws + L.vb);
+  t.seg = (int32_t*)(ws + L.seg);
+  t.hist = (int32_t*)(ws + L.hist);
+  t.offs = (int32_t*)(ws + L.offs);
+  t.parts = (int32_t*)(ws + L.parts);
+  int bits = 1;
+  while (bits < 32 && ((uint64_t)1 << bits) <= (uint64_t)a->num_kv_heads * a->kv_len) ++bits;
+  t.key_bits = bits;  // the sentinel Hkv * kv_len fits
+  return ESA_OK;
+}
 
 // Row stride of the backward's per-row workspace (delta, lse2): q_len rounded
 // up to 32, plus 32, so a 32-row step that starts on a valid row reads inside
@@ -378,10 +492,39 @@ esa_status esa_elastic_fwd_rows(const esa_fwd_args* a, const esa_pattern* p,
   s = check_gather_layout(a);
   if (s != ESA_OK) return s;
   GatherArgs g = gather_args_of(a);
-  g.w = p->attention_length;
-  g.pc = make_consts(*p);
-  g.positions = positions;
-  return hip_status(launch_gather_fwd(g, a->dtype == ESA_F32, true, (hipStream_t)stream));
+  g.src.w = p->attention_length;
+  g.src.pc = make_consts(*p);
+  g.src.positions = positions;
+  return hip_status(launch_gather_fwd(g, true, (hipStream_t)stream));
+}
+
+esa_status esa_elastic_fwd_naive(const esa_fwd_args* a, const esa_pattern* p,
+                                 const int64_t* positions, const esa_naive_opts* opts,
+                                 void* stream) {
+  esa_status s = check_fwd_common(a);
+  if (s != ESA_OK) return s;
+  s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  if (!opts) return ESA_ERR_NULL;
+  if (p->num_heads != a->num_heads) return ESA_ERR_SHAPE;
+  if (!positions && a->q_len > a->kv_len) return ESA_ERR_SHAPE;
+  if (!(opts->dropout_p >= 0.f && opts->dropout_p < 1.f)) return ESA_ERR_SHAPE;
+  // the weights are formed from the forward's log-sum-exp
+  if (opts->weights && !a->lse) return ESA_ERR_NULL;
+  s = check_gather_layout(a);
+  if (s != ESA_OK) return s;
+  GatherArgs g = gather_args_of(a);
+  g.src.w = p->attention_length;
+  g.src.pc = make_consts(*p);
+  g.src.positions = positions;
+  g.drop.p = opts->dropout_p;
+  g.drop.scale = opts->dropout_p > 0.f ? 1.0f / (1.0f - opts->dropout_p) : 1.0f;
+  g.drop.seed = opts->seed;
+  g.weights = opts->weights;
+  g.wsb = opts->weights_stride_b; g.wsh = opts->weights_stride_h; g.wss = opts->weights_stride_s;
+  hipError_t e = launch_gather_fwd(g, true, (hipStream_t)stream);
+  if (e == hipSuccess && opts->weights) e = launch_gather_weights(g, true, (hipStream_t)stream);
+  return hip_status(e);
 }
 
 esa_status esa_sparse_fwd(const esa_fwd_args* a, const void* indices, int32_t index_bytes,
@@ -397,11 +540,12 @@ esa_status esa_sparse_fwd(const esa_fwd_args* a, const void* indices, int32_t in
   s = check_gather_layout(a);
   if (s != ESA_OK) return s;
   GatherArgs g = gather_args_of(a);
-  g.w = attn_length;
-  g.indices = indices; g.mask = mask;
-  g.index_bytes = index_bytes; g.mask_bytes = mask_bytes;
-  g.ish = idx_stride_h; g.iss = idx_stride_s; g.msh = mask_stride_h; g.mss = mask_stride_s;
-  return hip_status(launch_gather_fwd(g, a->dtype == ESA_F32, false, (hipStream_t)stream));
+  g.src.w = attn_length;
+  g.src.indices = indices; g.src.mask = mask;
+  g.src.index_bytes = index_bytes; g.src.mask_bytes = mask_bytes;
+  g.src.ish = idx_stride_h; g.src.iss = idx_stride_s;
+  g.src.msh = mask_stride_h; g.src.mss = mask_stride_s;
+  return hip_status(launch_gather_fwd(g, false, (hipStream_t)stream));
 }
 
 esa_status esa_plan_bwd(const esa_pattern* p, const int32_t* row_ptr_host,
@@ -511,12 +655,52 @@ esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes
   return ESA_OK;
 }
 
-esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const int32_t* row_ptr,
-                           const int32_t* col_idx, const int32_t* q_items, int64_t num_q_items,
-                           const int32_t* tile_row, const int32_t* kv_ptr,
-                           const int32_t* kv_tiles, const int32_t* kv_items,
-                           int64_t num_kv_items, const uint32_t* mask_t, void* workspace,
-                           size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Workspace of esa_elastic_bwd_noalloc: one array per device, set up by the
+// code-object loader when the library's kernels are loaded on that device and
+// held until the process ends.  Host code never passes `scratch` itself (on
+// the host the name is a stand-in, not a device address): the device address
+// comes from hipGetSymbolAddress, once per device, in scratch_of.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device `stream` belongs to.
+esa_status scratch_of(hipStream_t stream, void** out) {
+  int dev = 0, cur = 0;
+  if (hipGetDevice(&cur) != hipSuccess) return ESA_ERR_HIP;
+  dev = cur;
+  if (stream && hipStreamGetDevice(stream, &dev) != hipSuccess) return ESA_ERR_HIP;
+  if (dev < 0 || dev >= kMaxDevices) return ESA_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    // the symbol's address on a device is looked up with that device current
+    if (dev != cur && hipSetDevice(dev) != hipSuccess) return ESA_ERR_HIP;
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (dev != cur && hipSetDevice(cur) != hipSuccess) return ESA_ERR_HIP;
+    if (e != hipSuccess || !ptr) return ESA_ERR_HIP;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return ESA_OK;
+}
+
+// The backward's argument checks and launches; `workspace` is the caller's
+// buffer (esa_elastic_bwd) or the device's scratch array
+// (esa_elastic_bwd_noalloc, workspace NULL until the checks pass).
+esa_status elastic_bwd_impl(const esa_bwd_args* a, const esa_pattern* p, const int32_t* row_ptr,
+                            const int32_t* col_idx, const int32_t* q_items, int64_t num_q_items,
+                            const int32_t* tile_row, const int32_t* kv_ptr,
+                            const int32_t* kv_tiles, const int32_t* kv_items,
+                            int64_t num_kv_items, const uint32_t* mask_t, void* workspace,
+                            size_t workspace_bytes, bool static_ws, void* stream) {
   if (!a || !a->q || !a->k || !a->v || !a->o || !a->dout || !a->dq || !a->dk || !a->dv || !a->lse)
     return ESA_ERR_NULL;
   esa_status s = check_pattern(p);
@@ -525,7 +709,7 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
   // kv_items NULL: dK / dV by the band-gathered kernel (no work list, tile
   // lists or masks)
   const bool band_dq = q_items == nullptr, band_dkdv = kv_items == nullptr;
-  if (!workspace || (!band_dq && (!row_ptr || !col_idx)) ||
+  if ((!static_ws && !workspace) || (!band_dq && (!row_ptr || !col_idx)) ||
       (!band_dkdv && (!tile_row || !kv_ptr || !kv_tiles || !mask_t)))
     return ESA_ERR_NULL;
   if ((band_dq || band_dkdv) && (p->attention_length > 64 || a->kv_len >= (1 << 24)))
@@ -564,7 +748,7 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
   size_t need = 0;
   esa_bwd_workspace_size(a, &need);
   if (workspace_bytes < need) return ESA_ERR_CAPACITY;
-  if (!aligned(workspace, 16)) return ESA_ERR_ALIGN;
+  if (!static_ws && !aligned(workspace, 16)) return ESA_ERR_ALIGN;
   const LayoutDims d = dims_of(*p);
   const int nq = (a->q_len + 127) / 128;
   const int64_t n_real = (int64_t)a->batch * a->num_heads * nq;
@@ -575,6 +759,10 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
       (num_kv_items < kv_real || num_kv_items > 8 * std::max<int64_t>(kv_real, 1)))
     return ESA_ERR_SHAPE;
   if (a->batch == 0 || a->q_len == 0) return ESA_OK;
+  if (static_ws) {
+    esa_status ss = scratch_of((hipStream_t)stream, &workspace);
+    if (ss != ESA_OK) return ss;
+  }
 
   BwdArgs t{};
   t.q = (const uint16_t*)a->q; t.k = (const uint16_t*)a->k; t.v = (const uint16_t*)a->v;
@@ -625,6 +813,82 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
   }
   return hip_status(launch_tile_bwd(t, a->head_dim, band_dq ? -1 : num_q_items,
                                     band_dkdv ? -1 : num_kv_items, (hipStream_t)stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const int32_t* row_ptr,
+                           const int32_t* col_idx, const int32_t* q_items, int64_t num_q_items,
+                           const int32_t* tile_row, const int32_t* kv_ptr,
+                           const int32_t* kv_tiles, const int32_t* kv_items,
+                           int64_t num_kv_items, const uint32_t* mask_t, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  return elastic_bwd_impl(a, p, row_ptr, col_idx, q_items, num_q_items, tile_row, kv_ptr,
+                          kv_tiles, kv_items, num_kv_items, mask_t, workspace, workspace_bytes,
+                          false, stream);
+}
+
+size_t esa_bwd_noalloc_max_workspace(void) { return kScratchBytes; }
+
+esa_status esa_elastic_bwd_noalloc(const esa_bwd_args* a, const esa_pattern* p,
+                                   const int32_t* row_ptr, const int32_t* col_idx,
+                                   const int32_t* q_items, int64_t num_q_items,
+                                   const int32_t* tile_row, const int32_t* kv_ptr,
+                                   const int32_t* kv_tiles, const int32_t* kv_items,
+                                   int64_t num_kv_items, const uint32_t* mask_t, void* stream) {
+  return elastic_bwd_impl(a, p, row_ptr, col_idx, q_items, num_q_items, tile_row, kv_ptr,
+                          kv_tiles, kv_items, num_kv_items, mask_t, nullptr, kScratchBytes, true,
+                          stream);
+}
+
+esa_status esa_gather_bwd_workspace_size(const esa_bwd_args* a, int32_t attn_length,
+                                         size_t* workspace_bytes) {
+  if (!a || !workspace_bytes) return ESA_ERR_NULL;
+  GatherBwdLayout L;
+  esa_status s = gather_bwd_layout(a, attn_length, &L);
+  if (s != ESA_OK) return s;
+  *workspace_bytes = L.total;
+  return ESA_OK;
+}
+
+esa_status esa_sparse_bwd(const esa_bwd_args* a, const void* indices, int32_t index_bytes,
+                          int64_t idx_stride_h, int64_t idx_stride_s, const void* mask,
+                          int32_t mask_bytes, int64_t mask_stride_h, int64_t mask_stride_s,
+                          int32_t attn_length, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  if (!indices || !mask) return ESA_ERR_NULL;
+  if (index_bytes != 4 && index_bytes != 8) return ESA_ERR_DTYPE;
+  if (mask_bytes != 1 && mask_bytes != 4 && mask_bytes != 8) return ESA_ERR_DTYPE;
+  GatherBwdArgs g;
+  esa_status s = gather_bwd_args(a, attn_length, workspace, workspace_bytes, &g);
+  if (s != ESA_OK || g.B == 0) return s;
+  g.src.indices = indices; g.src.mask = mask;
+  g.src.index_bytes = index_bytes; g.src.mask_bytes = mask_bytes;
+  g.src.ish = idx_stride_h; g.src.iss = idx_stride_s;
+  g.src.msh = mask_stride_h; g.src.mss = mask_stride_s;
+  return hip_status(launch_gather_bwd(g, false, (hipStream_t)stream));
+}
+
+esa_status esa_elastic_bwd_rows(const esa_bwd_args* a, const esa_pattern* p,
+                                const int64_t* positions, float dropout_p, uint64_t seed,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  esa_status s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  if (!a) return ESA_ERR_NULL;
+  if (p->num_heads != a->num_heads) return ESA_ERR_SHAPE;
+  if (!positions && a->q_len > a->kv_len) return ESA_ERR_SHAPE;
+  if (!(dropout_p >= 0.f && dropout_p < 1.f)) return ESA_ERR_SHAPE;
+  GatherBwdArgs g;
+  s = gather_bwd_args(a, p->attention_length, workspace, workspace_bytes, &g);
+  if (s != ESA_OK || g.B == 0) return s;
+  g.src.pc = make_consts(*p);
+  g.src.positions = positions;
+  g.drop.p = dropout_p;
+  g.drop.scale = dropout_p > 0.f ? 1.0f / (1.0f - dropout_p) : 1.0f;
+  g.drop.seed = seed;
+  return hip_status(launch_gather_bwd(g, true, (hipStream_t)stream));
 }
 
 esa_status esa_reachability(int32_t seq_len, int32_t attention_length,

@@ -56,6 +56,30 @@ struct BandArgs {
   PatternConsts pc;
 };
 
+// Where a query row's w entries come from: the elastic pattern (regenerated
+// on the device, rows at positions[r] or r) or explicit index / mask arrays
+// [H, q_len, w].
+struct IndexSource {
+  int w;       // entries per row
+  int kv_len;  // keys; pattern keys are clamped to [0, kv_len - 1]
+  // pattern source
+  PatternConsts pc;
+  const int64_t* positions;  // may be NULL (row r is position r)
+  // explicit-index source
+  const void* indices;
+  const void* mask;
+  int index_bytes, mask_bytes;
+  int64_t ish, iss, msh, mss;
+};
+
+// Attention dropout on the probabilities (the naive path in training mode,
+// elastic_sparse_attention.py:674): p = 0 switches it off.
+struct DropoutArgs {
+  float p;        // drop probability
+  float scale;    // 1 / (1 - p)
+  uint64_t seed;  // keep decisions are a function of (seed, b, h, row, entry)
+};
+
 // Arguments of the per-row gather forward.
 struct GatherArgs {
   const void* q;
@@ -70,15 +94,54 @@ struct GatherArgs {
   int64_t lsb, lsh;
   int B, H, groups, q_len, kv_len, D;
   float sm_scale;
-  int w;  // entries per row
-  // pattern source
-  PatternConsts pc;
-  const int64_t* positions;  // may be NULL (row r is position r)
-  // explicit-index source
-  const void* indices;
-  const void* mask;
-  int index_bytes, mask_bytes;
-  int64_t ish, iss, msh, mss;
+  int elem;  // Elem of q, k, v, o (0 float32, 1 bfloat16, 2 float16)
+  IndexSource src;
+  DropoutArgs drop;
+  // naive-path attention weights [B, H, q_len, w] in q's type (may be NULL;
+  // written by launch_gather_weights from the forward's lse)
+  void* weights;
+  int64_t wsb, wsh, wss;
+};
+
+// Arguments of the gather backward (any index source, float32 / bfloat16 /
+// float16): per-row pass (dQ and each entry's dK / dV coefficients), a stable
+// sort of the (kv head, key) of every valid entry, then a key-major pass.
+struct GatherBwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* o;
+  const void* dout;
+  void* dq;
+  void* dk;
+  void* dv;
+  const float* lse;
+  int64_t qsb, qsh, qss;
+  int64_t ksb, ksh, kss;
+  int64_t vsb, vsh, vss;
+  int64_t osb, osh, oss;
+  int64_t dosb, dosh, doss;
+  int64_t dqsb, dqsh, dqss;
+  int64_t dksb, dksh, dkss;
+  int64_t dvsb, dvsh, dvss;
+  int64_t lsb, lsh;
+  int B, H, Hkv, groups, q_len, kv_len, D;
+  float sm_scale;
+  int elem;
+  IndexSource src;
+  DropoutArgs drop;
+  int64_t E;          // entries per batch element: H * q_len * w
+  float* cp;          // [B][E] dV coefficient of each entry (dropout-scaled p)
+  float* cs;          // [B][E] dK coefficient of each entry (sm_scale * dS)
+  uint32_t* keys_in;  // [E] kv_head * kv_len + key of a valid in-range entry, else the sentinel
+  uint32_t* vals_in;  // [E] entry ids 0 .. E - 1
+  uint32_t* keys_out;
+  uint32_t* vals_out;
+  int32_t* seg;       // [Hkv * kv_len + 1] start of each (kv head, key) in the sorted order
+  int32_t* hist;      // radix sort: digit counts per tile, then their scan (offs)
+  int32_t* offs;
+  int32_t* parts;     // chunk sums of the scan
+  int key_bits;       // bits of the sort keys
 };
 
 // Arguments of the block-sparse MFMA backward (bf16).
@@ -143,7 +206,12 @@ hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2, boo
                           hipStream_t stream);
 hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,
                             hipStream_t stream);
-hipError_t launch_gather_fwd(const GatherArgs& a, bool f32, bool pattern, hipStream_t stream);
+hipError_t launch_gather_fwd(const GatherArgs& a, bool pattern, hipStream_t stream);
+hipError_t launch_gather_weights(const GatherArgs& a, bool pattern, hipStream_t stream);
+// int32 entries of the sort's digit histograms (and of their scan) and of
+// its scan's chunk sums, for n pairs
+void gather_bwd_sort_sizes(int64_t n, int64_t* hist_ints, int64_t* part_ints);
+hipError_t launch_gather_bwd(const GatherBwdArgs& a, bool pattern, hipStream_t stream);
 hipError_t launch_tile_masks(const PatternConsts& pc, const int32_t* row_ptr, const int32_t* col_idx,
                              int nqb, int q_len, uint32_t* mask_t, hipStream_t stream);
 hipError_t launch_reachability(const PatternConsts* layers, int num_layers, int position,

@@ -32,15 +32,25 @@ GPU, by the HIP index builder.
 
 Differences from the reference, all deliberate:
 * ``implementation`` accepts "triton", "naive" and "dense" (anything else is
-  the reference's ValueError); all three run the HIP kernels and return
-  ``None`` attention weights.  There is no CPU path: CPU tensors raise.
-* ``attention_dropout`` is ignored, as the reference's Triton path ignores it.
-* Backward: the prefill bf16 path (head_dim 64 or 128) backpropagates
-  through hand-written MFMA kernels, band-gathered or block-sparse like the
-  forward (deterministic, no atomics); the other paths (decode rows,
-  float32, explicit index lists) raise NotImplementedError in backward.
+  the reference's ValueError); all three run the HIP kernels.  "naive"
+  returns the attention weights ``[B, H, Lq, w]`` as the reference's naive
+  path does (:680; not differentiable here), the others ``None``.  There is
+  no CPU path: CPU tensors raise.
+* ``attention_dropout`` applies in training mode to "naive" and "dense" (as
+  the reference's naive and SDPA paths apply it, :674, :721) and not to
+  "triton" (whose kernel ignores it).  Keep decisions come from a
+  counter-based hash seeded from torch's generator, not torch's own random
+  stream, so the mask differs from torch.dropout's draw for the same seed.
+* Every path backpropagates, deterministically (no atomics on the
+  gradients): bf16 prefill with head_dim 64 or 128 through hand-written MFMA
+  kernels (band-gathered or block-sparse like the forward); the others
+  (decode rows, float32, float16, other head dims, dropout, explicit index
+  lists) through the gather backward (row pass, stable key sort, key-major
+  pass).
 * A query row with no valid entry (impossible for the elastic pattern, only
   reachable through explicit masks) gives output 0 rather than NaN.
+* A cache_position on the device is not range-checked on the host (that
+  would synchronise); an out-of-range position gives a NaN row.
 """
 from __future__ import annotations
 
@@ -51,7 +61,8 @@ from typing import Dict, Optional, Tuple
 import torch
 import torch.nn as nn
 
-from esa_native import (ESA_BF16, ESA_F32, EsaBwdArgs, EsaFwdArgs, EsaPattern, check, load)
+from esa_native import (ESA_BF16, ESA_F16, ESA_F32, EsaBwdArgs, EsaFwdArgs, EsaNaiveOpts,
+                        EsaPattern, check, load)
 
 logger = logging.getLogger(__name__)
 
@@ -83,7 +94,10 @@ def _dtype_code(dt: torch.dtype) -> int:
         return ESA_BF16
     if dt == torch.float32:
         return ESA_F32
-    raise ValueError(f"unsupported dtype {dt}: the HIP kernels take bfloat16 or float32")
+    if dt == torch.float16:
+        return ESA_F16
+    raise ValueError(f"unsupported dtype {dt}: the HIP kernels take bfloat16, float16 or "
+                     "float32")
 
 
 def _require_gpu(*ts: torch.Tensor) -> None:
@@ -326,6 +340,9 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
                          f"({k.shape[1]})")
 
 
+# input types the MFMA prefill kernels take (others run the per-row gather)
+MFMA_DTYPES = (torch.bfloat16,)
+
 # Measured crossover (MI355X) between the two prefill kernels: the band
 # kernel costs about the same per 16-row group at every layer, the tile
 # kernel about the same per staged 64 x 32 block, and the band kernel is the
@@ -422,24 +439,52 @@ def elastic_attention_band(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return o, lse
 
 
+def _positions_ptr(positions: Optional[torch.Tensor], q_len: int, device: torch.device):
+    if positions is None:
+        return None, None
+    if positions.dtype != torch.int64 or positions.device != device or \
+            positions.numel() != q_len:
+        raise ValueError("positions must be an int64 tensor of q_len entries on q's device")
+    positions = positions.contiguous()
+    return positions, ctypes.c_void_p(positions.data_ptr())
+
+
 def elastic_attention_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                            pattern: EsaPattern, scaling: float,
-                           positions: Optional[torch.Tensor] = None, return_lse: bool = True
-                           ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
-    """Per-row gather forward over the pattern; query row r is position
-    ``positions[r]`` (int64 on the device) or r.  Output ``[B, Lq, H, D]``."""
+                           positions: Optional[torch.Tensor] = None, return_lse: bool = True,
+                           dropout_p: float = 0.0, seed: int = 0, return_weights: bool = False
+                           ):
+    """Per-row gather forward over the pattern (float32, bfloat16 or
+    float16, any head_dim that is a multiple of 4 up to 256); query row r is
+    position ``positions[r]`` (int64 on the device) or r.  Output
+    ``[B, Lq, H, D]`` and, if asked, lse ``[B, H, Lq]``.
+
+    ``dropout_p`` > 0 applies attention dropout to the probabilities (the
+    naive path in training mode, :674) with keep decisions drawn from
+    ``seed``; ``return_weights`` also returns the naive path's attention
+    weights ``[B, H, Lq, w]`` (after dropout, :673-680) as a third value."""
     _check_qkv(q, k, v)
     B, H, Lq, D = q.shape
     q, k, v = _prep(q, 4), _prep(k, 4), _prep(v, 4)
     o = torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
-    lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
-    pos_ptr = None
-    if positions is not None:
-        if positions.dtype != torch.int64 or positions.device != q.device or positions.numel() != Lq:
-            raise ValueError("positions must be an int64 tensor of q_len entries on q's device")
-        positions = positions.contiguous()
-        pos_ptr = ctypes.c_void_p(positions.data_ptr())
+    need_lse = return_lse or return_weights
+    lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if need_lse else None
+    positions, pos_ptr = _positions_ptr(positions, Lq, q.device)
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
+    if dropout_p > 0.0 or return_weights:
+        wts = None
+        opts = EsaNaiveOpts()
+        opts.dropout_p = float(dropout_p)
+        opts.seed = int(seed) & ((1 << 64) - 1)
+        if return_weights:
+            wts = torch.empty(B, H, Lq, pattern.attention_length, dtype=q.dtype, device=q.device)
+            opts.weights = wts.data_ptr()
+            opts.weights_stride_b, opts.weights_stride_h, opts.weights_stride_s = wts.stride()[:3]
+        check(load().esa_elastic_fwd_naive(ctypes.byref(a), ctypes.byref(pattern), pos_ptr,
+                                           ctypes.byref(opts), _stream(q.device)),
+              "esa_elastic_fwd_naive")
+        lse_out = lse if return_lse else None
+        return (o, lse_out, wts) if return_weights else (o, lse_out)
     check(load().esa_elastic_fwd_rows(ctypes.byref(a), ctypes.byref(pattern), pos_ptr,
                                       _stream(q.device)), "esa_elastic_fwd_rows")
     return o, lse
@@ -465,13 +510,7 @@ def sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if sparse_indices.dtype not in (torch.int64, torch.int32):
         raise ValueError("sparse_indices must be int64 or int32")
     q, k, v = _prep(q, 4), _prep(k, 4), _prep(v, 4)
-    idx = sparse_indices.contiguous()
-    msk = sparse_mask
-    if msk.dtype == torch.bool:
-        msk = msk.to(torch.uint8)
-    elif msk.dtype not in (torch.int64, torch.int32, torch.uint8):
-        msk = msk.to(torch.int32)
-    msk = msk.contiguous()
+    idx, msk = _index_arrays(sparse_indices, sparse_mask)
     o = torch.empty(B, H, Lq, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device)
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(1), o.stride(2)), lse, sm_scale)
@@ -483,11 +522,108 @@ def sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return o, lse
 
 
+def _bwd_args(q, k, v, o, o_strides, lse, dout, dout_strides, dq, dk, dv, scaling) -> EsaBwdArgs:
+    B, H, Lq, D = q.shape
+    a = EsaBwdArgs()
+    a.dtype = _dtype_code(q.dtype)
+    a.batch, a.num_heads, a.num_kv_heads = B, H, k.shape[1]
+    a.q_len, a.kv_len, a.head_dim = Lq, k.shape[2], D
+    for name, t, strides in (("q", q, q.stride()[:3]), ("k", k, k.stride()[:3]),
+                             ("v", v, v.stride()[:3]), ("o", o, o_strides),
+                             ("dout", dout, dout_strides), ("dq", dq, dq.stride()[:3]),
+                             ("dk", dk, dk.stride()[:3]), ("dv", dv, dv.stride()[:3])):
+        setattr(a, name, t.data_ptr())
+        for ax, st in zip("bhs", strides):
+            setattr(a, f"{name}_stride_{ax}", st)
+    a.lse = lse.data_ptr()
+    a.lse_stride_b, a.lse_stride_h = lse.stride(0), lse.stride(1)
+    a.sm_scale = float(scaling)
+    return a
+
+
+def _gather_workspace(a: EsaBwdArgs, w: int, device: torch.device) -> torch.Tensor:
+    ws = ctypes.c_size_t()
+    check(load().esa_gather_bwd_workspace_size(ctypes.byref(a), int(w), ctypes.byref(ws)),
+          "esa_gather_bwd_workspace_size")
+    return torch.empty(max(ws.value, 256), dtype=torch.uint8, device=device)
+
+
+def elastic_attention_bwd_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                               o: torch.Tensor, lse: torch.Tensor, dout: torch.Tensor,
+                               pattern: EsaPattern, scaling: float,
+                               positions: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
+                               seed: int = 0
+                               ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gather backward of :func:`elastic_attention_rows` (any dtype it takes,
+    any head_dim, decode positions, dropout with the forward's seed): ``o``
+    and ``dout`` ``[B, Lq, H, D]``, ``lse`` ``[B, H, Lq]``.  Returns ``dq``
+    ``[B, H, Lq, D]``, ``dk`` and ``dv`` ``[B, Hkv, Lk, D]``; deterministic
+    (no atomics on the gradients)."""
+    _check_qkv(q, k, v)
+    B, H, Lq, D = q.shape
+    q, k, v = _prep(q, 4), _prep(k, 4), _prep(v, 4)
+    dout = dout.to(q.dtype)
+    lse = lse.contiguous()
+    dq = torch.empty(B, H, Lq, D, dtype=q.dtype, device=q.device)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    a = _bwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, dout,
+                  (dout.stride(0), dout.stride(2), dout.stride(1)), dq, dk, dv, scaling)
+    work = _gather_workspace(a, pattern.attention_length, q.device)
+    positions, pos_ptr = _positions_ptr(positions, Lq, q.device)
+    check(load().esa_elastic_bwd_rows(ctypes.byref(a), ctypes.byref(pattern), pos_ptr,
+                                      float(dropout_p), int(seed) & ((1 << 64) - 1),
+                                      ctypes.c_void_p(work.data_ptr()), work.numel(),
+                                      _stream(q.device)), "esa_elastic_bwd_rows")
+    return dq, dk, dv
+
+
+def _index_arrays(sparse_indices: torch.Tensor, sparse_mask: torch.Tensor):
+    idx = sparse_indices.contiguous()
+    msk = sparse_mask
+    if msk.dtype == torch.bool:
+        msk = msk.to(torch.uint8)
+    elif msk.dtype not in (torch.int64, torch.int32, torch.uint8):
+        msk = msk.to(torch.int32)
+    return idx, msk.contiguous()
+
+
+def sparse_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
+                         lse: torch.Tensor, dout: torch.Tensor, sparse_indices: torch.Tensor,
+                         sparse_mask: torch.Tensor, sm_scale: float
+                         ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Backward of :func:`sparse_attention_fwd` (the reference operator's
+    backward, :299-339): ``o`` and ``dout`` ``[B, H, Lq, D]``.  Returns
+    ``dq``, ``dk``, ``dv`` in the inputs' shapes and dtype; deterministic."""
+    _check_qkv(q, k, v)
+    B, H, Lq, D = q.shape
+    q, k, v = _prep(q, 4), _prep(k, 4), _prep(v, 4)
+    dout = dout.to(q.dtype)
+    idx, msk = _index_arrays(sparse_indices, sparse_mask)
+    dq = torch.empty(B, H, Lq, D, dtype=q.dtype, device=q.device)
+    dk = torch.empty_like(k, memory_format=torch.contiguous_format)
+    dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    a = _bwd_args(q, k, v, o, o.stride()[:3], lse.contiguous(), dout, dout.stride()[:3], dq, dk,
+                  dv, sm_scale)
+    work = _gather_workspace(a, idx.shape[2], q.device)
+    check(load().esa_sparse_bwd(ctypes.byref(a), ctypes.c_void_p(idx.data_ptr()),
+                                idx.element_size(), idx.stride(0), idx.stride(1),
+                                ctypes.c_void_p(msk.data_ptr()), msk.element_size(),
+                                msk.stride(0), msk.stride(1), idx.shape[2],
+                                ctypes.c_void_p(work.data_ptr()), work.numel(),
+                                _stream(q.device)), "esa_sparse_bwd")
+    return dq, dk, dv
+
+
 def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
                           lse: torch.Tensor, dout: torch.Tensor, layout: ElasticLayout,
-                          scaling: float, dq_kernel: str = "auto", dkdv_kernel: str = "auto"
+                          scaling: float, dq_kernel: str = "auto", dkdv_kernel: str = "auto",
+                          noalloc: bool = False
                           ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """MFMA backward of ``elastic_attention_fwd`` (prefill, bf16).
+
+    ``noalloc``: call ``esa_elastic_bwd_noalloc`` (the library's per-device
+    workspace array, no workspace allocation) instead of ``esa_elastic_bwd``.
 
     ``o`` and ``dout`` are ``[B, Lq, H, D]`` (the forward's output layout),
     ``lse`` float32 ``[B, H, Lq]``.  Returns ``dq`` ``[B, H, Lq, D]`` and
@@ -507,26 +643,15 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
     dq = torch.empty_like(q)
     dk = torch.empty(B, Hkv, Lk, D, dtype=k.dtype, device=k.device)
     dv = torch.empty(B, Hkv, Lk, D, dtype=v.dtype, device=v.device)
-    a = EsaBwdArgs()
-    a.dtype = _dtype_code(q.dtype)
-    a.batch, a.num_heads, a.num_kv_heads = B, H, Hkv
-    a.q_len, a.kv_len, a.head_dim = Lq, Lk, D
-    for name, t, strides in (("q", q, q.stride()[:3]), ("k", k, k.stride()[:3]),
-                             ("v", v, v.stride()[:3]),
-                             ("o", o, (o.stride(0), o.stride(2), o.stride(1))),
-                             ("dout", dout, (dout.stride(0), dout.stride(2), dout.stride(1))),
-                             ("dq", dq, dq.stride()[:3]), ("dk", dk, dk.stride()[:3]),
-                             ("dv", dv, dv.stride()[:3])):
-        setattr(a, name, t.data_ptr())
-        for ax, st in zip("bhs", strides):
-            setattr(a, f"{name}_stride_{ax}", st)
-    a.lse = lse.data_ptr()
-    a.lse_stride_b, a.lse_stride_h = lse.stride(0), lse.stride(1)
-    a.sm_scale = float(scaling)
+    a = _bwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, dout,
+                  (dout.stride(0), dout.stride(2), dout.stride(1)), dq, dk, dv, scaling)
     lib = load()
-    ws = ctypes.c_size_t()
-    check(lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(ws)), "esa_bwd_workspace_size")
-    work = torch.empty(max(ws.value // 4, 4), dtype=torch.float32, device=q.device)
+    work = None
+    if not noalloc:
+        ws = ctypes.c_size_t()
+        check(lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(ws)),
+              "esa_bwd_workspace_size")
+        work = torch.empty(max(ws.value // 4, 4), dtype=torch.float32, device=q.device)
     for name, val in (("dq_kernel", dq_kernel), ("dkdv_kernel", dkdv_kernel)):
         if val not in ("auto", "tile", "band"):
             raise ValueError(f"{name} must be 'auto', 'tile' or 'band', got {val!r}")
@@ -547,11 +672,18 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
     else:
         tile_row, kv_ptr, kv_tiles, kv_items, n_kv = layout.bwd_plan(Lq, B, Hkv)
         masks = layout.tile_masks(Lq)
-    check(lib.esa_elastic_bwd(ctypes.byref(a), ctypes.byref(layout.pattern),
-                              ptr(layout.row_ptr), ptr(layout.col_idx), ptr(items), n_items,
-                              ptr(tile_row), ptr(kv_ptr), ptr(kv_tiles), ptr(kv_items), n_kv,
-                              ptr(masks), ptr(work), work.numel() * 4, _stream(q.device)),
-          "esa_elastic_bwd")
+    if noalloc:
+        check(lib.esa_elastic_bwd_noalloc(ctypes.byref(a), ctypes.byref(layout.pattern),
+                                          ptr(layout.row_ptr), ptr(layout.col_idx), ptr(items),
+                                          n_items, ptr(tile_row), ptr(kv_ptr), ptr(kv_tiles),
+                                          ptr(kv_items), n_kv, ptr(masks), _stream(q.device)),
+              "esa_elastic_bwd_noalloc")
+    else:
+        check(lib.esa_elastic_bwd(ctypes.byref(a), ctypes.byref(layout.pattern),
+                                  ptr(layout.row_ptr), ptr(layout.col_idx), ptr(items), n_items,
+                                  ptr(tile_row), ptr(kv_ptr), ptr(kv_tiles), ptr(kv_items), n_kv,
+                                  ptr(masks), ptr(work), work.numel() * 4, _stream(q.device)),
+              "esa_elastic_bwd")
     return dq, dk, dv
 
 
@@ -577,30 +709,49 @@ class _ElasticTileAttention(torch.autograd.Function):
 
 class ElasticSparseAttentionFunction(torch.autograd.Function):
     """The reference's operator (:235-339): ``apply(q, k, v, sparse_indices,
-    sparse_mask, sm_scale, num_kv_groups) -> o [B, H, Lq, D]``.  Forward only;
-    ``backward`` raises NotImplementedError."""
+    sparse_mask, sm_scale, num_kv_groups) -> o [B, H, Lq, D]``, with its
+    backward (dq, dk, dv; none for the index arguments) by the gather
+    backward kernels, deterministic where the reference uses atomics."""
 
     @staticmethod
     def forward(ctx, q, k, v, sparse_indices, sparse_mask, sm_scale, num_kv_groups):
-        o, _ = sparse_attention_fwd(q, k, v, sparse_indices, sparse_mask, sm_scale,
-                                    num_kv_groups)
+        o, lse = sparse_attention_fwd(q, k, v, sparse_indices, sparse_mask, sm_scale,
+                                      num_kv_groups)
+        ctx.save_for_backward(q, k, v, o, lse, sparse_indices, sparse_mask)
+        ctx.sm_scale = sm_scale
         return o
 
     @staticmethod
     def backward(ctx, do):
-        raise NotImplementedError("the elastic sparse attention backward is not built")
+        q, k, v, o, lse, idx, msk = ctx.saved_tensors
+        dq, dk, dv = sparse_attention_bwd(q, k, v, o, lse, do, idx, msk, ctx.sm_scale)
+        return dq, dk, dv, None, None, None, None
 
 
-class _ForwardOnly(torch.autograd.Function):
-    """Marks a module output as not differentiable through this op."""
+class _ElasticRowsAttention(torch.autograd.Function):
+    """The per-row gather forward over the pattern with the gather backward:
+    ``apply(q, k, v, pattern, scaling, positions, dropout_p, seed,
+    with_weights) -> (o [B, Lq, H, D], weights)``; weights is the naive
+    path's ``[B, H, Lq, w]`` (not differentiable) or an empty tensor."""
 
     @staticmethod
-    def forward(ctx, out, *inputs):
-        return out
+    def forward(ctx, q, k, v, pattern, scaling, positions, dropout_p, seed, with_weights):
+        got = elastic_attention_rows(q, k, v, pattern, scaling, positions, return_lse=True,
+                                     dropout_p=dropout_p, seed=seed,
+                                     return_weights=with_weights)
+        o, lse = got[0], got[1]
+        wts = got[2] if with_weights else o.new_empty(0)
+        ctx.save_for_backward(q, k, v, o, lse, positions)
+        ctx.pattern, ctx.scaling, ctx.dropout_p, ctx.seed = pattern, scaling, dropout_p, seed
+        ctx.mark_non_differentiable(wts)
+        return o, wts
 
     @staticmethod
-    def backward(ctx, *grads):
-        raise NotImplementedError("the elastic sparse attention backward is not built")
+    def backward(ctx, do, _dw):
+        q, k, v, o, lse, positions = ctx.saved_tensors
+        dq, dk, dv = elastic_attention_bwd_rows(q, k, v, o, lse, do, ctx.pattern, ctx.scaling,
+                                                positions, ctx.dropout_p, ctx.seed)
+        return dq, dk, dv, None, None, None, None, None, None
 
 
 class ElasticSparseAttention(nn.Module):
@@ -723,25 +874,38 @@ class ElasticSparseAttention(nn.Module):
                 f"expected {self.num_attention_heads} query heads and "
                 f"{self.num_key_value_heads} key/value heads; got {H} and {k.shape[1]}")
         self._last_device = q.device
+        pos = None
         if cache_position is None:
             if Lq > kv_len:
                 raise ValueError(f"q_len ({Lq}) exceeds kv_len ({kv_len}) without cache_position")
-            if q.dtype == torch.bfloat16 and D in (64, 128):
-                if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or
-                                                v.requires_grad):
-                    o = _ElasticTileAttention.apply(q, k, v, self.layout(q.device), self.scaling,
-                                                    self.prefill_kernel)
-                    return o.reshape(B, Lq, H * D), None
-                o, _ = elastic_attention_fwd(q, k, v, self.layout(q.device), self.scaling,
-                                             return_lse=False, kernel=self.prefill_kernel)
-            else:
-                o, _ = elastic_attention_rows(q, k, v, self.pattern, self.scaling, None,
-                                              return_lse=False)
         else:
             pos = self._positions(cache_position, Lq, kv_len, q.device)
-            o, _ = elastic_attention_rows(q, k, v, self.pattern, self.scaling, pos,
-                                          return_lse=False)
-        out = o.view(B, Lq, H * D)                                         # :761-763
-        if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
-            out = _ForwardOnly.apply(out, q, k, v)
-        return out, None
+        grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or
+                                            v.requires_grad)
+        # the naive path returns its attention weights (:680); it and the
+        # dense path apply attention dropout in training mode (:674, :721),
+        # the Triton path does not
+        naive = self.implementation == "naive"
+        dropout_p = (float(self.attention_dropout)
+                     if self.training and self.implementation != "triton" else 0.0)
+        if pos is None and not naive and dropout_p == 0.0 and q.dtype in MFMA_DTYPES \
+                and D in (64, 128):
+            if grad:
+                o = _ElasticTileAttention.apply(q, k, v, self.layout(q.device), self.scaling,
+                                                self.prefill_kernel)
+                return o.reshape(B, Lq, H * D), None
+            o, _ = elastic_attention_fwd(q, k, v, self.layout(q.device), self.scaling,
+                                         return_lse=False, kernel=self.prefill_kernel)
+            return o.view(B, Lq, H * D), None                              # :761-763
+        # per-row gather: decode rows, float32 / float16, other head dims, the
+        # naive path; keep decisions of dropout drawn from torch's generator
+        seed = int(torch.randint(0, 1 << 62, (1,)).item()) if dropout_p > 0.0 else 0
+        if grad:
+            o, wts = _ElasticRowsAttention.apply(q, k, v, self.pattern, self.scaling, pos,
+                                                 dropout_p, seed, naive)
+        else:
+            got = elastic_attention_rows(q, k, v, self.pattern, self.scaling, pos,
+                                         return_lse=False, dropout_p=dropout_p, seed=seed,
+                                         return_weights=naive)
+            o, wts = got[0], (got[2] if naive else None)
+        return o.reshape(B, Lq, H * D), (wts if naive else None)          # :761-763

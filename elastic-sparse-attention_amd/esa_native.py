@@ -24,12 +24,15 @@ ESA_ERR_HIP = 7
 
 ESA_F32 = 0
 ESA_BF16 = 1
+ESA_F16 = 2
 
 EXPORTED = (
     "esa_status_string", "esa_version", "esa_layout_sizes", "esa_build_indices",
     "esa_build_layout", "esa_plan_schedule", "esa_elastic_fwd", "esa_elastic_fwd_band", "esa_elastic_fwd_rows",
     "esa_sparse_fwd", "esa_plan_bwd", "esa_build_tile_masks", "esa_bwd_workspace_size",
-    "esa_elastic_bwd", "esa_reachability",
+    "esa_elastic_bwd", "esa_elastic_bwd_noalloc", "esa_bwd_noalloc_max_workspace",
+    "esa_elastic_fwd_naive", "esa_gather_bwd_workspace_size", "esa_sparse_bwd",
+    "esa_elastic_bwd_rows", "esa_reachability",
 )
 
 
@@ -86,6 +89,16 @@ class EsaBwdArgs(ctypes.Structure):
     ]
 
 
+class EsaNaiveOpts(ctypes.Structure):
+    _fields_ = [
+        ("dropout_p", ctypes.c_float),
+        ("seed", ctypes.c_uint64),
+        ("weights", ctypes.c_void_p),
+        ("weights_stride_b", ctypes.c_int64), ("weights_stride_h", ctypes.c_int64),
+        ("weights_stride_s", ctypes.c_int64),
+    ]
+
+
 _lib: Optional[ctypes.CDLL] = None
 
 
@@ -139,6 +152,21 @@ def load() -> ctypes.CDLL:
     lib.esa_elastic_bwd.restype = st
     lib.esa_elastic_bwd.argtypes = [P(EsaBwdArgs), P(EsaPattern), vp, vp, vp, i64, vp, vp, vp, vp,
                                     i64, vp, vp, ctypes.c_size_t, vp]
+    lib.esa_elastic_bwd_noalloc.restype = st
+    lib.esa_elastic_bwd_noalloc.argtypes = [P(EsaBwdArgs), P(EsaPattern), vp, vp, vp, i64, vp, vp,
+                                            vp, vp, i64, vp, vp]
+    lib.esa_bwd_noalloc_max_workspace.restype = ctypes.c_size_t
+    lib.esa_bwd_noalloc_max_workspace.argtypes = []
+    lib.esa_elastic_fwd_naive.restype = st
+    lib.esa_elastic_fwd_naive.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp, P(EsaNaiveOpts), vp]
+    lib.esa_gather_bwd_workspace_size.restype = st
+    lib.esa_gather_bwd_workspace_size.argtypes = [P(EsaBwdArgs), i32, P(ctypes.c_size_t)]
+    lib.esa_sparse_bwd.restype = st
+    lib.esa_sparse_bwd.argtypes = [P(EsaBwdArgs), vp, i32, i64, i64, vp, i32, i64, i64, i32, vp,
+                                   ctypes.c_size_t, vp]
+    lib.esa_elastic_bwd_rows.restype = st
+    lib.esa_elastic_bwd_rows.argtypes = [P(EsaBwdArgs), P(EsaPattern), vp, ctypes.c_float,
+                                         ctypes.c_uint64, vp, ctypes.c_size_t, vp]
     i32 = ctypes.c_int32
     lib.esa_reachability.restype = st
     lib.esa_reachability.argtypes = [i32, i32, i32, i32, i32, vp, vp, vp, vp]

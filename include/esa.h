@@ -40,6 +40,7 @@ typedef int32_t esa_status;
 typedef int32_t esa_dtype;
 #define ESA_F32 0
 #define ESA_BF16 1
+#define ESA_F16 2
 
 /* Elastic pattern parameters: the constructor arguments that fix the index
  * set (elastic_sparse_attention.py:375-386, used at :477-535) plus the tile
@@ -176,10 +177,33 @@ esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, voi
  * (:588, :602-608), a negative position counting from kv_len as torch
  * indexing counts it; a row whose position lies outside [-kv_len, kv_len)
  * (the reference's indexing error) gets NaN output and NaN lse, so the call
- * never synchronises to check positions.  dtype ESA_F32 or ESA_BF16, head_dim a
- * multiple of 4, <= 256. */
+ * never synchronises to check positions.  dtype ESA_F32, ESA_BF16 or ESA_F16
+ * (computed in float32, stored in the inputs' type, as the Triton kernel
+ * does, :114, :163), head_dim a multiple of 4, <= 256. */
 esa_status esa_elastic_fwd_rows(const esa_fwd_args* a, const esa_pattern* p,
                                 const int64_t* positions, void* stream);
+
+/* Options of the naive path's forward (implementation="naive",
+ * elastic_sparse_attention.py:624-680). */
+typedef struct esa_naive_opts {
+  float dropout_p; /* attention dropout in [0, 1) (:674); 0 = none */
+  uint64_t seed;   /* keep decisions are a function of (seed, b, h, row, entry) */
+  void* weights;   /* [B, H, q_len, w] in the inputs' type, or NULL */
+  int64_t weights_stride_b, weights_stride_h, weights_stride_s;
+} esa_naive_opts;
+
+/* Replaces _naive_forward (:624-680): esa_elastic_fwd_rows plus the
+ * attention weights it returns, softmax(scores) over each row's entries
+ * (masked entries 0, :669-673), and attention dropout on them (:674): each
+ * probability is kept with probability 1 - dropout_p and then scaled by
+ * 1 / (1 - dropout_p), and O is formed from the kept weights.  lse is that
+ * of the undropped probabilities.  With opts->weights non-NULL, a->lse must
+ * be non-NULL (the weights are exp(s - lse)).  The keep decisions are a
+ * counter-based hash of (seed, b, h, row, entry), so esa_elastic_bwd_rows
+ * with the same seed reproduces them; they are not torch's random stream. */
+esa_status esa_elastic_fwd_naive(const esa_fwd_args* a, const esa_pattern* p,
+                                 const int64_t* positions, const esa_naive_opts* opts,
+                                 void* stream);
 
 /* Gather forward over explicit index lists: the operator
  * ElasticSparseAttentionFunction.forward(q, k, v, sparse_indices,
@@ -301,6 +325,72 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p,
                            int64_t num_kv_items, const uint32_t* mask_t,
                            void* workspace, size_t workspace_bytes,
                            void* stream);
+
+/* Host only.  Bytes of workspace esa_sparse_bwd and esa_elastic_bwd_rows
+ * need for index lists of attn_length entries per row: per batch element and
+ * entry two float32 coefficients, four uint32 arrays of entries for the sort,
+ * (num_kv_heads * kv_len + 1) int32 segment starts, and the sort's
+ * histograms (each region 256-byte aligned).  Requires num_heads * q_len *
+ * attn_length and num_kv_heads * kv_len below 2^31 - 1. */
+esa_status esa_gather_bwd_workspace_size(const esa_bwd_args* a, int32_t attn_length,
+                                         size_t* workspace_bytes);
+
+/* Backward of the operator over explicit index lists: replaces
+ * ElasticSparseAttentionFunction.backward (elastic_sparse_attention.py:
+ * 299-339) and the Triton kernel's backward branch (:168-233) with the same
+ * indices / mask arguments as esa_sparse_fwd, o and lse of that forward, and
+ * dout.  Writes dq, dk and dv (every element of dk and dv: keys no entry
+ * reaches get 0, as the reference's zeros_like does).  Semantics of the
+ * reference: p = exp(scale q.k - lse) on valid entries; an entry whose index
+ * lies outside [0, kv_len) scores 0 against zero K/V and adds nothing to dk or
+ * dv; an entry listed twice counts twice.  No atomics on the gradients: each
+ * entry's dK / dV coefficients go to the workspace, a stable radix sort
+ * groups them by key, and one wave sums each key's entries in entry order,
+ * so results are deterministic.  dtype ESA_F32, ESA_BF16 or ESA_F16
+ * (float32 arithmetic), head_dim a multiple of 4 up to 256, K / V rows
+ * aligned to 4 elements; workspace from esa_gather_bwd_workspace_size,
+ * 256-byte aligned. */
+esa_status esa_sparse_bwd(const esa_bwd_args* a, const void* indices, int32_t index_bytes,
+                          int64_t idx_stride_h, int64_t idx_stride_s, const void* mask,
+                          int32_t mask_bytes, int64_t mask_stride_h, int64_t mask_stride_s,
+                          int32_t attn_length, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* Backward of esa_elastic_fwd_rows / esa_elastic_fwd_naive (the pattern's
+ * rows at positions, or 0 .. q_len-1 when positions is NULL): the gradients
+ * of the module's float32, float16, decode and other-head_dim paths and of
+ * the naive path with dropout (dropout_p and seed as the forward used them).
+ * Same kernels, semantics and workspace as esa_sparse_bwd with the index
+ * lists regenerated on the device (masked entries 0, clamped to
+ * [0, kv_len - 1], :602-615). */
+esa_status esa_elastic_bwd_rows(const esa_bwd_args* a, const esa_pattern* p,
+                                const int64_t* positions, float dropout_p, uint64_t seed,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Allocation-free variant of esa_elastic_bwd, with the same arguments
+ * except the workspace.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * training or serving loops, harnesses that forbid hipMalloc).  The
+ * workspace is a file-scope device array of esa_bwd_noalloc_max_workspace()
+ * bytes (32 MiB) that each device the library runs on holds until the
+ * process ends; a call whose esa_bwd_workspace_size exceeds it returns
+ * ESA_ERR_CAPACITY before launching anything.  The call allocates nothing
+ * and issues no memset: the kernels clear what must start at zero (the split
+ * counters).  Every call on one device shares that device's array, so calls
+ * that overlap in time on one device (different streams, or host threads)
+ * race on it and must be serialised by the caller; consecutive calls on one
+ * stream are safe.  Results are bit-identical to esa_elastic_bwd's. */
+esa_status esa_elastic_bwd_noalloc(const esa_bwd_args* a, const esa_pattern* p,
+                                   const int32_t* row_ptr, const int32_t* col_idx,
+                                   const int32_t* q_items, int64_t num_q_items,
+                                   const int32_t* tile_row, const int32_t* kv_ptr,
+                                   const int32_t* kv_tiles, const int32_t* kv_items,
+                                   int64_t num_kv_items, const uint32_t* mask_t,
+                                   void* stream);
+
+/* Bytes of the per-device array esa_elastic_bwd_noalloc uses as its
+ * workspace (the largest esa_bwd_workspace_size it accepts).  Host only. */
+size_t esa_bwd_noalloc_max_workspace(void);
 
 /* Replaces check_attention_holes_pytorch (check_attn_hole.py:53-180): the
  * tokens `position` reaches through num_hidden_layers elastic layers of

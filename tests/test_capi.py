@@ -17,7 +17,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def header_functions():
     text = open(os.path.join(ROOT, "include", "esa.h")).read()
-    return re.findall(r"^(?:esa_status|const char\*)\s+(esa_\w+)\(", text, re.M)
+    return re.findall(r"^(?:esa_status|const char\*|size_t)\s+(esa_\w+)\(", text, re.M)
 
 
 def test_library_exports_header_symbols():
@@ -383,3 +383,125 @@ def test_hole_checker_validates_before_the_gpu():
         ch.attention_reachability(100, 8, 8, 64, position_id=100)
     with pytest.raises(ValueError, match="attn_length must be positive"):
         ch.attention_reachability(100, 8, 8, 0)
+
+
+def test_noalloc_rejects_oversized_workspace():
+    """esa_elastic_bwd_noalloc refuses a backward whose workspace would
+    exceed its per-device array before any HIP call (ESA_ERR_CAPACITY)."""
+    lib = en.load()
+    cap = lib.esa_bwd_noalloc_max_workspace()
+    a = en.EsaBwdArgs()
+    a.dtype = en.ESA_BF16
+    a.batch, a.num_heads, a.num_kv_heads, a.q_len, a.kv_len, a.head_dim = 8, 32, 32, 32768, 32768, 128
+    need = ctypes.c_size_t()
+    assert lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(need)) == en.ESA_OK
+    assert need.value > cap
+    fake = 1 << 20
+    for name in ("q", "k", "v", "o", "dout", "dq", "dk", "dv", "lse"):
+        setattr(a, name, fake)
+    a.q_stride_b, a.q_stride_h, a.q_stride_s = 32 * 32768 * 128, 32768 * 128, 128
+    for name in ("k", "v", "dq", "dk", "dv"):
+        setattr(a, f"{name}_stride_b", a.q_stride_b)
+        setattr(a, f"{name}_stride_h", a.q_stride_h)
+        setattr(a, f"{name}_stride_s", a.q_stride_s)
+    for name in ("o", "dout"):
+        setattr(a, f"{name}_stride_b", 32768 * 32 * 128)
+        setattr(a, f"{name}_stride_h", 128)
+        setattr(a, f"{name}_stride_s", 32 * 128)
+    a.lse_stride_b, a.lse_stride_h = 32 * 32768, 32768
+    a.sm_scale = 128 ** -0.5
+    p = en.EsaPattern(32768, 64, 4, 8, 32, 128, 128)
+    st = lib.esa_elastic_bwd_noalloc(ctypes.byref(a), ctypes.byref(p), None, None, None, 0, None,
+                                     None, None, None, 0, None, None)
+    assert st == en.ESA_ERR_CAPACITY
+
+
+def bwd_args(dtype=en.ESA_F32, B=2, H=4, Hkv=2, Lq=100, Lk=120, D=64, ptr=1 << 20):
+    a = en.EsaBwdArgs()
+    a.dtype, a.batch, a.num_heads, a.num_kv_heads = dtype, B, H, Hkv
+    a.q_len, a.kv_len, a.head_dim = Lq, Lk, D
+    for name in ("q", "o", "dout", "dq"):
+        setattr(a, name, ptr)
+        setattr(a, f"{name}_stride_b", H * Lq * D)
+        setattr(a, f"{name}_stride_h", Lq * D)
+        setattr(a, f"{name}_stride_s", D)
+    for name in ("k", "v", "dk", "dv"):
+        setattr(a, name, ptr)
+        setattr(a, f"{name}_stride_b", Hkv * Lk * D)
+        setattr(a, f"{name}_stride_h", Lk * D)
+        setattr(a, f"{name}_stride_s", D)
+    a.lse = ptr
+    a.lse_stride_b, a.lse_stride_h = H * Lq, Lq
+    a.sm_scale = D ** -0.5
+    return a
+
+
+def test_gather_bwd_workspace_size_host_only():
+    """The gather backward's workspace is a host-side formula (no device
+    query): per batch element and entry two float32 coefficients, four uint32
+    arrays of entries for the sort, Hkv * kv_len + 1 segment starts, and the
+    sort's per-tile digit histograms (256 per 4096 entries, twice) and their
+    scan's chunk sums, each region rounded up to 256 bytes."""
+    lib = en.load()
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    for (B, H, Hkv, Lq, Lk, w) in [(2, 4, 2, 100, 120, 24), (1, 32, 8, 32768, 32768, 64),
+                                   (3, 1, 1, 1, 5, 1)]:
+        a = bwd_args(B=B, H=H, Hkv=Hkv, Lq=Lq, Lk=Lk)
+        ws = ctypes.c_size_t()
+        assert lib.esa_gather_bwd_workspace_size(ctypes.byref(a), w, ctypes.byref(ws)) == 0
+        E = H * Lq * w
+        nb = (E + 4095) // 4096
+        want = (2 * up(B * E * 4) + 4 * up(E * 4) + up((Hkv * Lk + 1) * 4) +
+                2 * up(256 * nb * 4) + up((256 * nb + 2047) // 2048 * 4))
+        assert ws.value == want
+    a = bwd_args(H=32, Lq=1 << 20)
+    assert lib.esa_gather_bwd_workspace_size(ctypes.byref(a), 128, ctypes.byref(ws)) \
+        == en.ESA_ERR_SHAPE  # entry ids would pass 2^31
+
+
+def test_gather_entry_points_reject_bad_arguments():
+    lib = en.load()
+    fake = ctypes.c_void_p(1 << 20)
+    ws_need = ctypes.c_size_t()
+    a = bwd_args()
+    assert lib.esa_gather_bwd_workspace_size(ctypes.byref(a), 24, ctypes.byref(ws_need)) == 0
+
+    def sparse(b, w=24, ws=ws_need.value, ib=8, mb=8):
+        return lib.esa_sparse_bwd(ctypes.byref(b), fake, ib, 100 * w, w, fake, mb, 100 * w, w, w,
+                                  fake, ws, None)
+
+    assert sparse(a, ws=ws_need.value - 1) == en.ESA_ERR_CAPACITY
+    assert sparse(a, ib=2) == en.ESA_ERR_DTYPE
+    assert sparse(a, mb=2) == en.ESA_ERR_DTYPE
+    assert sparse(bwd_args(dtype=9)) == en.ESA_ERR_DTYPE
+    assert sparse(bwd_args(D=66)) == en.ESA_ERR_UNSUPPORTED
+    assert sparse(bwd_args(D=260)) == en.ESA_ERR_UNSUPPORTED
+    assert sparse(bwd_args(Hkv=3)) == en.ESA_ERR_SHAPE
+    b = bwd_args()
+    b.dk = None
+    assert sparse(b) == en.ESA_ERR_NULL
+    b = bwd_args(dtype=en.ESA_BF16)
+    b.k_stride_s = 66
+    assert sparse(b) == en.ESA_ERR_ALIGN
+    assert lib.esa_sparse_bwd(ctypes.byref(a), None, 8, 0, 0, fake, 8, 0, 0, 24, fake,
+                              ws_need.value, None) == en.ESA_ERR_NULL
+    # the pattern path
+    p = pat(L=1024, H=4, w=24)
+    assert lib.esa_elastic_bwd_rows(ctypes.byref(a), ctypes.byref(p), None, 1.0, 0, fake,
+                                    ws_need.value, None) == en.ESA_ERR_SHAPE  # dropout_p = 1
+    assert lib.esa_elastic_bwd_rows(ctypes.byref(a), ctypes.byref(pat(L=1024, H=8, w=24)), None,
+                                    0.0, 0, fake, ws_need.value, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_elastic_bwd_rows(ctypes.byref(a), ctypes.byref(p), None, 0.0, 0, None,
+                                    ws_need.value, None) == en.ESA_ERR_NULL
+    # the naive forward
+    f = fwd_args(dtype=en.ESA_F16, H=4, Hkv=4)
+    opts = en.EsaNaiveOpts()
+    opts.dropout_p = 1.5
+    assert lib.esa_elastic_fwd_naive(ctypes.byref(f), ctypes.byref(pat(L=1024, H=4)), None,
+                                     ctypes.byref(opts), None) == en.ESA_ERR_SHAPE
+    opts.dropout_p = 0.1
+    opts.weights = 1 << 20
+    assert lib.esa_elastic_fwd_naive(ctypes.byref(f), ctypes.byref(pat(L=1024, H=4)), None,
+                                     ctypes.byref(opts), None) == en.ESA_ERR_NULL  # no lse
+    assert lib.esa_elastic_fwd_naive(ctypes.byref(f), ctypes.byref(pat(L=1024, H=4)), None,
+                                     None, None) == en.ESA_ERR_NULL
