@@ -28,7 +28,8 @@ def rel_err(got, ref):
 
 
 def oracle_grads(q, k, v, idx, msk, sc, groups, g):
-    qf, kf, vf = (t.float().requires_grad_() for t in (q, k, v))
+    # (a copy: .float() of a float32 tensor is the tensor itself)
+    qf, kf, vf = (t.detach().float().clone().requires_grad_() for t in (q, k, v))
     o, _ = forward_fp32(qf, kf, vf, idx, msk, sc, groups, chunk_rows=512)
     (o * g).sum().backward()
     return o.detach(), qf.grad, kf.grad, vf.grad
@@ -193,7 +194,7 @@ def test_naive_dropout_training():
     frac = 1.0 - keep.sum().item() / valid.sum().item()
     assert abs(frac - p) < 0.02, frac
     # kept weights are the softmax probabilities scaled by 1 / (1 - p)
-    qf, kf, vf = (t.float().requires_grad_() for t in (q, k, v))
+    qf, kf, vf = (t.detach().clone().requires_grad_() for t in (q, k, v))
     gk = torch.take_along_dim(kf.unsqueeze(2), idx.unsqueeze(0).unsqueeze(-1), dim=3)
     gv = torch.take_along_dim(vf.unsqueeze(2), idx.unsqueeze(0).unsqueeze(-1), dim=3)
     s = (qf.unsqueeze(3) * gk).sum(-1) * m.scaling
