@@ -70,8 +70,10 @@ __device__ __forceinline__ uint32_t transpose32(uint32_t x, int lane) {
 // block), so where O's heads lie inside a row ([B, L, H, D], the forward's
 // output) neighbouring blocks read neighbouring bytes; otherwise the axes
 // swap.
-template <int D>
+template <int D, Elem E>
 __global__ __launch_bounds__(256) void prep_kernel(BwdArgs A, float* lse2, int heads_fast) {
+  using M = MmaT<E>;
+  using V8 = typename M::v8;
   const int rb = heads_fast ? blockIdx.y : blockIdx.x;
   const int row = rb * 16 + (threadIdx.x >> 4);
   const int h = heads_fast ? blockIdx.x : blockIdx.y, b = blockIdx.z;
@@ -85,7 +87,7 @@ __global__ __launch_bounds__(256) void prep_kernel(BwdArgs A, float* lse2, int h
     const uint16_t* o = A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)row * A.oss;
     const uint16_t* d = A.dout + (int64_t)b * A.dosb + (int64_t)h * A.dosh + (int64_t)row * A.doss;
 #pragma unroll
-    for (int e = 0; e < PER; ++e) acc += bf16_to_f32(o[g * PER + e]) * bf16_to_f32(d[g * PER + e]);
+    for (int e = 0; e < PER; ++e) acc += M::val(o[g * PER + e]) * M::val(d[g * PER + e]);
   }
 #pragma unroll
   for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
@@ -132,8 +134,10 @@ __global__ __launch_bounds__(256) void tile_mask_kernel(PatternConsts pc, const 
 // keys 32 (w % 4) .. + 31 of the block and the 32-row half w / 4 of every
 // 64-row Q / dO stage; the two halves' partial sums are added through LDS at
 // the end, in a fixed order.
-template <int D>
+template <int D, Elem E>
 __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs A, const float* lse2) {
+  using M = MmaT<E>;
+  using V8 = typename M::v8;
   using C = BwdCfg<D>;
   constexpr int KB = 128;                           // keys per item
   constexpr int KLOADS = KB * C::CPR / 512;         // 16-byte loads per lane per matrix (block)
@@ -269,15 +273,15 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs A, const float* ls
     mask_init<0>(sacc, ~(mw >> (4 * hf)));
 #pragma unroll
     for (int s = 0; s < C::NS; ++s) {
-      const bf16x8 qa = *(const bf16x8*)(qb_ + raddr(s) + qrow);
-      const bf16x8 kbv = *(const bf16x8*)(kblk + raddr(s));
-      sacc = mfma32(qa, kbv, sacc);
+      const V8 qa = *(const V8*)(qb_ + raddr(s) + qrow);
+      const V8 kbv = *(const V8*)(kblk + raddr(s));
+      sacc = M::mfma32(qa, kbv, sacc);
     }
 #pragma unroll
     for (int s = 0; s < C::NS; ++s) {
-      const bf16x8 oa = *(const bf16x8*)(ob_ + raddr(s) + qrow);
-      const bf16x8 vbv = *(const bf16x8*)(vblk + raddr(s));
-      dp = mfma32(oa, vbv, dp);
+      const V8 oa = *(const V8*)(ob_ + raddr(s) + qrow);
+      const V8 vbv = *(const V8*)(vblk + raddr(s));
+      dp = M::mfma32(oa, vbv, dp);
     }
     uint32_t pw[8], sw[8];
 #pragma unroll
@@ -291,10 +295,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs A, const float* ls
         p[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[4 * g + e], scale2, -lv[e]));
         ds[e] = p[e] * (dp[4 * g + e] - dv[e]);
       }
-      pw[2 * g] = pack_bf16x2(p[0], p[1]);
-      pw[2 * g + 1] = pack_bf16x2(p[2], p[3]);
-      sw[2 * g] = pack_bf16x2(ds[0], ds[1]);
-      sw[2 * g + 1] = pack_bf16x2(ds[2], ds[3]);
+      pw[2 * g] = M::pack2(p[0], p[1]);
+      pw[2 * g + 1] = M::pack2(p[2], p[3]);
+      sw[2 * g] = M::pack2(ds[0], ds[1]);
+      sw[2 * g + 1] = M::pack2(ds[2], ds[3]);
     }
     // dV^T += dO^T P and dK^T += Q^T dS (query permutation shared by A and B)
 #pragma unroll
@@ -309,8 +313,8 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs A, const float* ls
         const s16x4 oo[2] = {o1, o2}, qq[2] = {q1, q2};
         const u32x4 pq = {pw[4 * u], pw[4 * u + 1], pw[4 * u + 2], pw[4 * u + 3]};
         const u32x4 sq = {sw[4 * u], sw[4 * u + 1], sw[4 * u + 2], sw[4 * u + 3]};
-        dvacc[d] = mfma32(__builtin_bit_cast(bf16x8, oo), __builtin_bit_cast(bf16x8, pq), dvacc[d]);
-        dkacc[d] = mfma32(__builtin_bit_cast(bf16x8, qq), __builtin_bit_cast(bf16x8, sq), dkacc[d]);
+        dvacc[d] = M::mfma32(__builtin_bit_cast(V8, oo), __builtin_bit_cast(V8, pq), dvacc[d]);
+        dkacc[d] = M::mfma32(__builtin_bit_cast(V8, qq), __builtin_bit_cast(V8, sq), dkacc[d]);
       }
     }
   };
@@ -372,22 +376,24 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs A, const float* ls
     for (int d = 0; d < C::ND; ++d) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        bf16x4 kv4, vv4;
+        typename M::v4 kv4, vv4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          kv4[e] = (__bf16)(dkacc[d][4 * g + e] * A.sm_scale);
-          vv4[e] = (__bf16)(dvacc[d][4 * g + e]);
+          kv4[e] = (typename M::s)(dkacc[d][4 * g + e] * A.sm_scale);
+          vv4[e] = (typename M::s)(dvacc[d][4 * g + e]);
         }
-        *(bf16x4*)(dkr + 32 * d + 8 * g + 4 * hf) = kv4;
-        *(bf16x4*)(dvr + 32 * d + 8 * g + 4 * hf) = vv4;
+        *(typename M::v4*)(dkr + 32 * d + 8 * g + 4 * hf) = kv4;
+        *(typename M::v4*)(dvr + 32 * d + 8 * g + 4 * hf) = vv4;
       }
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, Elem E>
 __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2) {
+  using M = MmaT<E>;
+  using V8 = typename M::v8;
   using C = BwdCfg<D>;
   __shared__ __attribute__((aligned(1024))) uint16_t k_st0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint16_t v_st0[C::STAGE];
@@ -412,7 +418,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2
   const bool row_ok = i < A.q_len;
 
   // Q and dO of this lane's row as B operands (8 consecutive d per lane)
-  bf16x8 qop[C::NS], oop[C::NS];
+  V8 qop[C::NS], oop[C::NS];
   {
     const uint16_t* qr = A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)i * A.qss;
     const uint16_t* dr = A.dout + (int64_t)b * A.dosb + (int64_t)h * A.dosh + (int64_t)i * A.doss;
@@ -423,8 +429,8 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2
         qraw = *(const u32x4*)(qr + 16 * s + 8 * hf);
         draw = *(const u32x4*)(dr + 16 * s + 8 * hf);
       }
-      qop[s] = __builtin_bit_cast(bf16x8, qraw);
-      oop[s] = __builtin_bit_cast(bf16x8, draw);
+      qop[s] = __builtin_bit_cast(V8, qraw);
+      oop[s] = __builtin_bit_cast(V8, draw);
     }
   }
   float l2 = 0.f, dl = 0.f;
@@ -483,19 +489,19 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2
     // lane half hf holds keys 8 (r / 4) + 4 hf + r % 4 of the block
     const uint32_t mk = mbits >> (4 * hf);
     if (!wave_any(mk != 0u)) return;
-    bf16x8 ra[C::NS];
+    V8 ra[C::NS];
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) ra[s] = *(const bf16x8*)(Kb + raddr[s] + 32 * kbl * D);
+    for (int s = 0; s < C::NS; ++s) ra[s] = *(const V8*)(Kb + raddr[s] + 32 * kbl * D);
     // the mask enters as S's initial value (0 or -inf): p = 0 without a select
     f32x16 sacc;
     mask_init<0>(sacc, ~mk);
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) sacc = mfma32(ra[s], qop[s], sacc);
+    for (int s = 0; s < C::NS; ++s) sacc = M::mfma32(ra[s], qop[s], sacc);
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) ra[s] = *(const bf16x8*)(Vb + raddr[s] + 32 * kbl * D);
+    for (int s = 0; s < C::NS; ++s) ra[s] = *(const V8*)(Vb + raddr[s] + 32 * kbl * D);
     f32x16 dp = f32x16{};
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) dp = mfma32(ra[s], oop[s], dp);
+    for (int s = 0; s < C::NS; ++s) dp = M::mfma32(ra[s], oop[s], dp);
     uint32_t sw[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
@@ -506,7 +512,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2
         const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], scale2, -l2));
         ds[e] = p * (dp[r] - dl);
       }
-      sw[q] = pack_bf16x2(ds[0], ds[1]);
+      sw[q] = M::pack2(ds[0], ds[1]);
     }
 #pragma unroll
     for (int d = 0; d < C::ND; ++d) {
@@ -517,7 +523,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2
         const s16x4 k2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(Kb + taddr8[d] + ro));
         const s16x4 kk[2] = {k1, k2};
         const u32x4 sq = {sw[4 * u], sw[4 * u + 1], sw[4 * u + 2], sw[4 * u + 3]};
-        dqacc[d] = mfma32(__builtin_bit_cast(bf16x8, kk), __builtin_bit_cast(bf16x8, sq), dqacc[d]);
+        dqacc[d] = M::mfma32(__builtin_bit_cast(V8, kk), __builtin_bit_cast(V8, sq), dqacc[d]);
       }
     }
   };
@@ -546,10 +552,10 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2
     for (int d = 0; d < C::ND; ++d) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        bf16x4 q4;
+        typename M::v4 q4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) q4[e] = (__bf16)(dqacc[d][4 * g + e] * A.sm_scale);
-        *(bf16x4*)(dqr + 32 * d + 8 * g + 4 * hf) = q4;
+        for (int e = 0; e < 4; ++e) q4[e] = (typename M::s)(dqacc[d][4 * g + e] * A.sm_scale);
+        *(typename M::v4*)(dqr + 32 * d + 8 * g + 4 * hf) = q4;
       }
     }
   }
@@ -564,9 +570,9 @@ hipError_t launch_tile_masks(const PatternConsts& pc, const int32_t* row_ptr, co
   return hipGetLastError();
 }
 
-hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,
-                           int64_t num_kv_items, hipStream_t stream) {
-  if (a.q_len <= 0 || a.B <= 0) return hipSuccess;
+template <Elem E>
+static hipError_t launch_tile_bwd_elem(const BwdArgs& a, int head_dim, int64_t num_q_items,
+                                       int64_t num_kv_items, hipStream_t stream) {
   // lse in log2 units goes in the second half of the delta workspace
   float* lse2 = a.delta + (int64_t)a.B * a.H * a.qpad;
   if (num_q_items < 0 && num_kv_items < 0) {
@@ -583,9 +589,9 @@ hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,
   const dim3 pg = heads_fast ? dim3((unsigned)a.H, n_rb, (unsigned)a.B)
                              : dim3(n_rb, (unsigned)a.H, (unsigned)a.B);
   if (head_dim == 128)
-    prep_kernel<128><<<pg, 256, 0, stream>>>(a, lse2, heads_fast);
+    prep_kernel<128, E><<<pg, 256, 0, stream>>>(a, lse2, heads_fast);
   else
-    prep_kernel<64><<<pg, 256, 0, stream>>>(a, lse2, heads_fast);
+    prep_kernel<64, E><<<pg, 256, 0, stream>>>(a, lse2, heads_fast);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (num_kv_items < 0) {  // no work list: band-gathered dK / dV
@@ -593,21 +599,29 @@ hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,
     if (e != hipSuccess) return e;
   } else if (num_kv_items > 0) {
     if (head_dim == 128)
-      dkdv_kernel<128><<<dim3((unsigned)num_kv_items), 512, 0, stream>>>(a, lse2);
+      dkdv_kernel<128, E><<<dim3((unsigned)num_kv_items), 512, 0, stream>>>(a, lse2);
     else
-      dkdv_kernel<64><<<dim3((unsigned)num_kv_items), 512, 0, stream>>>(a, lse2);
+      dkdv_kernel<64, E><<<dim3((unsigned)num_kv_items), 512, 0, stream>>>(a, lse2);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   if (num_q_items < 0) return launch_band_dq(a, head_dim, lse2, false, stream);  // no work list
   if (num_q_items > 0) {
     if (head_dim == 128)
-      dq_kernel<128><<<dim3((unsigned)num_q_items), 256, 0, stream>>>(a, lse2);
+      dq_kernel<128, E><<<dim3((unsigned)num_q_items), 256, 0, stream>>>(a, lse2);
     else
-      dq_kernel<64><<<dim3((unsigned)num_q_items), 256, 0, stream>>>(a, lse2);
+      dq_kernel<64, E><<<dim3((unsigned)num_q_items), 256, 0, stream>>>(a, lse2);
     e = hipGetLastError();
   }
   return e;
+}
+
+hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,
+                           int64_t num_kv_items, hipStream_t stream) {
+  if (a.q_len <= 0 || a.B <= 0) return hipSuccess;
+  if (a.elem == (int)Elem::f16)
+    return launch_tile_bwd_elem<Elem::f16>(a, head_dim, num_q_items, num_kv_items, stream);
+  return launch_tile_bwd_elem<Elem::bf16>(a, head_dim, num_q_items, num_kv_items, stream);
 }
 
 }  // namespace esa

@@ -33,8 +33,10 @@ namespace esa {
 // dK/dV kernel, which then runs after it; block 0 also clears the split
 // arrival counters.  Used when both halves are band kernels, so no separate
 // pass re-reads O and dO.
-template <int D, bool VSKIP, bool PREP>
+template <int D, bool VSKIP, bool PREP, Elem E>
 __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* lse2) {
+  using M = MmaT<E>;
+  using V8 = typename M::v8;
   using C = BandCfg<D>;
   if (PREP && A.split_parts > 1 && blockIdx.x == 0)
     for (int t = threadIdx.x; t < A.n_bkv * A.split_blocks; t += 64) A.part_cnt[t] = 0;
@@ -66,7 +68,7 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   }
 
   // Q and dO of this lane's row as B operands: dims 32 s + 8 q .. + 8
-  bf16x8 qop[C::NS], dop[C::NS];
+  V8 qop[C::NS], dop[C::NS];
   {
     const uint16_t* qr = A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)i * A.qss;
     const uint16_t* dr =
@@ -78,8 +80,8 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
         qraw = *(const u32x4*)(qr + 32 * s + 8 * q);
         draw = *(const u32x4*)(dr + 32 * s + 8 * q);
       }
-      qop[s] = __builtin_bit_cast(bf16x8, qraw);
-      dop[s] = __builtin_bit_cast(bf16x8, draw);
+      qop[s] = __builtin_bit_cast(V8, qraw);
+      dop[s] = __builtin_bit_cast(V8, draw);
     }
   }
   float l2 = 0.f, dl = 0.f;
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
 #pragma unroll
           for (int e = PER * k; e < PER * k + PER; ++e) {
             const uint32_t w = raw[s][e / 2];
-            const float ov = __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+            const float ov = M::val((e & 1) ? (w >> 16) : (w & 0xffffu));
             acc += ov * (float)dop[s][e];
           }
           hs[s][k] = acc;
@@ -223,19 +225,19 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
     const int R = 4 * q + (n >> 2), dim0 = C::CW * (n & 3) + 4 * s;
     trd[s] = R * C::ROWB + 16 * kswz<D>(R, dim0 >> 3) + 2 * (dim0 & 7);
   }
-  auto read_rows = [&](const uint16_t* src, bf16x8 (&op)[C::NS]) {
+  auto read_rows = [&](const uint16_t* src, V8 (&op)[C::NS]) {
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) op[s] = *(const bf16x8*)((const char*)src + rrd[s]);
+    for (int s = 0; s < C::NS; ++s) op[s] = *(const V8*)((const char*)src + rrd[s]);
   };
   auto read_tr = [&](const uint16_t* src, s16x4 (&op)[C::NV]) {
 #pragma unroll
     for (int s = 0; s < C::NV; ++s)
       op[s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((const char*)src + trd[s]));
   };
-  auto product = [&](const bf16x8 (&a)[C::NS], const bf16x8 (&bop)[C::NS]) {
-    f32x4 acc = mfma16(a[0], bop[0], f32x4{});
+  auto product = [&](const V8 (&a)[C::NS], const V8 (&bop)[C::NS]) {
+    f32x4 acc = M::mfma16(a[0], bop[0], f32x4{});
 #pragma unroll
-    for (int s = 1; s < C::NS; ++s) acc = mfma16(a[s], bop[s], acc);
+    for (int s = 1; s < C::NS; ++s) acc = M::mfma16(a[s], bop[s], acc);
     return acc;
   };
 
@@ -253,7 +255,7 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
     const float s = (e & 2) ? s23 : s01;
     const float dp = (e & 2) ? dp23 : dp01;
     const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s, scale2, -l2));
-    const uint32_t w = (uint32_t)f32_to_bf16_bits(p * (dp - dl));
+    const uint32_t w = (uint32_t)M::bits(p * (dp - dl));
     return has ? ((uint64_t)w << (16 * e)) : 0ull;
   };
 
@@ -264,11 +266,11 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   auto dq_step = [&](const s16x4 (&ta)[C::NV], const s16x4 (&tb)[C::NV], uint64_t wa,
                      uint64_t wb) {
     const u32x4 sq = {(uint32_t)wa, (uint32_t)(wa >> 32), (uint32_t)wb, (uint32_t)(wb >> 32)};
-    const bf16x8 sop = __builtin_bit_cast(bf16x8, sq);
+    const V8 sop = __builtin_bit_cast(V8, sq);
 #pragma unroll
     for (int s = 0; s < C::NV; ++s) {
       const s16x4 kk[2] = {ta[s], tb[s]};
-      dqacc[s] = mfma16(__builtin_bit_cast(bf16x8, kk), sop, dqacc[s]);
+      dqacc[s] = M::mfma16(__builtin_bit_cast(V8, kk), sop, dqacc[s]);
     }
   };
 
@@ -314,7 +316,7 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
       s16x4 ta[C::NV], tb[C::NV];
       if (live) {
         {
-          bf16x8 ka[C::NS], kb[C::NS];
+          V8 ka[C::NS], kb[C::NS];
           read_rows(ks0, ka);
           read_rows(ks1, kb);
           sa = product(ka, qop);
@@ -328,7 +330,7 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
       load_k(na, lk0);
       load_k(nb, lk1);
       __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's V is in LDS
-      bf16x8 va[C::NS], vb[C::NS];
+      V8 va[C::NS], vb[C::NS];
       if (live) {
         read_rows(vs0, va);
         read_rows(vs1, vb);
@@ -372,7 +374,7 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
       load_k(ci, lk0);
       load_v(ci, lv0);
       __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-      bf16x8 kt[C::NS], vt[C::NS];
+      V8 kt[C::NS], vt[C::NS];
       s16x4 tt[C::NV], tz[C::NV];
       read_rows(ks0, kt);
       read_rows(vs0, vt);
@@ -389,13 +391,13 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
     uint16_t* dqr = A.dq + (int64_t)b * A.dqsb + (int64_t)h * A.dqsh + (int64_t)i * A.dqss;
 #pragma unroll
     for (int t = 0; t < C::NV / 2; ++t) {
-      bf16x8 ov;
+      V8 ov;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        ov[e] = (__bf16)(dqacc[2 * t][e] * A.sm_scale);
-        ov[4 + e] = (__bf16)(dqacc[2 * t + 1][e] * A.sm_scale);
+        ov[e] = (typename M::s)(dqacc[2 * t][e] * A.sm_scale);
+        ov[4 + e] = (typename M::s)(dqacc[2 * t + 1][e] * A.sm_scale);
       }
-      *(bf16x8*)(dqr + C::CW * q + 8 * t) = ov;
+      *(V8*)(dqr + C::CW * q + 8 * t) = ov;
     }
   }
 }
@@ -442,8 +444,10 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
 // order and writes the block, so results do not depend on which wave is
 // last.
 
-template <int D>
+template <int D, Elem E>
 __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float* lse2) {
+  using M = MmaT<E>;
+  using V8 = typename M::v8;
   using C = BandCfg<D>;
   constexpr int ROWS = 32;                // query rows per step
   constexpr int SLOT2 = ROWS * D;         // elements per Q or dO slot
@@ -488,7 +492,7 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
   const bool key_ok = key < A.kv_len;
 
   // the block's K and V as B operands: key n, dims 32 s + 8 q .. + 8
-  bf16x8 kop[C::NS], vop[C::NS];
+  V8 kop[C::NS], vop[C::NS];
   {
     const uint16_t* kr = A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh + (int64_t)key * A.kss;
     const uint16_t* vr = A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh + (int64_t)key * A.vss;
@@ -499,8 +503,8 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
         kraw = *(const u32x4*)(kr + 32 * s + 8 * q);
         vraw = *(const u32x4*)(vr + 32 * s + 8 * q);
       }
-      kop[s] = __builtin_bit_cast(bf16x8, kraw);
-      vop[s] = __builtin_bit_cast(bf16x8, vraw);
+      kop[s] = __builtin_bit_cast(V8, kraw);
+      vop[s] = __builtin_bit_cast(V8, vraw);
     }
   }
 
@@ -696,13 +700,13 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
       s16x4 qt[2][C::NV];
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        bf16x8 qa[C::NS];
+        V8 qa[C::NS];
 #pragma unroll
         for (int s = 0; s < C::NS; ++s)
-          qa[s] = *(const bf16x8*)((const char*)qsl + c * CHB + rrd[s]);
-        sacc[c] = mfma16(qa[0], kop[0], f32x4{});
+          qa[s] = *(const V8*)((const char*)qsl + c * CHB + rrd[s]);
+        sacc[c] = M::mfma16(qa[0], kop[0], f32x4{});
 #pragma unroll
-        for (int s = 1; s < C::NS; ++s) sacc[c] = mfma16(qa[s], kop[s], sacc[c]);
+        for (int s = 1; s < C::NS; ++s) sacc[c] = M::mfma16(qa[s], kop[s], sacc[c]);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -718,13 +722,13 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
       s16x4 ot[2][C::NV];
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        bf16x8 oa[C::NS];
+        V8 oa[C::NS];
 #pragma unroll
         for (int s = 0; s < C::NS; ++s)
-          oa[s] = *(const bf16x8*)((const char*)osl + c * CHB + rrd[s]);
-        pacc[c] = mfma16(oa[0], vop[0], f32x4{});
+          oa[s] = *(const V8*)((const char*)osl + c * CHB + rrd[s]);
+        pacc[c] = M::mfma16(oa[0], vop[0], f32x4{});
 #pragma unroll
-        for (int s = 1; s < C::NS; ++s) pacc[c] = mfma16(oa[s], vop[s], pacc[c]);
+        for (int s = 1; s < C::NS; ++s) pacc[c] = M::mfma16(oa[s], vop[s], pacc[c]);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -761,10 +765,10 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
           pv[e2] = has ? p : 0.f;
           dv[e2] = has ? p * (pacc[c][e2] - dlv[c][e2]) : 0.f;
         }
-        pw[2 * c] = pack_bf16x2(pv[0], pv[1]);
-        pw[2 * c + 1] = pack_bf16x2(pv[2], pv[3]);
-        sw[2 * c] = pack_bf16x2(dv[0], dv[1]);
-        sw[2 * c + 1] = pack_bf16x2(dv[2], dv[3]);
+        pw[2 * c] = M::pack2(pv[0], pv[1]);
+        pw[2 * c + 1] = M::pack2(pv[2], pv[3]);
+        sw[2 * c] = M::pack2(dv[0], dv[1]);
+        sw[2 * c + 1] = M::pack2(dv[2], dv[3]);
       }
       const u32x4 pq = {pw[0], pw[1], pw[2], pw[3]};
       const u32x4 sq = {sw[0], sw[1], sw[2], sw[3]};
@@ -772,10 +776,10 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
       for (int s = 0; s < C::NV; ++s) {
         const s16x4 oo[2] = {ot[0][s], ot[1][s]};
         dvacc[s] =
-            mfma16(__builtin_bit_cast(bf16x8, oo), __builtin_bit_cast(bf16x8, pq), dvacc[s]);
+            M::mfma16(__builtin_bit_cast(V8, oo), __builtin_bit_cast(V8, pq), dvacc[s]);
         const s16x4 qq[2] = {qt[0][s], qt[1][s]};
         dkacc[s] =
-            mfma16(__builtin_bit_cast(bf16x8, qq), __builtin_bit_cast(bf16x8, sq), dkacc[s]);
+            M::mfma16(__builtin_bit_cast(V8, qq), __builtin_bit_cast(V8, sq), dkacc[s]);
       }
       row_c = row_n;
       ent_c = ent_n;
@@ -826,18 +830,27 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
     uint16_t* dvr = A.dv + (int64_t)b * A.dvsb + (int64_t)kvh * A.dvsh + (int64_t)key * A.dvss;
 #pragma unroll
     for (int t = 0; t < C::NV / 2; ++t) {
-      bf16x8 kv, vv;
+      V8 kv, vv;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        kv[e] = (__bf16)(dkacc[2 * t][e] * A.sm_scale);
-        kv[4 + e] = (__bf16)(dkacc[2 * t + 1][e] * A.sm_scale);
-        vv[e] = (__bf16)dvacc[2 * t][e];
-        vv[4 + e] = (__bf16)dvacc[2 * t + 1][e];
+        kv[e] = (typename M::s)(dkacc[2 * t][e] * A.sm_scale);
+        kv[4 + e] = (typename M::s)(dkacc[2 * t + 1][e] * A.sm_scale);
+        vv[e] = (typename M::s)dvacc[2 * t][e];
+        vv[4 + e] = (typename M::s)dvacc[2 * t + 1][e];
       }
-      *(bf16x8*)(dkr + C::CW * q + 8 * t) = kv;
-      *(bf16x8*)(dvr + C::CW * q + 8 * t) = vv;
+      *(V8*)(dkr + C::CW * q + 8 * t) = kv;
+      *(V8*)(dvr + C::CW * q + 8 * t) = vv;
     }
   }
+}
+
+template <Elem E>
+static void launch_band_dkdv_elem(const BwdArgs& a, int head_dim, dim3 grid, const float* lse2,
+                                  hipStream_t stream) {
+  if (head_dim == 128)
+    band_dkdv_kernel<128, E><<<grid, 64, 0, stream>>>(a, lse2);
+  else
+    band_dkdv_kernel<64, E><<<grid, 64, 0, stream>>>(a, lse2);
 }
 
 hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,
@@ -845,37 +858,46 @@ hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,
   if (a.n_kblk <= 0 || a.kchunk <= 0) return hipSuccess;
   const int64_t chunks = (a.n_kblk + 8 * (int64_t)a.kchunk - 1) / (8 * (int64_t)a.kchunk);
   const dim3 grid((unsigned)(a.n_extra + chunks * 8 * a.kchunk));
-  if (head_dim == 128)
-    band_dkdv_kernel<128><<<grid, 64, 0, stream>>>(a, lse2);
+  if (a.elem == (int)Elem::f16)
+    launch_band_dkdv_elem<Elem::f16>(a, head_dim, grid, lse2, stream);
   else
-    band_dkdv_kernel<64><<<grid, 64, 0, stream>>>(a, lse2);
+    launch_band_dkdv_elem<Elem::bf16>(a, head_dim, grid, lse2, stream);
   return hipGetLastError();
 }
 
-template <int D, bool PREP>
+template <int D, bool PREP, Elem E>
 static void launch_band_dq_d(const BwdArgs& a, dim3 grid, const float* lse2, hipStream_t stream) {
   // V DMA skipping from interpolation weight 1/2 on, as for the forward's K
   if (a.pc.a >= 0.5f)
-    band_dq_kernel<D, true, PREP><<<grid, 64, 0, stream>>>(a, lse2);
+    band_dq_kernel<D, true, PREP, E><<<grid, 64, 0, stream>>>(a, lse2);
   else
-    band_dq_kernel<D, false, PREP><<<grid, 64, 0, stream>>>(a, lse2);
+    band_dq_kernel<D, false, PREP, E><<<grid, 64, 0, stream>>>(a, lse2);
+}
+
+template <Elem E>
+static void launch_band_dq_elem(const BwdArgs& a, int head_dim, dim3 grid, const float* lse2,
+                                bool prep, hipStream_t stream) {
+  if (head_dim == 128) {
+    if (prep)
+      launch_band_dq_d<128, true, E>(a, grid, lse2, stream);
+    else
+      launch_band_dq_d<128, false, E>(a, grid, lse2, stream);
+  } else {
+    if (prep)
+      launch_band_dq_d<64, true, E>(a, grid, lse2, stream);
+    else
+      launch_band_dq_d<64, false, E>(a, grid, lse2, stream);
+  }
 }
 
 hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2, bool prep,
                           hipStream_t stream) {
   if (a.n_groups <= 0) return hipSuccess;
   dim3 grid((unsigned)(8 * a.per_xcd));
-  if (head_dim == 128) {
-    if (prep)
-      launch_band_dq_d<128, true>(a, grid, lse2, stream);
-    else
-      launch_band_dq_d<128, false>(a, grid, lse2, stream);
-  } else {
-    if (prep)
-      launch_band_dq_d<64, true>(a, grid, lse2, stream);
-    else
-      launch_band_dq_d<64, false>(a, grid, lse2, stream);
-  }
+  if (a.elem == (int)Elem::f16)
+    launch_band_dq_elem<Elem::f16>(a, head_dim, grid, lse2, prep, stream);
+  else
+    launch_band_dq_elem<Elem::bf16>(a, head_dim, grid, lse2, prep, stream);
   return hipGetLastError();
 }
 

@@ -20,7 +20,7 @@
 // barriers, no LDS shared between waves.
 //
 // Per band and wave:
-//   S^T = K Q^T     D/32 x v_mfma_f32_16x16x32_bf16; A = K rows read from
+//   S^T = K Q^T     D/32 x v_mfma_f32_16x16x32_{bf16,f16}; A = K rows read from
 //                   LDS (lane m: key lo + m%16), B = Q held in registers for
 //                   the whole group
 //   select          each lane owns one row and 4 of the 16 keys; the lane
@@ -30,7 +30,7 @@
 //                   pair, lazy rescale (the running max moves only when a
 //                   score exceeds it by more than 8)
 //   O^T += V^T P^T  bands go in pairs (32 keys = one MFMA k-step): D/16 x
-//                   v_mfma_f32_16x16x32_bf16, A = V^T read with
+//                   v_mfma_f32_16x16x32_{bf16,f16}, A = V^T read with
 //                   ds_read_b64_tr_b16 from row-major V rows in LDS, B = P
 //                   straight from the select step
 // K and V rows reach LDS by buffer_load ... lds, whole rows per 16 lanes:
@@ -52,9 +52,11 @@ namespace esa {
 // where many bands are narrower than 16 keys (the dilated, late layers);
 // where nearly every band is 16 keys wide the run-time waits cost more than
 // the DMAs saved, so the host picks it by the pattern's interpolation weight.
-template <int D, bool KSKIP>
+template <int D, bool KSKIP, Elem E>
 __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   using C = BandCfg<D>;
+  using M = MmaT<E>;
+  using V8 = typename M::v8;
   // K and V slots of the pair's two bands (separate objects, so the compiler
   // can tell reads of one slot from the direct loads into another)
   __shared__ __attribute__((aligned(1024))) uint16_t ks0[C::SLOT];
@@ -86,14 +88,14 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   }
 
   // ---- Q as the B operand: row n, dims 32 s + 8 q .. + 8 for k-step s
-  bf16x8 qop[C::NS];
+  V8 qop[C::NS];
   {
     const uint16_t* qrow = A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)i * A.qss;
 #pragma unroll
     for (int s = 0; s < C::NS; ++s) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (row_ok) raw = *(const u32x4*)(qrow + 32 * s + 8 * q);
-      qop[s] = __builtin_bit_cast(bf16x8, raw);
+      qop[s] = __builtin_bit_cast(V8, raw);
     }
   }
 
@@ -170,9 +172,9 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   int krd[C::NS];
 #pragma unroll
   for (int s = 0; s < C::NS; ++s) krd[s] = n * C::ROWB + 16 * kswz<D>(n, 4 * s + q);
-  auto read_k = [&](const uint16_t* src, bf16x8 (&kb)[C::NS]) {
+  auto read_k = [&](const uint16_t* src, V8 (&kb)[C::NS]) {
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) kb[s] = *(const bf16x8*)((const char*)src + krd[s]);
+    for (int s = 0; s < C::NS; ++s) kb[s] = *(const V8*)((const char*)src + krd[s]);
   };
 
   // V^T operand read addresses (bytes within a slot) for slice s: lane x of
@@ -205,8 +207,8 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     return row4_max(has ? s * scale : -INFINITY);
   };
   // Online softmax over two bands' scores xa, xb (one running-max update per
-  // pair, so both probabilities share one scale) -> P words (bf16 at
-  // register e of the lane holding the key, else 0)
+  // pair, so both probabilities share one scale) -> P words (the input type
+  // at register e of the lane holding the key, else 0)
   auto pair_softmax = [&](float xa, bool ha, int ea, float xb, bool hb, int eb, uint64_t& pa,
                           uint64_t& pb) {
     const float xm = fmaxf(xa, xb);
@@ -230,19 +232,19 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     const float p1 = __builtin_amdgcn_exp2f(rb);
     l_run += p0;
     l_run += p1;
-    const uint32_t b0 = (uint32_t)f32_to_bf16_bits(p0);
-    const uint32_t b1 = (uint32_t)f32_to_bf16_bits(p1);
-    // O is normalised by the probabilities PV used (rounded to bf16)
-    n_run += __uint_as_float(b0 << 16);
-    n_run += __uint_as_float(b1 << 16);
+    const uint32_t b0 = (uint32_t)M::bits(p0);
+    const uint32_t b1 = (uint32_t)M::bits(p1);
+    // O is normalised by the probabilities PV used (rounded to the input type)
+    n_run += M::val(b0);
+    n_run += M::val(b1);
     pa = ha ? ((uint64_t)b0 << (16 * ea)) : 0ull;
     pb = hb ? ((uint64_t)b1 << (16 * eb)) : 0ull;
   };
 
-  auto scores = [&](const bf16x8 (&kb)[C::NS]) {
-    f32x4 sacc = mfma16(kb[0], qop[0], f32x4{});
+  auto scores = [&](const V8 (&kb)[C::NS]) {
+    f32x4 sacc = M::mfma16(kb[0], qop[0], f32x4{});
 #pragma unroll
-    for (int s = 1; s < C::NS; ++s) sacc = mfma16(kb[s], qop[s], sacc);
+    for (int s = 1; s < C::NS; ++s) sacc = M::mfma16(kb[s], qop[s], sacc);
     return sacc;
   };
 
@@ -259,11 +261,11 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
           (lds_s16x4*)((const char*)vb + vrd[s]));
     }
     const u32x4 pq = {(uint32_t)pa, (uint32_t)(pa >> 32), (uint32_t)pb, (uint32_t)(pb >> 32)};
-    const bf16x8 pop = __builtin_bit_cast(bf16x8, pq);
+    const V8 pop = __builtin_bit_cast(V8, pq);
 #pragma unroll
     for (int s = 0; s < C::NV; ++s) {
       const s16x4 vv[2] = {ta[s], tb[s]};
-      oacc[s] = mfma16(__builtin_bit_cast(bf16x8, vv), pop, oacc[s]);
+      oacc[s] = M::mfma16(__builtin_bit_cast(V8, vv), pop, oacc[s]);
     }
   };
 
@@ -304,7 +306,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
       const bool live = (ia | ib) != 0;  // some row of the group uses a band
       const int n_nxt = KSKIP ? n_loads(na) + n_loads(nb) : 2 * C::VLOADS;  // next K DMAs
       __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's K is in LDS
-      bf16x8 kopa[C::NS], kopb[C::NS];
+      V8 kopa[C::NS], kopb[C::NS];
       if (live) {
         read_k(ks0, kopa);
         read_k(ks1, kopb);
@@ -366,7 +368,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
       load_k(ci, lk0);
       load_v(ci, lv0);
       __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-      bf16x8 kt[C::NS];
+      V8 kt[C::NS];
       read_k(ks0, kt);
       const f32x4 st = scores(kt);
       bool ht;
@@ -386,19 +388,35 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     uint16_t* orow = A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)i * A.oss;
 #pragma unroll
     for (int t = 0; t < C::NV / 2; ++t) {
-      bf16x8 ov;
+      V8 ov;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        ov[e] = (__bf16)(oacc[2 * t][e] * inv);
-        ov[4 + e] = (__bf16)(oacc[2 * t + 1][e] * inv);
+        ov[e] = (typename M::s)(oacc[2 * t][e] * inv);
+        ov[4 + e] = (typename M::s)(oacc[2 * t + 1][e] * inv);
       }
-      *(bf16x8*)(orow + C::CW * q + 8 * t) = ov;
+      *(V8*)(orow + C::CW * q + 8 * t) = ov;
     }
     if (A.lse && q == 0) {
       const float lse = l_run > 0.f ? (m_run + __log2f(l_run)) * 0.69314718055994530942f
                                     : -INFINITY;
       A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + i] = lse;
     }
+  }
+}
+
+template <Elem E>
+void launch_band_elem(const BandArgs& a, int head_dim, dim3 grid, bool kskip,
+                      hipStream_t stream) {
+  if (head_dim == 128) {
+    if (kskip)
+      band_fwd_kernel<128, true, E><<<grid, 64, 0, stream>>>(a);
+    else
+      band_fwd_kernel<128, false, E><<<grid, 64, 0, stream>>>(a);
+  } else {
+    if (kskip)
+      band_fwd_kernel<64, true, E><<<grid, 64, 0, stream>>>(a);
+    else
+      band_fwd_kernel<64, false, E><<<grid, 64, 0, stream>>>(a);
   }
 }
 
@@ -409,17 +427,10 @@ hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) 
   // L=32768, D=128, w=64 over 8 layers: 1-7% faster at weights 4/7 .. 1,
   // even at 3/7, 3-4% slower at 1/7 and 2/7
   const bool kskip = a.pc.a >= 0.5f;
-  if (head_dim == 128) {
-    if (kskip)
-      band_fwd_kernel<128, true><<<grid, 64, 0, stream>>>(a);
-    else
-      band_fwd_kernel<128, false><<<grid, 64, 0, stream>>>(a);
-  } else {
-    if (kskip)
-      band_fwd_kernel<64, true><<<grid, 64, 0, stream>>>(a);
-    else
-      band_fwd_kernel<64, false><<<grid, 64, 0, stream>>>(a);
-  }
+  if (a.elem == (int)Elem::f16)
+    launch_band_elem<Elem::f16>(a, head_dim, grid, kskip, stream);
+  else
+    launch_band_elem<Elem::bf16>(a, head_dim, grid, kskip, stream);
   return hipGetLastError();
 }
 

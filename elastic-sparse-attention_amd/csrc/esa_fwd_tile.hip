@@ -28,7 +28,7 @@
 //                  others walk their elastic indices (the same float32
 //                  sequence as the layout builder) through the stage
 // then for each 32-key block of the stage:
-//   S^T = K Q^T    NS x v_mfma_f32_32x32x16_bf16 (A = K rows from LDS,
+//   S^T = K Q^T    NS x v_mfma_f32_32x32x16_{bf16,f16} (A = K rows from LDS,
 //                  B = Q kept in registers for the whole item)
 //   softmax        online, in registers, log2 domain.  The S^T accumulator
 //                  layout gives each lane one row and 16 of the block's keys;
@@ -38,7 +38,7 @@
 //                  The running max is raised only when a row's
 //                  block max exceeds it by more than 8 (log2), so the O
 //                  rescale is rare; probabilities stay below 2^8.
-//   O^T += V^T P^T 2 ND x v_mfma_f32_32x32x16_bf16 (A = V^T read with
+//   O^T += V^T P^T 2 ND x v_mfma_f32_32x32x16_{bf16,f16} (A = V^T read with
 //                  ds_read_b64_tr_b16 from row-major V in LDS, B = P straight
 //                  from the S^T accumulators: a key permutation shared by
 //                  both operands leaves the contraction unchanged)
@@ -76,7 +76,7 @@ struct TileCfg {
 // (the second launch bound is the minimum number of waves per SIMD: two,
 // so at most 256 VGPRs; LDS then allows two 128-row or four 64-row
 // workgroups per CU)
-template <int D, int BMQ>
+template <int D, int BMQ, Elem E>
 __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
   using C = TileCfg<D, BMQ>;
   // stage buffers (HALF rows x D, rows unpadded, chunks swizzled); separate
@@ -103,33 +103,18 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hf = lane >> 5, l32 = lane & 31;
+  const int l32 = lane & 31;
 
   const int i = qb * C::BM + wave * 32 + l32;  // this lane's query row = position
   const bool row_ok = i < A.q_len;
 
-  // Q as the B operand of S^T = K Q^T: 8 consecutive d per lane and k-step.
-  bf16x8 qop[C::NS];
-  {
-    const uint16_t* qrow = A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)i * A.qss;
-#pragma unroll
-    for (int s = 0; s < C::NS; ++s) {
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (row_ok) raw = *(const u32x4*)(qrow + 16 * s + 8 * hf);
-      qop[s] = __builtin_bit_cast(bf16x8, raw);
-    }
-  }
+  Rows32<D, E> rows;
+  rows.init(lane, A.scale_log2);  // scale > 0 (checked on the host)
+  rows.load_q(A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)i * A.qss, row_ok);
 
   // ---- this row's index list
   RowWalker walk;
   walk.init(A.pc, h, i, row_ok);
-
-  float m_run = -INFINITY;  // running max, log2 units (the same in both halves)
-  float l_run = 0.f;        // running sum of p over this lane's half of the keys (-> lse)
-  float n_run = 0.f;        // the same sum of p rounded to bf16, as PV sees it (-> O)
-  f32x16 oacc[C::ND];
-#pragma unroll
-  for (int d = 0; d < C::ND; ++d) oacc[d] = f32x16{};
 
   // ---- staging: buffer resources over this (batch, kv head)'s rows; keys at
   // or past kv_len are outside num_records and load as zeros (the host keeps
@@ -140,106 +125,8 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh), (short)0,
       (int)((int64_t)A.kv_len * A.vss * 2), 0x00020000);
-  // ---- LDS read addresses (elements), fixed for the whole item: K rows
-  // 32 kbl + l32 at chunk 2 s + hf; V rows 4 hf + lam / 4 (+ 32 kbl + 16 u,
-  // + 8) at column 32 d + 16 (g4 & 1) + 4 (lam & 3)
-  const int g4 = lane >> 4, lam = lane & 15;
-  int kaddr[C::NS], vaddr[C::ND];
-#pragma unroll
-  for (int s = 0; s < C::NS; ++s) kaddr[s] = l32 * D + 8 * ((2 * s + hf) ^ swz_k<D>(l32));
-  {
-    const int vrow = 4 * hf + (lam >> 2);
-#pragma unroll
-    for (int d = 0; d < C::ND; ++d) {
-      const int col = 32 * d + 16 * (g4 & 1) + 4 * (lam & 3);
-      vaddr[d] = vrow * D + 8 * ((col >> 3) ^ swz_v<D>(vrow)) + (col & 7);
-    }
-  }
-
-  const float scale = A.scale_log2;  // > 0 (checked on the host)
-
-  // One 32-key block: keys 32 kbl .. 32 kbl + 31 of a stage buffer (Kb, Vb),
-  // whose valid-key bits for this row are mbits.
   auto block = [&](const uint16_t* Kb, const uint16_t* Vb, int kbl, uint32_t mbits) {
-    // lane half hf holds keys 8*(r/4) + 4*hf + r%4 of the block
-    const uint32_t mk = mbits >> (4 * hf);
-    // a 32 x 32 block in which no row of the wave has a valid key contributes
-    // p = 0 to every row: its reads, MFMAs and softmax are all skipped (O, the
-    // running max and the sums are unchanged, bit for bit)
-    if (!wave_any(mk != 0u)) return;
-
-    // all K operand reads first, so their LDS latency overlaps
-    bf16x8 ka[C::NS];
-#pragma unroll
-    for (int s = 0; s < C::NS; ++s) ka[s] = *(const bf16x8*)(Kb + kaddr[s] + 32 * kbl * D);
-    // the mask enters as the accumulator's initial value: 0 for a valid key,
-    // -inf for a masked one
-    f32x16 sacc;
-    mask_init<0>(sacc, ~mk);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int s = 0; s < C::NS; ++s) sacc = mfma32(ka[s], qop[s], sacc);
-    // the V^T operands of this block, read while the softmax runs
-    s16x4 va[C::ND][4];
-#pragma unroll
-    for (int d = 0; d < C::ND; ++d) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const uint16_t* p1 = Vb + vaddr[d] + (32 * kbl + 16 * u) * D;
-        va[d][2 * u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p1);
-        va[d][2 * u + 1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1 + 8 * D));
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    uint32_t pw[8];  // P as packed bf16 pairs: pw[q] holds regs 2q, 2q+1
-    // x = scaled score relative to the running max (log2 units); a masked
-    // key stays -inf (scale > 0)
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    float smax = -INFINITY;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      sacc[r] = __builtin_fmaf(sacc[r], scale, -m_use);
-      smax = fmaxf(smax, sacc[r]);
-    }
-    smax = half_max(smax);
-    // raise the running max of a row when this block exceeds it by more
-    // than the slack (or when the row sees its first valid key)
-    const bool grow = m_run == -INFINITY ? smax != -INFINITY : smax > kRescaleSlack;
-    if (wave_any(grow)) {
-      const float delta = grow ? smax : 0.f;
-      // rows that do not grow keep alpha = 1 (m_run may still be -inf there)
-      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - (m_use + delta)) : 1.0f;
-      l_run *= alpha;
-      n_run *= alpha;
-#pragma unroll
-      for (int d = 0; d < C::ND; ++d) oacc[d] *= alpha;
-      m_run = grow ? m_use + delta : m_run;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[r] -= delta;
-    }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const float p0 = __builtin_amdgcn_exp2f(sacc[2 * q]);
-      const float p1 = __builtin_amdgcn_exp2f(sacc[2 * q + 1]);
-      l_run += p0;
-      l_run += p1;
-      pw[q] = pack_bf16x2(p0, p1);
-      // normalise O by the probabilities PV actually used, so a row led by
-      // one key reproduces that key's value row
-      n_run = dot2_bf16(pw[q], n_run);
-    }
-
-#pragma unroll
-    for (int d = 0; d < C::ND; ++d) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const s16x4 vv[2] = {va[d][2 * u], va[d][2 * u + 1]};
-        const bf16x8 a = __builtin_bit_cast(bf16x8, vv);
-        const u32x4 pq = {pw[4 * u], pw[4 * u + 1], pw[4 * u + 2], pw[4 * u + 3]};
-        oacc[d] = mfma32(a, __builtin_bit_cast(bf16x8, pq), oacc[d]);
-      }
-    }
+    rows.block(Kb, Vb, kbl, mbits);
   };
 
   const int64_t lrow = (int64_t)h * A.nqb + qb;
@@ -302,26 +189,22 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
   }
 
   // ---- epilogue: normalise and store O rows and the log-sum-exp
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-  const float n_tot = n_run + __shfl_xor(n_run, 32, 64);
-  if (row_ok) {
-    const float inv = n_tot > 0.f ? 1.f / n_tot : 0.f;
-    uint16_t* orow = A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)i * A.oss;
-#pragma unroll
-    for (int d = 0; d < C::ND; ++d) {
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        bf16x4 ov;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ov[e] = (__bf16)(oacc[d][4 * q4 + e] * inv);
-        *(bf16x4*)(orow + 32 * d + 8 * q4 + 4 * hf) = ov;
-      }
-    }
-    if (A.lse && hf == 0) {
-      const float lse = l_tot > 0.f ? (m_run + __log2f(l_tot)) * 0.69314718055994530942f
-                                    : -INFINITY;
-      A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + i] = lse;
-    }
+  rows.store(A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)i * A.oss,
+             A.lse ? A.lse + (int64_t)b * A.lsb + (int64_t)h * A.lsh + i : nullptr, row_ok);
+}
+
+template <Elem E>
+void launch_tile_elem(const TileArgs& a, int head_dim, dim3 grid, hipStream_t stream) {
+  if (a.rows64) {
+    if (head_dim == 128)
+      tile_fwd_kernel<128, 64, E><<<grid, 128, 0, stream>>>(a);
+    else
+      tile_fwd_kernel<64, 64, E><<<grid, 128, 0, stream>>>(a);
+  } else {
+    if (head_dim == 128)
+      tile_fwd_kernel<128, 128, E><<<grid, 256, 0, stream>>>(a);
+    else
+      tile_fwd_kernel<64, 128, E><<<grid, 256, 0, stream>>>(a);
   }
 }
 
@@ -329,17 +212,10 @@ hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
                            hipStream_t stream) {
   if (num_items <= 0) return hipSuccess;
   dim3 grid((unsigned)num_items);
-  if (a.rows64) {
-    if (head_dim == 128)
-      tile_fwd_kernel<128, 64><<<grid, 128, 0, stream>>>(a);
-    else
-      tile_fwd_kernel<64, 64><<<grid, 128, 0, stream>>>(a);
-  } else {
-    if (head_dim == 128)
-      tile_fwd_kernel<128, 128><<<grid, 256, 0, stream>>>(a);
-    else
-      tile_fwd_kernel<64, 128><<<grid, 256, 0, stream>>>(a);
-  }
+  if (a.elem == (int)Elem::f16)
+    launch_tile_elem<Elem::f16>(a, head_dim, grid, stream);
+  else
+    launch_tile_elem<Elem::bf16>(a, head_dim, grid, stream);
   return hipGetLastError();
 }
 

@@ -4,6 +4,7 @@
 // layout's tiles.
 #pragma once
 #include "esa_internal.hpp"
+#include "esa_mma.hpp"
 
 namespace esa {
 
@@ -176,6 +177,182 @@ struct RowWalker {
         for (int q = NW; q < 2 * NW; ++q) mb[q] = 0u;
       }
     }
+  }
+};
+
+// Online-softmax attention of 32 query rows (one wave) against 32-key blocks
+// staged in LDS, shared by the block-sparse and the sliding-window forwards.
+// Each lane owns row l % 32 of the wave and half hf = l / 32 of each block's
+// keys.  Per block:
+//   S^T = K Q^T    D/16 x v_mfma_f32_32x32x16 (A = K rows from LDS, B = Q
+//                  kept in registers for the whole item)
+//   softmax        online, log2 domain; the mask enters as the accumulator's
+//                  initial value (0 or -inf); a block holding no valid key for
+//                  any row of the wave is skipped whole; the running max is
+//                  raised only when a row's block max exceeds it by more than
+//                  kRescaleSlack, so probabilities stay below 2^8
+//   O^T += V^T P^T D/16 x v_mfma_f32_32x32x16 (A = V^T read with
+//                  ds_read_b64_tr_b16 from row-major V in LDS, B = P straight
+//                  from the S^T accumulators: a key permutation shared by both
+//                  operands leaves the contraction unchanged)
+// LDS rows are unpadded with XOR-swizzled 16-byte chunks (swz_k / swz_v).
+template <int D, Elem E>
+struct Rows32 {
+  static constexpr int NS = D / 16;  // k-steps of QK^T
+  static constexpr int ND = D / 32;  // 32-wide d blocks of PV
+  using M = MmaT<E>;
+  using V8 = typename M::v8;
+
+  V8 qop[NS];      // Q as the B operand: 8 consecutive d per lane and k-step
+  int kaddr[NS];   // K operand read offsets (elements) within a 32-key block
+  int vaddr[ND];   // V^T operand read offsets
+  f32x16 oacc[ND];
+  float m_run;     // running max, log2 units (the same in both halves)
+  float l_run;     // running sum of p over this lane's half of the keys (-> lse)
+  float n_run;     // the same sum of p rounded to the input type, as PV sees it (-> O)
+  float scale;     // sm_scale * log2(e), > 0
+  int hf;
+
+  __device__ __forceinline__ void init(int lane, float scale_log2) {
+    hf = lane >> 5;
+    const int l32 = lane & 31, g4 = lane >> 4, lam = lane & 15;
+    scale = scale_log2;
+    // K rows l32 at chunk 2 s + hf; V rows 4 hf + lam / 4 (+ 16 u, + 8) at
+    // column 32 d + 16 (g4 & 1) + 4 (lam & 3)
+#pragma unroll
+    for (int s = 0; s < NS; ++s) kaddr[s] = l32 * D + 8 * ((2 * s + hf) ^ swz_k<D>(l32));
+    const int vrow = 4 * hf + (lam >> 2);
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+      const int col = 32 * d + 16 * (g4 & 1) + 4 * (lam & 3);
+      vaddr[d] = vrow * D + 8 * ((col >> 3) ^ swz_v<D>(vrow)) + (col & 7);
+    }
+    reset();
+  }
+
+  __device__ __forceinline__ void reset() {
+    m_run = -INFINITY;
+    l_run = 0.f;
+    n_run = 0.f;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) oacc[d] = f32x16{};
+  }
+
+  // Q row `row` of 16-bit elements (zeros when !ok)
+  __device__ __forceinline__ void load_q(const uint16_t* qrow, bool ok) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (ok) raw = *(const u32x4*)(qrow + 16 * s + 8 * hf);
+      qop[s] = __builtin_bit_cast(V8, raw);
+    }
+  }
+
+  // One 32-key block: keys 32 kbl .. 32 kbl + 31 of the LDS buffers (Kb, Vb),
+  // whose valid-key bits for this lane's row are mbits (bit k: key k).
+  __device__ __forceinline__ void block(const uint16_t* Kb, const uint16_t* Vb, int kbl,
+                                        uint32_t mbits) {
+    // lane half hf holds keys 8*(r/4) + 4*hf + r%4 of the block
+    const uint32_t mk = mbits >> (4 * hf);
+    // a 32 x 32 block in which no row of the wave has a valid key contributes
+    // p = 0 to every row: its reads, MFMAs and softmax are all skipped (O, the
+    // running max and the sums are unchanged, bit for bit)
+    if (!wave_any(mk != 0u)) return;
+
+    // all K operand reads first, so their LDS latency overlaps
+    V8 ka[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) ka[s] = *(const V8*)(Kb + kaddr[s] + 32 * kbl * D);
+    // the mask enters as the accumulator's initial value: 0 for a valid key,
+    // -inf for a masked one
+    f32x16 sacc;
+    mask_init<0>(sacc, ~mk);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) sacc = M::mfma32(ka[s], qop[s], sacc);
+    // the V^T operands of this block, read while the softmax runs
+    s16x4 va[ND][4];
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const uint16_t* p1 = Vb + vaddr[d] + (32 * kbl + 16 * u) * D;
+        va[d][2 * u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p1);
+        va[d][2 * u + 1] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1 + 8 * D));
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    uint32_t pw[8];  // P as packed 16-bit pairs: pw[q] holds regs 2q, 2q+1
+    // x = scaled score relative to the running max (log2 units); a masked
+    // key stays -inf (scale > 0)
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float smax = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sacc[r] = __builtin_fmaf(sacc[r], scale, -m_use);
+      smax = fmaxf(smax, sacc[r]);
+    }
+    smax = half_max(smax);
+    // raise the running max of a row when this block exceeds it by more
+    // than the slack (or when the row sees its first valid key)
+    const bool grow = m_run == -INFINITY ? smax != -INFINITY : smax > kRescaleSlack;
+    if (wave_any(grow)) {
+      const float delta = grow ? smax : 0.f;
+      // rows that do not grow keep alpha = 1 (m_run may still be -inf there)
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - (m_use + delta)) : 1.0f;
+      l_run *= alpha;
+      n_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < ND; ++d) oacc[d] *= alpha;
+      m_run = grow ? m_use + delta : m_run;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] -= delta;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float p0 = __builtin_amdgcn_exp2f(sacc[2 * q]);
+      const float p1 = __builtin_amdgcn_exp2f(sacc[2 * q + 1]);
+      l_run += p0;
+      l_run += p1;
+      pw[q] = M::pack2(p0, p1);
+      // normalise O by the probabilities PV actually used, so a row led by
+      // one key reproduces that key's value row
+      n_run = M::dot2(pw[q], n_run);
+    }
+
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const s16x4 vv[2] = {va[d][2 * u], va[d][2 * u + 1]};
+        const V8 a = __builtin_bit_cast(V8, vv);
+        const u32x4 pq = {pw[4 * u], pw[4 * u + 1], pw[4 * u + 2], pw[4 * u + 3]};
+        oacc[d] = M::mfma32(a, __builtin_bit_cast(V8, pq), oacc[d]);
+      }
+    }
+  }
+
+  // Epilogue: O normalised by the rounded probabilities PV used (a row led by
+  // one key reproduces that key's value row), lse by the exact float32 sum
+  // (natural log); rows with no valid key get O = 0 and lse = -inf.
+  __device__ __forceinline__ void store(uint16_t* orow, float* lse, bool row_ok) {
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float n_tot = n_run + __shfl_xor(n_run, 32, 64);
+    if (!row_ok) return;
+    const float inv = n_tot > 0.f ? 1.f / n_tot : 0.f;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        typename M::v4 ov;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ov[e] = (typename M::s)(oacc[d][4 * q4 + e] * inv);
+        *(typename M::v4*)(orow + 32 * d + 8 * q4 + 4 * hf) = ov;
+      }
+    }
+    if (lse && hf == 0)
+      *lse = l_tot > 0.f ? (m_run + __log2f(l_tot)) * 0.69314718055994530942f : -INFINITY;
   }
 };
 

@@ -137,7 +137,8 @@ esa_status esa_plan_schedule(const esa_pattern* p, const int32_t* row_ptr_host,
  * per 128 query rows, 64-key stages) or 64 x 32 (two waves per 64 query
  * rows, 32-key stages, the fastest in general); in the finer layouts the
  * parts of a 128-key tile that no row of the query block needs are never
- * staged.  All give the same output bit for bit.  Requires dtype ESA_BF16,
+ * staged.  All give the same output bit for bit.  Requires dtype ESA_BF16
+ * or ESA_F16 (the MFMAs and P in that type, float32 accumulation),
  * head_dim 64 or 128, (block_m, block_n) in {(128, 128), (128, 64),
  * (64, 32)}, a finite sm_scale > 0
  * (ESA_ERR_UNSUPPORTED otherwise; esa_elastic_fwd_rows takes any), K and V
@@ -162,11 +163,27 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p,
  * one wave gathers each band's keys once for its 16 rows and runs QK^T and
  * PV on bf16 MFMA with float32 accumulation and online softmax.  Same
  * outputs as esa_elastic_fwd within bf16 rounding.  Requires dtype
- * ESA_BF16, head_dim 64 or 128, attention_length <= 64, kv_len < 2^24,
+ * ESA_BF16 or ESA_F16, head_dim 64 or 128, attention_length <= 64, kv_len < 2^24,
  * (kv_len + 16) * K/V row stride * 2 < 2^31, row strides >= head_dim,
  * q_len <= kv_len, q_len <= p->seq_len, finite sm_scale > 0, 16-byte
  * aligned q, k, v, o and strides (elements) that are multiples of 8. */
 esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, void* stream);
+
+/* Sliding-window forward for layer 0 of the elastic pattern, prefill rows
+ * 0 .. q_len-1 (no layout needed).  Replaces the Triton forward
+ * (elastic_sparse_attention.py:117-166) as _triton_forward launches it for
+ * prefill (:592-622) where layer_idx = 0: there the recipe of :482-533 gives
+ * every row of every head the contiguous keys [max(0, i - w + 1), i], i.e.
+ * causal sliding-window attention.  Each workgroup streams a run of
+ * consecutive 64-row query blocks of one (batch, head) through a ring of
+ * K/V blocks in LDS, loading the next block while computing the current
+ * one, so K and V are read about once.  Same outputs as esa_elastic_fwd
+ * within bf16 rounding.  Requires layer_idx 0, attention_length <= 64,
+ * dtype ESA_BF16 or ESA_F16, head_dim 64 or 128, q_len < 2^21,
+ * q_len <= kv_len, q_len <= p->seq_len, a finite sm_scale > 0, (kv_len + 64)
+ * * K/V row stride * 2 < 2^31, row strides >= head_dim, 16-byte aligned
+ * q, k, v rows (strides multiples of 8 elements), 8-byte aligned o rows. */
+esa_status esa_elastic_fwd_window(const esa_fwd_args* a, const esa_pattern* p, void* stream);
 
 /* Per-row gather forward over the elastic pattern for arbitrary query
  * positions: row r of q is position positions[r] (int64 device array, as
@@ -229,7 +246,7 @@ esa_status esa_sparse_fwd(const esa_fwd_args* a, const void* indices,
  * (elastic_sparse_attention.py:299-339).  All bf16 except lse (float32,
  * natural log, [B, H, q_len] with contiguous rows). */
 typedef struct esa_bwd_args {
-  esa_dtype dtype; /* ESA_BF16 */
+  esa_dtype dtype; /* ESA_BF16 or ESA_F16 (esa_elastic_bwd); any (gather backward) */
   int32_t batch, num_heads, num_kv_heads, q_len, kv_len, head_dim;
   const void* q;
   int64_t q_stride_b, q_stride_h, q_stride_s;
@@ -315,7 +332,7 @@ esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes
  * instead (same limits; tile_row, kv_ptr, kv_tiles, mask_t and num_kv_items
  * are ignored).  With both NULL no layout is read (row_ptr, col_idx may be
  * NULL).  All lists and masks are device memory.
- * Requires dtype ESA_BF16, head_dim 64 or 128, block 128 x 128, a finite
+ * Requires dtype ESA_BF16 or ESA_F16, head_dim 64 or 128, block 128 x 128, a finite
  * sm_scale > 0, q_len <= kv_len, 16-byte aligned rows. */
 esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p,
                            const int32_t* row_ptr, const int32_t* col_idx,
