@@ -7,8 +7,7 @@
 A step is one ElasticSparseAttention.forward over one batch of synthetic
 input already resident in HBM (the module's drop-in HIP path: one kernel
 launch, the band-gathered kernel or the block-sparse tile kernel, whichever
-is faster for the shape, or at layer 0 the sliding-window kernel;
-config.kernel names it).  The block layout is built
+is faster for the shape; config.kernel names it).  The block layout is built
 before the timed region, as the reference builds its index cache at
 construction; its build time is reported separately.
 
@@ -172,27 +171,9 @@ def band_executed_flops(B: int, H: int, L: int, D: int, w: int) -> float:
     return float(B * H * pairs * (2 * (D // 32) + D // 16) * 16384)
 
 
-def window_executed_flops(B: int, H: int, L: int, D: int, w: int) -> float:
-    """MFMA flops the window kernel issues: per 32-row wave and 64-row query
-    block, the four 32-key blocks 2 qb - 2 .. 2 qb + 1 that hold a valid key
-    for some row of the wave (row i's keys are [max(0, i - w + 1), i]), each
-    4 x 32 x 32 x D."""
-    blocks = 0
-    for r0 in range(0, L, 32):
-        r1 = min(L, r0 + 32) - 1
-        qb = r0 // 64
-        for kb in range(2 * qb - 2, 2 * qb + 2):
-            k0, k1 = 32 * kb, 32 * kb + 31
-            if k1 >= max(0, r0 - w + 1) and k0 <= r1 and k1 >= 0:
-                blocks += 1
-    return float(B * H * blocks * 4 * 32 * 32 * D)
-
-
 def executed_flops(torch, kernel: str, lay, B: int, H: int, L: int, D: int) -> float:
     if kernel == "tile":
         return B * executed_blocks(torch, lay, L) * 4.0 * 32 * 32 * D
-    if kernel == "window":
-        return window_executed_flops(B, H, L, D, W)
     return band_executed_flops(B, H, L, D, W)
 
 
@@ -368,7 +349,7 @@ def main() -> None:
     ap.add_argument("--config", default="32k", choices=sorted(CONFIGS))
     ap.add_argument("--layer", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--kernel", default="auto", choices=["auto", "band", "tile", "window"],
+    ap.add_argument("--kernel", default="auto", choices=["auto", "band", "tile"],
                     help="prefill kernel the module runs (default: the faster for the shape)")
     ap.add_argument("--no-backward", dest="backward", action="store_false",
                     help="skip timing the backward (reported beside the forward by default)")

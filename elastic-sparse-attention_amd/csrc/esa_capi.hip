@@ -483,63 +483,6 @@ esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, voi
   return hip_status(launch_band_fwd(t, a->head_dim, (hipStream_t)stream));
 }
 
-esa_status esa_elastic_fwd_window(const esa_fwd_args* a, const esa_pattern* p, void* stream) {
-  esa_status s = check_fwd_common(a);
-  if (s != ESA_OK) return s;
-  s = check_pattern(p);
-  if (s != ESA_OK) return s;
-  if (a->dtype != ESA_BF16 && a->dtype != ESA_F16) return ESA_ERR_DTYPE;
-  if (a->head_dim != 64 && a->head_dim != 128) return ESA_ERR_UNSUPPORTED;
-  // the contiguous runs of layer 0 (interpolation weight 0), at most 64 keys
-  // (the ring holds keys [q0 - 64, q0 + 64) of a 64-row block), exact below
-  // 2^21 (RowWalker's contiguous-run bound)
-  if (p->layer_idx != 0 || p->attention_length > 64) return ESA_ERR_UNSUPPORTED;
-  if (p->num_heads != a->num_heads) return ESA_ERR_SHAPE;
-  if (a->q_len > a->kv_len || a->q_len > p->seq_len) return ESA_ERR_SHAPE;
-  if (a->q_len >= (1 << 21)) return ESA_ERR_UNSUPPORTED;
-  if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale)) return ESA_ERR_UNSUPPORTED;
-  // K/V rows are addressed through 32-bit buffer offsets per (batch, kv head)
-  // (up to one 64-row block past kv_len, read as zeros)
-  if ((int64_t)(a->kv_len + 64) * a->k_stride_s * 2 >= (int64_t(1) << 31) ||
-      (int64_t)(a->kv_len + 64) * a->v_stride_s * 2 >= (int64_t(1) << 31) ||
-      a->k_stride_s < a->head_dim || a->v_stride_s < a->head_dim)
-    return ESA_ERR_UNSUPPORTED;
-  if (!aligned(a->q, 16) || !aligned(a->k, 16) || !aligned(a->v, 16) || !aligned(a->o, 8))
-    return ESA_ERR_ALIGN;
-  const int64_t st[] = {a->q_stride_b, a->q_stride_h, a->q_stride_s, a->k_stride_b,
-                        a->k_stride_h, a->k_stride_s, a->v_stride_b, a->v_stride_h,
-                        a->v_stride_s};
-  for (int64_t x : st)
-    if (x % 8 != 0) return ESA_ERR_ALIGN;
-  if (a->o_stride_b % 4 || a->o_stride_h % 4 || a->o_stride_s % 4) return ESA_ERR_ALIGN;
-  if (a->batch == 0 || a->q_len == 0) return ESA_OK;
-  WindowArgs t{};
-  t.q = (const uint16_t*)a->q; t.k = (const uint16_t*)a->k; t.v = (const uint16_t*)a->v;
-  t.o = (uint16_t*)a->o; t.lse = a->lse;
-  t.qsb = a->q_stride_b; t.qsh = a->q_stride_h; t.qss = a->q_stride_s;
-  t.ksb = a->k_stride_b; t.ksh = a->k_stride_h; t.kss = a->k_stride_s;
-  t.vsb = a->v_stride_b; t.vsh = a->v_stride_h; t.vss = a->v_stride_s;
-  t.osb = a->o_stride_b; t.osh = a->o_stride_h; t.oss = a->o_stride_s;
-  t.lsb = a->lse_stride_b; t.lsh = a->lse_stride_h;
-  t.H = a->num_heads; t.groups = a->num_heads / a->num_kv_heads;
-  t.q_len = a->q_len; t.kv_len = a->kv_len; t.w = p->attention_length;
-  t.nq = (a->q_len + 63) / 64;
-  // runs of consecutive query blocks: about four rounds of the resident
-  // workgroups (one per CU at D = 128, whose ring takes 96 KB of LDS; three
-  // at D = 64), between 2 and 16 blocks per run
-  const int64_t total = (int64_t)a->batch * a->num_heads * t.nq;
-  const int64_t resident = 256 * (a->head_dim == 128 ? 1 : 3);
-  t.nrun = (int)std::min<int64_t>(16, std::max<int64_t>(2, (total + 4 * resident - 1) / (4 * resident)));
-  t.runs_per_bh = (t.nq + t.nrun - 1) / t.nrun;
-  const int64_t n_runs = (int64_t)a->batch * a->num_heads * t.runs_per_bh;
-  if (n_runs > INT32_MAX / 2) return ESA_ERR_SHAPE;
-  t.n_runs = (int)n_runs;
-  t.per_xcd = (int)((n_runs + 7) / 8);
-  t.scale_log2 = a->sm_scale * 1.4426950408889634f;
-  t.elem = a->dtype;
-  return hip_status(launch_window_fwd(t, a->head_dim, (hipStream_t)stream));
-}
-
 esa_status esa_elastic_fwd_rows(const esa_fwd_args* a, const esa_pattern* p,
                                 const int64_t* positions, void* stream) {
   esa_status s = check_fwd_common(a);

@@ -82,30 +82,6 @@ struct DropoutArgs {
   uint64_t seed;  // keep decisions are a function of (seed, b, h, row, entry)
 };
 
-// Arguments of the sliding-window forward (the pattern at layer 0): runs of
-// nrun consecutive 64-row query blocks of one (batch, head).
-struct WindowArgs {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
-  uint16_t* o;
-  float* lse;
-  int64_t qsb, qsh, qss;
-  int64_t ksb, ksh, kss;
-  int64_t vsb, vsh, vss;
-  int64_t osb, osh, oss;
-  int64_t lsb, lsh;
-  int H, groups, q_len, kv_len;
-  int w;           // window (attention_length)
-  int nq;          // 64-row query blocks per (batch, head)
-  int nrun;        // query blocks per run
-  int runs_per_bh;
-  int n_runs;      // batch * H * runs_per_bh
-  int per_xcd;     // runs per XCD range
-  float scale_log2;
-  int elem;        // Elem of q, k, v, o: bf16 or f16
-};
-
 // Arguments of the per-row gather forward.
 struct GatherArgs {
   const void* q;
@@ -228,7 +204,6 @@ hipError_t launch_layout(const PatternConsts& pc, const LayoutDims& ld, int32_t*
 hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
                            hipStream_t stream);
 hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream);
-hipError_t launch_window_fwd(const WindowArgs& a, int head_dim, hipStream_t stream);
 // prep: the kernel forms and stores delta / lse2 itself (see band_dq_kernel)
 hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2, bool prep,
                           hipStream_t stream);

@@ -77,7 +77,6 @@ __all__ = [
     "build_indices",
     "elastic_attention_fwd",
     "elastic_attention_rows",
-    "elastic_attention_window",
     "sparse_attention_fwd",
     "elastic_attention_bwd",
 ]
@@ -352,14 +351,9 @@ BAND_CROSSOVER = {128: 16.5, 64: 12.5}
 
 
 def prefill_kernel(layout: ElasticLayout, q_len: int, batch: int, head_dim: int) -> str:
-    """"window", "band" or "tile": the faster prefill kernel for this pattern
-    and shape.  Layer 0 (a causal sliding window) takes the window kernel
-    (attention_length <= 64, q_len < 2^21); the band kernel needs
-    attention_length <= 64 and kv_len < 2^24."""
+    """"band" or "tile": the faster prefill kernel for this pattern and shape
+    (the band kernel needs attention_length <= 64 and kv_len < 2^24)."""
     p = layout.pattern
-    if p.layer_idx == 0 and p.attention_length <= 64 and head_dim in (64, 128) and \
-            q_len < (1 << 21):
-        return "window"
     if p.attention_length > 64 or head_dim not in BAND_CROSSOVER or p.seq_len >= (1 << 24):
         return "tile"
     groups = batch * p.num_heads * ((q_len + 15) // 16)
@@ -374,7 +368,6 @@ def bwd_kernels(layout: ElasticLayout, q_len: int, batch: int, head_dim: int
     layer of six shapes (D = 64 and 128, GQA included) the fastest pair was
     the forward's kind for both halves or within 1% of it."""
     kind = prefill_kernel(layout, q_len, batch, head_dim)
-    kind = "tile" if kind == "window" else kind  # layer 0's backward: block-sparse
     return kind, kind
 
 
@@ -400,16 +393,14 @@ def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     """
     _check_qkv(q, k, v)
     B, H, Lq, D = q.shape
-    if kernel not in ("auto", "tile", "band", "window"):
-        raise ValueError(f"kernel must be 'auto', 'tile', 'band' or 'window', got {kernel!r}")
+    if kernel not in ("auto", "tile", "band"):
+        raise ValueError(f"kernel must be 'auto', 'tile' or 'band', got {kernel!r}")
     if kernel == "auto":
         kernel = prefill_kernel(layout, Lq, B, D)
-        if out is not None and out.data_ptr() % 16 != 0 and kernel == "band":
+        if out is not None and out.data_ptr() % 16 != 0:
             kernel = "tile"
     if kernel == "band":
         return elastic_attention_band(q, k, v, layout.pattern, scaling, return_lse, out)
-    if kernel == "window":
-        return elastic_attention_window(q, k, v, layout.pattern, scaling, return_lse, out)
     q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
     o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
@@ -456,27 +447,6 @@ def _positions_ptr(positions: Optional[torch.Tensor], q_len: int, device: torch.
         raise ValueError("positions must be an int64 tensor of q_len entries on q's device")
     positions = positions.contiguous()
     return positions, ctypes.c_void_p(positions.data_ptr())
-
-
-def elastic_attention_window(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                             pattern: EsaPattern, scaling: float, return_lse: bool = True,
-                             out: Optional[torch.Tensor] = None
-                             ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
-    """Sliding-window MFMA forward of layer 0 (prefill: query row r is
-    position r): at layer_idx 0 every row's index list is the contiguous run
-    [max(0, r - w + 1), r], and each workgroup streams a run of 64-row query
-    blocks through a ring of K/V blocks in LDS.  Returns ``o`` ``[B, Lq, H,
-    D]`` and, if asked, ``lse`` float32 ``[B, H, Lq]``, as
-    :func:`elastic_attention_fwd`."""
-    _check_qkv(q, k, v)
-    B, H, Lq, D = q.shape
-    q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
-    o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
-    lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
-    a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
-    check(load().esa_elastic_fwd_window(ctypes.byref(a), ctypes.byref(pattern), _stream(q.device)),
-          "esa_elastic_fwd_window")
-    return o, lse
 
 
 def elastic_attention_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,

@@ -169,22 +169,6 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p,
  * aligned q, k, v, o and strides (elements) that are multiples of 8. */
 esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, void* stream);
 
-/* Sliding-window forward for layer 0 of the elastic pattern, prefill rows
- * 0 .. q_len-1 (no layout needed).  Replaces the Triton forward
- * (elastic_sparse_attention.py:117-166) as _triton_forward launches it for
- * prefill (:592-622) where layer_idx = 0: there the recipe of :482-533 gives
- * every row of every head the contiguous keys [max(0, i - w + 1), i], i.e.
- * causal sliding-window attention.  Each workgroup streams a run of
- * consecutive 64-row query blocks of one (batch, head) through a ring of
- * K/V blocks in LDS, loading the next block while computing the current
- * one, so K and V are read about once.  Same outputs as esa_elastic_fwd
- * within bf16 rounding.  Requires layer_idx 0, attention_length <= 64,
- * dtype ESA_BF16 or ESA_F16, head_dim 64 or 128, q_len < 2^21,
- * q_len <= kv_len, q_len <= p->seq_len, a finite sm_scale > 0, (kv_len + 64)
- * * K/V row stride * 2 < 2^31, row strides >= head_dim, 16-byte aligned
- * q, k, v rows (strides multiples of 8 elements), 8-byte aligned o rows. */
-esa_status esa_elastic_fwd_window(const esa_fwd_args* a, const esa_pattern* p, void* stream);
-
 /* Per-row gather forward over the elastic pattern for arbitrary query
  * positions: row r of q is position positions[r] (int64 device array, as
  * cache_position, :602-608), or r when positions is NULL.  Replaces the

@@ -16,8 +16,7 @@ from esa_oracle import (elastic_indices, forward_fp32, prepared_rows, scaling_fo
                         seeded_inputs)
 from elastic_sparse_attention import (ElasticLayout, ElasticSparseAttention,
                                       ElasticSparseAttentionFunction, elastic_attention_band,
-                                      elastic_attention_fwd, elastic_attention_window,
-                                      prefill_kernel,
+                                      elastic_attention_fwd, prefill_kernel,
                                       elastic_attention_rows, make_pattern,
                                       sparse_attention_fwd)
 
@@ -259,71 +258,14 @@ def test_band_sharp_softmax_outliers():
 
 
 @pytest.mark.parametrize("L,H,B,D,layer,want", [
-    (32768, 32, 1, 128, 4, "band"), (32768, 32, 1, 128, 0, "window"), (8192, 32, 1, 128, 3, "tile"),
+    (32768, 32, 1, 128, 4, "band"), (32768, 32, 1, 128, 0, "tile"), (8192, 32, 1, 128, 3, "tile"),
     (8192, 32, 1, 128, 4, "band"), (4096, 16, 8, 64, 5, "tile"), (4096, 16, 8, 64, 6, "band"),
 ])
 def test_prefill_kernel_choice(L, H, B, D, layer, want):
-    # layer 0 (a sliding window) takes the window kernel; otherwise the
-    # measured crossover: the band kernel where a group's rows stage many
+    # the measured crossover: the band kernel where a group's rows stage many
     # 64 x 32 blocks, the tile kernel where they stage few
     lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
     assert prefill_kernel(lay, L, B, D) == want
-
-
-# ---------------------------------------------------------------- sliding-window kernel (layer 0)
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("B,H,Hkv,L,Lq,D,w", [
-    (1, 4, 4, 1024, 1024, 128, 64),   # 16 query blocks: every ring phase, several runs
-    (2, 4, 2, 1000, 937, 64, 64),     # GQA, ragged q_len < kv_len
-    (1, 2, 1, 700, 700, 128, 33),     # odd window, MQA
-    (3, 1, 1, 200, 200, 64, 16),      # short window, batch
-    (1, 3, 3, 50, 50, 128, 64),       # shorter than one block
-    (1, 2, 2, 129, 129, 64, 1),       # one key per row
-])
-def test_window_kernel(dtype, B, H, Hkv, L, Lq, D, w):
-    print(f"window {dtype} B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} w={w}", flush=True)
-    q, k, v, idx, msk = case(B, H, Hkv, L, D, dtype, 0, w=w, seed=w + D, scale=1.0, Lq=Lq)
-    sc = scaling_for(D)
-    o, lse = elastic_attention_window(q.to(DEV), k.to(DEV), v.to(DEV),
-                                      make_pattern(L, w, 0, 8, H), sc)
-    pi, pm = prepared_rows(idx, msk, Lq, L, L)
-    ro, rl = oracle(q, k, v, pi, pm, sc, H // Hkv)
-    assert (to_bhsd(o).float().cpu() - ro).abs().max().item() <= BF16_TOL
-    assert (lse.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
-
-
-@pytest.mark.parametrize("B,H,L,D", [(1, 32, 32768, 128), (8, 16, 4096, 64)])
-def test_window_full_size(B, H, L, D):
-    """The configured layer-0 shapes: sampled rows against the oracle, every
-    row against the float32 per-row gather kernel and against the tile
-    kernel."""
-    q, k, v = seeded_inputs(B, H, H, L, D, torch.bfloat16, seed=1, scale=D ** -0.25)
-    sc = scaling_for(D)
-    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
-    pat = make_pattern(L, 64, 0, 8, H)
-    o, lse = elastic_attention_window(qd, kd, vd, pat, sc)
-    rows = torch.cat([torch.tensor([0, 1, 62, 63, 64, 127, 128, L - 65, L - 1]),
-                      torch.randint(0, L, (128,), generator=torch.Generator().manual_seed(0))])
-    rows = rows.unique()
-    idx, msk = elastic_indices(L, 0, 8, H, 64)
-    ro, rl = oracle(q, k, v, idx, msk, sc, 1, rows)
-    assert (to_bhsd(o)[:, :, rows.to(DEV)].float().cpu() - ro).abs().max().item() <= BF16_TOL
-    assert (lse[:, :, rows.to(DEV)].cpu() - rl).abs().max().item() <= BF16_LSE_TOL
-    og, lg = elastic_attention_rows(qd.float(), kd.float(), vd.float(), pat, sc)
-    assert (o.float() - og).abs().max().item() <= BF16_TOL
-    assert (lse - lg).abs().max().item() <= BF16_LSE_TOL
-    lay = ElasticLayout(pat, DEV)
-    ot, lt = elastic_attention_fwd(qd, kd, vd, lay, sc, kernel="tile")
-    assert (o.float() - ot.float()).abs().max().item() <= 4e-3
-    assert (lse - lt).abs().max().item() <= 1e-4
-
-
-def test_window_rejects_other_layers():
-    q = torch.zeros(1, 2, 64, 128, dtype=torch.bfloat16, device=DEV)
-    with pytest.raises(Exception, match="unsupported"):
-        elastic_attention_window(q, q, q, make_pattern(64, 64, 1, 8, 2), 0.1)
-    with pytest.raises(Exception, match="unsupported"):
-        elastic_attention_window(q, q, q, make_pattern(64, 100, 0, 8, 2), 0.1)
 
 
 def test_band_rejects_unsupported():
