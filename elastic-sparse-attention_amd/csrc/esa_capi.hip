@@ -430,7 +430,15 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
   return hip_status(launch_tile_fwd(t, a->head_dim, num_items, (hipStream_t)stream));
 }
 
-esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Checks and arguments shared by the band-gathered and the staged-band
+// forwards; rows_per_item: query rows per work item (16 or 128), pad_rows:
+// rows past kv_len (or q_len) whose 32-bit buffer offsets are formed.
+esa_status band_args_of(const esa_fwd_args* a, const esa_pattern* p, int rows_per_item,
+                        int pad_rows, BandArgs* out) {
   esa_status s = check_fwd_common(a);
   if (s != ESA_OK) return s;
   s = check_pattern(p);
@@ -448,8 +456,8 @@ esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, voi
   // band descriptors pack the first key in 24 bits; K/V rows are addressed
   // through 32-bit buffer offsets per (batch, kv head)
   if (a->kv_len >= (1 << 24)) return ESA_ERR_UNSUPPORTED;
-  if ((int64_t)(a->kv_len + 16) * a->k_stride_s * 2 >= (int64_t(1) << 31) ||
-      (int64_t)(a->kv_len + 16) * a->v_stride_s * 2 >= (int64_t(1) << 31) ||
+  if ((int64_t)(a->kv_len + pad_rows) * a->k_stride_s * 2 >= (int64_t(1) << 31) ||
+      (int64_t)(a->kv_len + pad_rows) * a->v_stride_s * 2 >= (int64_t(1) << 31) ||
       a->k_stride_s < a->head_dim || a->v_stride_s < a->head_dim)
     return ESA_ERR_UNSUPPORTED;
   // 16-byte row loads and stores
@@ -460,12 +468,12 @@ esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, voi
                         a->v_stride_s, a->o_stride_b, a->o_stride_h, a->o_stride_s};
   for (int64_t x : st)
     if (x % 8 != 0) return ESA_ERR_ALIGN;
+  BandArgs& t = *out;
+  t = BandArgs{};
   if (a->batch == 0 || a->q_len == 0) return ESA_OK;
-  const int ng = (a->q_len + 15) / 16;
+  const int ng = (a->q_len + rows_per_item - 1) / rows_per_item;
   const int64_t n_groups = (int64_t)a->batch * a->num_heads * ng;
   if (n_groups > INT32_MAX / 2) return ESA_ERR_SHAPE;
-
-  BandArgs t{};
   t.q = (const uint16_t*)a->q; t.k = (const uint16_t*)a->k; t.v = (const uint16_t*)a->v;
   t.o = (uint16_t*)a->o; t.lse = a->lse;
   t.qsb = a->q_stride_b; t.qsh = a->q_stride_h; t.qss = a->q_stride_s;
@@ -480,7 +488,26 @@ esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, voi
   t.scale_log2 = a->sm_scale * 1.4426950408889634f;
   t.pc = make_consts(*p);
   t.elem = a->dtype;
+  return ESA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, void* stream) {
+  BandArgs t;
+  esa_status s = band_args_of(a, p, 16, 16, &t);
+  if (s != ESA_OK || t.n_groups == 0) return s;
   return hip_status(launch_band_fwd(t, a->head_dim, (hipStream_t)stream));
+}
+
+esa_status esa_elastic_fwd_sband(const esa_fwd_args* a, const esa_pattern* p, void* stream) {
+  // the ring loads up to 16 chunks of 16 keys past a block's last key
+  BandArgs t;
+  esa_status s = band_args_of(a, p, sband_rows(), 272, &t);
+  if (s != ESA_OK || t.n_groups == 0) return s;
+  return hip_status(launch_sband_fwd(t, a->head_dim, (hipStream_t)stream));
 }
 
 esa_status esa_elastic_fwd_rows(const esa_fwd_args* a, const esa_pattern* p,
