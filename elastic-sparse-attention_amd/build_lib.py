@@ -18,7 +18,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
-SOURCES = ["esa_capi.hip", "esa_layout.hip", "esa_fwd_tile.hip", "esa_fwd_band.hip", "esa_fwd_sband.hip",
+SOURCES = ["esa_capi.hip", "esa_layout.hip", "esa_fwd_tile.hip", "esa_fwd_band.hip",
            "esa_bwd_band.hip", "esa_fwd_gather.hip", "esa_bwd_gather.hip", "esa_bwd.hip",
            "esa_reach.hip"]
 LIB = os.path.join(HERE, "libesa.so")

@@ -434,11 +434,10 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
 
 namespace {
 
-// Checks and arguments shared by the band-gathered and the staged-band
-// forwards; rows_per_item: query rows per work item (16 or 128), pad_rows:
-// rows past kv_len (or q_len) whose 32-bit buffer offsets are formed.
-esa_status band_args_of(const esa_fwd_args* a, const esa_pattern* p, int rows_per_item,
-                        int pad_rows, BandArgs* out) {
+// Checks and arguments of the band-gathered forward (16 query rows per
+// group; a band's buffer offsets reach up to 16 rows past kv_len).
+esa_status band_args_of(const esa_fwd_args* a, const esa_pattern* p, BandArgs* out) {
+  constexpr int rows_per_item = 16, pad_rows = 16;
   esa_status s = check_fwd_common(a);
   if (s != ESA_OK) return s;
   s = check_pattern(p);
@@ -497,17 +496,9 @@ extern "C" {
 
 esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, void* stream) {
   BandArgs t;
-  esa_status s = band_args_of(a, p, 16, 16, &t);
+  esa_status s = band_args_of(a, p, &t);
   if (s != ESA_OK || t.n_groups == 0) return s;
   return hip_status(launch_band_fwd(t, a->head_dim, (hipStream_t)stream));
-}
-
-esa_status esa_elastic_fwd_sband(const esa_fwd_args* a, const esa_pattern* p, void* stream) {
-  // the ring loads up to 16 chunks of 16 keys past a block's last key
-  BandArgs t;
-  esa_status s = band_args_of(a, p, sband_rows(), 272, &t);
-  if (s != ESA_OK || t.n_groups == 0) return s;
-  return hip_status(launch_sband_fwd(t, a->head_dim, (hipStream_t)stream));
 }
 
 esa_status esa_elastic_fwd_rows(const esa_fwd_args* a, const esa_pattern* p,

@@ -204,9 +204,6 @@ hipError_t launch_layout(const PatternConsts& pc, const LayoutDims& ld, int32_t*
 hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
                            hipStream_t stream);
 hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream);
-// staged-band forward: ng = row blocks of sband_rows() rows per (b, h)
-int sband_rows();
-hipError_t launch_sband_fwd(const BandArgs& a, int head_dim, hipStream_t stream);
 // prep: the kernel forms and stores delta / lse2 itself (see band_dq_kernel)
 hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2, bool prep,
                           hipStream_t stream);

@@ -181,7 +181,7 @@ struct RowWalker {
 };
 
 // Online-softmax attention of 32 query rows (one wave) against 32-key blocks
-// staged in LDS, shared by the block-sparse and the sliding-window forwards.
+// staged in LDS: the block-sparse forward's per-wave step.
 // Each lane owns row l % 32 of the wave and half hf = l / 32 of each block's
 // keys.  Per block:
 //   S^T = K Q^T    D/16 x v_mfma_f32_32x32x16 (A = K rows from LDS, B = Q

@@ -393,15 +393,14 @@ def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     """
     _check_qkv(q, k, v)
     B, H, Lq, D = q.shape
-    if kernel not in ("auto", "tile", "band", "sband"):
-        raise ValueError(f"kernel must be 'auto', 'tile', 'band' or 'sband', got {kernel!r}")
+    if kernel not in ("auto", "tile", "band"):
+        raise ValueError(f"kernel must be 'auto', 'tile' or 'band', got {kernel!r}")
     if kernel == "auto":
         kernel = prefill_kernel(layout, Lq, B, D)
         if out is not None and out.data_ptr() % 16 != 0:
             kernel = "tile"
-    if kernel in ("band", "sband"):
-        return elastic_attention_band(q, k, v, layout.pattern, scaling, return_lse, out,
-                                      staged=kernel == "sband")
+    if kernel == "band":
+        return elastic_attention_band(q, k, v, layout.pattern, scaling, return_lse, out)
     q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
     o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
@@ -422,24 +421,21 @@ def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
 def elastic_attention_band(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                            pattern: EsaPattern, scaling: float, return_lse: bool = True,
-                           out: Optional[torch.Tensor] = None, staged: bool = False
+                           out: Optional[torch.Tensor] = None
                            ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Band-gathered MFMA forward (prefill: query row r is position r), no
     layout needed: each wave takes 16 query rows and, for every entry j of
     their index lists, gathers the at most 16 consecutive keys those rows use
-    at entry j.  ``staged``: the staged-band kernel, where a workgroup of 128
-    rows streams the keys its bands touch through LDS once instead.  Returns
-    ``o`` ``[B, Lq, H, D]`` and, if asked, ``lse`` float32 ``[B, H, Lq]``, as
-    :func:`elastic_attention_fwd`."""
+    at entry j.  Returns ``o`` ``[B, Lq, H, D]`` and, if asked, ``lse``
+    float32 ``[B, H, Lq]``, as :func:`elastic_attention_fwd`."""
     _check_qkv(q, k, v)
     B, H, Lq, D = q.shape
     q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
     o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
-    fn = load().esa_elastic_fwd_sband if staged else load().esa_elastic_fwd_band
-    check(fn(ctypes.byref(a), ctypes.byref(pattern), _stream(q.device)),
-          "esa_elastic_fwd_sband" if staged else "esa_elastic_fwd_band")
+    check(load().esa_elastic_fwd_band(ctypes.byref(a), ctypes.byref(pattern), _stream(q.device)),
+          "esa_elastic_fwd_band")
     return o, lse
 
 

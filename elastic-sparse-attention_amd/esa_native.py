@@ -29,7 +29,7 @@ ESA_F16 = 2
 EXPORTED = (
     "esa_status_string", "esa_version", "esa_layout_sizes", "esa_build_indices",
     "esa_build_layout", "esa_plan_schedule", "esa_elastic_fwd", "esa_elastic_fwd_band",
-    "esa_elastic_fwd_sband", "esa_elastic_fwd_rows",
+    "esa_elastic_fwd_rows",
     "esa_sparse_fwd", "esa_plan_bwd", "esa_build_tile_masks", "esa_bwd_workspace_size",
     "esa_elastic_bwd", "esa_elastic_bwd_noalloc", "esa_bwd_noalloc_max_workspace",
     "esa_elastic_fwd_naive", "esa_gather_bwd_workspace_size", "esa_sparse_bwd",
@@ -136,8 +136,6 @@ def load() -> ctypes.CDLL:
     lib.esa_elastic_fwd.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp, vp, vp, ctypes.c_int64, vp]
     lib.esa_elastic_fwd_band.restype = st
     lib.esa_elastic_fwd_band.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp]
-    lib.esa_elastic_fwd_sband.restype = st
-    lib.esa_elastic_fwd_sband.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp]
     lib.esa_elastic_fwd_rows.restype = st
     lib.esa_elastic_fwd_rows.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp, vp]
     lib.esa_sparse_fwd.restype = st

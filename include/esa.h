@@ -169,17 +169,6 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p,
  * aligned q, k, v, o and strides (elements) that are multiples of 8. */
 esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, void* stream);
 
-/* Staged-band forward over the elastic pattern, prefill rows 0 .. q_len-1
- * (no layout needed): the arithmetic of esa_elastic_fwd_band (each index-list
- * entry's keys for 16 rows as a 16-key band on MFMA, one key per row kept)
- * over K/V that a workgroup of 128 consecutive rows stages once, streaming
- * the keys its bands touch in ascending order through a ring in LDS.  Pays
- * where rows are short (neighbouring groups' bands overlap); replaces the
- * same reference code as esa_elastic_fwd_band.  Same outputs within bf16
- * rounding and the same requirements, with (kv_len + 272) * K/V row stride *
- * 2 < 2^31. */
-esa_status esa_elastic_fwd_sband(const esa_fwd_args* a, const esa_pattern* p, void* stream);
-
 /* Per-row gather forward over the elastic pattern for arbitrary query
  * positions: row r of q is position positions[r] (int64 device array, as
  * cache_position, :602-608), or r when positions is NULL.  Replaces the

@@ -268,52 +268,6 @@ def test_prefill_kernel_choice(L, H, B, D, layer, want):
     assert prefill_kernel(lay, L, B, D) == want
 
 
-# ---------------------------------------------------------------- staged-band kernel
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("B,H,Hkv,L,Lq,D,w", [
-    (1, 4, 4, 1024, 1024, 128, 64),
-    (2, 4, 2, 1000, 937, 64, 64),     # GQA, ragged q_len < kv_len
-    (1, 3, 1, 700, 700, 128, 33),     # odd head count (bands of 17 keys: two windows)
-    (3, 2, 2, 300, 300, 64, 16),      # short lists, batch
-    (1, 2, 2, 50, 50, 128, 64),       # shorter than one block
-])
-def test_sband_all_layers(dtype, B, H, Hkv, L, Lq, D, w):
-    for layer in range(8):
-        print(f"sband {dtype} B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} w={w} layer={layer}",
-              flush=True)
-        q, k, v, idx, msk = case(B, H, Hkv, L, D, dtype, layer, w=w, seed=w + layer, scale=1.0,
-                                 Lq=Lq)
-        sc = scaling_for(D)
-        o, lse = elastic_attention_band(q.to(DEV), k.to(DEV), v.to(DEV),
-                                        make_pattern(L, w, layer, 8, H), sc, staged=True)
-        pi, pm = prepared_rows(idx, msk, Lq, L, L)
-        ro, rl = oracle(q, k, v, pi, pm, sc, H // Hkv)
-        assert (to_bhsd(o).float().cpu() - ro).abs().max().item() <= BF16_TOL
-        assert (lse.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
-
-
-@pytest.mark.parametrize("B,H,L,D,layer", [(1, 32, 8192, 128, 4), (8, 16, 4096, 64, 4),
-                                           (8, 16, 4096, 64, 7), (1, 32, 8192, 128, 1)])
-def test_sband_full_size(B, H, L, D, layer):
-    """The short configured shapes: every row against the band kernel and the
-    float32 per-row gather kernel, sampled rows against the oracle."""
-    q, k, v = seeded_inputs(B, H, H, L, D, torch.bfloat16, seed=2, scale=D ** -0.25)
-    sc = scaling_for(D)
-    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
-    pat = make_pattern(L, 64, layer, 8, H)
-    o, lse = elastic_attention_band(qd, kd, vd, pat, sc, staged=True)
-    ob, lb = elastic_attention_band(qd, kd, vd, pat, sc)
-    assert (o.float() - ob.float()).abs().max().item() <= 4e-3
-    assert (lse - lb).abs().max().item() <= 1e-4
-    og, lg = elastic_attention_rows(qd.float(), kd.float(), vd.float(), pat, sc)
-    assert (o.float() - og).abs().max().item() <= BF16_TOL
-    assert (lse - lg).abs().max().item() <= BF16_LSE_TOL
-    rows = torch.randint(0, L, (96,), generator=torch.Generator().manual_seed(1)).unique()
-    idx, msk = elastic_indices(L, layer, 8, H, 64)
-    ro, rl = oracle(q[:1], k[:1], v[:1], idx, msk, sc, 1, rows)
-    assert (to_bhsd(o)[:1, :, rows.to(DEV)].float().cpu() - ro).abs().max().item() <= BF16_TOL
-
-
 def test_band_rejects_unsupported():
     q = torch.zeros(1, 2, 64, 128, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(RuntimeError):
