@@ -42,11 +42,11 @@ Differences from the reference, all deliberate:
   counter-based hash seeded from torch's generator, not torch's own random
   stream, so the mask differs from torch.dropout's draw for the same seed.
 * Every path backpropagates, deterministically (no atomics on the
-  gradients): bf16 prefill with head_dim 64 or 128 through hand-written MFMA
-  kernels (band-gathered or block-sparse like the forward); the others
-  (decode rows, float32, float16, other head dims, dropout, explicit index
-  lists) through the gather backward (row pass, stable key sort, key-major
-  pass).
+  gradients): bf16 or fp16 prefill with head_dim 64 or 128 through
+  hand-written MFMA kernels (band-gathered or block-sparse like the
+  forward); the others (decode rows, float32, other head dims, dropout,
+  explicit index lists) through the gather backward (row pass, stable key
+  sort, key-major pass).
 * A query row with no valid entry (impossible for the elastic pattern, only
   reachable through explicit masks) gives output 0 rather than NaN.
 * A cache_position on the device is not range-checked on the host (that
@@ -373,8 +373,8 @@ def bwd_kernels(layout: ElasticLayout, q_len: int, batch: int, head_dim: int
 
 def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           layout: ElasticLayout, scaling: float, return_lse: bool = True,
-                          out: Optional[torch.Tensor] = None, key_block: int = 32,
-                          query_block: int = 64, kernel: str = "auto"
+                          out: Optional[torch.Tensor] = None, key_block: Optional[int] = None,
+                          query_block: Optional[int] = None, kernel: str = "auto"
                           ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Prefill forward over the elastic pattern (query row r is position r).
 
@@ -385,11 +385,14 @@ def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     "band" the band-gathered kernel (:func:`elastic_attention_band`); "auto"
     takes the faster for the shape (:func:`prefill_kernel`).  Both agree to
     bf16 rounding.  For the tile kernel the staging unit is ``query_block``
-    x ``key_block``: by default each workgroup of two waves takes 64 query
+    x ``key_block``: (64, 32) gives each workgroup of two waves 64 query
     rows and stages K/V in 32-key blocks from the pattern's 64 x 32 layout;
     (128, 64) gives four waves 128 rows and 64-key stages (halves of 128-key
     tiles no row needs are skipped); (128, 128) stages whole 128-key tiles of
-    ``layout``.  All tile variants give the same output bit for bit.
+    ``layout``.  All tile variants give the same output bit for bit.  By
+    default (128, 64) at layer 0 (a sliding window: 1.5 staged keys per row
+    instead of 2, 4-8% faster at four of the five measured shapes) and
+    (64, 32) at the dilated layers.
     """
     _check_qkv(q, k, v)
     B, H, Lq, D = q.shape
@@ -404,6 +407,8 @@ def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
     o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
+    if query_block is None and key_block is None:
+        query_block, key_block = (128, 64) if layout.pattern.layer_idx == 0 else (64, 32)
     if (query_block, key_block) not in ((128, 64), (128, 128), (64, 32)):
         raise ValueError(f"(query_block, key_block) must be (128, 64), (128, 128) or (64, 32), "
                          f"got ({query_block}, {key_block})")
