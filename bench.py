@@ -386,7 +386,10 @@ def main() -> None:
     lay = m.layout(dev)           # 128 x 128 tiles: the declared (counted) tile
     kernel = prefill_kernel(lay, L, B, D) if args.kernel == "auto" else args.kernel
     if kernel == "tile":
-        lay.stages().schedule(L, B)   # 64 x 32 blocks: the tile kernel's staging unit
+        st = lay.stages(64, 128)      # 128 x 64 blocks: the tile kernel's staging unit
+        st.schedule(L, B)
+        if args.layer > 0:
+            st.stage_masks()          # per-stage row masks, once per pattern
     m.prefill_kernel = kernel
     torch.cuda.synchronize()
     layout_ms = (time.perf_counter() - t0) * 1e3

@@ -365,8 +365,8 @@ esa_status esa_plan_schedule(const esa_pattern* p, const int32_t* row_ptr_host, 
 }
 
 esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const int32_t* row_ptr,
-                           const int32_t* col_idx, const int32_t* items, int64_t num_items,
-                           void* stream) {
+                           const int32_t* col_idx, const uint32_t* stage_masks,
+                           const int32_t* items, int64_t num_items, void* stream) {
   esa_status s = check_fwd_common(a);
   if (s != ESA_OK) return s;
   s = check_pattern(p);
@@ -379,6 +379,9 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
   const bool rows64 = p->block_m == 64 && p->block_n == 32;
   if (!rows64 && (p->block_m != 128 || (p->block_n != 128 && p->block_n != 64)))
     return ESA_ERR_UNSUPPORTED;
+  // stage masks exist for layouts whose key blocks are the stages
+  if (stage_masks && p->block_n == 128) return ESA_ERR_UNSUPPORTED;
+  if (stage_masks && !aligned(stage_masks, 8)) return ESA_ERR_ALIGN;
   // The per-tile key masks assume strictly rising indices, which holds for
   // 0 <= alpha <= 1.
   if (p->layer_idx < 0 || p->layer_idx > std::max(p->num_hidden_layers - 1, 0))
@@ -426,6 +429,7 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
   t.scale_log2 = a->sm_scale * 1.4426950408889634f;
   t.pc = make_consts(*p);
   t.row_ptr = row_ptr; t.col_idx = col_idx; t.items = items;
+  t.smask = stage_masks;
   t.elem = a->dtype;
   return hip_status(launch_tile_fwd(t, a->head_dim, num_items, (hipStream_t)stream));
 }
@@ -639,6 +643,36 @@ esa_status esa_build_tile_masks(const esa_pattern* p, const int32_t* row_ptr,
   if (!aligned(mask_t, 4)) return ESA_ERR_ALIGN;
   return hip_status(launch_tile_masks(make_consts(*p), row_ptr, col_idx, d.nqb, q_len, mask_t,
                                       (hipStream_t)stream));
+}
+
+esa_status esa_stage_masks_size(const esa_pattern* p, const int32_t* row_ptr_host,
+                                int64_t* words) {
+  if (!p || !row_ptr_host || !words) return ESA_ERR_NULL;
+  esa_status s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  const bool ok = (p->block_m == 64 && p->block_n == 32) || (p->block_m == 128 && p->block_n == 64);
+  if (!ok) return ESA_ERR_UNSUPPORTED;
+  const LayoutDims d = dims_of(*p);
+  const int64_t tiles = row_ptr_host[(int64_t)p->num_heads * d.nqb];
+  if (tiles < 0) return ESA_ERR_SHAPE;
+  *words = tiles * p->block_m * (p->block_n / 32);
+  return ESA_OK;
+}
+
+esa_status esa_build_stage_masks(const esa_pattern* p, const int32_t* row_ptr,
+                                 const int32_t* col_idx, const int32_t* row_ptr_host,
+                                 uint32_t* masks, int64_t capacity_words, void* stream) {
+  int64_t need = 0;
+  esa_status s = esa_stage_masks_size(p, row_ptr_host, &need);
+  if (s != ESA_OK) return s;
+  if (!row_ptr || !col_idx || !masks) return ESA_ERR_NULL;
+  if (p->layer_idx < 0 || p->layer_idx > std::max(p->num_hidden_layers - 1, 0))
+    return ESA_ERR_UNSUPPORTED;
+  if (capacity_words < need) return ESA_ERR_CAPACITY;
+  if (!aligned(masks, 8)) return ESA_ERR_ALIGN;
+  if (need == 0) return ESA_OK;
+  return hip_status(launch_stage_masks(make_consts(*p), dims_of(*p), row_ptr, col_idx, masks,
+                                       (hipStream_t)stream));
 }
 
 // The band dK/dV's split at the last layer of a pattern (alpha = 1): entry 0

@@ -76,7 +76,13 @@ struct TileCfg {
 // (the second launch bound is the minimum number of waves per SIMD: two,
 // so at most 256 VGPRs; LDS then allows two 128-row or four 64-row
 // workgroups per CU)
-template <int D, int BMQ, Elem E>
+//
+// PRE: each row's valid keys per stage come from A.smask (written once per
+// layout by stage_mask_kernel: the same bits the walk below computes, for a
+// layout whose stages are its key blocks), one load per stage instead of
+// the index walk, which at dilated layers costs about a third of the
+// kernel's VALU work and is the same for every batch element.
+template <int D, int BMQ, Elem E, bool PRE>
 __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
   using C = TileCfg<D, BMQ>;
   // stage buffers (HALF rows x D, rows unpadded, chunks swizzled); separate
@@ -114,7 +120,7 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
 
   // ---- this row's index list
   RowWalker walk;
-  walk.init(A.pc, h, i, row_ok);
+  if constexpr (!PRE) walk.init(A.pc, h, i, row_ok);
 
   // ---- staging: buffer resources over this (batch, kv head)'s rows; keys at
   // or past kv_len are outside num_records and load as zeros (the host keeps
@@ -159,11 +165,28 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
     }
   };
 
+  // PRE: this row's mask words of stages st (and st + 1 if has_b) -> mb;
+  // zeros for rows past q_len, as the walk gives them
+  const int64_t mrow = (int64_t)(wave * 32 + l32) * C::NB;
+  auto load_masks = [&](int st, bool has_b, uint32_t (&mb)[2 * C::NB]) {
+    const uint32_t* m0 = A.smask + (int64_t)st * (C::BM * C::NB) + mrow;
+#pragma unroll
+    for (int j = 0; j < C::NB; ++j) {
+      mb[j] = row_ok ? m0[j] : 0u;
+      mb[C::NB + j] = row_ok && has_b ? m0[C::BM * C::NB + j] : 0u;
+    }
+  };
+  uint32_t mnext[2 * C::NB];
+  if constexpr (PRE) {
+    if (s0 < s1) load_masks(s0, s0 + 1 < s1, mnext);
+  }
+
   // ---- two stage buffers, one stage ahead: each barrier retires every
   // wave's reads of the other buffer before the next stage is loaded into it.
   // Stages go in pairs (buffer 0, buffer 1); this row's valid keys of both
-  // are walked first.  The next two stage keys are read together at the top
-  // of a pair (clamped indices: unconditional scalar loads, one wait).
+  // are walked first (or, with PRE, were loaded during the previous pair).
+  // The next two stage keys are read together at the top of a pair (clamped
+  // indices: unconditional scalar loads, one wait).
   int ka = s0 < s1 ? stage_key0(s0) : 0;
   if (s0 < s1) issue(ka, k_st0, v_st0);
   for (int st = s0; st < s1; st += 2) {
@@ -171,11 +194,21 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
     const int kb = stage_key0(min(st + 1, s1 - 1));
     const int kc = stage_key0(min(st + 2, s1 - 1));
     uint32_t mb[2 * C::NB];
-    walk.stage_pair<C::NB>(ka, kb, has_b, mb);
+    if constexpr (PRE) {
+#pragma unroll
+      for (int j = 0; j < 2 * C::NB; ++j) mb[j] = mnext[j];
+    } else {
+      walk.stage_pair<C::NB>(ka, kb, has_b, mb);
+    }
 
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
     if (has_b) issue(kb, k_st1, v_st1);
+    // the next pair's masks, in flight during this pair's blocks (the waits
+    // above the next barriers cover them)
+    if constexpr (PRE) {
+      if (has_c) load_masks(st + 2, st + 3 < s1, mnext);
+    }
 #pragma unroll
     for (int j = 0; j < C::NB; ++j) block(k_st0, v_st0, j, mb[j]);
     if (!has_b) break;
@@ -193,19 +226,65 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
              A.lse ? A.lse + (int64_t)b * A.lsb + (int64_t)h * A.lsh + i : nullptr, row_ok);
 }
 
-template <Elem E>
-void launch_tile_elem(const TileArgs& a, int head_dim, dim3 grid, hipStream_t stream) {
+template <Elem E, bool PRE>
+void launch_tile_pre(const TileArgs& a, int head_dim, dim3 grid, hipStream_t stream) {
   if (a.rows64) {
     if (head_dim == 128)
-      tile_fwd_kernel<128, 64, E><<<grid, 128, 0, stream>>>(a);
+      tile_fwd_kernel<128, 64, E, PRE><<<grid, 128, 0, stream>>>(a);
     else
-      tile_fwd_kernel<64, 64, E><<<grid, 128, 0, stream>>>(a);
+      tile_fwd_kernel<64, 64, E, PRE><<<grid, 128, 0, stream>>>(a);
   } else {
     if (head_dim == 128)
-      tile_fwd_kernel<128, 128, E><<<grid, 256, 0, stream>>>(a);
+      tile_fwd_kernel<128, 128, E, PRE><<<grid, 256, 0, stream>>>(a);
     else
-      tile_fwd_kernel<64, 128, E><<<grid, 256, 0, stream>>>(a);
+      tile_fwd_kernel<64, 128, E, PRE><<<grid, 256, 0, stream>>>(a);
   }
+}
+
+template <Elem E>
+void launch_tile_elem(const TileArgs& a, int head_dim, dim3 grid, hipStream_t stream) {
+  if (a.smask)
+    launch_tile_pre<E, true>(a, head_dim, grid, stream);
+  else
+    launch_tile_pre<E, false>(a, head_dim, grid, stream);
+}
+
+// One workgroup per (head, query block) of a 64 x 32 or 128 x 64 layout, one
+// lane per query row: each lane walks its row's index list through the
+// block's stages (the key blocks col_idx lists, ascending) as the forward
+// does and stores the valid-key bits, word q of stage st for row r at
+// masks[(st * BMQ + r) * NW + q].  Rows past the pattern get zeros.
+template <int BMQ, int NW>
+__global__ __launch_bounds__(BMQ) void stage_mask_kernel(PatternConsts pc, int nqb, int seq_len,
+                                                         int log_bn, const int32_t* row_ptr,
+                                                         const int32_t* col_idx,
+                                                         uint32_t* masks) {
+  const int item = blockIdx.x;  // h * nqb + qb
+  const int h = item / nqb, qb = item % nqb;
+  const int r = threadIdx.x, i = qb * BMQ + r;
+  RowWalker walk;
+  walk.init(pc, h, i, i < seq_len);
+  const int s0 = row_ptr[item], s1 = row_ptr[item + 1];
+  for (int st = s0; st < s1; ++st) {
+    uint32_t mb[NW];
+    walk.span<NW>(col_idx[st] << log_bn, mb);
+#pragma unroll
+    for (int q = 0; q < NW; ++q) masks[((int64_t)st * BMQ + r) * NW + q] = mb[q];
+  }
+}
+
+hipError_t launch_stage_masks(const PatternConsts& pc, const LayoutDims& ld, const int32_t* row_ptr,
+                              const int32_t* col_idx, uint32_t* masks, hipStream_t stream) {
+  const int64_t items = (int64_t)pc.H * ld.nqb;
+  if (items <= 0) return hipSuccess;
+  dim3 grid((unsigned)items);
+  if (ld.bm == 64)
+    stage_mask_kernel<64, 1><<<grid, 64, 0, stream>>>(pc, ld.nqb, ld.seq_len, 5, row_ptr, col_idx,
+                                                       masks);
+  else
+    stage_mask_kernel<128, 2><<<grid, 128, 0, stream>>>(pc, ld.nqb, ld.seq_len, 6, row_ptr,
+                                                         col_idx, masks);
+  return hipGetLastError();
 }
 
 hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,

@@ -68,6 +68,11 @@ logger = logging.getLogger(__name__)
 
 BLOCK_M = 128
 BLOCK_N = 128
+# Largest per-stage row masks (bytes) a stage layout keeps for the tile
+# forward: 4 bytes per (stage, row), about 8 MB at B=8 H=16 L=4096 layer 4,
+# 63 MB at H=32 L=8192 layer 3; longer sequences (where the band kernel runs)
+# fall back to the in-kernel walk.
+STAGE_MASK_BUDGET = 256 << 20
 
 __all__ = [
     "ElasticSparseAttention",
@@ -189,6 +194,7 @@ class ElasticLayout:
         self._bwd_plans: Dict[Tuple[int, int, int], Tuple[torch.Tensor, ...]] = {}
         self._masks: Dict[int, torch.Tensor] = {}
         self._stages: Dict[Tuple[int, int], "ElasticLayout"] = {}
+        self._stage_masks = None  # tensor, False (none: 128 x 128 or over budget), or unbuilt
 
     def stages(self, block_n: int = 32, block_m: Optional[int] = 64) -> "ElasticLayout":
         """The same pattern's layout at ``block_m`` x ``block_n`` blocks, the
@@ -208,6 +214,35 @@ class ElasticLayout:
                              p.num_heads, block_m, block_n), self.device)
             self._stages[(block_m, block_n)] = got
         return got
+
+    def stage_masks(self) -> Optional[torch.Tensor]:
+        """This stage layout's per-stage row masks (esa_build_stage_masks),
+        built once and cached, for the tile forward to load instead of walking
+        each row's index list per stage; None for a 128 x 128 layout or when
+        they would exceed STAGE_MASK_BUDGET bytes (then the kernel walks)."""
+        if self._stage_masks is False:
+            return None
+        if self._stage_masks is not None:
+            return self._stage_masks
+        p = self.pattern
+        if (p.block_m, p.block_n) not in ((64, 32), (128, 64)):
+            self._stage_masks = False
+            return None
+        lib = load()
+        words = ctypes.c_int64()
+        rp = ctypes.c_void_p(self.row_ptr_host.data_ptr())
+        check(lib.esa_stage_masks_size(ctypes.byref(p), rp, ctypes.byref(words)),
+              "esa_stage_masks_size")
+        if words.value * 4 > STAGE_MASK_BUDGET:
+            self._stage_masks = False
+            return None
+        masks = torch.empty(max(2, words.value), dtype=torch.int32, device=self.device)
+        check(lib.esa_build_stage_masks(ctypes.byref(p), ctypes.c_void_p(self.row_ptr.data_ptr()),
+                                        ctypes.c_void_p(self.col_idx.data_ptr()), rp,
+                                        ctypes.c_void_p(masks.data_ptr()), masks.numel(),
+                                        _stream(self.device)), "esa_build_stage_masks")
+        self._stage_masks = masks
+        return masks
 
     def tiles_for(self, q_len: int) -> int:
         """Active tiles over the query blocks a q_len-row prefill visits,
@@ -343,38 +378,55 @@ def _check_qkv(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
 # input types the MFMA prefill kernels take (others run the per-row gather)
 MFMA_DTYPES = (torch.bfloat16, torch.float16)
 
-# Measured crossover (MI355X) between the two prefill kernels: the band
-# kernel costs about the same per 16-row group at every layer, the tile
-# kernel about the same per staged 64 x 32 block, and the band kernel is the
-# faster one once a group's rows stage more than this many blocks.
-BAND_CROSSOVER = {128: 16.5, 64: 12.5}
+# Measured crossovers (MI355X) between the band and the tile kernels: the
+# band kernels cost about the same per 16-row group at every layer, the tile
+# kernels about the same per staged 64 x 32 block, and the band kernel is the
+# faster one once a group's rows stage more than this many blocks.  Forward
+# (tile kernel with per-stage masks, 128 x 64 stages), over every dilated
+# layer of B=1 H=32 L=8192 and 16384, B=4 H=32 L=4096, B=8 H=16 L=4096 and
+# B=2 H=16 L=16384: at D = 128 the tile kernel is faster up to 14.4 blocks
+# per group, the band kernel from 21.8; in between, interleaved same-process
+# runs put the band kernel 3.5% ahead at 18.7 (L=8192 layer 4) and the tile
+# kernel 3% ahead at 19.0 (L=16384 layer 2).  At D = 64 the tile kernel is
+# faster up to 14.0 (L=4096 layer 6, by 1%), the band kernel from 15.5 (by
+# 6%).  Backward (both halves of a kind): between 14.4 and 18.7 at D = 128,
+# 11.9 and 14.0 at D = 64.
+BAND_CROSSOVER = {128: 18.5, 64: 14.75}
+BWD_BAND_CROSSOVER = {128: 16.5, 64: 12.5}
+
+
+def _band_beats_tile(layout: ElasticLayout, q_len: int, batch: int, head_dim: int,
+                     crossover: Dict[int, float]) -> bool:
+    p = layout.pattern
+    if p.attention_length > 64 or head_dim not in crossover or p.seq_len >= (1 << 24):
+        return False  # the band kernels need attention_length <= 64 and kv_len < 2^24
+    groups = batch * p.num_heads * ((q_len + 15) // 16)
+    staged = batch * layout.stages().tiles_for(q_len)
+    return staged > crossover[head_dim] * groups
 
 
 def prefill_kernel(layout: ElasticLayout, q_len: int, batch: int, head_dim: int) -> str:
     """"band" or "tile": the faster prefill kernel for this pattern and shape
     (the band kernel needs attention_length <= 64 and kv_len < 2^24)."""
-    p = layout.pattern
-    if p.attention_length > 64 or head_dim not in BAND_CROSSOVER or p.seq_len >= (1 << 24):
-        return "tile"
-    groups = batch * p.num_heads * ((q_len + 15) // 16)
-    staged = batch * layout.stages().tiles_for(q_len)
-    return "band" if staged > BAND_CROSSOVER[head_dim] * groups else "tile"
+    return "band" if _band_beats_tile(layout, q_len, batch, head_dim, BAND_CROSSOVER) else "tile"
 
 
 def bwd_kernels(layout: ElasticLayout, q_len: int, batch: int, head_dim: int
                 ) -> Tuple[str, str]:
     """("band" | "tile", "band" | "tile"): the faster dQ and dK/dV kernels for
-    this pattern and shape.  Both follow the forward's choice: over every
-    layer of six shapes (D = 64 and 128, GQA included) the fastest pair was
-    the forward's kind for both halves or within 1% of it."""
-    kind = prefill_kernel(layout, q_len, batch, head_dim)
+    this pattern and shape.  Both halves are of one kind: over every layer of
+    six shapes (D = 64 and 128, GQA included) the fastest pair was one kind
+    for both halves or within 1% of it, switching at BWD_BAND_CROSSOVER."""
+    band = _band_beats_tile(layout, q_len, batch, head_dim, BWD_BAND_CROSSOVER)
+    kind = "band" if band else "tile"
     return kind, kind
 
 
 def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           layout: ElasticLayout, scaling: float, return_lse: bool = True,
                           out: Optional[torch.Tensor] = None, key_block: Optional[int] = None,
-                          query_block: Optional[int] = None, kernel: str = "auto"
+                          query_block: Optional[int] = None, kernel: str = "auto",
+                          stage_masks: bool = True
                           ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Prefill forward over the elastic pattern (query row r is position r).
 
@@ -390,9 +442,15 @@ def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     (128, 64) gives four waves 128 rows and 64-key stages (halves of 128-key
     tiles no row needs are skipped); (128, 128) stages whole 128-key tiles of
     ``layout``.  All tile variants give the same output bit for bit.  By
-    default (128, 64) at layer 0 (a sliding window: 1.5 staged keys per row
-    instead of 2, 4-8% faster at four of the five measured shapes) and
-    (64, 32) at the dilated layers.
+    default (128, 64): at layer 0 (a sliding window) 1.5 staged keys per row
+    instead of 2, 4-8% faster at four of the five measured shapes; at the
+    dilated layers, with per-stage masks, 2-11% faster than (64, 32) at every
+    shape and layer where the tile kernel is the faster prefill kernel.
+    ``stage_masks``: at dilated layers the
+    kernel loads each row's valid keys per stage from masks built once per
+    layout (:meth:`ElasticLayout.stage_masks`, within STAGE_MASK_BUDGET)
+    instead of walking the row's index list; the output is the same bit for
+    bit.
     """
     _check_qkv(q, k, v)
     B, H, Lq, D = q.shape
@@ -408,17 +466,20 @@ def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
     if query_block is None and key_block is None:
-        query_block, key_block = (128, 64) if layout.pattern.layer_idx == 0 else (64, 32)
+        query_block, key_block = 128, 64
     if (query_block, key_block) not in ((128, 64), (128, 128), (64, 32)):
         raise ValueError(f"(query_block, key_block) must be (128, 64), (128, 128) or (64, 32), "
                          f"got ({query_block}, {key_block})")
     st = layout if (query_block, key_block) == (128, 128) else layout.stages(key_block,
                                                                              query_block)
     items, n = st.schedule(Lq, B)
+    # layer 0 rows are contiguous runs: the kernel sets them without a walk
+    masks = st.stage_masks() if stage_masks and st.pattern.layer_idx > 0 else None
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
     check(load().esa_elastic_fwd(ctypes.byref(a), ctypes.byref(st.pattern),
                                  ctypes.c_void_p(st.row_ptr.data_ptr()),
                                  ctypes.c_void_p(st.col_idx.data_ptr()),
+                                 ctypes.c_void_p(masks.data_ptr() if masks is not None else None),
                                  ctypes.c_void_p(items.data_ptr()), n, _stream(q.device)),
           "esa_elastic_fwd")
     return o, lse

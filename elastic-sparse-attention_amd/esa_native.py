@@ -28,7 +28,8 @@ ESA_F16 = 2
 
 EXPORTED = (
     "esa_status_string", "esa_version", "esa_layout_sizes", "esa_build_indices",
-    "esa_build_layout", "esa_plan_schedule", "esa_elastic_fwd", "esa_elastic_fwd_band",
+    "esa_build_layout", "esa_plan_schedule", "esa_elastic_fwd", "esa_stage_masks_size",
+    "esa_build_stage_masks", "esa_elastic_fwd_band",
     "esa_elastic_fwd_rows",
     "esa_sparse_fwd", "esa_plan_bwd", "esa_build_tile_masks", "esa_bwd_workspace_size",
     "esa_elastic_bwd", "esa_elastic_bwd_noalloc", "esa_bwd_noalloc_max_workspace",
@@ -133,7 +134,12 @@ def load() -> ctypes.CDLL:
     lib.esa_plan_schedule.argtypes = [P(EsaPattern), vp, ctypes.c_int32, ctypes.c_int32, vp,
                                       ctypes.c_int64, P(ctypes.c_int64)]
     lib.esa_elastic_fwd.restype = st
-    lib.esa_elastic_fwd.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp, vp, vp, ctypes.c_int64, vp]
+    lib.esa_elastic_fwd.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp, vp, vp, vp, ctypes.c_int64,
+                                    vp]
+    lib.esa_stage_masks_size.restype = st
+    lib.esa_stage_masks_size.argtypes = [P(EsaPattern), vp, P(ctypes.c_int64)]
+    lib.esa_build_stage_masks.restype = st
+    lib.esa_build_stage_masks.argtypes = [P(EsaPattern), vp, vp, vp, vp, ctypes.c_int64, vp]
     lib.esa_elastic_fwd_band.restype = st
     lib.esa_elastic_fwd_band.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp]
     lib.esa_elastic_fwd_rows.restype = st

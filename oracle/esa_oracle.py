@@ -146,8 +146,8 @@ def block_layout(indices: torch.Tensor, mask: torch.Tensor, bm: int, bn: int
 
     A tile ``kb`` is active for query block ``qb`` of head ``h`` when some row
     ``i`` in ``[qb*bm, (qb+1)*bm)`` has a valid entry with ``idx // bn == kb``.
-    Returns ``row_ptr`` int32 ``[H, nqb + 1]`` (offsets into one flat
-    ``col_idx``, rows ordered head-major) and ``col_idx`` int32, sorted
+    Returns ``row_ptr`` int32 ``[H * nqb + 1]`` (offsets into one flat
+    ``col_idx``, rows ordered ``h * nqb + qb``) and ``col_idx`` int32, sorted
     ascending within each row.
     """
     H, L, w = indices.shape

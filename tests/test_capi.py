@@ -95,8 +95,9 @@ def test_forward_entry_points_reject_bad_arguments():
     fake = ctypes.c_void_p(4096)
     n = 4 * 2
 
-    def call(a, pp=p, items=n):
-        return lib.esa_elastic_fwd(ctypes.byref(a), ctypes.byref(pp), fake, fake, fake, items, None)
+    def call(a, pp=p, items=n, masks=None):
+        return lib.esa_elastic_fwd(ctypes.byref(a), ctypes.byref(pp), fake, fake, masks, fake,
+                                   items, None)
 
     a = fwd_args()
     a.q = None
@@ -119,6 +120,10 @@ def test_forward_entry_points_reject_bad_arguments():
         a.sm_scale = bad_scale
         assert call(a) == en.ESA_ERR_UNSUPPORTED
     assert call(fwd_args(), pp=pat(L=1024, H=4, layer=9)) == en.ESA_ERR_UNSUPPORTED
+    # stage masks: not for 128 x 128 layouts; 8-byte aligned
+    assert call(fwd_args(), masks=fake) == en.ESA_ERR_UNSUPPORTED
+    assert call(fwd_args(), pp=pat(L=1024, H=4, bm=64, bn=32), items=4 * 16,
+                masks=ctypes.c_void_p(4100)) == en.ESA_ERR_ALIGN
 
     assert lib.esa_elastic_fwd_rows(ctypes.byref(fwd_args(D=258)), ctypes.byref(p), None, None) \
         == en.ESA_ERR_UNSUPPORTED
@@ -189,6 +194,34 @@ def test_plan_schedule_xcd_runs(L, Lq, B, H, layer):
     for run in runs:
         c = sum(cost(x) for x in run if x >= 0)
         assert c <= total / 8 + biggest + 1
+
+
+@pytest.mark.parametrize("bm,bn", [(64, 32), (128, 64)])
+def test_stage_masks_size_and_rejects(bm, bn):
+    """Stage-mask words = tiles of the layout x block_m x block_n / 32, from
+    the host row_ptr (here the oracle's layout of the same pattern)."""
+    lib = en.load()
+    L, H, layer = 1000, 3, 5
+    p = pat(L=L, H=H, layer=layer, bm=bm, bn=bn)
+    idx, msk = elastic_indices(L, layer, 8, H, 64)
+    rp, _ = block_layout(idx, msk, bm, bn)
+    rph = rp.reshape(-1).to(torch.int32).contiguous()
+    assert rph.numel() == H * ((L + bm - 1) // bm) + 1
+    words = ctypes.c_int64()
+    assert lib.esa_stage_masks_size(ctypes.byref(p), ctypes.c_void_p(rph.data_ptr()),
+                                    ctypes.byref(words)) == en.ESA_OK
+    assert words.value == int(rph[-1]) * bm * (bn // 32) > 0
+    fake = ctypes.c_void_p(4096)
+    rpp = ctypes.c_void_p(rph.data_ptr())
+    assert lib.esa_build_stage_masks(ctypes.byref(p), fake, fake, rpp, fake, words.value - 1,
+                                     None) == en.ESA_ERR_CAPACITY
+    assert lib.esa_build_stage_masks(ctypes.byref(p), fake, fake, rpp, ctypes.c_void_p(4100),
+                                     words.value, None) == en.ESA_ERR_ALIGN
+    assert lib.esa_build_stage_masks(ctypes.byref(p), None, fake, rpp, fake, words.value,
+                                     None) == en.ESA_ERR_NULL
+    p128 = pat(L=L, H=H, layer=layer)
+    assert lib.esa_stage_masks_size(ctypes.byref(p128), rpp, ctypes.byref(words)) \
+        == en.ESA_ERR_UNSUPPORTED
 
 
 def test_plan_schedule_rejects():

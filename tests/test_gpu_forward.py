@@ -16,7 +16,7 @@ from esa_oracle import (elastic_indices, forward_fp32, prepared_rows, scaling_fo
                         seeded_inputs)
 from elastic_sparse_attention import (ElasticLayout, ElasticSparseAttention,
                                       ElasticSparseAttentionFunction, elastic_attention_band,
-                                      elastic_attention_fwd, prefill_kernel,
+                                      elastic_attention_fwd, prefill_kernel, bwd_kernels,
                                       elastic_attention_rows, make_pattern,
                                       sparse_attention_fwd)
 
@@ -160,6 +160,69 @@ def full_size_check(B, H, L, D, layer, scale, outlier, seed, n_rows=384, band=Fa
     assert e_o <= BF16_TOL and e_l <= BF16_LSE_TOL
 
 
+@pytest.mark.parametrize("bm,bn", [(64, 32), (128, 64)])
+@pytest.mark.parametrize("L,H,layer,w", [(1000, 3, 5, 64), (777, 4, 7, 64), (513, 2, 2, 100),
+                                         (300, 5, 1, 16)])
+def test_stage_masks_match_oracle(bm, bn, L, H, layer, w):
+    """esa_build_stage_masks: word q of stage st for row r holds exactly the
+    row's valid keys (oracle index sets) among the stage's keys."""
+    print(f"stage masks bm={bm} bn={bn} L={L} H={H} layer={layer} w={w}", flush=True)
+    lay = ElasticLayout(make_pattern(L, w, layer, 8, H), DEV).stages(bn, bm)
+    masks = lay.stage_masks()
+    assert masks is not None
+    nw = bn // 32
+    got = masks.cpu()[:lay.num_tiles * bm * nw].view(lay.num_tiles, bm, nw).to(torch.int64)
+    got = got & 0xFFFFFFFF
+    idx, msk = elastic_indices(L, layer, 8, H, w)
+    rp = lay.row_ptr_host.view(-1)
+    ci = lay.col_idx[:lay.num_tiles].cpu().to(torch.int64)
+    nqb = (L + bm - 1) // bm
+    want = torch.zeros(lay.num_tiles, bm, nw, dtype=torch.int64)
+    weights = (1 << torch.arange(32, dtype=torch.int64))
+    for h in range(H):
+        for qb in range(nqb):
+            s0, s1 = int(rp[h * nqb + qb]), int(rp[h * nqb + qb + 1])
+            if s0 == s1:
+                continue
+            rows = torch.arange(qb * bm, min((qb + 1) * bm, L))
+            keys, ok = idx[h, rows], msk[h, rows].bool()               # [R, w]
+            rel = keys.unsqueeze(0) - (ci[s0:s1] * bn).view(-1, 1, 1)   # [S, R, w]
+            inr = ok.unsqueeze(0) & (rel >= 0) & (rel < bn)
+            hit = torch.zeros(s1 - s0, len(rows), bn, dtype=torch.bool)
+            si, ri, ei = torch.nonzero(inr, as_tuple=True)
+            hit[si, ri, rel[si, ri, ei]] = True
+            words = (hit.view(s1 - s0, len(rows), nw, 32).to(torch.int64) * weights).sum(-1)
+            want[s0:s1, :len(rows)] = words
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,H,Hkv,L,Lq,D", [(2, 4, 2, 1000, 937, 64), (1, 8, 8, 2048, 2048, 128),
+                                           (3, 2, 1, 777, 700, 128)])
+def test_tile_stage_masks_bit_identical(dtype, B, H, Hkv, L, Lq, D):
+    """The tile forward with per-stage masks loaded gives the same bits as
+    with the in-kernel index walk, for both staging shapes and every
+    dilated layer; and meets the oracle."""
+    for layer in range(1, 8):
+        print(f"tile masks {dtype} B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} layer={layer}",
+              flush=True)
+        q, k, v, idx, msk = case(B, H, Hkv, L, D, dtype, layer, seed=layer + 5, Lq=Lq)
+        qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+        lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+        sc = scaling_for(D)
+        for qbk in ((64, 32), (128, 64)):
+            assert lay.stages(qbk[1], qbk[0]).stage_masks() is not None
+            o1, l1 = elastic_attention_fwd(qd, kd, vd, lay, sc, kernel="tile", query_block=qbk[0],
+                                           key_block=qbk[1], stage_masks=True)
+            o0, l0 = elastic_attention_fwd(qd, kd, vd, lay, sc, kernel="tile", query_block=qbk[0],
+                                           key_block=qbk[1], stage_masks=False)
+            assert torch.equal(o1, o0) and torch.equal(l1, l0)
+        pi, pm = prepared_rows(idx, msk, Lq, L, L)
+        ro, rl = oracle(q, k, v, pi, pm, sc, H // Hkv)
+        assert (to_bhsd(o1).float().cpu() - ro).abs().max().item() <= BF16_TOL
+        assert (l1.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
+
+
 @pytest.mark.parametrize("B,H,Hkv,L,Lq,D,layer", [
     (1, 8, 8, 4096, 4096, 128, 4), (1, 8, 8, 4096, 4096, 128, 7), (1, 8, 8, 4096, 4096, 128, 0),
     (2, 8, 2, 3000, 2500, 64, 5), (1, 4, 4, 1000, 1000, 128, 1),
@@ -257,15 +320,19 @@ def test_band_sharp_softmax_outliers():
     assert (lse.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
 
 
-@pytest.mark.parametrize("L,H,B,D,layer,want", [
-    (32768, 32, 1, 128, 4, "band"), (32768, 32, 1, 128, 0, "tile"), (8192, 32, 1, 128, 3, "tile"),
-    (8192, 32, 1, 128, 4, "band"), (4096, 16, 8, 64, 5, "tile"), (4096, 16, 8, 64, 6, "band"),
+@pytest.mark.parametrize("L,H,B,D,layer,want,want_bwd", [
+    (32768, 32, 1, 128, 4, "band", "band"), (32768, 32, 1, 128, 0, "tile", "tile"),
+    (8192, 32, 1, 128, 3, "tile", "tile"), (8192, 32, 1, 128, 4, "band", "band"),
+    (4096, 32, 4, 128, 7, "tile", "tile"),
+    (8192, 32, 1, 128, 5, "band", "band"), (4096, 16, 8, 64, 6, "tile", "band"),
+    (4096, 16, 8, 64, 7, "band", "band"), (4096, 16, 8, 64, 4, "tile", "tile"),
 ])
-def test_prefill_kernel_choice(L, H, B, D, layer, want):
-    # the measured crossover: the band kernel where a group's rows stage many
-    # 64 x 32 blocks, the tile kernel where they stage few
+def test_prefill_kernel_choice(L, H, B, D, layer, want, want_bwd):
+    # the measured crossovers: the band kernels where a group's rows stage
+    # many 64 x 32 blocks, the tile kernels where they stage few
     lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
     assert prefill_kernel(lay, L, B, D) == want
+    assert bwd_kernels(lay, L, B, D) == (want_bwd, want_bwd)
 
 
 def test_band_rejects_unsupported():
