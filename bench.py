@@ -389,7 +389,7 @@ def main() -> None:
         st = lay.stages(64, 128)      # 128 x 64 blocks: the tile kernel's staging unit
         st.schedule(L, B)
         if args.layer > 0:
-            st.stage_masks(D)         # per-stage masks, once per pattern
+            st.stage_masks()          # per-stage row masks, once per pattern
     m.prefill_kernel = kernel
     torch.cuda.synchronize()
     layout_ms = (time.perf_counter() - t0) * 1e3

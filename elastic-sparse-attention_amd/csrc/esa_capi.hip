@@ -646,27 +646,24 @@ esa_status esa_build_tile_masks(const esa_pattern* p, const int32_t* row_ptr,
 }
 
 esa_status esa_stage_masks_size(const esa_pattern* p, const int32_t* row_ptr_host,
-                                int32_t head_dim, int64_t* words) {
+                                int64_t* words) {
   if (!p || !row_ptr_host || !words) return ESA_ERR_NULL;
   esa_status s = check_pattern(p);
   if (s != ESA_OK) return s;
   const bool ok = (p->block_m == 64 && p->block_n == 32) || (p->block_m == 128 && p->block_n == 64);
-  if (!ok || (head_dim != 64 && head_dim != 128)) return ESA_ERR_UNSUPPORTED;
+  if (!ok) return ESA_ERR_UNSUPPORTED;
   const LayoutDims d = dims_of(*p);
   const int64_t tiles = row_ptr_host[(int64_t)p->num_heads * d.nqb];
   if (tiles < 0) return ESA_ERR_SHAPE;
-  // per stage: block_m x block_n / 32 words of masks, and at D = 64 (lane
-  // masks) block_m / 32 flags
-  *words = tiles * (p->block_m * (p->block_n / 32) + (head_dim == 64 ? p->block_m / 32 : 0));
+  *words = tiles * p->block_m * (p->block_n / 32);
   return ESA_OK;
 }
 
 esa_status esa_build_stage_masks(const esa_pattern* p, const int32_t* row_ptr,
                                  const int32_t* col_idx, const int32_t* row_ptr_host,
-                                 int32_t head_dim, uint32_t* masks, int64_t capacity_words,
-                                 void* stream) {
+                                 uint32_t* masks, int64_t capacity_words, void* stream) {
   int64_t need = 0;
-  esa_status s = esa_stage_masks_size(p, row_ptr_host, head_dim, &need);
+  esa_status s = esa_stage_masks_size(p, row_ptr_host, &need);
   if (s != ESA_OK) return s;
   if (!row_ptr || !col_idx || !masks) return ESA_ERR_NULL;
   if (p->layer_idx < 0 || p->layer_idx > std::max(p->num_hidden_layers - 1, 0))
@@ -675,7 +672,7 @@ esa_status esa_build_stage_masks(const esa_pattern* p, const int32_t* row_ptr,
   if (!aligned(masks, 8)) return ESA_ERR_ALIGN;
   if (need == 0) return ESA_OK;
   return hip_status(launch_stage_masks(make_consts(*p), dims_of(*p), row_ptr, col_idx, masks,
-                                       head_dim == 64, (hipStream_t)stream));
+                                       (hipStream_t)stream));
 }
 
 // The band dK/dV's split at the last layer of a pattern (alpha = 1): entry 0

@@ -77,21 +77,12 @@ struct TileCfg {
 // so at most 256 VGPRs; LDS then allows two 128-row or four 64-row
 // workgroups per CU)
 //
-// MODE: where each row's valid keys per stage come from.  kWalk: the kernel
-// walks the row's index list (float32 index sequence per entry).  With
-// per-stage masks in A.smask (written once per layout by stage_mask_kernel:
-// the bits the walk computes, for a layout whose stages are its key blocks),
-// which replace the walk (at dilated layers about a third of the kernel's
-// VALU work, the same for every batch element): kRowMasks, one word per row
-// and 32-key block, loaded a stage pair ahead into vector registers (D =
-// 128); kLaneMasks, 16 lane masks per wave and block in scalar registers,
-// which enter the accumulator with one v_cndmask per register instead of a
-// bit extract and an and (D = 64: 6-8% faster than row masks at B=8 H=16
-// L=4096; at D = 128, two waves per SIMD and scalar registers at their limit,
-// 5-10% slower).
-constexpr int kWalk = 0, kRowMasks = 1, kLaneMasks = 2;
-
-template <int D, int BMQ, Elem E, int MODE>
+// PRE: each row's valid keys per stage come from A.smask (written once per
+// layout by stage_mask_kernel: the same bits the walk below computes, for a
+// layout whose stages are its key blocks), one load per stage instead of
+// the index walk, which at dilated layers costs about a third of the
+// kernel's VALU work and is the same for every batch element.
+template <int D, int BMQ, Elem E, bool PRE>
 __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
   using C = TileCfg<D, BMQ>;
   // stage buffers (HALF rows x D, rows unpadded, chunks swizzled); separate
@@ -129,7 +120,7 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
 
   // ---- this row's index list
   RowWalker walk;
-  if constexpr (MODE == kWalk) walk.init(A.pc, h, i, row_ok);
+  if constexpr (!PRE) walk.init(A.pc, h, i, row_ok);
 
   // ---- staging: buffer resources over this (batch, kv head)'s rows; keys at
   // or past kv_len are outside num_records and load as zeros (the host keeps
@@ -174,8 +165,8 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
     }
   };
 
-  // kRowMasks: this row's mask words of stages st (and st + 1 if has_b) ->
-  // mb; zeros for rows past q_len, as the walk gives them
+  // PRE: this row's mask words of stages st (and st + 1 if has_b) -> mb;
+  // zeros for rows past q_len, as the walk gives them
   const int64_t mrow = (int64_t)(wave * 32 + l32) * C::NB;
   auto load_masks = [&](int st, bool has_b, uint32_t (&mb)[2 * C::NB]) {
     const uint32_t* m0 = A.smask + (int64_t)st * (C::BM * C::NB) + mrow;
@@ -186,41 +177,16 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
     }
   };
   uint32_t mnext[2 * C::NB];
-  if constexpr (MODE == kRowMasks) {
+  if constexpr (PRE) {
     if (s0 < s1) load_masks(s0, s0 + 1 < s1, mnext);
-  }
-
-  // kLaneMasks: per stage, the wave's 16 lane masks of each 32-key block (W x
-  // NB x 16 64-bit words) and then one flag word per wave (bit j: block j
-  // holds a valid key for some row of the wave); the flags of the next stage
-  // pair are read during this one.  Lanes of rows past q_len are cleared
-  // (okm), as the walk gives them.
-  constexpr int kStageWords = C::W * C::NB * 32 + C::W;  // 32-bit words per stage
-  const uint64_t okm = __builtin_amdgcn_ballot_w64(row_ok);
-  auto flags_of = [&](int st) {
-    return ((cptr_i32)A.smask)[(int64_t)st * kStageWords + C::W * C::NB * 32 + wave];
-  };
-  auto block_pre = [&](const uint16_t* Kb, const uint16_t* Vb, int st, int j, int flags) {
-    if (!((flags >> j) & 1)) return;  // no row of the wave has a valid key here
-    const cptr_u64 src =
-        (cptr_u64)((cptr_i32)A.smask + (int64_t)st * kStageWords) + ((wave * C::NB + j) << 4);
-    uint64_t lm[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) lm[r] = src[r];
-    rows.block_lm(Kb, Vb, j, lm, okm);
-  };
-  int fl_a = 0, fl_b = 0;  // flags of the current stage pair
-  if constexpr (MODE == kLaneMasks) {
-    if (s0 < s1) fl_a = flags_of(s0);
-    if (s0 + 1 < s1) fl_b = flags_of(s0 + 1);
   }
 
   // ---- two stage buffers, one stage ahead: each barrier retires every
   // wave's reads of the other buffer before the next stage is loaded into it.
-  // Stages go in pairs (buffer 0, buffer 1); with kWalk this row's valid
-  // keys of both are walked first.  The next two stage keys are read together
-  // at the top of a pair (clamped indices: unconditional scalar loads, one
-  // wait).
+  // Stages go in pairs (buffer 0, buffer 1); this row's valid keys of both
+  // are walked first (or, with PRE, were loaded during the previous pair).
+  // The next two stage keys are read together at the top of a pair (clamped
+  // indices: unconditional scalar loads, one wait).
   int ka = s0 < s1 ? stage_key0(s0) : 0;
   if (s0 < s1) issue(ka, k_st0, v_st0);
   for (int st = s0; st < s1; st += 2) {
@@ -228,48 +194,31 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
     const int kb = stage_key0(min(st + 1, s1 - 1));
     const int kc = stage_key0(min(st + 2, s1 - 1));
     uint32_t mb[2 * C::NB];
-    if constexpr (MODE == kWalk) {
-      walk.stage_pair<C::NB>(ka, kb, has_b, mb);
-    } else if constexpr (MODE == kRowMasks) {
+    if constexpr (PRE) {
 #pragma unroll
       for (int j = 0; j < 2 * C::NB; ++j) mb[j] = mnext[j];
-    }
-    int fn_a = 0, fn_b = 0;  // the next pair's flags (kLaneMasks)
-    if constexpr (MODE == kLaneMasks) {
-      if (has_c) fn_a = flags_of(st + 2);
-      if (st + 3 < s1) fn_b = flags_of(st + 3);
+    } else {
+      walk.stage_pair<C::NB>(ka, kb, has_b, mb);
     }
 
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
     if (has_b) issue(kb, k_st1, v_st1);
-    // the next pair's row masks, in flight during this pair's blocks (the
-    // waits above the next barriers cover them)
-    if constexpr (MODE == kRowMasks) {
+    // the next pair's masks, in flight during this pair's blocks (the waits
+    // above the next barriers cover them)
+    if constexpr (PRE) {
       if (has_c) load_masks(st + 2, st + 3 < s1, mnext);
     }
 #pragma unroll
-    for (int j = 0; j < C::NB; ++j) {
-      if constexpr (MODE == kLaneMasks)
-        block_pre(k_st0, v_st0, st, j, fl_a);
-      else
-        block(k_st0, v_st0, j, mb[j]);
-    }
+    for (int j = 0; j < C::NB; ++j) block(k_st0, v_st0, j, mb[j]);
     if (!has_b) break;
 
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
     if (has_c) issue(kc, k_st0, v_st0);
 #pragma unroll
-    for (int j = 0; j < C::NB; ++j) {
-      if constexpr (MODE == kLaneMasks)
-        block_pre(k_st1, v_st1, st + 1, j, fl_b);
-      else
-        block(k_st1, v_st1, j, mb[C::NB + j]);
-    }
+    for (int j = 0; j < C::NB; ++j) block(k_st1, v_st1, j, mb[C::NB + j]);
     ka = kc;
-    fl_a = fn_a;
-    fl_b = fn_b;
   }
 
   // ---- epilogue: normalise and store O rows and the log-sum-exp
@@ -277,113 +226,64 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
              A.lse ? A.lse + (int64_t)b * A.lsb + (int64_t)h * A.lsh + i : nullptr, row_ok);
 }
 
-template <int D, Elem E, int MODE>
-void launch_tile_mode(const TileArgs& a, dim3 grid, hipStream_t stream) {
-  if (a.rows64)
-    tile_fwd_kernel<D, 64, E, MODE><<<grid, 128, 0, stream>>>(a);
-  else
-    tile_fwd_kernel<D, 128, E, MODE><<<grid, 256, 0, stream>>>(a);
+template <Elem E, bool PRE>
+void launch_tile_pre(const TileArgs& a, int head_dim, dim3 grid, hipStream_t stream) {
+  if (a.rows64) {
+    if (head_dim == 128)
+      tile_fwd_kernel<128, 64, E, PRE><<<grid, 128, 0, stream>>>(a);
+    else
+      tile_fwd_kernel<64, 64, E, PRE><<<grid, 128, 0, stream>>>(a);
+  } else {
+    if (head_dim == 128)
+      tile_fwd_kernel<128, 128, E, PRE><<<grid, 256, 0, stream>>>(a);
+    else
+      tile_fwd_kernel<64, 128, E, PRE><<<grid, 256, 0, stream>>>(a);
+  }
 }
 
 template <Elem E>
 void launch_tile_elem(const TileArgs& a, int head_dim, dim3 grid, hipStream_t stream) {
-  if (head_dim == 128) {
-    if (a.smask)
-      launch_tile_mode<128, E, kRowMasks>(a, grid, stream);
-    else
-      launch_tile_mode<128, E, kWalk>(a, grid, stream);
-  } else {
-    if (a.smask)
-      launch_tile_mode<64, E, kLaneMasks>(a, grid, stream);
-    else
-      launch_tile_mode<64, E, kWalk>(a, grid, stream);
-  }
+  if (a.smask)
+    launch_tile_pre<E, true>(a, head_dim, grid, stream);
+  else
+    launch_tile_pre<E, false>(a, head_dim, grid, stream);
 }
 
 // One workgroup per (head, query block) of a 64 x 32 or 128 x 64 layout, one
 // lane per query row: each lane walks its row's index list through the
 // block's stages (the key blocks col_idx lists, ascending) as the forward
-// does.  Rows past the pattern get zeros.
-// Row masks (!LANES): word q of stage st for row r at (st * BMQ + r) * NW + q.
-// Lane masks (LANES): ballots turn the rows' bits into the forward's lane
-// masks.  Per stage st, W = BMQ / 32 forward waves (rows 32 fw .. 32 fw + 31
-// of the block) and NW 32-key blocks: first W x NW x 16 64-bit masks, the one
-// for wave fw, block j and accumulator register r at 64-bit index
-// (fw * NW + j) * 16 + r with bit l set when key 8 (r / 4) + 4 (l / 32) +
-// r % 4 of the block is valid for row 32 fw + l % 32; then W 32-bit flag
-// words, bit j of wave fw's set when any of its masks of block j is nonzero.
-// A stage takes W (32 NW + 1) 32-bit words.
-template <int BMQ, int NW, bool LANES>
+// does and stores the valid-key bits, word q of stage st for row r at
+// masks[(st * BMQ + r) * NW + q].  Rows past the pattern get zeros.
+template <int BMQ, int NW>
 __global__ __launch_bounds__(BMQ) void stage_mask_kernel(PatternConsts pc, int nqb, int seq_len,
                                                          int log_bn, const int32_t* row_ptr,
                                                          const int32_t* col_idx,
                                                          uint32_t* masks) {
-  constexpr int W = BMQ / 32;
-  constexpr int kStageWords = W * NW * 32 + W;
   const int item = blockIdx.x;  // h * nqb + qb
   const int h = item / nqb, qb = item % nqb;
   const int r = threadIdx.x, i = qb * BMQ + r;
-  const int lane = r & 63, bw = r >> 6;  // builder wave bw: forward waves 2 bw, 2 bw + 1
   RowWalker walk;
   walk.init(pc, h, i, i < seq_len);
   const int s0 = row_ptr[item], s1 = row_ptr[item + 1];
   for (int st = s0; st < s1; ++st) {
     uint32_t mb[NW];
     walk.span<NW>(col_idx[st] << log_bn, mb);
-    if constexpr (!LANES) {
 #pragma unroll
-      for (int q = 0; q < NW; ++q) masks[((int64_t)st * BMQ + r) * NW + q] = mb[q];
-      continue;
-    }
-    uint32_t* base = masks + (int64_t)st * kStageWords;
-    uint32_t flag[2] = {0u, 0u};  // of forward waves 2 bw, 2 bw + 1
-#pragma unroll
-    for (int j = 0; j < NW; ++j) {
-      // lane t < 32 collects the mask of forward wave 2 bw + t / 16, register t % 16
-      uint64_t mine = 0;
-#pragma unroll
-      for (int rr = 0; rr < 16; ++rr) {
-        const int kb0 = 8 * (rr >> 2) + (rr & 3);
-        const uint64_t b0 = __builtin_amdgcn_ballot_w64((mb[j] >> kb0) & 1u);
-        const uint64_t b1 = __builtin_amdgcn_ballot_w64((mb[j] >> (kb0 + 4)) & 1u);
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          const uint64_t m = ((b0 >> (32 * s)) & 0xffffffffull) | (((b1 >> (32 * s)) << 32));
-          mine = lane == 16 * s + rr ? m : mine;
-          flag[s] |= m != 0 ? 1u << j : 0u;
-        }
-      }
-      if (lane < 32) {
-        const int fw = 2 * bw + (lane >> 4);
-        ((uint64_t*)base)[(fw * NW + j) * 16 + (lane & 15)] = mine;
-      }
-    }
-    if (lane < 2) base[W * NW * 32 + 2 * bw + lane] = lane == 0 ? flag[0] : flag[1];
+    for (int q = 0; q < NW; ++q) masks[((int64_t)st * BMQ + r) * NW + q] = mb[q];
   }
 }
 
-template <bool LANES>
-void launch_stage_masks_fmt(const PatternConsts& pc, const LayoutDims& ld, const int32_t* row_ptr,
-                            const int32_t* col_idx, uint32_t* masks, dim3 grid,
-                            hipStream_t stream) {
-  if (ld.bm == 64)
-    stage_mask_kernel<64, 1, LANES><<<grid, 64, 0, stream>>>(pc, ld.nqb, ld.seq_len, 5, row_ptr,
-                                                              col_idx, masks);
-  else
-    stage_mask_kernel<128, 2, LANES><<<grid, 128, 0, stream>>>(pc, ld.nqb, ld.seq_len, 6,
-                                                                row_ptr, col_idx, masks);
-}
-
 hipError_t launch_stage_masks(const PatternConsts& pc, const LayoutDims& ld, const int32_t* row_ptr,
-                              const int32_t* col_idx, uint32_t* masks, bool lanes,
-                              hipStream_t stream) {
+                              const int32_t* col_idx, uint32_t* masks, hipStream_t stream) {
   const int64_t items = (int64_t)pc.H * ld.nqb;
   if (items <= 0) return hipSuccess;
   dim3 grid((unsigned)items);
-  if (lanes)
-    launch_stage_masks_fmt<true>(pc, ld, row_ptr, col_idx, masks, grid, stream);
+  if (ld.bm == 64)
+    stage_mask_kernel<64, 1><<<grid, 64, 0, stream>>>(pc, ld.nqb, ld.seq_len, 5, row_ptr, col_idx,
+                                                       masks);
   else
-    launch_stage_masks_fmt<false>(pc, ld, row_ptr, col_idx, masks, grid, stream);
+    stage_mask_kernel<128, 2><<<grid, 128, 0, stream>>>(pc, ld.nqb, ld.seq_len, 6, row_ptr,
+                                                         col_idx, masks);
   return hipGetLastError();
 }
 

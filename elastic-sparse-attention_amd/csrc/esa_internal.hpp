@@ -35,9 +35,8 @@ struct TileArgs {
   const int32_t* row_ptr;
   const int32_t* col_idx;
   const int32_t* items;
-  // per-stage masks from esa_build_stage_masks (stage layouts only; the
-  // format of the head dim), or nullptr: the kernel walks each row's index
-  // list itself
+  // per-stage row masks from esa_build_stage_masks (stage layouts only), or
+  // nullptr: the kernel walks each row's index list itself
   const uint32_t* smask;
 };
 
@@ -205,12 +204,10 @@ hipError_t launch_indices(const PatternConsts& pc, int row0, int nrows, void* in
                           int elem_bytes, hipStream_t stream);
 hipError_t launch_layout(const PatternConsts& pc, const LayoutDims& ld, int32_t* row_ptr,
                          int32_t* col_idx, void* workspace, hipStream_t stream);
-// per-stage masks of a 64 x 32 or 128 x 64 layout: row masks (num_tiles x
-// block_m x block_n / 32 words) or lane masks with per-wave flags (num_tiles x
-// (block_m x block_n / 32 + block_m / 32) words)
+// per-stage row masks of a 64 x 32 or 128 x 64 layout: num_tiles x block_m x
+// (block_n / 32) words
 hipError_t launch_stage_masks(const PatternConsts& pc, const LayoutDims& ld, const int32_t* row_ptr,
-                              const int32_t* col_idx, uint32_t* masks, bool lanes,
-                              hipStream_t stream);
+                              const int32_t* col_idx, uint32_t* masks, hipStream_t stream);
 hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
                            hipStream_t stream);
 hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream);

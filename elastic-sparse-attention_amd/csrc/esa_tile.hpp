@@ -85,7 +85,6 @@ __device__ __forceinline__ bool wave_any(bool p) {
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) void lds_void;
 typedef const __attribute__((address_space(4))) int32_t* cptr_i32;
-typedef const __attribute__((address_space(4))) uint64_t* cptr_u64;
 
 // 16 bytes per lane from a buffer resource at voffset + soffset straight into
 // LDS at dst + 16 * lane (dst uniform)
@@ -209,7 +208,8 @@ struct Rows32 {
   int vaddr[ND];   // V^T operand read offsets
   f32x16 oacc[ND];
   float m_run;     // running max, log2 units (the same in both halves)
-  float l_run;     // running sum of p over this lane's half of the keys (-> lse, O)
+  float l_run;     // running sum of p over this lane's half of the keys (-> lse)
+  float n_run;     // the same sum of p rounded to the input type, as PV sees it (-> O)
   float scale;     // sm_scale * log2(e), > 0
   int hf;
 
@@ -233,6 +233,7 @@ struct Rows32 {
   __device__ __forceinline__ void reset() {
     m_run = -INFINITY;
     l_run = 0.f;
+    n_run = 0.f;
 #pragma unroll
     for (int d = 0; d < ND; ++d) oacc[d] = f32x16{};
   }
@@ -257,43 +258,18 @@ struct Rows32 {
     // p = 0 to every row: its reads, MFMAs and softmax are all skipped (O, the
     // running max and the sums are unchanged, bit for bit)
     if (!wave_any(mk != 0u)) return;
-    // the mask enters as the accumulator's initial value: 0 for a valid key,
-    // -inf for a masked one
-    step(Kb, Vb, kbl, [&](f32x16& sacc) { mask_init<0>(sacc, ~mk); }, [] {});
-  }
 
-  // The same block with the mask as 16 lane masks (scalar register pairs),
-  // for a block the caller knows holds a valid key for some row of the wave:
-  // bit l of lm[r] & okm says whether register r of lane l (key 8*(r/4) +
-  // 4*(l/32) + r%4 of the block, row l % 32) is a valid key.  One v_cndmask
-  // per register forms the initial accumulator.  The masks are first used
-  // after the K operand reads are issued, so their scalar loads and the LDS
-  // reads are in flight together.
-  __device__ __forceinline__ void block_lm(const uint16_t* Kb, const uint16_t* Vb, int kbl,
-                                           const uint64_t (&lm)[16], uint64_t okm) {
-    step(Kb, Vb, kbl, [&](f32x16& sacc) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r)
-        sacc[r] = __builtin_amdgcn_inverse_ballot_w64(lm[r] & okm) ? 0.f : -INFINITY;
-    }, [] {});
-  }
-
-  // The block's products and softmax; init sets the S^T accumulator's initial
-  // value (0 for a valid key, -inf for a masked one); after runs once the
-  // QK^T MFMAs are issued.
-  template <class Init, class After>
-  __device__ __forceinline__ void step(const uint16_t* Kb, const uint16_t* Vb, int kbl,
-                                       Init&& init, After&& after) {
     // all K operand reads first, so their LDS latency overlaps
     V8 ka[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) ka[s] = *(const V8*)(Kb + kaddr[s] + 32 * kbl * D);
+    // the mask enters as the accumulator's initial value: 0 for a valid key,
+    // -inf for a masked one
     f32x16 sacc;
-    init(sacc);
+    mask_init<0>(sacc, ~mk);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < NS; ++s) sacc = M::mfma32(ka[s], qop[s], sacc);
-    after();
     // the V^T operands of this block, read while the softmax runs
     s16x4 va[ND][4];
 #pragma unroll
@@ -326,6 +302,7 @@ struct Rows32 {
       // rows that do not grow keep alpha = 1 (m_run may still be -inf there)
       const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - (m_use + delta)) : 1.0f;
       l_run *= alpha;
+      n_run *= alpha;
 #pragma unroll
       for (int d = 0; d < ND; ++d) oacc[d] *= alpha;
       m_run = grow ? m_use + delta : m_run;
@@ -339,6 +316,9 @@ struct Rows32 {
       l_run += p0;
       l_run += p1;
       pw[q] = M::pack2(p0, p1);
+      // normalise O by the probabilities PV actually used, so a row led by
+      // one key reproduces that key's value row
+      n_run = M::dot2(pw[q], n_run);
     }
 
 #pragma unroll
@@ -353,15 +333,14 @@ struct Rows32 {
     }
   }
 
-  // Epilogue: O and lse (natural log) from the exact float32 sum of the
-  // probabilities (PV used them rounded to the input type: O is within one
-  // rounding, 2^-9 relative for bf16, of the float32 result; a row whose only
-  // key has p = 1 reproduces that key's value row exactly); rows with no
-  // valid key get O = 0 and lse = -inf.
+  // Epilogue: O normalised by the rounded probabilities PV used (a row led by
+  // one key reproduces that key's value row), lse by the exact float32 sum
+  // (natural log); rows with no valid key get O = 0 and lse = -inf.
   __device__ __forceinline__ void store(uint16_t* orow, float* lse, bool row_ok) {
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float n_tot = n_run + __shfl_xor(n_run, 32, 64);
     if (!row_ok) return;
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const float inv = n_tot > 0.f ? 1.f / n_tot : 0.f;
 #pragma unroll
     for (int d = 0; d < ND; ++d) {
 #pragma unroll

@@ -194,8 +194,7 @@ class ElasticLayout:
         self._bwd_plans: Dict[Tuple[int, int, int], Tuple[torch.Tensor, ...]] = {}
         self._masks: Dict[int, torch.Tensor] = {}
         self._stages: Dict[Tuple[int, int], "ElasticLayout"] = {}
-        # per head dim: tensor, or False (none: 128 x 128 or over budget)
-        self._stage_masks: Dict[int, object] = {}
+        self._stage_masks = None  # tensor, False (none: 128 x 128 or over budget), or unbuilt
 
     def stages(self, block_n: int = 32, block_m: Optional[int] = 64) -> "ElasticLayout":
         """The same pattern's layout at ``block_m`` x ``block_n`` blocks, the
@@ -216,34 +215,33 @@ class ElasticLayout:
             self._stages[(block_m, block_n)] = got
         return got
 
-    def stage_masks(self, head_dim: int) -> Optional[torch.Tensor]:
-        """This stage layout's per-stage masks for the tile forward at
-        ``head_dim`` (esa_build_stage_masks: row masks at 128, lane masks at
-        64), built once per head dim and cached, for the kernel to load
-        instead of walking each row's index list per stage; None for a
-        128 x 128 layout or when they would exceed STAGE_MASK_BUDGET bytes
-        (then the kernel walks)."""
-        got = self._stage_masks.get(head_dim)
-        if got is not None:
-            return got if isinstance(got, torch.Tensor) else None
+    def stage_masks(self) -> Optional[torch.Tensor]:
+        """This stage layout's per-stage row masks (esa_build_stage_masks),
+        built once and cached, for the tile forward to load instead of walking
+        each row's index list per stage; None for a 128 x 128 layout or when
+        they would exceed STAGE_MASK_BUDGET bytes (then the kernel walks)."""
+        if self._stage_masks is False:
+            return None
+        if self._stage_masks is not None:
+            return self._stage_masks
         p = self.pattern
-        if (p.block_m, p.block_n) not in ((64, 32), (128, 64)) or head_dim not in (64, 128):
-            self._stage_masks[head_dim] = False
+        if (p.block_m, p.block_n) not in ((64, 32), (128, 64)):
+            self._stage_masks = False
             return None
         lib = load()
         words = ctypes.c_int64()
         rp = ctypes.c_void_p(self.row_ptr_host.data_ptr())
-        check(lib.esa_stage_masks_size(ctypes.byref(p), rp, head_dim, ctypes.byref(words)),
+        check(lib.esa_stage_masks_size(ctypes.byref(p), rp, ctypes.byref(words)),
               "esa_stage_masks_size")
         if words.value * 4 > STAGE_MASK_BUDGET:
-            self._stage_masks[head_dim] = False
+            self._stage_masks = False
             return None
         masks = torch.empty(max(2, words.value), dtype=torch.int32, device=self.device)
         check(lib.esa_build_stage_masks(ctypes.byref(p), ctypes.c_void_p(self.row_ptr.data_ptr()),
-                                        ctypes.c_void_p(self.col_idx.data_ptr()), rp, head_dim,
+                                        ctypes.c_void_p(self.col_idx.data_ptr()), rp,
                                         ctypes.c_void_p(masks.data_ptr()), masks.numel(),
                                         _stream(self.device)), "esa_build_stage_masks")
-        self._stage_masks[head_dim] = masks
+        self._stage_masks = masks
         return masks
 
     def tiles_for(self, q_len: int) -> int:
@@ -476,7 +474,7 @@ def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                                                              query_block)
     items, n = st.schedule(Lq, B)
     # layer 0 rows are contiguous runs: the kernel sets them without a walk
-    masks = st.stage_masks(D) if stage_masks and st.pattern.layer_idx > 0 else None
+    masks = st.stage_masks() if stage_masks and st.pattern.layer_idx > 0 else None
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
     check(load().esa_elastic_fwd(ctypes.byref(a), ctypes.byref(st.pattern),
                                  ctypes.c_void_p(st.row_ptr.data_ptr()),

@@ -137,10 +137,9 @@ def load() -> ctypes.CDLL:
     lib.esa_elastic_fwd.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp, vp, vp, vp, ctypes.c_int64,
                                     vp]
     lib.esa_stage_masks_size.restype = st
-    lib.esa_stage_masks_size.argtypes = [P(EsaPattern), vp, ctypes.c_int32, P(ctypes.c_int64)]
+    lib.esa_stage_masks_size.argtypes = [P(EsaPattern), vp, P(ctypes.c_int64)]
     lib.esa_build_stage_masks.restype = st
-    lib.esa_build_stage_masks.argtypes = [P(EsaPattern), vp, vp, vp, ctypes.c_int32, vp,
-                                          ctypes.c_int64, vp]
+    lib.esa_build_stage_masks.argtypes = [P(EsaPattern), vp, vp, vp, vp, ctypes.c_int64, vp]
     lib.esa_elastic_fwd_band.restype = st
     lib.esa_elastic_fwd_band.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp]
     lib.esa_elastic_fwd_rows.restype = st

@@ -148,42 +148,31 @@ esa_status esa_plan_schedule(const esa_pattern* p, const int32_t* row_ptr_host,
  * esa_plan_schedule (copied to device memory); item ids outside the forward
  * are skipped.  stage_masks: NULL (each row's valid keys per stage are
  * computed in the kernel from the pattern), or, for a 64 x 32 or 128 x 64
- * layout, the masks esa_build_stage_masks wrote for this layout and
- * head_dim (8-byte aligned); same output bit for bit, without the per-row
- * index walk. */
+ * layout, the masks esa_build_stage_masks wrote for this layout (8-byte
+ * aligned); same output bit for bit, without the per-row index walk. */
 esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p,
                            const int32_t* row_ptr, const int32_t* col_idx,
                            const uint32_t* stage_masks, const int32_t* items,
                            int64_t num_items, void* stream);
 
 /* Host only.  32-bit words of the stage masks of a 64 x 32 or 128 x 64
- * layout (block_m x block_n of p) for the forward at head_dim 64 or 128:
- * num_tiles x block_m x block_n / 32, plus num_tiles x block_m / 32 at
- * head_dim 64, with num_tiles = row_ptr_host[num_heads * num_qblocks]. */
+ * layout (block_m x block_n of p): num_tiles x block_m x block_n / 32, with
+ * num_tiles = row_ptr_host[num_heads * num_qblocks]. */
 esa_status esa_stage_masks_size(const esa_pattern* p, const int32_t* row_ptr_host,
-                                int32_t head_dim, int64_t* words);
+                                int64_t* words);
 
-/* Per-stage masks of a 64 x 32 or 128 x 64 layout, for esa_elastic_fwd at
- * the same head_dim: the valid keys of _create_elastic_sparse_indices
- * (elastic_sparse_attention.py:470-535), as the forward's in-kernel walk
- * computes them, once per layout instead of once per batch element and
- * forward.  With B_M = block_m, NB = block_n / 32 blocks of 32 keys per
- * stage (key block) st and W = block_m / 32 waves of 32 rows:
- * head_dim 128 (row masks): word j of row r (of the query block) at
- * (st B_M + r) NB + j, bit k set when key 32 j + k of the stage is valid for
- * the row.
- * head_dim 64 (lane masks): stage st takes W (32 NB + 1) words from word
- * st W (32 NB + 1): first W x NB x 16 64-bit lane masks, the one of wave fw,
- * block j and register r at 64-bit index (fw NB + j) 16 + r, whose bit l is
- * set when key 8 (r / 4) + 4 (l / 32) + r % 4 of block j is valid for row
- * 32 fw + l % 32; then W flag words, bit j of wave fw's set when one of its
- * masks of block j is nonzero.
- * row_ptr / col_idx from esa_build_layout with the same pattern,
- * row_ptr_host its host copy; capacity_words >= esa_stage_masks_size. */
+/* Per-stage row masks of a 64 x 32 or 128 x 64 layout, for esa_elastic_fwd:
+ * for stage (key block) st of the layout and query row r of its block, the
+ * row's valid keys among the block's keys as block_n / 32 words at
+ * masks[(st * block_m + r) * block_n / 32 ..].  The bits of
+ * _create_elastic_sparse_indices (elastic_sparse_attention.py:470-535), as
+ * the forward's in-kernel walk computes them, once per layout instead of
+ * once per batch element and forward.  row_ptr / col_idx from
+ * esa_build_layout with the same pattern, row_ptr_host its host copy;
+ * capacity_words >= esa_stage_masks_size. */
 esa_status esa_build_stage_masks(const esa_pattern* p, const int32_t* row_ptr,
                                  const int32_t* col_idx, const int32_t* row_ptr_host,
-                                 int32_t head_dim, uint32_t* masks, int64_t capacity_words,
-                                 void* stream);
+                                 uint32_t* masks, int64_t capacity_words, void* stream);
 
 /* Band-gathered forward over the elastic pattern, prefill rows 0 .. q_len-1
  * (no layout needed).  Replaces the forward branch of the Triton kernel

@@ -196,9 +196,8 @@ def test_plan_schedule_xcd_runs(L, Lq, B, H, layer):
         assert c <= total / 8 + biggest + 1
 
 
-@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("bm,bn", [(64, 32), (128, 64)])
-def test_stage_masks_size_and_rejects(bm, bn, D):
+def test_stage_masks_size_and_rejects(bm, bn):
     """Stage-mask words = tiles of the layout x block_m x block_n / 32, from
     the host row_ptr (here the oracle's layout of the same pattern)."""
     lib = en.load()
@@ -209,22 +208,19 @@ def test_stage_masks_size_and_rejects(bm, bn, D):
     rph = rp.reshape(-1).to(torch.int32).contiguous()
     assert rph.numel() == H * ((L + bm - 1) // bm) + 1
     words = ctypes.c_int64()
-    assert lib.esa_stage_masks_size(ctypes.byref(p), ctypes.c_void_p(rph.data_ptr()), D,
+    assert lib.esa_stage_masks_size(ctypes.byref(p), ctypes.c_void_p(rph.data_ptr()),
                                     ctypes.byref(words)) == en.ESA_OK
-    flags = bm // 32 if D == 64 else 0
-    assert words.value == int(rph[-1]) * (bm * (bn // 32) + flags) > 0
+    assert words.value == int(rph[-1]) * bm * (bn // 32) > 0
     fake = ctypes.c_void_p(4096)
     rpp = ctypes.c_void_p(rph.data_ptr())
-    assert lib.esa_build_stage_masks(ctypes.byref(p), fake, fake, rpp, D, fake, words.value - 1,
+    assert lib.esa_build_stage_masks(ctypes.byref(p), fake, fake, rpp, fake, words.value - 1,
                                      None) == en.ESA_ERR_CAPACITY
-    assert lib.esa_build_stage_masks(ctypes.byref(p), fake, fake, rpp, D, ctypes.c_void_p(4100),
+    assert lib.esa_build_stage_masks(ctypes.byref(p), fake, fake, rpp, ctypes.c_void_p(4100),
                                      words.value, None) == en.ESA_ERR_ALIGN
-    assert lib.esa_build_stage_masks(ctypes.byref(p), None, fake, rpp, D, fake, words.value,
+    assert lib.esa_build_stage_masks(ctypes.byref(p), None, fake, rpp, fake, words.value,
                                      None) == en.ESA_ERR_NULL
-    assert lib.esa_stage_masks_size(ctypes.byref(p), rpp, 96, ctypes.byref(words)) \
-        == en.ESA_ERR_UNSUPPORTED
     p128 = pat(L=L, H=H, layer=layer)
-    assert lib.esa_stage_masks_size(ctypes.byref(p128), rpp, D, ctypes.byref(words)) \
+    assert lib.esa_stage_masks_size(ctypes.byref(p128), rpp, ctypes.byref(words)) \
         == en.ESA_ERR_UNSUPPORTED
 
 
