@@ -132,8 +132,9 @@ def copy_calibration(torch) -> None:
 
 
 def event_ms(torch, fn, steps: int, warmup: int) -> float:
-    """Mean time of `fn` over `steps` calls, each between two HIP events on
-    torch's current stream (the stream the library launches on)."""
+    """Median time of `fn` over `steps` calls after `warmup` untimed ones,
+    each between two HIP events on torch's current stream (the stream the
+    library launches on)."""
     for _ in range(warmup):
         fn()
     stream = torch.cuda.current_stream()
@@ -145,7 +146,7 @@ def event_ms(torch, fn, steps: int, warmup: int) -> float:
         fn()
         e_ev.record(stream)
     torch.cuda.synchronize()
-    return statistics.mean(a.elapsed_time(b) for a, b in evs)
+    return statistics.median(a.elapsed_time(b) for a, b in evs)
 
 
 def executed_blocks(torch, lay, L: int) -> int:
@@ -226,7 +227,7 @@ def make_inputs(torch, cfg: str, dev, on_device: bool):
 
 def time_backward(torch, lay, q, k, v, scaling, counted_fwd, steps, warmup) -> dict:
     """The backward (dQ, dK, dV from the forward's O and LSE, with the
-    kernels `bwd_kernels` picks) on the same inputs: mean of `steps`
+    kernels `bwd_kernels` picks) on the same inputs: median of `steps`
     launches (HIP events on the launch stream) after `warmup`; for a
     block-sparse half the tile masks and work lists are built (and cached)
     before timing, as the layout is.  counted_tflops counts 2.5x the
@@ -357,7 +358,7 @@ def main() -> None:
                     help="skip timing one decode step of a serving batch (reported by default)")
     ap.add_argument("--no-configs", dest="configs", action="store_false",
                     help="skip the per-configuration forward/backward table")
-    ap.add_argument("--config-steps", type=int, default=5)
+    ap.add_argument("--config-steps", type=int, default=20)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of known size (HBM counter scale)")
     args = ap.parse_args()
@@ -472,7 +473,7 @@ def main() -> None:
             for layer in layers:
                 key = f"{cfg}/layer{layer}"
                 try:
-                    rows[key] = one_config(torch, cfg, layer, dev, args.config_steps, 2,
+                    rows[key] = one_config(torch, cfg, layer, dev, args.config_steps, 5,
                                            args.backward)
                 except Exception as exc:  # noqa: BLE001
                     rows[key] = {"error": f"{type(exc).__name__}: {exc}"}
