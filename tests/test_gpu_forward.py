@@ -249,22 +249,22 @@ def test_stage_layout_matches_tile_layout(B, H, Hkv, L, Lq, D, layer):
 
 @pytest.mark.parametrize("layer", [0, 4, 7])
 def test_full_size_8k(layer):
-    full_size_check(1, 32, 8192, 128, layer, 128 ** -0.25, 0.0, seed=20 + layer)
+    full_size_check(1, 32, 8192, 128, layer, 128 ** -0.25, 0.0, seed=20 + layer, n_rows=1024)
 
 
 @pytest.mark.parametrize("layer", [0, 4, 7])
 def test_full_size_headline_32k(layer):
-    full_size_check(1, 32, 32768, 128, layer, 128 ** -0.25, 0.0, seed=30 + layer, n_rows=256)
+    full_size_check(1, 32, 32768, 128, layer, 128 ** -0.25, 0.0, seed=30 + layer, n_rows=1024)
 
 
 @pytest.mark.parametrize("layer", [0, 4, 7])
 def test_full_size_batched_4k(layer):
-    full_size_check(8, 16, 4096, 64, layer, 1.0, 0.0, seed=40 + layer, n_rows=128)
+    full_size_check(8, 16, 4096, 64, layer, 1.0, 0.0, seed=40 + layer, n_rows=1024)
 
 
 @pytest.mark.parametrize("layer", [0, 4, 7])
 def test_full_size_long_outliers_128k(layer):
-    full_size_check(1, 8, 131072, 128, layer, 1.0, 0.01, seed=50 + layer, n_rows=128)
+    full_size_check(1, 8, 131072, 128, layer, 1.0, 0.01, seed=50 + layer, n_rows=512)
 
 
 # ---------------------------------------------------------------- band-gathered kernel
@@ -348,20 +348,20 @@ def test_band_rejects_unsupported():
 
 @pytest.mark.parametrize("layer", [4, 7])
 def test_band_full_size_headline_32k(layer):
-    full_size_check(1, 32, 32768, 128, layer, 128 ** -0.25, 0.0, seed=60 + layer, n_rows=256,
+    full_size_check(1, 32, 32768, 128, layer, 128 ** -0.25, 0.0, seed=60 + layer, n_rows=1024,
                     band=True)
 
 
 def test_band_full_size_8k():
-    full_size_check(1, 32, 8192, 128, 4, 128 ** -0.25, 0.0, seed=70, band=True)
+    full_size_check(1, 32, 8192, 128, 4, 128 ** -0.25, 0.0, seed=70, n_rows=1024, band=True)
 
 
 def test_band_full_size_batched_4k():
-    full_size_check(8, 16, 4096, 64, 7, 1.0, 0.0, seed=71, n_rows=128, band=True)
+    full_size_check(8, 16, 4096, 64, 7, 1.0, 0.0, seed=71, n_rows=1024, band=True)
 
 
 def test_band_full_size_long_outliers_128k():
-    full_size_check(1, 8, 131072, 128, 4, 1.0, 0.01, seed=72, n_rows=128, band=True)
+    full_size_check(1, 8, 131072, 128, 4, 1.0, 0.01, seed=72, n_rows=512, band=True)
 
 
 # ---------------------------------------------------------------- per-row gather kernel
