@@ -390,7 +390,10 @@ __global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs A, const float* ls
 }
 
 // ---------------------------------------------------------------------------
-template <int D, Elem E>
+// PRE: each row's valid keys per tile come from A.qmask (written once per
+// layout by stage_mask_kernel, the bits the walk computes), one 16-byte load
+// per tile, issued a tile ahead, in place of the index walk.
+template <int D, Elem E, bool PRE>
 __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2) {
   using M = MmaT<E>;
   using V8 = typename M::v8;
@@ -440,7 +443,7 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2
     dl = A.delta[at];
   }
   RowWalker walk;
-  walk.init(A.pc, h, i, row_ok);
+  if (!PRE) walk.init(A.pc, h, i, row_ok);
   f32x16 dqacc[C::ND];
 #pragma unroll
   for (int d = 0; d < C::ND; ++d) dqacc[d] = f32x16{};
@@ -528,14 +531,29 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2
     }
   };
 
+  // row r's words of tile t at qmask[(t * 128 + r) * 4 ..]
+  const uint32_t* qm = PRE ? A.qmask + (wave * 32 + l32) * 4 : nullptr;
+  auto load_masks = [&](int t, uint32_t (&m)[4]) {
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (row_ok) w = *(const u32x4*)(qm + (int64_t)t * 512);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) m[q] = w[q];
+  };
+  uint32_t mnext[4] = {0u, 0u, 0u, 0u};
+  if (PRE && t0 < t1) load_masks(t0, mnext);
   if (t0 < t1) issue(t0, 0, k_st0, v_st0);
   for (int t = t0; t < t1; ++t) {
-    const int k0 = col_idx[t] * 128;
     uint32_t mb[4];
-    walk.tile(k0, mb);
+    if (PRE) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) mb[q] = mnext[q];
+    } else {
+      walk.tile(col_idx[t] * 128, mb);
+    }
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
     issue(t, 1, k_st1, v_st1);
+    if (PRE && t + 1 < t1) load_masks(t + 1, mnext);
     block(k_st0, v_st0, 0, mb[0]);
     block(k_st0, v_st0, 1, mb[1]);
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
@@ -607,10 +625,15 @@ static hipError_t launch_tile_bwd_elem(const BwdArgs& a, int head_dim, int64_t n
   }
   if (num_q_items < 0) return launch_band_dq(a, head_dim, lse2, false, stream);  // no work list
   if (num_q_items > 0) {
-    if (head_dim == 128)
-      dq_kernel<128, E><<<dim3((unsigned)num_q_items), 256, 0, stream>>>(a, lse2);
+    const dim3 grid((unsigned)num_q_items);
+    if (head_dim == 128 && a.qmask)
+      dq_kernel<128, E, true><<<grid, 256, 0, stream>>>(a, lse2);
+    else if (head_dim == 128)
+      dq_kernel<128, E, false><<<grid, 256, 0, stream>>>(a, lse2);
+    else if (a.qmask)
+      dq_kernel<64, E, true><<<grid, 256, 0, stream>>>(a, lse2);
     else
-      dq_kernel<64, E><<<dim3((unsigned)num_q_items), 256, 0, stream>>>(a, lse2);
+      dq_kernel<64, E, false><<<grid, 256, 0, stream>>>(a, lse2);
     e = hipGetLastError();
   }
   return e;

@@ -650,7 +650,8 @@ esa_status esa_stage_masks_size(const esa_pattern* p, const int32_t* row_ptr_hos
   if (!p || !row_ptr_host || !words) return ESA_ERR_NULL;
   esa_status s = check_pattern(p);
   if (s != ESA_OK) return s;
-  const bool ok = (p->block_m == 64 && p->block_n == 32) || (p->block_m == 128 && p->block_n == 64);
+  const bool ok = (p->block_m == 64 && p->block_n == 32) ||
+                  (p->block_m == 128 && (p->block_n == 64 || p->block_n == 128));
   if (!ok) return ESA_ERR_UNSUPPORTED;
   const LayoutDims d = dims_of(*p);
   const int64_t tiles = row_ptr_host[(int64_t)p->num_heads * d.nqb];
@@ -753,8 +754,9 @@ esa_status elastic_bwd_impl(const esa_bwd_args* a, const esa_pattern* p, const i
                             const int32_t* col_idx, const int32_t* q_items, int64_t num_q_items,
                             const int32_t* tile_row, const int32_t* kv_ptr,
                             const int32_t* kv_tiles, const int32_t* kv_items,
-                            int64_t num_kv_items, const uint32_t* mask_t, void* workspace,
-                            size_t workspace_bytes, bool static_ws, void* stream) {
+                            int64_t num_kv_items, const uint32_t* mask_t,
+                            const uint32_t* q_masks, void* workspace, size_t workspace_bytes,
+                            bool static_ws, void* stream) {
   if (!a || !a->q || !a->k || !a->v || !a->o || !a->dout || !a->dq || !a->dk || !a->dv || !a->lse)
     return ESA_ERR_NULL;
   esa_status s = check_pattern(p);
@@ -803,6 +805,9 @@ esa_status elastic_bwd_impl(const esa_bwd_args* a, const esa_pattern* p, const i
   esa_bwd_workspace_size(a, &need);
   if (workspace_bytes < need) return ESA_ERR_CAPACITY;
   if (!static_ws && !aligned(workspace, 16)) return ESA_ERR_ALIGN;
+  // row masks serve the block-sparse dQ only (16-byte loads)
+  if (q_masks && band_dq) return ESA_ERR_UNSUPPORTED;
+  if (q_masks && !aligned(q_masks, 16)) return ESA_ERR_ALIGN;
   const LayoutDims d = dims_of(*p);
   const int nq = (a->q_len + 127) / 128;
   const int64_t n_real = (int64_t)a->batch * a->num_heads * nq;
@@ -822,7 +827,7 @@ esa_status elastic_bwd_impl(const esa_bwd_args* a, const esa_pattern* p, const i
   t.q = (const uint16_t*)a->q; t.k = (const uint16_t*)a->k; t.v = (const uint16_t*)a->v;
   t.o = (const uint16_t*)a->o; t.dout = (const uint16_t*)a->dout;
   t.dq = (uint16_t*)a->dq; t.dk = (uint16_t*)a->dk; t.dv = (uint16_t*)a->dv;
-  t.lse = a->lse; t.delta = (float*)workspace; t.mask_t = mask_t;
+  t.lse = a->lse; t.delta = (float*)workspace; t.mask_t = mask_t; t.qmask = q_masks;
   t.qsb = a->q_stride_b; t.qsh = a->q_stride_h; t.qss = a->q_stride_s;
   t.ksb = a->k_stride_b; t.ksh = a->k_stride_h; t.kss = a->k_stride_s;
   t.vsb = a->v_stride_b; t.vsh = a->v_stride_h; t.vss = a->v_stride_s;
@@ -878,11 +883,12 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const in
                            const int32_t* col_idx, const int32_t* q_items, int64_t num_q_items,
                            const int32_t* tile_row, const int32_t* kv_ptr,
                            const int32_t* kv_tiles, const int32_t* kv_items,
-                           int64_t num_kv_items, const uint32_t* mask_t, void* workspace,
-                           size_t workspace_bytes, void* stream) {
+                           int64_t num_kv_items, const uint32_t* mask_t,
+                           const uint32_t* q_masks, void* workspace, size_t workspace_bytes,
+                           void* stream) {
   return elastic_bwd_impl(a, p, row_ptr, col_idx, q_items, num_q_items, tile_row, kv_ptr,
-                          kv_tiles, kv_items, num_kv_items, mask_t, workspace, workspace_bytes,
-                          false, stream);
+                          kv_tiles, kv_items, num_kv_items, mask_t, q_masks, workspace,
+                          workspace_bytes, false, stream);
 }
 
 size_t esa_bwd_noalloc_max_workspace(void) { return kScratchBytes; }
@@ -892,10 +898,11 @@ esa_status esa_elastic_bwd_noalloc(const esa_bwd_args* a, const esa_pattern* p,
                                    const int32_t* q_items, int64_t num_q_items,
                                    const int32_t* tile_row, const int32_t* kv_ptr,
                                    const int32_t* kv_tiles, const int32_t* kv_items,
-                                   int64_t num_kv_items, const uint32_t* mask_t, void* stream) {
+                                   int64_t num_kv_items, const uint32_t* mask_t,
+                                   const uint32_t* q_masks, void* stream) {
   return elastic_bwd_impl(a, p, row_ptr, col_idx, q_items, num_q_items, tile_row, kv_ptr,
-                          kv_tiles, kv_items, num_kv_items, mask_t, nullptr, kScratchBytes, true,
-                          stream);
+                          kv_tiles, kv_items, num_kv_items, mask_t, q_masks, nullptr,
+                          kScratchBytes, true, stream);
 }
 
 esa_status esa_gather_bwd_workspace_size(const esa_bwd_args* a, int32_t attn_length,

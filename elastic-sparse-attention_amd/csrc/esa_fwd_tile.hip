@@ -249,11 +249,11 @@ void launch_tile_elem(const TileArgs& a, int head_dim, dim3 grid, hipStream_t st
     launch_tile_pre<E, false>(a, head_dim, grid, stream);
 }
 
-// One workgroup per (head, query block) of a 64 x 32 or 128 x 64 layout, one
-// lane per query row: each lane walks its row's index list through the
-// block's stages (the key blocks col_idx lists, ascending) as the forward
-// does and stores the valid-key bits, word q of stage st for row r at
-// masks[(st * BMQ + r) * NW + q].  Rows past the pattern get zeros.
+// One workgroup per (head, query block) of a 64 x 32, 128 x 64 or 128 x 128
+// layout, one lane per query row: each lane walks its row's index list
+// through the block's stages (the key blocks col_idx lists, ascending) as
+// the forward does and stores the valid-key bits, word q of stage st for row
+// r at masks[(st * BMQ + r) * NW + q].  Rows past the pattern get zeros.
 template <int BMQ, int NW>
 __global__ __launch_bounds__(BMQ) void stage_mask_kernel(PatternConsts pc, int nqb, int seq_len,
                                                          int log_bn, const int32_t* row_ptr,
@@ -281,8 +281,11 @@ hipError_t launch_stage_masks(const PatternConsts& pc, const LayoutDims& ld, con
   if (ld.bm == 64)
     stage_mask_kernel<64, 1><<<grid, 64, 0, stream>>>(pc, ld.nqb, ld.seq_len, 5, row_ptr, col_idx,
                                                        masks);
-  else
+  else if (ld.bn == 64)
     stage_mask_kernel<128, 2><<<grid, 128, 0, stream>>>(pc, ld.nqb, ld.seq_len, 6, row_ptr,
+                                                         col_idx, masks);
+  else  // 128 x 128 tiles (the backward's dQ)
+    stage_mask_kernel<128, 4><<<grid, 128, 0, stream>>>(pc, ld.nqb, ld.seq_len, 7, row_ptr,
                                                          col_idx, masks);
   return hipGetLastError();
 }

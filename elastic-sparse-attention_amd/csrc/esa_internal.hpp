@@ -162,6 +162,7 @@ struct BwdArgs {
   const float* lse;      // forward log-sum-exp, natural log, [B, H, q_len]
   float* delta;          // workspace [B, H, qpad]: rowsum(dO * O) (then lse2)
   const uint32_t* mask_t;  // [tiles][4 query sub-blocks][128 keys] key-major tile masks
+  const uint32_t* qmask;   // [tiles][128 rows][4 words] row-major tile masks, or NULL (walk)
   int64_t qsb, qsh, qss;
   int64_t ksb, ksh, kss;
   int64_t vsb, vsh, vss;

@@ -194,7 +194,7 @@ class ElasticLayout:
         self._bwd_plans: Dict[Tuple[int, int, int], Tuple[torch.Tensor, ...]] = {}
         self._masks: Dict[int, torch.Tensor] = {}
         self._stages: Dict[Tuple[int, int], "ElasticLayout"] = {}
-        self._stage_masks = None  # tensor, False (none: 128 x 128 or over budget), or unbuilt
+        self._stage_masks = None  # tensor, False (none: over budget), or unbuilt
 
     def stages(self, block_n: int = 32, block_m: Optional[int] = 64) -> "ElasticLayout":
         """The same pattern's layout at ``block_m`` x ``block_n`` blocks, the
@@ -216,16 +216,17 @@ class ElasticLayout:
         return got
 
     def stage_masks(self) -> Optional[torch.Tensor]:
-        """This stage layout's per-stage row masks (esa_build_stage_masks),
-        built once and cached, for the tile forward to load instead of walking
-        each row's index list per stage; None for a 128 x 128 layout or when
+        """This layout's per-stage row masks (esa_build_stage_masks), built
+        once and cached, for the tile forward (64 x 32 or 128 x 64 stages) or
+        the tile backward's dQ (128 x 128 tiles) to load instead of walking
+        each row's index list per stage; None for other block shapes or when
         they would exceed STAGE_MASK_BUDGET bytes (then the kernel walks)."""
         if self._stage_masks is False:
             return None
         if self._stage_masks is not None:
             return self._stage_masks
         p = self.pattern
-        if (p.block_m, p.block_n) not in ((64, 32), (128, 64)):
+        if (p.block_m, p.block_n) not in ((64, 32), (128, 64), (128, 128)):
             self._stage_masks = False
             return None
         lib = load()
@@ -236,7 +237,7 @@ class ElasticLayout:
         if words.value * 4 > STAGE_MASK_BUDGET:
             self._stage_masks = False
             return None
-        masks = torch.empty(max(2, words.value), dtype=torch.int32, device=self.device)
+        masks = torch.empty(max(4, words.value), dtype=torch.int32, device=self.device)
         check(lib.esa_build_stage_masks(ctypes.byref(p), ctypes.c_void_p(self.row_ptr.data_ptr()),
                                         ctypes.c_void_p(self.col_idx.data_ptr()), rp,
                                         ctypes.c_void_p(masks.data_ptr()), masks.numel(),
@@ -473,8 +474,10 @@ def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     st = layout if (query_block, key_block) == (128, 128) else layout.stages(key_block,
                                                                              query_block)
     items, n = st.schedule(Lq, B)
-    # layer 0 rows are contiguous runs: the kernel sets them without a walk
-    masks = st.stage_masks() if stage_masks and st.pattern.layer_idx > 0 else None
+    # layer 0 rows are contiguous runs: the kernel sets them without a walk;
+    # whole-tile staging walks
+    use = stage_masks and st.pattern.layer_idx > 0 and st.pattern.block_n != 128
+    masks = st.stage_masks() if use else None
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
     check(load().esa_elastic_fwd(ctypes.byref(a), ctypes.byref(st.pattern),
                                  ctypes.c_void_p(st.row_ptr.data_ptr()),
@@ -684,12 +687,16 @@ def sparse_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: t
 def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor,
                           lse: torch.Tensor, dout: torch.Tensor, layout: ElasticLayout,
                           scaling: float, dq_kernel: str = "auto", dkdv_kernel: str = "auto",
-                          noalloc: bool = False
+                          noalloc: bool = False, stage_masks: bool = True
                           ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """MFMA backward of ``elastic_attention_fwd`` (prefill, bf16 or fp16).
 
     ``noalloc``: call ``esa_elastic_bwd_noalloc`` (the library's per-device
     workspace array, no workspace allocation) instead of ``esa_elastic_bwd``.
+    ``stage_masks``: at dilated layers the block-sparse dQ loads each row's
+    valid keys per tile from the layout's row masks
+    (:meth:`ElasticLayout.stage_masks`, within STAGE_MASK_BUDGET) instead of
+    walking the row's index list; the gradients are the same bit for bit.
 
     ``o`` and ``dout`` are ``[B, Lq, H, D]`` (the forward's output layout),
     ``lse`` float32 ``[B, H, Lq]``.  Returns ``dq`` ``[B, H, Lq, D]`` and
@@ -732,6 +739,9 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
     # a band half takes no work list (its kernel covers every row group or
     # key block), and no layout arrays when both halves are band-gathered
     items, n_items = (None, 0) if dq_kernel == "band" else layout.schedule(Lq, B)
+    q_masks = None
+    if dq_kernel == "tile" and stage_masks and layout.pattern.layer_idx > 0:
+        q_masks = layout.stage_masks()
     if dkdv_kernel == "band":
         tile_row = kv_ptr = kv_tiles = kv_items = masks = None
         n_kv = 0
@@ -742,13 +752,15 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
         check(lib.esa_elastic_bwd_noalloc(ctypes.byref(a), ctypes.byref(layout.pattern),
                                           ptr(layout.row_ptr), ptr(layout.col_idx), ptr(items),
                                           n_items, ptr(tile_row), ptr(kv_ptr), ptr(kv_tiles),
-                                          ptr(kv_items), n_kv, ptr(masks), _stream(q.device)),
+                                          ptr(kv_items), n_kv, ptr(masks), ptr(q_masks),
+                                          _stream(q.device)),
               "esa_elastic_bwd_noalloc")
     else:
         check(lib.esa_elastic_bwd(ctypes.byref(a), ctypes.byref(layout.pattern),
                                   ptr(layout.row_ptr), ptr(layout.col_idx), ptr(items), n_items,
                                   ptr(tile_row), ptr(kv_ptr), ptr(kv_tiles), ptr(kv_items), n_kv,
-                                  ptr(masks), ptr(work), work.numel() * 4, _stream(q.device)),
+                                  ptr(masks), ptr(q_masks), ptr(work), work.numel() * 4,
+                                  _stream(q.device)),
               "esa_elastic_bwd")
     return dq, dk, dv
 

@@ -158,10 +158,10 @@ def load() -> ctypes.CDLL:
     lib.esa_bwd_workspace_size.argtypes = [P(EsaBwdArgs), P(ctypes.c_size_t)]
     lib.esa_elastic_bwd.restype = st
     lib.esa_elastic_bwd.argtypes = [P(EsaBwdArgs), P(EsaPattern), vp, vp, vp, i64, vp, vp, vp, vp,
-                                    i64, vp, vp, ctypes.c_size_t, vp]
+                                    i64, vp, vp, vp, ctypes.c_size_t, vp]
     lib.esa_elastic_bwd_noalloc.restype = st
     lib.esa_elastic_bwd_noalloc.argtypes = [P(EsaBwdArgs), P(EsaPattern), vp, vp, vp, i64, vp, vp,
-                                            vp, vp, i64, vp, vp]
+                                            vp, vp, i64, vp, vp, vp]
     lib.esa_bwd_noalloc_max_workspace.restype = ctypes.c_size_t
     lib.esa_bwd_noalloc_max_workspace.argtypes = []
     lib.esa_elastic_fwd_naive.restype = st

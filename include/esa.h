@@ -155,14 +155,15 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p,
                            const uint32_t* stage_masks, const int32_t* items,
                            int64_t num_items, void* stream);
 
-/* Host only.  32-bit words of the stage masks of a 64 x 32 or 128 x 64
- * layout (block_m x block_n of p): num_tiles x block_m x block_n / 32, with
- * num_tiles = row_ptr_host[num_heads * num_qblocks]. */
+/* Host only.  32-bit words of the stage masks of a 64 x 32, 128 x 64 or
+ * 128 x 128 layout (block_m x block_n of p): num_tiles x block_m x
+ * block_n / 32, with num_tiles = row_ptr_host[num_heads * num_qblocks]. */
 esa_status esa_stage_masks_size(const esa_pattern* p, const int32_t* row_ptr_host,
                                 int64_t* words);
 
-/* Per-stage row masks of a 64 x 32 or 128 x 64 layout, for esa_elastic_fwd:
- * for stage (key block) st of the layout and query row r of its block, the
+/* Per-stage row masks of a 64 x 32 or 128 x 64 layout, for esa_elastic_fwd,
+ * or of a 128 x 128 layout, for esa_elastic_bwd's block-sparse dQ: for stage
+ * (key block) st of the layout and query row r of its block, the
  * row's valid keys among the block's keys as block_n / 32 words at
  * masks[(st * block_m + r) * block_n / 32 ..].  The bits of
  * _create_elastic_sparse_indices (elastic_sparse_attention.py:470-535), as
@@ -337,7 +338,11 @@ esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes
  * kv_items NULL computes dK and dV with the band-gathered key-major kernel
  * instead (same limits; tile_row, kv_ptr, kv_tiles, mask_t and num_kv_items
  * are ignored).  With both NULL no layout is read (row_ptr, col_idx may be
- * NULL).  All lists and masks are device memory.
+ * NULL).  q_masks: NULL (the block-sparse dQ computes each row's valid keys
+ * per tile from the pattern), or esa_build_stage_masks' masks of this 128 x
+ * 128 layout (16-byte aligned; only with q_items, ESA_ERR_UNSUPPORTED
+ * otherwise): same results bit for bit, without the per-row index walk.
+ * All lists and masks are device memory.
  * Requires dtype ESA_BF16 or ESA_F16, head_dim 64 or 128, block 128 x 128, a finite
  * sm_scale > 0, q_len <= kv_len, 16-byte aligned rows. */
 esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p,
@@ -346,8 +351,8 @@ esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p,
                            const int32_t* tile_row, const int32_t* kv_ptr,
                            const int32_t* kv_tiles, const int32_t* kv_items,
                            int64_t num_kv_items, const uint32_t* mask_t,
-                           void* workspace, size_t workspace_bytes,
-                           void* stream);
+                           const uint32_t* q_masks, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /* Host only.  Bytes of workspace esa_sparse_bwd and esa_elastic_bwd_rows
  * need for index lists of attn_length entries per row: per batch element and
@@ -409,7 +414,7 @@ esa_status esa_elastic_bwd_noalloc(const esa_bwd_args* a, const esa_pattern* p,
                                    const int32_t* tile_row, const int32_t* kv_ptr,
                                    const int32_t* kv_tiles, const int32_t* kv_items,
                                    int64_t num_kv_items, const uint32_t* mask_t,
-                                   void* stream);
+                                   const uint32_t* q_masks, void* stream);
 
 /* Bytes of the per-device array esa_elastic_bwd_noalloc uses as its
  * workspace (the largest esa_bwd_workspace_size it accepts).  Host only. */

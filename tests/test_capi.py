@@ -196,7 +196,7 @@ def test_plan_schedule_xcd_runs(L, Lq, B, H, layer):
         assert c <= total / 8 + biggest + 1
 
 
-@pytest.mark.parametrize("bm,bn", [(64, 32), (128, 64)])
+@pytest.mark.parametrize("bm,bn", [(64, 32), (128, 64), (128, 128)])
 def test_stage_masks_size_and_rejects(bm, bn):
     """Stage-mask words = tiles of the layout x block_m x block_n / 32, from
     the host row_ptr (here the oracle's layout of the same pattern)."""
@@ -219,8 +219,8 @@ def test_stage_masks_size_and_rejects(bm, bn):
                                      words.value, None) == en.ESA_ERR_ALIGN
     assert lib.esa_build_stage_masks(ctypes.byref(p), None, fake, rpp, fake, words.value,
                                      None) == en.ESA_ERR_NULL
-    p128 = pat(L=L, H=H, layer=layer)
-    assert lib.esa_stage_masks_size(ctypes.byref(p128), rpp, ctypes.byref(words)) \
+    p64 = pat(L=L, H=H, layer=layer, bm=64, bn=64)
+    assert lib.esa_stage_masks_size(ctypes.byref(p64), rpp, ctypes.byref(words)) \
         == en.ESA_ERR_UNSUPPORTED
 
 
@@ -312,10 +312,10 @@ def test_bwd_entry_points_reject_bad_arguments():
     assert ws.value == 2 * 1 * 4 * (256 + 32) * 4   # rows padded to 32, + 32
 
     def call(args, items=8, kv_items=64, wsb=ws.value, pat_=p, layout=fake, q_list=fake,
-             kv_lists=fake, kv_list=fake, masks=fake):
+             kv_lists=fake, kv_list=fake, masks=fake, q_masks=None):
         return lib.esa_elastic_bwd(ctypes.byref(args), ctypes.byref(pat_), layout, layout, q_list,
                                    items, kv_lists, kv_lists, kv_lists, kv_list, kv_items, masks,
-                                   fake, wsb, None)
+                                   q_masks, fake, wsb, None)
 
     # the block-sparse halves need their layout, lists and masks; the band
     # halves need none of them, and attention_length <= 64
@@ -327,6 +327,9 @@ def test_bwd_entry_points_reject_bad_arguments():
     assert call(a, q_list=None, kv_list=None, pat_=pat(L=1024, H=4, w=65)) \
         == en.ESA_ERR_UNSUPPORTED
     assert call(a, kv_list=None, kv_items=31, wsb=16) == en.ESA_ERR_CAPACITY  # count ignored
+    # row masks serve the block-sparse dQ only, 16-byte aligned
+    assert call(a, q_list=None, q_masks=fake) == en.ESA_ERR_UNSUPPORTED
+    assert call(a, q_masks=ctypes.c_void_p(4104)) == en.ESA_ERR_ALIGN
 
     assert call(a, wsb=16) == en.ESA_ERR_CAPACITY
     assert call(a, items=7) == en.ESA_ERR_SHAPE
@@ -445,7 +448,7 @@ def test_noalloc_rejects_oversized_workspace():
     a.sm_scale = 128 ** -0.5
     p = en.EsaPattern(32768, 64, 4, 8, 32, 128, 128)
     st = lib.esa_elastic_bwd_noalloc(ctypes.byref(a), ctypes.byref(p), None, None, None, 0, None,
-                                     None, None, None, 0, None, None)
+                                     None, None, None, 0, None, None, None)
     assert st == en.ESA_ERR_CAPACITY
 
 

@@ -102,6 +102,42 @@ def test_backward_attention_lengths(B, H, Hkv, L, D, layer, w, kernels):
     assert max(e) <= REL
 
 
+@pytest.mark.parametrize("B,H,Hkv,L,Lq,D,w", [
+    (1, 4, 4, 1024, 1024, 128, 64),
+    (2, 8, 2, 1500, 1200, 64, 64),    # GQA, batch, q_len < kv_len, ragged blocks
+    (1, 4, 2, 1100, 1100, 128, 100),  # longer index lists
+])
+def test_tile_dq_row_masks_bit_identical(B, H, Hkv, L, Lq, D, w):
+    """The block-sparse dQ with the layout's row masks loaded gives the same
+    bits as with the in-kernel index walk at every dilated layer (dK / dV
+    untouched), and meets autograd at one of them."""
+    for layer in range(1, 8):
+        print(f"dq row masks B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} w={w} layer={layer}",
+              flush=True)
+        q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=layer + 11, scale=1.0,
+                                Lq=Lq)
+        sc = scaling_for(D)
+        lay = ElasticLayout(make_pattern(L, w, layer, 8, H), DEV)
+        assert lay.stage_masks() is not None
+        qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+        o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc, kernel="tile")
+        g = torch.randn(B, H, Lq, D, generator=torch.Generator().manual_seed(layer))
+        g = g.to(torch.bfloat16)
+        do = g.to(DEV).permute(0, 2, 1, 3).contiguous()
+        got = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="tile",
+                                    dkdv_kernel="tile", stage_masks=True)
+        walk = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="tile",
+                                     dkdv_kernel="tile", stage_masks=False)
+        assert all(torch.equal(x, y) for x, y in zip(got, walk))
+        if layer == 5:
+            idx, msk = elastic_indices(L, layer, 8, H, w)
+            pi, pm = prepared_rows(idx, msk, Lq, L, L)
+            ref = reference_grads(q, k, v, pi, pm, sc, H // Hkv, g.float())
+            e = [rel_err(x, r) for x, r in zip(got, ref)]
+            print(f"  rel err dq {e[0]:.3e} dk {e[1]:.3e} dv {e[2]:.3e}", flush=True)
+            assert max(e) <= REL
+
+
 @pytest.mark.parametrize("B,H,Hkv,L,D,layer,w", [
     (1, 4, 2, 1100, 128, 4, 100),
     (1, 4, 4, 1024, 64, 6, 128),

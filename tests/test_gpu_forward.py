@@ -160,7 +160,7 @@ def full_size_check(B, H, L, D, layer, scale, outlier, seed, n_rows=384, band=Fa
     assert e_o <= BF16_TOL and e_l <= BF16_LSE_TOL
 
 
-@pytest.mark.parametrize("bm,bn", [(64, 32), (128, 64)])
+@pytest.mark.parametrize("bm,bn", [(64, 32), (128, 64), (128, 128)])
 @pytest.mark.parametrize("L,H,layer,w", [(1000, 3, 5, 64), (777, 4, 7, 64), (513, 2, 2, 100),
                                          (300, 5, 1, 16)])
 def test_stage_masks_match_oracle(bm, bn, L, H, layer, w):
