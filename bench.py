@@ -3,6 +3,7 @@
     python bench.py [--steps K] [--warmup W] [--config 32k|8k|batched|128k]
                     [--layer N] [--no-cpu] [--no-backward] [--no-decode]
                     [--no-configs]
+    python bench.py --peaks            (only the rate probes, one JSON line)
 
 A step is one ElasticSparseAttention.forward over one batch of synthetic
 input already resident in HBM (the module's drop-in HIP path: one kernel
@@ -32,8 +33,8 @@ roofline         the timed kernel against the resource it uses, from the work
                  scaled by a plain copy's readings), from the committed
                  summary in profiles/, else null.
 l2_to_cu         what bounds the kernels at dilated layers: bytes gathered
-                 from L2 (profiled) over the kernel time, against the rate a
-                 copy kernel reaches from L2.
+                 from L2 (profiled) over the kernel time, against the L2 ->
+                 LDS rate `bench.py --peaks` measures.
 configs          every configured workload (forward and backward kernel
                  times, kernel-only, a few steps each) at layers 0, 4 and 7.
 backward         the backward of the headline forward (dQ, dK, dV).
@@ -70,10 +71,11 @@ W, NL = 64, 8
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 METRIC = "active-block TFLOP/s + % of bf16 MFMA peak, elastic attn fwd, 1 GPU, L=32K"
-# L2 -> CU streaming rate of MI355X measured with a copy kernel reading 4 KB
-# row blocks from an L2-resident buffer (buffer_load ... lds or into
-# registers, 4-10 waves per CU): the ceiling of the gather-bound forwards
-L2_TO_CU_TBS = 36.0
+# L2 -> CU streaming rate of MI355X through buffer_load ... lds (the path the
+# MFMA kernels stage K and V through), measured by `bench.py --peaks`
+# (esa_probe_l2_to_lds: 16 KB rounds from a 1 MiB L2-resident region, 8
+# workgroups per CU, 32.4-33.1 TB/s): the ceiling of the gather-bound forwards
+L2_TO_CU_TBS = 33.0
 
 
 def host_cores() -> int:
@@ -129,6 +131,86 @@ def copy_calibration(torch) -> None:
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes": COPY_BYTES, "copies": 3}), flush=True)
+
+
+def peaks(torch, steps: int = 10) -> None:
+    """The rates the roofline is stated against, measured on this GPU with
+    libesa_probe.so (include/esa_probe.h), each the median of `steps` timed
+    launches after warm-ups, with its closed-form result checked, and the
+    best over a few launch shapes (workgroups per CU) reported with its
+    shape: dense bf16 MFMA (four independent 32x32x16 chains per wave), HBM
+    read (a 4 GiB buffer streamed once), a device copy (1 GiB, read +
+    write), and L2 -> LDS through buffer_load ... lds (a 1 MiB region every
+    XCD's L2 holds, 16 KB rounds per workgroup, two in flight)."""
+    import ctypes
+    import esa_native as en
+    lib = en.load_probe()
+    dev = torch.device("cuda", 0)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    vp = ctypes.c_void_p
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    out = {"cus": cus}
+
+    def best(rates):
+        per, rate = max(rates.items(), key=lambda kv: kv[1])
+        return per, rate, {str(k): round(v, 3) for k, v in rates.items()}
+
+    rates = {}
+    for per in (2, 4):
+        wg, iters = per * cus, 32768 // per
+        sink = torch.empty(wg * 256, dtype=torch.float32, device=dev)
+        ms = event_ms(torch, lambda: en.check(lib.esa_probe_mfma_bf16(
+            wg, iters, 0x3f80, vp(sink.data_ptr()), sink.numel(), stream), "mfma probe"),
+            steps, 3)
+        assert bool(torch.all(sink == 64.0 * 16 * iters)), "mfma probe result"
+        rates[per] = wg * 4 * iters * 4 * 32768 / (ms * 1e-3) / 1e12
+        del sink
+    per, tf, sweep = best(rates)
+    out["mfma_bf16"] = {"tflops": round(tf, 1), "workgroups_per_cu": per, "sweep": sweep,
+                        "published": PEAK_BF16_TFLOPS,
+                        "frac_of_published": round(tf / PEAK_BF16_TFLOPS, 4)}
+
+    nbytes = 4 << 30
+    src = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    rates = {}
+    for per in (1, 2, 3, 4, 32):
+        wg = per * cus
+        sink = torch.empty(wg * 256, dtype=torch.int32, device=dev)
+        ms = event_ms(torch, lambda: en.check(lib.esa_probe_hbm_read(
+            vp(src.data_ptr()), nbytes, wg, vp(sink.data_ptr()), sink.numel(), stream),
+            "hbm probe"), steps, 3)
+        assert int(sink.to(torch.int64).sum().item()) % (1 << 32) == \
+            (nbytes // 4) % (1 << 32), "hbm probe result"
+        rates[per] = nbytes / (ms * 1e-3) / 1e12
+        del sink
+    per, tbs, sweep = best(rates)
+    out["hbm_read"] = {"tbs": round(tbs, 3), "workgroups_per_cu": per, "sweep": sweep,
+                       "published": PEAK_HBM_GBS / 1e3,
+                       "frac_of_published": round(tbs * 1e3 / PEAK_HBM_GBS, 4)}
+    del src
+
+    a = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    ms = event_ms(torch, lambda: b.copy_(a), steps, 3)
+    out["copy"] = {"tbs_read_plus_write": round(2 * COPY_BYTES / (ms * 1e-3) / 1e12, 3)}
+    del a, b
+
+    region = 1 << 20
+    src = torch.full((region // 2,), 1, dtype=torch.int16, device=dev)
+    rates = {}
+    for per in (2, 5, 8):
+        wg, iters = per * cus, 2048 // per
+        sink = torch.empty(wg * 256, dtype=torch.int32, device=dev)
+        ms = event_ms(torch, lambda: en.check(lib.esa_probe_l2_to_lds(
+            vp(src.data_ptr()), region, wg, iters, vp(sink.data_ptr()), sink.numel(), stream),
+            "l2 probe"), steps, 3)
+        assert bool(torch.all(sink == 8)), "l2 probe result"
+        rates[per] = wg * iters * 16384 / (ms * 1e-3) / 1e12
+        del sink
+    per, tbs, sweep = best(rates)
+    out["l2_to_lds"] = {"tbs": round(tbs, 2), "workgroups_per_cu": per, "sweep": sweep,
+                        "bench_ceiling": L2_TO_CU_TBS}
+    print(json.dumps({"peaks": out}), flush=True)
 
 
 def event_ms(torch, fn, steps: int, warmup: int) -> float:
@@ -361,6 +443,8 @@ def main() -> None:
     ap.add_argument("--config-steps", type=int, default=20)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of known size (HBM counter scale)")
+    ap.add_argument("--peaks", action="store_true",
+                    help="run only the rate probes (bf16 MFMA, HBM read, copy, L2 -> LDS)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU: every box here has one, "
@@ -371,6 +455,9 @@ def main() -> None:
     import torch
     if args.copy_calibration:
         copy_calibration(torch)
+        return
+    if args.peaks:
+        peaks(torch)
         return
     from elastic_sparse_attention import ElasticSparseAttention, prefill_kernel
 

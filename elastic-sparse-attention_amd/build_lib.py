@@ -1,11 +1,12 @@
-"""Builds libesa.so (the HIP kernels and the C ABI) for gfx950 in place.
+"""Builds libesa.so (the HIP kernels and the C ABI) and libesa_probe.so (the
+rate probes bench.py --peaks runs) for gfx950 in place.
 
     python elastic-sparse-attention_amd/build_lib.py [-v]
 
 hipcc cross-compiles without a GPU.  Each source is compiled to an object
 (in parallel) under _build/ next to this file, then the objects are linked
-into libesa.so, which lands next to this file, where esa_native.py loads it
-from.
+into libesa.so and libesa_probe.so, which land next to this file, where
+esa_native.py loads them from.
 """
 from __future__ import annotations
 
@@ -21,7 +22,9 @@ BUILD = os.path.join(HERE, "_build")
 SOURCES = ["esa_capi.hip", "esa_layout.hip", "esa_fwd_tile.hip", "esa_fwd_band.hip",
            "esa_bwd_band.hip", "esa_fwd_gather.hip", "esa_bwd_gather.hip", "esa_bwd.hip",
            "esa_reach.hip"]
+PROBE_SOURCES = ["esa_probe.hip"]
 LIB = os.path.join(HERE, "libesa.so")
+PROBE_LIB = os.path.join(HERE, "libesa_probe.so")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
          # packed fp32 VALU forms are kept out of every kernel
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -56,20 +59,28 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    """Compiles every source and links libesa.so; returns its path."""
-    os.makedirs(BUILD, exist_ok=True)
-    workers = min(len(SOURCES), max(1, min(os.cpu_count() or 1, 8)))
-    with cf.ThreadPoolExecutor(workers) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
-    tmp = LIB + ".tmp"
+def _link(objs: list, lib: str, verbose: bool) -> None:
+    tmp = lib + ".tmp"
     cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError("linking libesa.so failed:\n" + "\n".join(_messages(res)))
-    os.replace(tmp, LIB)
+        raise RuntimeError(f"linking {os.path.basename(lib)} failed:\n" +
+                           "\n".join(_messages(res)))
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False) -> str:
+    """Compiles every source, links libesa.so and libesa_probe.so; returns
+    libesa.so's path."""
+    os.makedirs(BUILD, exist_ok=True)
+    srcs = SOURCES + PROBE_SOURCES
+    workers = min(len(srcs), max(1, min(os.cpu_count() or 1, 8)))
+    with cf.ThreadPoolExecutor(workers) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
+    _link(objs[:len(SOURCES)], LIB, verbose)
+    _link(objs[len(SOURCES):], PROBE_LIB, verbose)
     return LIB
 
 

@@ -1,0 +1,125 @@
+// Rate probes (gfx950): dense bf16 MFMA, HBM read, and L2 -> LDS through
+// the buffer_load ... lds path the MFMA kernels stage K and V with.  Built
+// into libesa_probe.so; declared in include/esa_probe.h.
+#include <hip/hip_runtime.h>
+
+#include "esa_probe.h"
+#include "esa_tile.hpp"
+
+namespace esa {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kChunk = 16384;  // bytes one workgroup round moves (256 lanes x 4 x 16 B)
+// s_waitcnt with vmcnt(8) and the other counters left alone (gfx9 encoding)
+constexpr int kWaitVmcnt8 = 0x0F78;
+
+__global__ __launch_bounds__(kThreads) void mfma_probe_kernel(int iters, uint16_t one, float* sink) {
+  bf16x8 a;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a[e] = __builtin_bit_cast(__bf16, one);
+  f32x16 c[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) c[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, a, c[j], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += c[j][r];
+  sink[(int64_t)blockIdx.x * kThreads + threadIdx.x] = s;
+}
+
+__global__ __launch_bounds__(kThreads) void l2_lds_probe_kernel(const uint16_t* src, int n_chunks,
+                                                                int iters, uint32_t* sink) {
+  __shared__ __attribute__((aligned(1024))) uint16_t buf0[kChunk / 2];
+  __shared__ __attribute__((aligned(1024))) uint16_t buf1[kChunk / 2];
+  const int t = threadIdx.x, wave = t >> 6;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)src, (short)0, n_chunks * kChunk, 0x00020000);
+  for (int i = 0; i < iters; ++i) {
+    const int c = (int)(((int64_t)blockIdx.x * 7 + i) % n_chunks);
+    uint16_t* dst = (i & 1) ? buf1 : buf0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)  // load j: bytes (256 j + t) * 16 of the chunk
+      load_lds16(rs, dst + (j * kThreads + wave * 64) * 8, (j * kThreads + t) * 16, c * kChunk);
+    // at most the last two rounds in flight: the round that wrote this
+    // buffer before has landed
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt8);
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+  const uint16_t* last = ((iters - 1) & 1) ? buf1 : buf0;
+  const u32x4 w = *(const u32x4*)(last + t * 8);  // load 0 of thread t
+  uint32_t s = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) s += (w[e] & 0xffffu) + (w[e] >> 16);
+  sink[(int64_t)blockIdx.x * kThreads + t] = s;
+}
+
+__global__ __launch_bounds__(kThreads) void hbm_read_probe_kernel(const u32x4* src, int64_t n16,
+                                                                  uint32_t* sink) {
+  const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * kThreads;
+  uint32_t acc = 0;
+  int64_t k = gid;
+  // four loads in flight per thread
+  for (; k + 3 * stride < n16; k += 4 * stride) {
+    u32x4 x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = __builtin_nontemporal_load(src + k + u * stride);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc += x[u][0] + x[u][1] + x[u][2] + x[u][3];
+  }
+  for (; k < n16; k += stride) {
+    const u32x4 x = __builtin_nontemporal_load(src + k);
+    acc += x[0] + x[1] + x[2] + x[3];
+  }
+  sink[gid] = acc;
+}
+
+esa_status launched() { return hipGetLastError() == hipSuccess ? ESA_OK : ESA_ERR_HIP; }
+
+}  // namespace
+}  // namespace esa
+
+using namespace esa;
+
+extern "C" {
+
+esa_status esa_probe_mfma_bf16(int32_t workgroups, int32_t iters, uint16_t one, float* sink,
+                               int64_t sink_elems, void* stream) {
+  if (!sink) return ESA_ERR_NULL;
+  if (workgroups < 1 || workgroups > (1 << 20) || iters < 1 || iters > 16384) return ESA_ERR_SHAPE;
+  if (sink_elems < (int64_t)workgroups * kThreads) return ESA_ERR_CAPACITY;
+  mfma_probe_kernel<<<workgroups, kThreads, 0, (hipStream_t)stream>>>(iters, one, sink);
+  return launched();
+}
+
+esa_status esa_probe_l2_to_lds(const void* src, int64_t region_bytes, int32_t workgroups,
+                               int32_t iters, uint32_t* sink, int64_t sink_elems, void* stream) {
+  if (!src || !sink) return ESA_ERR_NULL;
+  if (region_bytes < kChunk || region_bytes % kChunk != 0 || region_bytes >= (int64_t(1) << 31) ||
+      workgroups < 1 || workgroups > (1 << 20) || iters < 1 || iters > (1 << 20))
+    return ESA_ERR_SHAPE;
+  if ((uintptr_t)src % 16 != 0) return ESA_ERR_ALIGN;
+  if (sink_elems < (int64_t)workgroups * kThreads) return ESA_ERR_CAPACITY;
+  l2_lds_probe_kernel<<<workgroups, kThreads, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)src, (int)(region_bytes / kChunk), iters, sink);
+  return launched();
+}
+
+esa_status esa_probe_hbm_read(const void* src, int64_t bytes, int32_t workgroups, uint32_t* sink,
+                              int64_t sink_elems, void* stream) {
+  if (!src || !sink) return ESA_ERR_NULL;
+  if (bytes < 64 || bytes % 64 != 0 || workgroups < 1 || workgroups > (1 << 20))
+    return ESA_ERR_SHAPE;
+  if ((uintptr_t)src % 16 != 0) return ESA_ERR_ALIGN;
+  if (sink_elems < (int64_t)workgroups * kThreads) return ESA_ERR_CAPACITY;
+  hbm_read_probe_kernel<<<workgroups, kThreads, 0, (hipStream_t)stream>>>(
+      (const u32x4*)src, bytes / 16, sink);
+  return launched();
+}
+
+}  // extern "C"

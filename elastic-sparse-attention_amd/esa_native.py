@@ -12,6 +12,7 @@ from typing import Optional
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libesa.so")
+PROBE_LIB_PATH = os.path.join(HERE, "libesa_probe.so")
 
 ESA_OK = 0
 ESA_ERR_NULL = 1
@@ -178,6 +179,32 @@ def load() -> ctypes.CDLL:
     lib.esa_reachability.restype = st
     lib.esa_reachability.argtypes = [i32, i32, i32, i32, i32, vp, vp, vp, vp]
     _lib = lib
+    return lib
+
+
+PROBE_EXPORTED = ("esa_probe_mfma_bf16", "esa_probe_l2_to_lds", "esa_probe_hbm_read")
+_probe: Optional[ctypes.CDLL] = None
+
+
+def load_probe() -> ctypes.CDLL:
+    """Loads libesa_probe.so (include/esa_probe.h: the rate probes bench.py
+    --peaks runs) once and declares its entry points."""
+    global _probe
+    if _probe is not None:
+        return _probe
+    if not os.path.exists(PROBE_LIB_PATH):
+        raise RuntimeError(
+            f"{PROBE_LIB_PATH} is missing: build it with "
+            "`python elastic-sparse-attention_amd/build_lib.py` (hipcc, gfx950)")
+    lib = ctypes.CDLL(PROBE_LIB_PATH)
+    st, vp, i32, i64 = ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64
+    lib.esa_probe_mfma_bf16.restype = st
+    lib.esa_probe_mfma_bf16.argtypes = [i32, i32, ctypes.c_uint16, vp, i64, vp]
+    lib.esa_probe_l2_to_lds.restype = st
+    lib.esa_probe_l2_to_lds.argtypes = [vp, i64, i32, i32, vp, i64, vp]
+    lib.esa_probe_hbm_read.restype = st
+    lib.esa_probe_hbm_read.argtypes = [vp, i64, i32, vp, i64, vp]
+    _probe = lib
     return lib
 
 

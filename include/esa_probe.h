@@ -1,0 +1,61 @@
+/*
+ * Rate probes for MI355X (gfx950) -- C ABI of libesa_probe.so.
+ *
+ * No counterpart in the reference: these measure, on the GPU they run on,
+ * the rates the attention kernels are judged against -- dense bf16 MFMA
+ * throughput, HBM read bandwidth, and the L2 -> LDS rate of the
+ * buffer_load ... lds path the MFMA kernels stage K and V through.  They
+ * are measurement tools (bench.py --peaks), not part of the attention path,
+ * and live in their own library so libesa.so's interface stays the drop-in
+ * one.
+ *
+ * Conventions are those of esa.h: an esa_status per call, arguments checked
+ * on the host before any launch, device pointers owned by the caller,
+ * asynchronous launches on `stream` (a hipStream_t as void*).  Each probe
+ * writes one value per thread to `sink` (workgroups x 256 entries, capacity
+ * `sink_elems`) so its work cannot be optimised away, and the value is a
+ * closed form of the inputs the caller can check.
+ */
+#ifndef ESA_PROBE_H_
+#define ESA_PROBE_H_
+
+#include "esa.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Dense bf16 MFMA: each wave of `workgroups` 256-thread workgroups runs
+ * `iters` rounds of four independent v_mfma_f32_32x32x16_bf16 chains on
+ * operands held in registers (A and B all equal to `one`, a bf16 bit
+ * pattern, so the compiler cannot fold them).  Work = workgroups * 4 waves
+ * * iters * 4 * 32768 flop.  sink[t] = 64 * 16 * iters * one^2 (float), exact
+ * for one = 1.0 and iters <= 16384.  workgroups in [1, 2^20], iters in
+ * [1, 16384]. */
+esa_status esa_probe_mfma_bf16(int32_t workgroups, int32_t iters, uint16_t one, float* sink,
+                               int64_t sink_elems, void* stream);
+
+/* L2 -> LDS through buffer_load_dwordx4 ... lds, the MFMA kernels' staging
+ * path: each workgroup copies `iters` 16 KB chunks of the `region_bytes`
+ * region at src (chunk (workgroup * 7 + i) mod region_bytes / 16384) into
+ * two LDS buffers, two chunks in flight.  A region of a few MB stays
+ * resident in every XCD's L2, so the rate is L2 -> CU.  Bytes moved =
+ * workgroups * iters * 16384.  sink[t] = the sum of the eight 16-bit words
+ * thread t's last DMA wrote to LDS (as uint32).  region_bytes a multiple of
+ * 16384 in [16384, 2^31), src 16-byte aligned, workgroups in [1, 2^20],
+ * iters in [1, 2^20]. */
+esa_status esa_probe_l2_to_lds(const void* src, int64_t region_bytes, int32_t workgroups,
+                               int32_t iters, uint32_t* sink, int64_t sink_elems, void* stream);
+
+/* HBM read: `workgroups` 256-thread workgroups stream `bytes` of src once
+ * (16-byte loads, grid-stride, four in flight per thread) and sum the
+ * 32-bit words each thread read, modulo 2^32, into sink[t].  bytes a
+ * positive multiple of 64, src 16-byte aligned, workgroups in [1, 2^20]. */
+esa_status esa_probe_hbm_read(const void* src, int64_t bytes, int32_t workgroups, uint32_t* sink,
+                              int64_t sink_elems, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ESA_PROBE_H_ */

@@ -15,8 +15,8 @@ from esa_oracle import block_layout, elastic_indices
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def header_functions():
-    text = open(os.path.join(ROOT, "include", "esa.h")).read()
+def header_functions(name="esa.h"):
+    text = open(os.path.join(ROOT, "include", name)).read()
     return re.findall(r"^(?:esa_status|const char\*|size_t)\s+(esa_\w+)\(", text, re.M)
 
 
@@ -29,6 +29,27 @@ def test_library_exports_header_symbols():
     assert set(names) == set(en.EXPORTED)
     assert lib.esa_version().decode().startswith("esa-gfx950")
     assert lib.esa_status_string(en.ESA_ERR_ALIGN).decode() == "misaligned pointer or stride"
+
+
+def test_probe_library_exports_and_rejects():
+    """libesa_probe.so exports what include/esa_probe.h declares and checks
+    its arguments on the host (nothing is launched)."""
+    lib = en.load_probe()
+    names = header_functions("esa_probe.h")
+    assert set(names) == set(en.PROBE_EXPORTED)
+    fake = ctypes.c_void_p(4096)
+    assert lib.esa_probe_mfma_bf16(8, 16, 0x3f80, None, 2048, None) == en.ESA_ERR_NULL
+    assert lib.esa_probe_mfma_bf16(0, 16, 0x3f80, fake, 2048, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_mfma_bf16(8, 16385, 0x3f80, fake, 2048, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_mfma_bf16(8, 16, 0x3f80, fake, 2047, None) == en.ESA_ERR_CAPACITY
+    assert lib.esa_probe_l2_to_lds(fake, 16384 * 3 + 1, 8, 4, fake, 2048, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_l2_to_lds(fake, 1 << 31, 8, 4, fake, 2048, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_l2_to_lds(ctypes.c_void_p(4100), 16384, 8, 4, fake, 2048, None) \
+        == en.ESA_ERR_ALIGN
+    assert lib.esa_probe_l2_to_lds(fake, 16384, 8, 4, fake, 100, None) == en.ESA_ERR_CAPACITY
+    assert lib.esa_probe_hbm_read(fake, 100, 8, fake, 2048, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_hbm_read(None, 128, 8, fake, 2048, None) == en.ESA_ERR_NULL
+    assert lib.esa_probe_hbm_read(fake, 128, 8, fake, 2047, None) == en.ESA_ERR_CAPACITY
 
 
 def pat(L=32768, w=64, layer=4, nl=8, H=32, bm=128, bn=128):

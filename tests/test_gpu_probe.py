@@ -1,0 +1,52 @@
+"""The rate probes of libesa_probe.so (GPU): each writes a closed form of its
+inputs per thread, which pins that the work the rate is computed from was
+done (bench.py --peaks times them)."""
+import ctypes
+
+import pytest
+import torch
+
+import esa_native as en
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream)
+
+
+def test_mfma_probe_closed_form():
+    lib = en.load_probe()
+    wg, iters = 64, 100
+    sink = torch.full((wg * 256,), -1.0, dtype=torch.float32, device=DEV)
+    en.check(lib.esa_probe_mfma_bf16(wg, iters, 0x3f80, ctypes.c_void_p(sink.data_ptr()),
+                                     sink.numel(), _stream()), "esa_probe_mfma_bf16")
+    torch.cuda.synchronize()
+    # 4 chains x 16 accumulators per lane, each + 16 per MFMA (1.0 x 1.0 over k = 16)
+    assert torch.all(sink == 64.0 * 16 * iters)
+
+
+def test_l2_to_lds_probe_closed_form():
+    lib = en.load_probe()
+    wg, iters, region = 48, 37, 16384 * 5
+    src = torch.full((region // 2,), 3, dtype=torch.int16, device=DEV)
+    sink = torch.zeros(wg * 256, dtype=torch.int32, device=DEV)
+    en.check(lib.esa_probe_l2_to_lds(ctypes.c_void_p(src.data_ptr()), region, wg, iters,
+                                     ctypes.c_void_p(sink.data_ptr()), sink.numel(), _stream()),
+             "esa_probe_l2_to_lds")
+    torch.cuda.synchronize()
+    assert torch.all(sink == 8 * 3)
+
+
+def test_hbm_read_probe_closed_form():
+    lib = en.load_probe()
+    wg, n = 40, (1 << 20) + 48  # words: not a multiple of the grid, tail loop taken
+    src = torch.arange(n, dtype=torch.int32, device=DEV)
+    sink = torch.zeros(wg * 256, dtype=torch.int32, device=DEV)
+    en.check(lib.esa_probe_hbm_read(ctypes.c_void_p(src.data_ptr()), n * 4, wg,
+                                    ctypes.c_void_p(sink.data_ptr()), sink.numel(), _stream()),
+             "esa_probe_hbm_read")
+    torch.cuda.synchronize()
+    total = int(sink.to(torch.int64).sum().item()) % (1 << 32)
+    assert total == (n * (n - 1) // 2) % (1 << 32)
