@@ -141,7 +141,8 @@ def peaks(torch, steps: int = 10) -> None:
     shape: dense bf16 MFMA (four independent 32x32x16 chains per wave), HBM
     read (a 4 GiB buffer streamed once), a device copy (1 GiB, read +
     write), and L2 -> LDS through buffer_load ... lds (a 1 MiB region every
-    XCD's L2 holds, 16 KB rounds per workgroup, two in flight)."""
+    XCD's L2 holds, 16 KB rounds per workgroup, two in flight) and HBM ->
+    LDS through the same path (a 2 GiB region read once)."""
     import ctypes
     import esa_native as en
     lib = en.load_probe()
@@ -202,14 +203,32 @@ def peaks(torch, steps: int = 10) -> None:
         wg, iters = per * cus, 2048 // per
         sink = torch.empty(wg * 256, dtype=torch.int32, device=dev)
         ms = event_ms(torch, lambda: en.check(lib.esa_probe_l2_to_lds(
-            vp(src.data_ptr()), region, wg, iters, vp(sink.data_ptr()), sink.numel(), stream),
-            "l2 probe"), steps, 3)
+            vp(src.data_ptr()), region, wg, iters, 7, vp(sink.data_ptr()), sink.numel(),
+            stream), "l2 probe"), steps, 3)
         assert bool(torch.all(sink == 8)), "l2 probe result"
         rates[per] = wg * iters * 16384 / (ms * 1e-3) / 1e12
         del sink
     per, tbs, sweep = best(rates)
     out["l2_to_lds"] = {"tbs": round(tbs, 2), "workgroups_per_cu": per, "sweep": sweep,
                         "bench_ceiling": L2_TO_CU_TBS}
+    del src
+
+    # the same DMA path from HBM: a 2 GiB region, each chunk read once
+    region = (1 << 31) - 16384
+    src = torch.full((region // 2,), 1, dtype=torch.int16, device=dev)
+    rates = {}
+    for per in (2, 4, 8):
+        wg = per * cus
+        iters = region // 16384 // wg
+        sink = torch.empty(wg * 256, dtype=torch.int32, device=dev)
+        ms = event_ms(torch, lambda: en.check(lib.esa_probe_l2_to_lds(
+            vp(src.data_ptr()), region, wg, iters, iters, vp(sink.data_ptr()), sink.numel(),
+            stream), "hbm -> lds probe"), steps, 3)
+        assert bool(torch.all(sink == 8)), "hbm -> lds probe result"
+        rates[per] = wg * iters * 16384 / (ms * 1e-3) / 1e12
+        del sink
+    per, tbs, sweep = best(rates)
+    out["hbm_to_lds"] = {"tbs": round(tbs, 3), "workgroups_per_cu": per, "sweep": sweep}
     print(json.dumps({"peaks": out}), flush=True)
 
 

@@ -1,6 +1,6 @@
-// Rate probes (gfx950): dense bf16 MFMA, HBM read, and L2 -> LDS through
-// the buffer_load ... lds path the MFMA kernels stage K and V with.  Built
-// into libesa_probe.so; declared in include/esa_probe.h.
+// Rate probes (gfx950): dense bf16 MFMA, HBM read, and L2 -> LDS or HBM ->
+// LDS through the buffer_load ... lds path the MFMA kernels stage K and V
+// with.  Built into libesa_probe.so; declared in include/esa_probe.h.
 #include <hip/hip_runtime.h>
 
 #include "esa_probe.h"
@@ -32,14 +32,15 @@ __global__ __launch_bounds__(kThreads) void mfma_probe_kernel(int iters, uint16_
 }
 
 __global__ __launch_bounds__(kThreads) void l2_lds_probe_kernel(const uint16_t* src, int n_chunks,
-                                                                int iters, uint32_t* sink) {
+                                                                int iters, int chunk_stride,
+                                                                uint32_t* sink) {
   __shared__ __attribute__((aligned(1024))) uint16_t buf0[kChunk / 2];
   __shared__ __attribute__((aligned(1024))) uint16_t buf1[kChunk / 2];
   const int t = threadIdx.x, wave = t >> 6;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       (void*)src, (short)0, n_chunks * kChunk, 0x00020000);
   for (int i = 0; i < iters; ++i) {
-    const int c = (int)(((int64_t)blockIdx.x * 7 + i) % n_chunks);
+    const int c = (int)(((int64_t)blockIdx.x * chunk_stride + i) % n_chunks);
     uint16_t* dst = (i & 1) ? buf1 : buf0;
 #pragma unroll
     for (int j = 0; j < 4; ++j)  // load j: bytes (256 j + t) * 16 of the chunk
@@ -98,15 +99,17 @@ esa_status esa_probe_mfma_bf16(int32_t workgroups, int32_t iters, uint16_t one, 
 }
 
 esa_status esa_probe_l2_to_lds(const void* src, int64_t region_bytes, int32_t workgroups,
-                               int32_t iters, uint32_t* sink, int64_t sink_elems, void* stream) {
+                               int32_t iters, int32_t chunk_stride, uint32_t* sink,
+                               int64_t sink_elems, void* stream) {
   if (!src || !sink) return ESA_ERR_NULL;
   if (region_bytes < kChunk || region_bytes % kChunk != 0 || region_bytes >= (int64_t(1) << 31) ||
-      workgroups < 1 || workgroups > (1 << 20) || iters < 1 || iters > (1 << 20))
+      workgroups < 1 || workgroups > (1 << 20) || iters < 1 || iters > (1 << 20) ||
+      chunk_stride < 0 || chunk_stride > (1 << 20))
     return ESA_ERR_SHAPE;
   if ((uintptr_t)src % 16 != 0) return ESA_ERR_ALIGN;
   if (sink_elems < (int64_t)workgroups * kThreads) return ESA_ERR_CAPACITY;
   l2_lds_probe_kernel<<<workgroups, kThreads, 0, (hipStream_t)stream>>>(
-      (const uint16_t*)src, (int)(region_bytes / kChunk), iters, sink);
+      (const uint16_t*)src, (int)(region_bytes / kChunk), iters, chunk_stride, sink);
   return launched();
 }
 

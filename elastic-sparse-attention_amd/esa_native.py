@@ -201,7 +201,7 @@ def load_probe() -> ctypes.CDLL:
     lib.esa_probe_mfma_bf16.restype = st
     lib.esa_probe_mfma_bf16.argtypes = [i32, i32, ctypes.c_uint16, vp, i64, vp]
     lib.esa_probe_l2_to_lds.restype = st
-    lib.esa_probe_l2_to_lds.argtypes = [vp, i64, i32, i32, vp, i64, vp]
+    lib.esa_probe_l2_to_lds.argtypes = [vp, i64, i32, i32, i32, vp, i64, vp]
     lib.esa_probe_hbm_read.restype = st
     lib.esa_probe_hbm_read.argtypes = [vp, i64, i32, vp, i64, vp]
     _probe = lib

@@ -35,17 +35,20 @@ extern "C" {
 esa_status esa_probe_mfma_bf16(int32_t workgroups, int32_t iters, uint16_t one, float* sink,
                                int64_t sink_elems, void* stream);
 
-/* L2 -> LDS through buffer_load_dwordx4 ... lds, the MFMA kernels' staging
- * path: each workgroup copies `iters` 16 KB chunks of the `region_bytes`
- * region at src (chunk (workgroup * 7 + i) mod region_bytes / 16384) into
- * two LDS buffers, two chunks in flight.  A region of a few MB stays
- * resident in every XCD's L2, so the rate is L2 -> CU.  Bytes moved =
+/* Global memory -> LDS through buffer_load_dwordx4 ... lds, the MFMA
+ * kernels' staging path: each workgroup copies `iters` 16 KB chunks of the
+ * `region_bytes` region at src (chunk (workgroup * chunk_stride + i) mod
+ * region_bytes / 16384) into two LDS buffers, two chunks in flight.  A
+ * region of a few MB with a small chunk_stride stays resident in every
+ * XCD's L2, so the rate is L2 -> CU; a region larger than the caches read
+ * once (chunk_stride = iters) gives the HBM -> LDS rate.  Bytes moved =
  * workgroups * iters * 16384.  sink[t] = the sum of the eight 16-bit words
  * thread t's last DMA wrote to LDS (as uint32).  region_bytes a multiple of
  * 16384 in [16384, 2^31), src 16-byte aligned, workgroups in [1, 2^20],
- * iters in [1, 2^20]. */
+ * iters in [1, 2^20], chunk_stride in [0, 2^20]. */
 esa_status esa_probe_l2_to_lds(const void* src, int64_t region_bytes, int32_t workgroups,
-                               int32_t iters, uint32_t* sink, int64_t sink_elems, void* stream);
+                               int32_t iters, int32_t chunk_stride, uint32_t* sink,
+                               int64_t sink_elems, void* stream);
 
 /* HBM read: `workgroups` 256-thread workgroups stream `bytes` of src once
  * (16-byte loads, grid-stride, four in flight per thread) and sum the

@@ -42,11 +42,13 @@ def test_probe_library_exports_and_rejects():
     assert lib.esa_probe_mfma_bf16(0, 16, 0x3f80, fake, 2048, None) == en.ESA_ERR_SHAPE
     assert lib.esa_probe_mfma_bf16(8, 16385, 0x3f80, fake, 2048, None) == en.ESA_ERR_SHAPE
     assert lib.esa_probe_mfma_bf16(8, 16, 0x3f80, fake, 2047, None) == en.ESA_ERR_CAPACITY
-    assert lib.esa_probe_l2_to_lds(fake, 16384 * 3 + 1, 8, 4, fake, 2048, None) == en.ESA_ERR_SHAPE
-    assert lib.esa_probe_l2_to_lds(fake, 1 << 31, 8, 4, fake, 2048, None) == en.ESA_ERR_SHAPE
-    assert lib.esa_probe_l2_to_lds(ctypes.c_void_p(4100), 16384, 8, 4, fake, 2048, None) \
+    assert lib.esa_probe_l2_to_lds(fake, 16384 * 3 + 1, 8, 4, 7, fake, 2048, None) \
+        == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_l2_to_lds(fake, 1 << 31, 8, 4, 7, fake, 2048, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_l2_to_lds(fake, 16384, 8, 4, -1, fake, 2048, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_l2_to_lds(ctypes.c_void_p(4100), 16384, 8, 4, 7, fake, 2048, None) \
         == en.ESA_ERR_ALIGN
-    assert lib.esa_probe_l2_to_lds(fake, 16384, 8, 4, fake, 100, None) == en.ESA_ERR_CAPACITY
+    assert lib.esa_probe_l2_to_lds(fake, 16384, 8, 4, 7, fake, 100, None) == en.ESA_ERR_CAPACITY
     assert lib.esa_probe_hbm_read(fake, 100, 8, fake, 2048, None) == en.ESA_ERR_SHAPE
     assert lib.esa_probe_hbm_read(None, 128, 8, fake, 2048, None) == en.ESA_ERR_NULL
     assert lib.esa_probe_hbm_read(fake, 128, 8, fake, 2047, None) == en.ESA_ERR_CAPACITY

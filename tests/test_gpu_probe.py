@@ -32,11 +32,13 @@ def test_l2_to_lds_probe_closed_form():
     wg, iters, region = 48, 37, 16384 * 5
     src = torch.full((region // 2,), 3, dtype=torch.int16, device=DEV)
     sink = torch.zeros(wg * 256, dtype=torch.int32, device=DEV)
-    en.check(lib.esa_probe_l2_to_lds(ctypes.c_void_p(src.data_ptr()), region, wg, iters,
-                                     ctypes.c_void_p(sink.data_ptr()), sink.numel(), _stream()),
-             "esa_probe_l2_to_lds")
-    torch.cuda.synchronize()
-    assert torch.all(sink == 8 * 3)
+    for stride in (7, iters):
+        sink.zero_()
+        en.check(lib.esa_probe_l2_to_lds(ctypes.c_void_p(src.data_ptr()), region, wg, iters,
+                                         stride, ctypes.c_void_p(sink.data_ptr()), sink.numel(),
+                                         _stream()), "esa_probe_l2_to_lds")
+        torch.cuda.synchronize()
+        assert torch.all(sink == 8 * 3)
 
 
 def test_hbm_read_probe_closed_form():
