@@ -128,14 +128,18 @@ __global__ __launch_bounds__(256) void tile_mask_kernel(PatternConsts pc, const 
 
 // ---------------------------------------------------------------------------
 // dK, dV of one (batch, kv head, 128-key block): 8 waves, one workgroup per
-// CU.  The block's K and V rows are staged into LDS once (64 KB at D = 128)
-// and read as MFMA operands from there, so each wave keeps only its dK^T and
-// dV^T accumulators resident and two waves share each SIMD.  Wave w owns
+// CU at D = 128.  The block's K and V rows are staged into LDS once (64 KB at
+// D = 128) and read as MFMA operands from there, so each wave keeps only its
+// dK^T and dV^T accumulators resident and two waves share each SIMD.  At
+// D = 64 the workgroup takes 66.5 KB of LDS and the launch bound holds it to
+// 128 VGPRs (four spilled: one 8-byte reload per key-block tile), so two
+// workgroups share a CU: 7-12% faster than one at 133 VGPRs (B=8 H=16 L=4096 and B=4 H=32
+// L=4096, layers 0-5), the same bits.  Wave w owns
 // keys 32 (w % 4) .. + 31 of the block and the 32-row half w / 4 of every
 // 64-row Q / dO stage; the two halves' partial sums are added through LDS at
 // the end, in a fixed order.
 template <int D, Elem E>
-__global__ __launch_bounds__(512, 1) void dkdv_kernel(BwdArgs A, const float* lse2) {
+__global__ __launch_bounds__(512, D == 64 ? 4 : 1) void dkdv_kernel(BwdArgs A, const float* lse2) {
   using M = MmaT<E>;
   using V8 = typename M::v8;
   using C = BwdCfg<D>;

@@ -390,10 +390,16 @@ MFMA_DTYPES = (torch.bfloat16, torch.float16)
 # runs put the band kernel 3.5% ahead at 18.7 (L=8192 layer 4) and the tile
 # kernel 3% ahead at 19.0 (L=16384 layer 2).  At D = 64 the tile kernel is
 # faster up to 14.0 (L=4096 layer 6, by 1%), the band kernel from 15.5 (by
-# 6%).  Backward (both halves of a kind): between 14.4 and 18.7 at D = 128,
-# 11.9 and 14.0 at D = 64.
+# 6%).  Backward, each half on its own (all four dQ / dK-dV pairs timed at
+# every dilated layer of B=1 H=32 L=8192 with 32 and 8 kv heads, B=8 H=16
+# L=4096, B=4 H=32/8 L=4096, B=4 H=16 L=8192 with 16 and 4 kv heads and B=2
+# H=16 L=16384): at D = 128 both halves switch between 14.4 and 18.7; at
+# D = 64 the tile dQ is faster up to 14.0 (by 1.3%) and even at 14.4, the
+# band dQ from 15.5; the tile dK/dV up to 15.5 (by 6-17%), the band dK/dV
+# from 18.7.
 BAND_CROSSOVER = {128: 18.5, 64: 14.75}
-BWD_BAND_CROSSOVER = {128: 16.5, 64: 12.5}
+BWD_DQ_CROSSOVER = {128: 16.5, 64: 14.5}
+BWD_DKDV_CROSSOVER = {128: 16.5, 64: 17.0}
 
 
 def _band_beats_tile(layout: ElasticLayout, q_len: int, batch: int, head_dim: int,
@@ -415,12 +421,11 @@ def prefill_kernel(layout: ElasticLayout, q_len: int, batch: int, head_dim: int)
 def bwd_kernels(layout: ElasticLayout, q_len: int, batch: int, head_dim: int
                 ) -> Tuple[str, str]:
     """("band" | "tile", "band" | "tile"): the faster dQ and dK/dV kernels for
-    this pattern and shape.  Both halves are of one kind: over every layer of
-    six shapes (D = 64 and 128, GQA included) the fastest pair was one kind
-    for both halves or within 1% of it, switching at BWD_BAND_CROSSOVER."""
-    band = _band_beats_tile(layout, q_len, batch, head_dim, BWD_BAND_CROSSOVER)
-    kind = "band" if band else "tile"
-    return kind, kind
+    this pattern and shape, each half switching to its band kernel at its own
+    measured crossover (BWD_DQ_CROSSOVER, BWD_DKDV_CROSSOVER)."""
+    dq = _band_beats_tile(layout, q_len, batch, head_dim, BWD_DQ_CROSSOVER)
+    dkdv = _band_beats_tile(layout, q_len, batch, head_dim, BWD_DKDV_CROSSOVER)
+    return "band" if dq else "tile", "band" if dkdv else "tile"
 
 
 def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
