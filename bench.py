@@ -142,7 +142,8 @@ def peaks(torch, steps: int = 10) -> None:
     read (a 4 GiB buffer streamed once), a device copy (1 GiB, read +
     write), and L2 -> LDS through buffer_load ... lds (a 1 MiB region every
     XCD's L2 holds, 16 KB rounds per workgroup, two in flight) and HBM ->
-    LDS through the same path (a 2 GiB region read once)."""
+    LDS through the same path (a 2 GiB region read once), and 256-byte row
+    gathers at random positions (the decode step's access pattern)."""
     import ctypes
     import esa_native as en
     lib = en.load_probe()
@@ -229,6 +230,29 @@ def peaks(torch, steps: int = 10) -> None:
         del sink
     per, tbs, sweep = best(rates)
     out["hbm_to_lds"] = {"tbs": round(tbs, 3), "workgroups_per_cu": per, "sweep": sweep}
+    del src
+
+    # 256-byte row gathers at random positions of a 4 GiB region (the decode
+    # step's access pattern: 524288 rows, as B=128 x H=32 x 64 K and V rows)
+    src_rows = (4 << 30) // 256
+    src = torch.ones(src_rows * 64, dtype=torch.int32, device=dev)
+    n = 128 * 32 * 64 * 2
+    g = torch.Generator(device=dev).manual_seed(11)
+    rows = torch.randint(0, src_rows, (n,), generator=g, device=dev, dtype=torch.int32)
+    rates = {}
+    for per in (2, 4, 8):
+        wg = per * cus
+        sink = torch.empty(wg * 256, dtype=torch.int32, device=dev)
+        ms = event_ms(torch, lambda: en.check(lib.esa_probe_gather_read(
+            vp(src.data_ptr()), src_rows, vp(rows.data_ptr()), n, wg, vp(sink.data_ptr()),
+            sink.numel(), stream), "gather probe"), steps, 3)
+        assert int(sink.to(torch.int64).sum().item()) % (1 << 32) == (n * 64) % (1 << 32), \
+            "gather probe result"
+        rates[per] = n * 256 / (ms * 1e-3) / 1e12
+        del sink
+    per, tbs, sweep = best(rates)
+    out["hbm_gather_256b"] = {"tbs": round(tbs, 3), "workgroups_per_cu": per, "sweep": sweep,
+                              "rows": n}
     print(json.dumps({"peaks": out}), flush=True)
 
 

@@ -1,6 +1,7 @@
-// Rate probes (gfx950): dense bf16 MFMA, HBM read, and L2 -> LDS or HBM ->
-// LDS through the buffer_load ... lds path the MFMA kernels stage K and V
-// with.  Built into libesa_probe.so; declared in include/esa_probe.h.
+// Rate probes (gfx950): dense bf16 MFMA, HBM read, L2 -> LDS or HBM -> LDS
+// through the buffer_load ... lds path the MFMA kernels stage K and V with,
+// and 256-byte row gathers from HBM (the decode step's access pattern).
+// Built into libesa_probe.so; declared in include/esa_probe.h.
 #include <hip/hip_runtime.h>
 
 #include "esa_probe.h"
@@ -80,6 +81,31 @@ __global__ __launch_bounds__(kThreads) void hbm_read_probe_kernel(const u32x4* s
   sink[gid] = acc;
 }
 
+__global__ __launch_bounds__(kThreads) void gather_probe_kernel(const u32x4* src, int64_t src_rows,
+                                                                const int32_t* rows,
+                                                                int64_t n_rows, uint32_t* sink) {
+  const int lane = threadIdx.x & 63;
+  const int sub = lane >> 4, part = lane & 15;  // row of an instruction, 16-byte piece
+  const int64_t gid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int64_t wave_id = gid >> 6, n_waves = (int64_t)gridDim.x * (kThreads / 64);
+  uint32_t acc = 0;
+  // each round of a wave: 8 instructions x 4 rows
+  for (int64_t base = wave_id * 32; base < n_rows; base += n_waves * 32) {
+    u32x4 x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t r = base + 4 * u + sub;
+      int64_t row = r < n_rows ? rows[r] : 0;
+      row = row < 0 ? 0 : (row >= src_rows ? src_rows - 1 : row);
+      x[u] = src[row * 16 + part];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (base + 4 * u + sub < n_rows) acc += x[u][0] + x[u][1] + x[u][2] + x[u][3];
+  }
+  sink[gid] = acc;
+}
+
 esa_status launched() { return hipGetLastError() == hipSuccess ? ESA_OK : ESA_ERR_HIP; }
 
 }  // namespace
@@ -122,6 +148,19 @@ esa_status esa_probe_hbm_read(const void* src, int64_t bytes, int32_t workgroups
   if (sink_elems < (int64_t)workgroups * kThreads) return ESA_ERR_CAPACITY;
   hbm_read_probe_kernel<<<workgroups, kThreads, 0, (hipStream_t)stream>>>(
       (const u32x4*)src, bytes / 16, sink);
+  return launched();
+}
+
+esa_status esa_probe_gather_read(const void* src, int64_t src_rows, const int32_t* rows,
+                                 int64_t n_rows, int32_t workgroups, uint32_t* sink,
+                                 int64_t sink_elems, void* stream) {
+  if (!src || !rows || !sink) return ESA_ERR_NULL;
+  if (src_rows < 1 || n_rows < 1 || workgroups < 1 || workgroups > (1 << 20))
+    return ESA_ERR_SHAPE;
+  if ((uintptr_t)src % 16 != 0 || (uintptr_t)rows % 4 != 0) return ESA_ERR_ALIGN;
+  if (sink_elems < (int64_t)workgroups * kThreads) return ESA_ERR_CAPACITY;
+  gather_probe_kernel<<<workgroups, kThreads, 0, (hipStream_t)stream>>>(
+      (const u32x4*)src, src_rows, rows, n_rows, sink);
   return launched();
 }
 

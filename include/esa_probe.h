@@ -57,6 +57,17 @@ esa_status esa_probe_l2_to_lds(const void* src, int64_t region_bytes, int32_t wo
 esa_status esa_probe_hbm_read(const void* src, int64_t bytes, int32_t workgroups, uint32_t* sink,
                               int64_t sink_elems, void* stream);
 
+/* HBM gather: `workgroups` 256-thread workgroups read the n_rows rows
+ * rows[0 .. n_rows) (int32 indices, device memory) of 256 bytes each from
+ * src -- the access pattern of the decode step's K / V row gathers -- 16
+ * lanes per row, eight rows per lane in flight, and sum the 32-bit words
+ * each thread read, modulo 2^32, into sink[t].  Indices are clamped to
+ * [0, src_rows - 1] on the device.  src 16-byte aligned, src_rows >= 1,
+ * n_rows >= 1, workgroups in [1, 2^20]. */
+esa_status esa_probe_gather_read(const void* src, int64_t src_rows, const int32_t* rows,
+                                 int64_t n_rows, int32_t workgroups, uint32_t* sink,
+                                 int64_t sink_elems, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

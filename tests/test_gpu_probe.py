@@ -52,3 +52,21 @@ def test_hbm_read_probe_closed_form():
     torch.cuda.synchronize()
     total = int(sink.to(torch.int64).sum().item()) % (1 << 32)
     assert total == (n * (n - 1) // 2) % (1 << 32)
+
+
+def test_gather_probe_closed_form():
+    lib = en.load_probe()
+    wg, src_rows, n = 24, 5000, 20011  # a ragged last round
+    src = torch.arange(src_rows * 64, dtype=torch.int32, device=DEV)  # 256-byte rows
+    g = torch.Generator(device="cpu").manual_seed(5)
+    rows = torch.randint(-3, src_rows + 3, (n,), generator=g, dtype=torch.int32)  # some clamped
+    rows_d = rows.to(DEV)
+    sink = torch.zeros(wg * 256, dtype=torch.int32, device=DEV)
+    en.check(lib.esa_probe_gather_read(ctypes.c_void_p(src.data_ptr()), src_rows,
+                                       ctypes.c_void_p(rows_d.data_ptr()), n, wg,
+                                       ctypes.c_void_p(sink.data_ptr()), sink.numel(), _stream()),
+             "esa_probe_gather_read")
+    torch.cuda.synchronize()
+    r = rows.clamp(0, src_rows - 1).to(torch.int64)
+    want = int((r * 64 * 64 + 63 * 64 // 2).sum().item()) % (1 << 32)  # sum of row r's words
+    assert int(sink.to(torch.int64).sum().item()) % (1 << 32) == want
