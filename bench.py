@@ -142,8 +142,10 @@ def peaks(torch, steps: int = 10) -> None:
     read (a 4 GiB buffer streamed once), a device copy (1 GiB, read +
     write), and L2 -> LDS through buffer_load ... lds (a 1 MiB region every
     XCD's L2 holds, 16 KB rounds per workgroup, two in flight) and HBM ->
-    LDS through the same path (a 2 GiB region read once), and 256-byte row
-    gathers at random positions (the decode step's access pattern)."""
+    LDS through the same path (a 2 GiB region read once), 256-byte rows at
+    random positions of the L2-resident region into LDS (the band kernels'
+    pattern), and 256-byte row gathers at random positions of HBM into
+    registers (the decode step's)."""
     import ctypes
     import esa_native as en
     lib = en.load_probe()
@@ -212,7 +214,26 @@ def peaks(torch, steps: int = 10) -> None:
     per, tbs, sweep = best(rates)
     out["l2_to_lds"] = {"tbs": round(tbs, 2), "workgroups_per_cu": per, "sweep": sweep,
                         "bench_ceiling": L2_TO_CU_TBS}
-    del src
+
+    # the band kernels' pattern: 256-byte rows at random positions of the
+    # same L2-resident region, four rows per DMA instruction
+    n = 1 << 20
+    g = torch.Generator(device=dev).manual_seed(12)
+    rows = torch.randint(0, region // 256, (n,), generator=g, device=dev, dtype=torch.int32)
+    rates = {}
+    for per in (2, 5, 8):
+        wg, iters = per * cus, 2048 // per
+        sink = torch.empty(wg * 256, dtype=torch.int32, device=dev)
+        ms = event_ms(torch, lambda: en.check(lib.esa_probe_gather_to_lds(
+            vp(src.data_ptr()), region // 256, vp(rows.data_ptr()), n, wg, iters,
+            vp(sink.data_ptr()), sink.numel(), stream), "l2 gather probe"), steps, 3)
+        assert bool(torch.all(sink == 8)), "l2 gather probe result"
+        rates[per] = wg * iters * 16384 / (ms * 1e-3) / 1e12
+        del sink
+    per, tbs, sweep = best(rates)
+    out["l2_gather_256b_to_lds"] = {"tbs": round(tbs, 2), "workgroups_per_cu": per,
+                                    "sweep": sweep}
+    del src, rows
 
     # the same DMA path from HBM: a 2 GiB region, each chunk read once
     region = (1 << 31) - 16384

@@ -1,6 +1,7 @@
 // Rate probes (gfx950): dense bf16 MFMA, HBM read, L2 -> LDS or HBM -> LDS
 // through the buffer_load ... lds path the MFMA kernels stage K and V with,
-// and 256-byte row gathers from HBM (the decode step's access pattern).
+// 256-byte row gathers into LDS (the band kernels' pattern) and from HBM
+// into registers (the decode step's).
 // Built into libesa_probe.so; declared in include/esa_probe.h.
 #include <hip/hip_runtime.h>
 
@@ -11,6 +12,7 @@ namespace esa {
 namespace {
 
 constexpr int kThreads = 256;
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 constexpr int kChunk = 16384;  // bytes one workgroup round moves (256 lanes x 4 x 16 B)
 // s_waitcnt with vmcnt(8) and the other counters left alone (gfx9 encoding)
 constexpr int kWaitVmcnt8 = 0x0F78;
@@ -81,6 +83,46 @@ __global__ __launch_bounds__(kThreads) void hbm_read_probe_kernel(const u32x4* s
   sink[gid] = acc;
 }
 
+__global__ __launch_bounds__(kThreads) void gather_lds_probe_kernel(const uint16_t* src, int src_rows,
+                                                                    const int32_t* rows,
+                                                                    int n_blocks, int iters,
+                                                                    uint32_t* sink) {
+  __shared__ __attribute__((aligned(1024))) uint16_t buf0[kChunk / 2];
+  __shared__ __attribute__((aligned(1024))) uint16_t buf1[kChunk / 2];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int sub = lane >> 4, part = lane & 15;  // row of a DMA, 16-byte piece of it
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)src, (short)0, src_rows * 256, 0x00020000);
+  const cptr_i32 rp = (cptr_i32)rows;  // uniform index reads: scalar loads
+  for (int i = 0; i < iters; ++i) {
+    // this wave's 16 rows of the round (n_blocks blocks of 64 indices)
+    const int blk = (int)(((int64_t)blockIdx.x * iters + i) % n_blocks);
+    // the 16 indices in one scalar load (64-byte aligned: rows is, and
+    // blk * 64 + wave * 16 is a multiple of 16)
+    const i32x16 ix = *(const __attribute__((address_space(4))) i32x16*)(rp + blk * 64 + wave * 16);
+    uint16_t* dst = (i & 1) ? buf1 : buf0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r0 = ix[4 * j], r1 = ix[4 * j + 1], r2 = ix[4 * j + 2], r3 = ix[4 * j + 3];
+      const bool odd = sub & 1, high = sub & 2;
+      const int lo = odd ? r1 : r0, hi = odd ? r3 : r2;
+      int r = high ? hi : lo;
+      r = r < 0 ? 0 : (r >= src_rows ? src_rows - 1 : r);
+      load_lds16(rs, dst + (j * kThreads + wave * 64) * 8, r * 256 + part * 16, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt8);
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+  const uint16_t* last = ((iters - 1) & 1) ? buf1 : buf0;
+  const u32x4 w = *(const u32x4*)(last + t * 8);  // DMA 0 of thread t
+  uint32_t s = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) s += (w[e] & 0xffffu) + (w[e] >> 16);
+  sink[(int64_t)blockIdx.x * kThreads + t] = s;
+}
+
 __global__ __launch_bounds__(kThreads) void gather_probe_kernel(const u32x4* src, int64_t src_rows,
                                                                 const int32_t* rows,
                                                                 int64_t n_rows, uint32_t* sink) {
@@ -148,6 +190,21 @@ esa_status esa_probe_hbm_read(const void* src, int64_t bytes, int32_t workgroups
   if (sink_elems < (int64_t)workgroups * kThreads) return ESA_ERR_CAPACITY;
   hbm_read_probe_kernel<<<workgroups, kThreads, 0, (hipStream_t)stream>>>(
       (const u32x4*)src, bytes / 16, sink);
+  return launched();
+}
+
+esa_status esa_probe_gather_to_lds(const void* src, int64_t src_rows, const int32_t* rows,
+                                   int64_t n_rows, int32_t workgroups, int32_t iters,
+                                   uint32_t* sink, int64_t sink_elems, void* stream) {
+  if (!src || !rows || !sink) return ESA_ERR_NULL;
+  if (src_rows < 1 || src_rows * 256 >= (int64_t(1) << 31) || n_rows < 64 || n_rows % 64 != 0 ||
+      n_rows >= (int64_t(1) << 31) || workgroups < 1 || workgroups > (1 << 20) || iters < 1 ||
+      iters > (1 << 20))
+    return ESA_ERR_SHAPE;
+  if ((uintptr_t)src % 16 != 0 || (uintptr_t)rows % 64 != 0) return ESA_ERR_ALIGN;
+  if (sink_elems < (int64_t)workgroups * kThreads) return ESA_ERR_CAPACITY;
+  gather_lds_probe_kernel<<<workgroups, kThreads, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)src, (int)src_rows, rows, (int)(n_rows / 64), iters, sink);
   return launched();
 }
 

@@ -57,6 +57,21 @@ esa_status esa_probe_l2_to_lds(const void* src, int64_t region_bytes, int32_t wo
 esa_status esa_probe_hbm_read(const void* src, int64_t bytes, int32_t workgroups, uint32_t* sink,
                               int64_t sink_elems, void* stream);
 
+/* Row gathers into LDS through buffer_load_dwordx4 ... lds, the band
+ * kernels' access pattern: each workgroup copies `iters` rounds of 64 rows
+ * of 256 bytes (16 lanes per row, four rows per DMA instruction, two rounds
+ * in flight) into two LDS buffers; round i of workgroup b takes the 64 row
+ * indices rows[((b * iters + i) * 64) mod n_rows ..] (int32, clamped to
+ * [0, src_rows - 1]).  With src_rows * 256 bytes of a few MB the rows stay
+ * in every XCD's L2, so the rate is L2 -> CU for scattered 256-byte rows.
+ * Bytes moved = workgroups * iters * 16384.  sink[t] = the sum of the
+ * eight 16-bit words thread t's last DMA wrote (as uint32).  src 16-byte
+ * aligned, src_rows * 256 < 2^31, n_rows a positive multiple of 64, rows
+ * 64-byte aligned, workgroups in [1, 2^20], iters in [1, 2^20]. */
+esa_status esa_probe_gather_to_lds(const void* src, int64_t src_rows, const int32_t* rows,
+                                   int64_t n_rows, int32_t workgroups, int32_t iters,
+                                   uint32_t* sink, int64_t sink_elems, void* stream);
+
 /* HBM gather: `workgroups` 256-thread workgroups read the n_rows rows
  * rows[0 .. n_rows) (int32 indices, device memory) of 256 bytes each from
  * src -- the access pattern of the decode step's K / V row gathers -- 16

@@ -52,6 +52,14 @@ def test_probe_library_exports_and_rejects():
     assert lib.esa_probe_hbm_read(fake, 100, 8, fake, 2048, None) == en.ESA_ERR_SHAPE
     assert lib.esa_probe_hbm_read(None, 128, 8, fake, 2048, None) == en.ESA_ERR_NULL
     assert lib.esa_probe_hbm_read(fake, 128, 8, fake, 2047, None) == en.ESA_ERR_CAPACITY
+    assert lib.esa_probe_gather_to_lds(fake, 100, fake, 100, 8, 4, fake, 2048, None) \
+        == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_gather_to_lds(fake, 1 << 23, fake, 128, 8, 4, fake, 2048, None) \
+        == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_gather_to_lds(fake, 100, ctypes.c_void_p(4096 + 32), 128, 8, 4, fake,
+                                       2048, None) == en.ESA_ERR_ALIGN
+    assert lib.esa_probe_gather_to_lds(fake, 100, fake, 128, 8, 4, fake, 2047, None) \
+        == en.ESA_ERR_CAPACITY
     assert lib.esa_probe_gather_read(fake, 0, fake, 10, 8, fake, 2048, None) == en.ESA_ERR_SHAPE
     assert lib.esa_probe_gather_read(fake, 10, None, 10, 8, fake, 2048, None) == en.ESA_ERR_NULL
     assert lib.esa_probe_gather_read(fake, 10, ctypes.c_void_p(4098), 10, 8, fake, 2048, None) \

@@ -70,3 +70,18 @@ def test_gather_probe_closed_form():
     r = rows.clamp(0, src_rows - 1).to(torch.int64)
     want = int((r * 64 * 64 + 63 * 64 // 2).sum().item()) % (1 << 32)  # sum of row r's words
     assert int(sink.to(torch.int64).sum().item()) % (1 << 32) == want
+
+
+def test_gather_to_lds_probe_closed_form():
+    lib = en.load_probe()
+    wg, iters, src_rows, n = 40, 9, 777, 64 * 13
+    src = torch.full((src_rows * 128,), 5, dtype=torch.int16, device=DEV)
+    g = torch.Generator(device="cpu").manual_seed(6)
+    rows = torch.randint(-2, src_rows + 2, (n,), generator=g, dtype=torch.int32).to(DEV)
+    sink = torch.zeros(wg * 256, dtype=torch.int32, device=DEV)
+    en.check(lib.esa_probe_gather_to_lds(ctypes.c_void_p(src.data_ptr()), src_rows,
+                                         ctypes.c_void_p(rows.data_ptr()), n, wg, iters,
+                                         ctypes.c_void_p(sink.data_ptr()), sink.numel(),
+                                         _stream()), "esa_probe_gather_to_lds")
+    torch.cuda.synchronize()
+    assert torch.all(sink == 8 * 5)
