@@ -48,10 +48,10 @@ __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const 
 __device__ __forceinline__ float row4_max(float v) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
                                                   false);
-  const float m1 = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const float m1 = max_nq(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m1), __float_as_uint(m1),
                                                   false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return max_nq(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 // min / max over the 16 lanes of a lane group (DPP row rotations)

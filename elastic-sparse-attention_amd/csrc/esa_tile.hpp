@@ -48,11 +48,22 @@ __device__ __forceinline__ float dot2_bf16(uint32_t pair, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), one, c, false);
 }
 
+// max of two floats, neither a signalling NaN, as one v_max_f32: fmaxf of a
+// lane swap's results would first quiet each input (a v_max_f32 of the value
+// with itself, since the compiler cannot tell they are not signalling NaNs),
+// two extra instructions on each reduction's dependent chain.  Scores and
+// running maxima are never signalling NaNs, so the result is fmaxf's.
+__device__ __forceinline__ float max_nq(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 // max of v over lanes l and l ^ 32 (v_permlane32_swap)
 __device__ __forceinline__ float half_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
                                                   false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max_nq(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // Bits [a - 32 w, b - 32 w] of word w of a 128-bit mask (a <= b, both in [0, 127]).
