@@ -215,7 +215,9 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     float ra = xa - m_use, rb = xb - m_use;
     const float rm = xm - m_use;
-    const bool grow = m_run == -INFINITY ? xm != -INFINITY : rm > kRescaleSlack;
+    // (a row's first valid key: threshold -inf, and rm = xm there)
+    const float thr = m_run == -INFINITY ? -INFINITY : kRescaleSlack;
+    const bool grow = rm > thr;
     if (wave_any(grow)) {
       const float delta = grow ? rm : 0.f;
       // rows that do not grow keep alpha = 1 (m_run may still be -inf there)

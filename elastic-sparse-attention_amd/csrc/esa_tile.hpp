@@ -306,8 +306,10 @@ struct Rows32 {
     }
     smax = half_max(smax);
     // raise the running max of a row when this block exceeds it by more
-    // than the slack (or when the row sees its first valid key)
-    const bool grow = m_run == -INFINITY ? smax != -INFINITY : smax > kRescaleSlack;
+    // than the slack (or when the row sees its first valid key: then the
+    // threshold is -inf, and smax > -inf is smax != -inf)
+    const float thr = m_run == -INFINITY ? -INFINITY : kRescaleSlack;
+    const bool grow = smax > thr;
     if (wave_any(grow)) {
       const float delta = grow ? smax : 0.f;
       // rows that do not grow keep alpha = 1 (m_run may still be -inf there)
