@@ -74,6 +74,13 @@ bool aligned(const void* ptr, size_t a) { return ((uintptr_t)ptr % a) == 0; }
 
 size_t elem_bytes(esa_dtype t) { return t == ESA_F32 ? 4 : 2; }
 
+// rows rows of `stride` 16-bit elements span less than 2 GiB (the kernels'
+// 32-bit buffer offsets); the stride is bounded first, so the product cannot
+// overflow for any argument (rows <= kMaxSeqLen + 128)
+bool span_fits_2g(int64_t rows, int64_t stride) {
+  return stride >= 0 && stride < (int64_t(1) << 31) && rows * stride * 2 < (int64_t(1) << 31);
+}
+
 esa_status check_fwd_common(const esa_fwd_args* a) {
   if (!a || !a->q || !a->k || !a->v || !a->o) return ESA_ERR_NULL;
   if (a->dtype != ESA_F32 && a->dtype != ESA_BF16 && a->dtype != ESA_F16) return ESA_ERR_DTYPE;
@@ -392,9 +399,9 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
   if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale)) return ESA_ERR_UNSUPPORTED;
   // K/V rows are addressed through 32-bit buffer offsets per (batch, kv head)
   // (rows up to one tile past kv_len are addressed, and read as zeros)
-  if ((int64_t)(a->kv_len + 128) * a->k_stride_s * 2 >= (int64_t(1) << 31) ||
-      (int64_t)(a->kv_len + 128) * a->v_stride_s * 2 >= (int64_t(1) << 31) ||
-      a->k_stride_s < a->head_dim || a->v_stride_s < a->head_dim)
+  if (!span_fits_2g((int64_t)a->kv_len + 128, a->k_stride_s) ||
+      !span_fits_2g((int64_t)a->kv_len + 128, a->v_stride_s) || a->k_stride_s < a->head_dim ||
+      a->v_stride_s < a->head_dim)
     return ESA_ERR_UNSUPPORTED;
   const LayoutDims d = dims_of(*p);
   const int nq = (a->q_len + p->block_m - 1) / p->block_m;
@@ -459,8 +466,8 @@ esa_status band_args_of(const esa_fwd_args* a, const esa_pattern* p, BandArgs* o
   // band descriptors pack the first key in 24 bits; K/V rows are addressed
   // through 32-bit buffer offsets per (batch, kv head)
   if (a->kv_len >= (1 << 24)) return ESA_ERR_UNSUPPORTED;
-  if ((int64_t)(a->kv_len + pad_rows) * a->k_stride_s * 2 >= (int64_t(1) << 31) ||
-      (int64_t)(a->kv_len + pad_rows) * a->v_stride_s * 2 >= (int64_t(1) << 31) ||
+  if (!span_fits_2g((int64_t)a->kv_len + pad_rows, a->k_stride_s) ||
+      !span_fits_2g((int64_t)a->kv_len + pad_rows, a->v_stride_s) ||
       a->k_stride_s < a->head_dim || a->v_stride_s < a->head_dim)
     return ESA_ERR_UNSUPPORTED;
   // 16-byte row loads and stores
@@ -782,12 +789,11 @@ esa_status elastic_bwd_impl(const esa_bwd_args* a, const esa_pattern* p, const i
   // the block-sparse dK/dV writes the key blocks of the pattern's seq_len only
   if (!band_dkdv && a->kv_len > p->seq_len) return ESA_ERR_SHAPE;
   if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale)) return ESA_ERR_UNSUPPORTED;
-  const int64_t lim = int64_t(1) << 31;
   // (rows up to one tile past the length are addressed, and read as zeros)
-  if ((int64_t)(a->kv_len + 128) * a->k_stride_s * 2 >= lim ||
-      (int64_t)(a->kv_len + 128) * a->v_stride_s * 2 >= lim ||
-      (int64_t)(a->q_len + 128) * a->q_stride_s * 2 >= lim ||
-      (int64_t)(a->q_len + 128) * a->dout_stride_s * 2 >= lim || a->q_stride_s < a->head_dim ||
+  if (!span_fits_2g((int64_t)a->kv_len + 128, a->k_stride_s) ||
+      !span_fits_2g((int64_t)a->kv_len + 128, a->v_stride_s) ||
+      !span_fits_2g((int64_t)a->q_len + 128, a->q_stride_s) ||
+      !span_fits_2g((int64_t)a->q_len + 128, a->dout_stride_s) || a->q_stride_s < a->head_dim ||
       a->dout_stride_s < a->head_dim || a->k_stride_s < a->head_dim || a->v_stride_s < a->head_dim)
     return ESA_ERR_UNSUPPORTED;
   const void* ptrs[] = {a->q, a->k, a->v, a->o, a->dout, a->dq, a->dk, a->dv};
@@ -856,7 +862,8 @@ esa_status elastic_bwd_impl(const esa_bwd_args* a, const esa_pattern* p, const i
   const int64_t n_kblk = (int64_t)a->batch * a->num_kv_heads * t.nkb16;
   if (band_dkdv && n_kblk > INT32_MAX / 2) return ESA_ERR_SHAPE;
   // (the band dK/dV reaches lse2 from a delta row by a 32-bit buffer offset)
-  if (band_dkdv && (int64_t)a->batch * a->num_heads * t.qpad * 8 >= lim) return ESA_ERR_UNSUPPORTED;
+  if (band_dkdv && (int64_t)a->batch * a->num_heads * t.qpad * 8 >= (int64_t(1) << 31))
+    return ESA_ERR_UNSUPPORTED;
   t.n_kblk = (int)n_kblk;
   t.kchunk = ((int64_t)a->batch * a->num_kv_heads) % 8 == 0 ? (int)(n_kblk / 8) : 8;
   t.split_parts = 1;

@@ -151,6 +151,15 @@ def test_forward_entry_points_reject_bad_arguments():
     a = fwd_args()
     a.k_stride_s = 130
     assert call(a) == en.ESA_ERR_ALIGN
+    # row strides whose span cannot be addressed by 32-bit offsets, including
+    # ones whose span overflows int64 (the check must not wrap)
+    for big in (1 << 24, 1 << 40, 1 << 62, -(1 << 62)):
+        for t in "kv":
+            a = fwd_args()
+            setattr(a, f"{t}_stride_s", big)
+            assert call(a) == en.ESA_ERR_UNSUPPORTED, (t, big)
+            assert lib.esa_elastic_fwd_band(ctypes.byref(a), ctypes.byref(p), None) \
+                == en.ESA_ERR_UNSUPPORTED, (t, big)
     assert call(fwd_args(), pp=pat(L=1024, H=4, bm=64)) == en.ESA_ERR_UNSUPPORTED
     for bad_scale in (0.0, -0.1, float("inf"), float("nan")):
         a = fwd_args()
@@ -389,6 +398,12 @@ def test_bwd_entry_points_reject_bad_arguments():
     b = en.EsaBwdArgs.from_buffer_copy(a)
     b.dq_stride_s = 130
     assert call(b) == en.ESA_ERR_ALIGN
+    # row strides past 32-bit offsets, including spans that overflow int64
+    for big in (1 << 24, 1 << 40, 1 << 62):
+        for name in ("q", "k", "v", "dout"):
+            b = en.EsaBwdArgs.from_buffer_copy(a)
+            setattr(b, f"{name}_stride_s", big)
+            assert call(b) == en.ESA_ERR_UNSUPPORTED, (name, big)
     # capacity is checked against the tiles of the query blocks q_len covers,
     # read from the host copy of row_ptr
     nqb = (p.seq_len + 127) // 128
