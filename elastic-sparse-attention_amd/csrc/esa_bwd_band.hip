@@ -152,8 +152,12 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   }
 
   int kreg[16], info[16];
-  // entry rotation: 64 / 256 resident waves per XCD per dispatched group
-  band_rows(A.pc, h, i, row_ok, q, ((bid >> 3) / 4) & 63, kreg, info);
+  // entry rotation, in 64ths of an entry per group dispatched on the XCD: a
+  // little ahead of the dispatch rate, 64 / (resident waves per XCD) = 16/64
+  // at D = 128 (256 resident) and 10.7/64 at D = 64 (384), as in the
+  // forward; measured 1-4% faster than 16/64 at B=1 H=8 L=131072 layers 4
+  // and 7, unchanged at B=1 H=32 L=32768
+  band_rows(A.pc, h, i, row_ok, q, ((bid >> 3) * (D == 128 ? 19 : 12) / 64) & 63, kreg, info);
 
   const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
   const char* const vbase = (const char*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh);
@@ -433,9 +437,9 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
 // (with whole kv heads per XCD, batch * kv heads a multiple of 8, one chunk
 // per XCD, each a contiguous range; otherwise chunks of 8 blocks, which
 // balance the heavy low blocks over the XCDs), and each block starts its
-// walk at entry rot, 1/4 entry further per block dispatched on the XCD, so
-// the resident blocks walk neighbouring entries (the rotation of
-// band_rows).  At the last layer of a pattern key block 0 takes far more
+// walk at entry rot, a little more than 64 / (resident waves per XCD) of an
+// entry further per block dispatched on the XCD, so the resident blocks walk
+// neighbouring entries (the rotation of band_rows).  At the last layer of a pattern key block 0 takes far more
 // rows than the rest (entry 0 of the heads with small interpolation weight
 // stays in it for thousands of rows), so the host splits blocks
 // 0 .. split_blocks - 1 (block 0) over split_parts waves each: each part
@@ -478,11 +482,13 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
   const int bkv = g / A.nkb16, kb = g % A.nkb16;
   const bool split = A.split_parts > 1 && kb < A.split_blocks;
   // entry rotation (as in band_rows): lane r of the walk holds entry
-  // (r + rot) mod 64, rot growing by 1/4 entry per block dispatched on the
-  // XCD (256 resident waves), so the blocks resident at once walk
-  // neighbouring entries and share Q / dO rows in L2.  The parts of a split
-  // block walk one sequence: no rotation there.
-  const int rot = split ? 0 : (((bid - A.n_extra) >> 3) / 4) & 63;
+  // (r + rot) mod 64, rot growing by 19/64 (D = 128: 256 resident waves per
+  // XCD) or 12/64 (D = 64: 384) of an entry per block dispatched on the XCD,
+  // so the blocks resident at once walk neighbouring entries and share Q /
+  // dO rows in L2.  The parts of a split block walk one sequence: no
+  // rotation there.
+  const int rot =
+      split ? 0 : ((((bid - A.n_extra) >> 3) * (D == 128 ? 19 : 12)) / 64) & 63;
   const int kvh = bkv % A.Hkv, b = bkv / A.Hkv;
   const int u0 = 16 * kb;
 

@@ -102,9 +102,16 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   // ---- this row's keys of bands 16 q .. 16 q + 15 (-1: no key), and the
   // group's band descriptors for the same bands (every lane of group q)
   int kreg[16], info[16];
-  // entry rotation: about 64 / 320 resident waves per XCD (LDS holds ten
-  // waves per CU) per dispatched group, 3/16
-  band_rows(A.pc, h, i, row_ok, q, ((bid >> 3) * 3 / 16) & 63, kreg, info);
+  // entry rotation, in 64ths of an entry per group dispatched on the XCD:
+  // an XCD keeps 320 waves resident at D = 128 (ten per CU, by LDS) and 512
+  // at D = 64 (sixteen, by registers), so a group is dispatched about every
+  // 64 / 320 = 12.8/64 or 64 / 512 = 8/64 of a wave's walk; the rotation
+  // leads that by a little.  Measured rates per 64th: 15 and 9 are the best
+  // or within 2% of it at every layer of B=1 H=8 L=131072, where an XCD's L2
+  // cannot hold the resident groups' rows across entries (12/64 there was
+  // 8-11% slower at D = 128 layers 4-7 and 17-22% at D = 64), and shapes up
+  // to L=32768 do not move with the rate.
+  band_rows(A.pc, h, i, row_ok, q, ((bid >> 3) * (D == 128 ? 15 : 9) / 64) & 63, kreg, info);
 
   const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
   const char* const vbase = (const char*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh);
