@@ -84,11 +84,12 @@ __device__ __forceinline__ int row16_max(int v) {
 // onto an XCD's resident waves, each walking its 64 entries in the same
 // time, so with rot = 0 the groups resident at once sit at every stage of
 // their walk and touch the K/V rows of all 64 entries.  Starting each group
-// at the entry the groups dispatched before it are at (rot growing by about
-// 64 / resident waves per dispatched group) keeps the resident groups on
-// neighbouring entries, whose keys overlap: an L2 model of one XCD (4 MB
-// LRU, 320 resident waves) at B=1 H=32 L=32768 layer 4 puts the hit rate at
-// 0.79 without and 0.94 with the rotation.
+// at the entry the groups dispatched before it are at (rot growing by a
+// little more than 64 / resident waves per dispatched group; the callers
+// give their measured rates) keeps the resident groups on neighbouring
+// entries, whose keys overlap: an L2 model of one XCD (4 MB LRU, 320
+// resident waves) at B=1 H=32 L=32768 layer 4 puts the hit rate at 0.79
+// without and 0.94 with the rotation.
 __device__ __forceinline__ void band_rows(const PatternConsts& pc, int h, int i, bool row_ok,
                                           int q, int rot, int (&kreg)[16], int (&info)[16]) {
   const HeadWeights hw = head_weights(pc, h);
