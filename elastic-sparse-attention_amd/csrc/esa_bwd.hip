@@ -65,38 +65,60 @@ __device__ __forceinline__ uint32_t transpose32(uint32_t x, int lane) {
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// delta and lse in log2 units, one 16-lane group per query row.  heads_fast:
-// the grid's fastest axis is the head (blockIdx.x = h, blockIdx.y = 16-row
-// block), so where O's heads lie inside a row ([B, L, H, D], the forward's
-// output) neighbouring blocks read neighbouring bytes; otherwise the axes
-// swap.
+// delta and lse in log2 units, one 16-lane group per query row, PREP_ROWS
+// rows per workgroup (four 16-row passes, every pass's O and dO loads issued
+// before the first sum: a 16-row workgroup per launch slot left the kernel
+// bound by load latency, 3 TB/s at B=8 H=16 L=4096 D=64).  Each row's sum
+// runs in the same order as before and as the band dQ kernel's (lane g adds
+// its D/16 products in turn, then xor shuffles 8, 4, 2, 1).  heads_fast: the
+// grid's fastest axis is the head (blockIdx.x = h, blockIdx.y = row block),
+// so where O's heads lie inside a row ([B, L, H, D], the forward's output)
+// neighbouring blocks read neighbouring bytes; otherwise the axes swap.
+constexpr int PREP_ROWS = 64;
+
 template <int D, Elem E>
 __global__ __launch_bounds__(256) void prep_kernel(BwdArgs A, float* lse2, int heads_fast) {
   using M = MmaT<E>;
-  using V8 = typename M::v8;
+  constexpr int PER = D / 16;  // elements per lane
+  constexpr int PASSES = PREP_ROWS / 16;
+  // PER 16-bit elements as one load
+  typedef uint32_t chunk_t __attribute__((ext_vector_type(PER / 2)));
   const int rb = heads_fast ? blockIdx.y : blockIdx.x;
-  const int row = rb * 16 + (threadIdx.x >> 4);
   const int h = heads_fast ? blockIdx.x : blockIdx.y, b = blockIdx.z;
   const int g = threadIdx.x & 15;
-  constexpr int PER = D / 16;  // elements per lane
   if (A.split_parts > 1 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
     for (int i = threadIdx.x; i < A.n_bkv * A.split_blocks; i += 256)
       A.part_cnt[i] = 0;  // split arrivals
-  float acc = 0.f;
-  if (row < A.q_len) {
-    const uint16_t* o = A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)row * A.oss;
-    const uint16_t* d = A.dout + (int64_t)b * A.dosb + (int64_t)h * A.dosh + (int64_t)row * A.doss;
+  const uint16_t* ob = A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + g * PER;
+  const uint16_t* db = A.dout + (int64_t)b * A.dosb + (int64_t)h * A.dosh + g * PER;
+  chunk_t ov[PASSES], dv[PASSES];
 #pragma unroll
-    for (int e = 0; e < PER; ++e) acc += M::val(o[g * PER + e]) * M::val(d[g * PER + e]);
+  for (int p = 0; p < PASSES; ++p) {
+    const int row = rb * PREP_ROWS + p * 16 + (threadIdx.x >> 4);
+    ov[p] = dv[p] = chunk_t{};
+    if (row < A.q_len) {
+      ov[p] = *(const chunk_t*)(ob + (int64_t)row * A.oss);
+      dv[p] = *(const chunk_t*)(db + (int64_t)row * A.doss);
+    }
   }
 #pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
-  if (row < A.q_len && g == 0) {
-    const int64_t at = ((int64_t)b * A.H + h) * A.qpad + row;
-    A.delta[at] = acc;
-    // kept finite: masked scores enter as -inf, and -inf - (-inf) would be NaN
-    lse2[at] = fmaxf(A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + row] * 1.4426950408889634f,
-                     -3.0e38f);
+  for (int p = 0; p < PASSES; ++p) {
+    const int row = rb * PREP_ROWS + p * 16 + (threadIdx.x >> 4);
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const uint32_t ow = ov[p][e >> 1], dw = dv[p][e >> 1];
+      acc += M::val(e & 1 ? ow >> 16 : ow & 0xffffu) * M::val(e & 1 ? dw >> 16 : dw & 0xffffu);
+    }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 16);
+    if (row < A.q_len && g == 0) {
+      const int64_t at = ((int64_t)b * A.H + h) * A.qpad + row;
+      A.delta[at] = acc;
+      // kept finite: masked scores enter as -inf, and -inf - (-inf) would be NaN
+      lse2[at] = fmaxf(A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + row] * 1.4426950408889634f,
+                       -3.0e38f);
+    }
   }
 }
 
@@ -604,7 +626,7 @@ static hipError_t launch_tile_bwd_elem(const BwdArgs& a, int head_dim, int64_t n
     if (e0 != hipSuccess) return e0;
     return launch_band_dkdv(a, head_dim, lse2, stream);
   }
-  const unsigned n_rb = (unsigned)((a.q_len + 15) / 16);
+  const unsigned n_rb = (unsigned)((a.q_len + PREP_ROWS - 1) / PREP_ROWS);
   // heads fastest where O interleaves heads within a row and the row blocks
   // fit the grid's second axis (65535)
   const int heads_fast = a.osh < a.oss && n_rb <= 65535u;

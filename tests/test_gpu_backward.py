@@ -376,3 +376,25 @@ def test_head_major_o_and_dout(kernels):
                                 dkdv_kernel=dkdv_kind)
     for name, x, y in zip(("dq", "dk", "dv"), ref, got):
         assert torch.equal(x, y), name
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_band_dq_delta_matches_prep_kernel(D):
+    """With both halves band the band dQ kernel forms delta = rowsum(dO * O)
+    and lse2 itself; beside a block-sparse dK/dV they come from prep_kernel.
+    Both sum each row in the same order, so the band dQ is the same bit for
+    bit either way (GQA, a ragged q_len, the forward's [B, L, H, D] O)."""
+    B, H, Hkv, L, Lq, layer = 2, 8, 2, 1300, 1237, 5
+    print(f"band dQ delta vs prep_kernel D={D}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=23, scale=D ** -0.25, Lq=Lq)
+    sc = scaling_for(D)
+    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc)
+    do = torch.randn(B, Lq, H, D, generator=torch.Generator().manual_seed(9))
+    do = do.to(torch.bfloat16).to(DEV)
+    own = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="band",
+                                dkdv_kernel="band")
+    prep = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel="band",
+                                 dkdv_kernel="tile")
+    assert torch.equal(own[0], prep[0])
