@@ -218,7 +218,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   // at register e of the lane holding the key, else 0)
   auto pair_softmax = [&](float xa, bool ha, int ea, float xb, bool hb, int eb, uint64_t& pa,
                           uint64_t& pb) {
-    const float xm = fmaxf(xa, xb);
+    const float xm = max_nq(xa, xb);
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     float ra = xa - m_use, rb = xb - m_use;
     const float rm = xm - m_use;
