@@ -90,7 +90,16 @@ __all__ = [
 # ---------------------------------------------------------------------------
 # helpers
 # ---------------------------------------------------------------------------
+# torch's current-stream handle as an integer, without building a Stream
+# object (about 2 us per call less on the decode path); the public API where
+# this torch build lacks it
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(device: torch.device) -> ctypes.c_void_p:
+    if _RAW_STREAM is not None:
+        index = device.index if device.index is not None else torch.cuda.current_device()
+        return ctypes.c_void_p(_RAW_STREAM(index))
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
@@ -195,6 +204,7 @@ class ElasticLayout:
         self._masks: Dict[int, torch.Tensor] = {}
         self._stages: Dict[Tuple[int, int], "ElasticLayout"] = {}
         self._stage_masks = None  # tensor, False (none: over budget), or unbuilt
+        self._tiles_for: Dict[int, int] = {}
 
     def stages(self, block_n: int = 32, block_m: Optional[int] = 64) -> "ElasticLayout":
         """The same pattern's layout at ``block_m`` x ``block_n`` blocks, the
@@ -247,11 +257,17 @@ class ElasticLayout:
 
     def tiles_for(self, q_len: int) -> int:
         """Active tiles over the query blocks a q_len-row prefill visits,
-        summed over heads (one batch element)."""
+        summed over heads (one batch element); cached per q_len (the kernel
+        choice asks on every forward)."""
+        got = self._tiles_for.get(int(q_len))
+        if got is not None:
+            return got
         nq = (q_len + self.pattern.block_m - 1) // self.pattern.block_m
         rp = self.row_ptr_host.view(-1)[:-1].view(self.pattern.num_heads, self.num_qblocks)
         nxt = self.row_ptr_host.view(-1)[1:].view(self.pattern.num_heads, self.num_qblocks)
-        return int((nxt[:, :nq] - rp[:, :nq]).sum())
+        got = int((nxt[:, :nq] - rp[:, :nq]).sum())
+        self._tiles_for[int(q_len)] = got
+        return got
 
     def schedule(self, q_len: int, batch: int) -> Tuple[torch.Tensor, int]:
         key = (int(q_len), int(batch))
@@ -344,11 +360,11 @@ def _fwd_args(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor
     a.batch, a.num_heads, a.num_kv_heads = B, H, k.shape[1]
     a.q_len, a.kv_len, a.head_dim = Lq, k.shape[2], D
     a.q = q.data_ptr()
-    a.q_stride_b, a.q_stride_h, a.q_stride_s = q.stride(0), q.stride(1), q.stride(2)
+    a.q_stride_b, a.q_stride_h, a.q_stride_s = q.stride()[:3]
     a.k = k.data_ptr()
-    a.k_stride_b, a.k_stride_h, a.k_stride_s = k.stride(0), k.stride(1), k.stride(2)
+    a.k_stride_b, a.k_stride_h, a.k_stride_s = k.stride()[:3]
     a.v = v.data_ptr()
-    a.v_stride_b, a.v_stride_h, a.v_stride_s = v.stride(0), v.stride(1), v.stride(2)
+    a.v_stride_b, a.v_stride_h, a.v_stride_s = v.stride()[:3]
     a.o = o.data_ptr()
     a.o_stride_b, a.o_stride_h, a.o_stride_s = o_strides
     if lse is not None:
@@ -459,6 +475,14 @@ def elastic_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     bit.
     """
     _check_qkv(q, k, v)
+    return _prefill_fwd(q, k, v, layout, scaling, return_lse, out, key_block, query_block,
+                        kernel, stage_masks)
+
+
+def _prefill_fwd(q, k, v, layout, scaling, return_lse, out, key_block, query_block, kernel,
+                 stage_masks):
+    """elastic_attention_fwd after its q / k / v checks (the module, which
+    checks them itself, calls this directly)."""
     B, H, Lq, D = q.shape
     if kernel not in ("auto", "tile", "band"):
         raise ValueError(f"kernel must be 'auto', 'tile' or 'band', got {kernel!r}")
@@ -538,6 +562,14 @@ def elastic_attention_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     ``seed``; ``return_weights`` also returns the naive path's attention
     weights ``[B, H, Lq, w]`` (after dropout, :673-680) as a third value."""
     _check_qkv(q, k, v)
+    return _rows_fwd(q, k, v, pattern, scaling, positions, return_lse, dropout_p, seed,
+                     return_weights)
+
+
+def _rows_fwd(q, k, v, pattern, scaling, positions, return_lse, dropout_p, seed,
+              return_weights):
+    """elastic_attention_rows after its argument checks (the module, which
+    checks q, k, v itself, calls this directly)."""
     B, H, Lq, D = q.shape
     q, k, v = _prep(q, 4), _prep(k, 4), _prep(v, 4)
     o = torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
@@ -977,8 +1009,8 @@ class ElasticSparseAttention(nn.Module):
                 o = _ElasticTileAttention.apply(q, k, v, self.layout(q.device), self.scaling,
                                                 self.prefill_kernel)
                 return o.reshape(B, Lq, H * D), None
-            o, _ = elastic_attention_fwd(q, k, v, self.layout(q.device), self.scaling,
-                                         return_lse=False, kernel=self.prefill_kernel)
+            o, _ = _prefill_fwd(q, k, v, self.layout(q.device), self.scaling, False, None, None,
+                                None, self.prefill_kernel, True)
             return o.view(B, Lq, H * D), None                              # :761-763
         # per-row gather: decode rows, float32 / float16, other head dims, the
         # naive path; keep decisions of dropout drawn from torch's generator
@@ -987,8 +1019,7 @@ class ElasticSparseAttention(nn.Module):
             o, wts = _ElasticRowsAttention.apply(q, k, v, self.pattern, self.scaling, pos,
                                                  dropout_p, seed, naive)
         else:
-            got = elastic_attention_rows(q, k, v, self.pattern, self.scaling, pos,
-                                         return_lse=False, dropout_p=dropout_p, seed=seed,
-                                         return_weights=naive)
+            got = _rows_fwd(q, k, v, self.pattern, self.scaling, pos, False, dropout_p, seed,
+                            naive)
             o, wts = got[0], (got[2] if naive else None)
         return o.reshape(B, Lq, H * D), (wts if naive else None)          # :761-763
