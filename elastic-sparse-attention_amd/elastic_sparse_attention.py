@@ -500,6 +500,8 @@ def _prefill_fwd(q, k, v, layout, scaling, return_lse, out, key_block, query_blo
     if (query_block, key_block) not in ((128, 64), (128, 128), (64, 32)):
         raise ValueError(f"(query_block, key_block) must be (128, 64), (128, 128) or (64, 32), "
                          f"got ({query_block}, {key_block})")
+    if B == 0 or Lq == 0:
+        return o, lse  # no rows: nothing to launch (empty tensors may have no address)
     st = layout if (query_block, key_block) == (128, 128) else layout.stages(key_block,
                                                                              query_block)
     items, n = st.schedule(Lq, B)
@@ -531,6 +533,8 @@ def elastic_attention_band(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
     o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
+    if B == 0 or Lq == 0:
+        return o, lse
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
     check(load().esa_elastic_fwd_band(ctypes.byref(a), ctypes.byref(pattern), _stream(q.device)),
           "esa_elastic_fwd_band")
@@ -576,6 +580,13 @@ def _rows_fwd(q, k, v, pattern, scaling, positions, return_lse, dropout_p, seed,
     need_lse = return_lse or return_weights
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if need_lse else None
     positions, pos_ptr = _positions_ptr(positions, Lq, q.device)
+    if B == 0 or Lq == 0:
+        lse_out = lse if return_lse else None
+        if return_weights:
+            wts = torch.empty(B, H, Lq, pattern.attention_length, dtype=q.dtype,
+                              device=q.device)
+            return o, lse_out, wts
+        return o, lse_out
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
     if dropout_p > 0.0 or return_weights:
         wts = None
@@ -619,6 +630,8 @@ def sparse_attention_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     idx, msk = _index_arrays(sparse_indices, sparse_mask)
     o = torch.empty(B, H, Lq, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device)
+    if B == 0 or Lq == 0:
+        return o, lse
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(1), o.stride(2)), lse, sm_scale)
     check(load().esa_sparse_fwd(ctypes.byref(a), ctypes.c_void_p(idx.data_ptr()),
                                 idx.element_size(), idx.stride(0), idx.stride(1),
@@ -673,6 +686,8 @@ def elastic_attention_bwd_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
     dq = torch.empty(B, H, Lq, D, dtype=q.dtype, device=q.device)
     dk = torch.empty_like(k, memory_format=torch.contiguous_format)
     dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    if B == 0 or Lq == 0:
+        return dq, dk.zero_(), dv.zero_()  # no query row reaches a key
     a = _bwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, dout,
                   (dout.stride(0), dout.stride(2), dout.stride(1)), dq, dk, dv, scaling)
     work = _gather_workspace(a, pattern.attention_length, q.device)
@@ -709,6 +724,8 @@ def sparse_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: t
     dq = torch.empty(B, H, Lq, D, dtype=q.dtype, device=q.device)
     dk = torch.empty_like(k, memory_format=torch.contiguous_format)
     dv = torch.empty_like(v, memory_format=torch.contiguous_format)
+    if B == 0 or Lq == 0:
+        return dq, dk.zero_(), dv.zero_()
     a = _bwd_args(q, k, v, o, o.stride()[:3], lse.contiguous(), dout, dout.stride()[:3], dq, dk,
                   dv, sm_scale)
     work = _gather_workspace(a, idx.shape[2], q.device)
@@ -753,6 +770,11 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
     dq = torch.empty_like(q)
     dk = torch.empty(B, Hkv, Lk, D, dtype=k.dtype, device=k.device)
     dv = torch.empty(B, Hkv, Lk, D, dtype=v.dtype, device=v.device)
+    for name, val in (("dq_kernel", dq_kernel), ("dkdv_kernel", dkdv_kernel)):
+        if val not in ("auto", "tile", "band"):
+            raise ValueError(f"{name} must be 'auto', 'tile' or 'band', got {val!r}")
+    if B == 0 or Lq == 0:
+        return dq, dk.zero_(), dv.zero_()  # no query row reaches a key
     a = _bwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, dout,
                   (dout.stride(0), dout.stride(2), dout.stride(1)), dq, dk, dv, scaling)
     lib = load()
@@ -762,9 +784,6 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
         check(lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(ws)),
               "esa_bwd_workspace_size")
         work = torch.empty(max(ws.value // 4, 4), dtype=torch.float32, device=q.device)
-    for name, val in (("dq_kernel", dq_kernel), ("dkdv_kernel", dkdv_kernel)):
-        if val not in ("auto", "tile", "band"):
-            raise ValueError(f"{name} must be 'auto', 'tile' or 'band', got {val!r}")
     auto_dq, auto_dkdv = bwd_kernels(layout, Lq, B, D)
     dq_kernel = auto_dq if dq_kernel == "auto" else dq_kernel
     dkdv_kernel = auto_dkdv if dkdv_kernel == "auto" else dkdv_kernel

@@ -564,3 +564,38 @@ def test_module_index_buffers_on_gpu():
     assert torch.equal(m.sparse_causal_mask.cpu(), rm)
     a, b = m._get_prepared_indices_and_mask(100)
     assert a.shape == (4, 100, 64)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_empty_inputs(D):
+    """Batch 0 and zero query rows: empty outputs, nothing launched that
+    could fault, through the module (prefill, decode, backward) and the
+    kernels' own entry points."""
+    H, L = 4, 256
+    m = ElasticSparseAttention(3, 8, H, D, 64, L)
+    for B, Lq, Lk in ((0, 256, 256), (0, 1, 256), (2, 0, 256)):
+        print(f"empty B={B} Lq={Lq} Lk={Lk} D={D}", flush=True)
+        q = torch.randn(B, H, Lq, D, device=DEV).bfloat16()
+        k = torch.randn(B, H, Lk, D, device=DEV).bfloat16()
+        v = torch.randn(B, H, Lk, D, device=DEV).bfloat16()
+        lay = m.layout(DEV)
+        for kern in ("tile", "band"):
+            o, lse = elastic_attention_fwd(q, k, v, lay, m.scaling, kernel=kern)
+            assert o.shape == (B, Lq, H, D) and lse.shape == (B, H, Lq)
+        o, _ = elastic_attention_rows(q, k, v, lay.pattern, m.scaling, return_lse=False)
+        assert o.shape == (B, Lq, H, D)
+        if Lq == 1:
+            cp = torch.full((1,), Lk - 1, device=DEV, dtype=torch.long)
+            out, _ = m(q, k, v, cache_position=cp)
+        else:
+            out, _ = m(q, k, v)
+        assert out.shape == (B, Lq, H * D)
+        if Lq == Lk or Lq == 0:
+            qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+            out, _ = m(qg, kg, vg)
+            out.float().sum().backward()
+            assert qg.grad.shape == q.shape and kg.grad.shape == k.shape
+            assert vg.grad.shape == v.shape
+            if kg.grad.numel():
+                assert torch.count_nonzero(kg.grad) == 0 and torch.count_nonzero(vg.grad) == 0
+    torch.cuda.synchronize()
