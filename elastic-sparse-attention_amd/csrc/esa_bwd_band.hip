@@ -157,7 +157,10 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   // at D = 128 (256 resident) and 10.7/64 at D = 64 (384), as in the
   // forward; measured 1-4% faster than 16/64 at B=1 H=8 L=131072 layers 4
   // and 7, unchanged at B=1 H=32 L=32768
-  band_rows(A.pc, h, i, row_ok, q, ((bid >> 3) * (D == 128 ? 19 : 12) / 64) & 63, kreg, info);
+  // (unsigned: the product wraps for grids near 2^31 blocks; only the value
+  // mod 64 matters)
+  band_rows(A.pc, h, i, row_ok, q,
+            (int)(((unsigned)(bid >> 3) * (D == 128 ? 19u : 12u) / 64u) & 63u), kreg, info);
 
   const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
   const char* const vbase = (const char*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh);
@@ -488,7 +491,8 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
   // dO rows in L2.  The parts of a split block walk one sequence: no
   // rotation there.
   const int rot =
-      split ? 0 : ((((bid - A.n_extra) >> 3) * (D == 128 ? 19 : 12)) / 64) & 63;
+      split ? 0
+            : (int)(((unsigned)((bid - A.n_extra) >> 3) * (D == 128 ? 19u : 12u) / 64u) & 63u);
   const int kvh = bkv % A.Hkv, b = bkv / A.Hkv;
   const int u0 = 16 * kb;
 

@@ -111,7 +111,10 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   // cannot hold the resident groups' rows across entries (12/64 there was
   // 8-11% slower at D = 128 layers 4-7 and 17-22% at D = 64), and shapes up
   // to L=32768 do not move with the rate.
-  band_rows(A.pc, h, i, row_ok, q, ((bid >> 3) * (D == 128 ? 15 : 9) / 64) & 63, kreg, info);
+  // (unsigned: the product wraps for grids near 2^31 blocks; only the value
+  // mod 64 matters)
+  band_rows(A.pc, h, i, row_ok, q,
+            (int)(((unsigned)(bid >> 3) * (D == 128 ? 15u : 9u) / 64u) & 63u), kreg, info);
 
   const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
   const char* const vbase = (const char*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh);
