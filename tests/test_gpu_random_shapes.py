@@ -1,0 +1,140 @@
+"""Every forward kernel against the float32 oracle on seeded random shapes.
+
+The fixed-case tests pick shapes by hand; this sweep draws them: head counts
+with every GQA ratio, ragged lengths (q_len below kv_len, lengths that are
+not multiples of any block), attention lengths from 8 to 100, 1 to 12
+layers at any layer index, head dims 64 / 128 for the MFMA kernels and
+others for the per-row gather, bf16 and fp16, flat and sharp logits.  Each
+configuration runs the tile kernel at both staging shapes (with and without
+stage masks), the band kernel where it applies (attention_length <= 64) and
+the per-row gather, all against the oracle at the usual bars (bf16 / fp16
+output 2e-2, lse 2e-3; float32 1e-4).  The backward sweep runs every
+dQ / dK-dV kernel pair that applies against torch autograd through the
+oracle (max error 2e-2 of the reference's max per gradient) and checks a
+second run gives the same bits.
+"""
+import random
+
+import pytest
+import torch
+
+from esa_oracle import elastic_indices, forward_fp32, prepared_rows, scaling_for, seeded_inputs
+from elastic_sparse_attention import (ElasticLayout, elastic_attention_band, elastic_attention_bwd,
+                                      elastic_attention_fwd, elastic_attention_rows, make_pattern)
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+TOL = {torch.bfloat16: (2e-2, 2e-3), torch.float16: (2e-2, 2e-3), torch.float32: (1e-4, 1e-4)}
+
+
+def draw(seed):
+    r = random.Random(seed)
+    H = r.choice([1, 2, 3, 4, 6, 8])
+    Hkv = r.choice([d for d in range(1, H + 1) if H % d == 0])
+    L = r.randint(17, 1500)
+    Lq = L if r.random() < 0.6 else r.randint(1, L)
+    nl = r.choice([1, 2, 5, 8, 12])
+    layer = r.randrange(nl)
+    w = r.choice([8, 16, 24, 33, 48, 64, 64, 100])
+    D = r.choice([64, 128, 128])
+    dtype = r.choice([torch.bfloat16, torch.bfloat16, torch.float16])
+    B = r.choice([1, 2])
+    scale = r.choice([D ** -0.25, 1.0])
+    return B, H, Hkv, L, Lq, D, nl, layer, w, dtype, scale
+
+
+def check(o_bshd, lse, ro, rl, tol, ltol, what):
+    got = o_bshd.permute(0, 2, 1, 3).float().cpu()
+    err = (got - ro).abs().max().item()
+    assert err <= tol, f"{what}: output max-abs {err:.3e} > {tol}"
+    if lse is not None:
+        lerr = (lse.cpu() - rl).abs().max().item()
+        assert lerr <= ltol, f"{what}: lse max-abs {lerr:.3e} > {ltol}"
+
+
+@pytest.mark.parametrize("seed", range(96))
+def test_random_shapes_all_forward_kernels(seed):
+    B, H, Hkv, L, Lq, D, nl, layer, w, dtype, scale = draw(seed)
+    print(f"seed={seed} B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} nl={nl} layer={layer} w={w} "
+          f"{dtype} scale={scale:.3f}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, dtype, seed=100 + seed, scale=scale, Lq=Lq)
+    idx, msk = elastic_indices(L, layer, nl, H, w)
+    pi, pm = prepared_rows(idx, msk, Lq, L, L)
+    sc = scaling_for(D)
+    ro, rl = forward_fp32(q, k, v, pi, pm, sc, H // Hkv)
+    tol, ltol = TOL[dtype]
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    lay = ElasticLayout(make_pattern(L, w, layer, nl, H), DEV)
+    for qb, kb in ((128, 64), (64, 32), (128, 128)):
+        for masks in (True, False):
+            o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc, kernel="tile", query_block=qb,
+                                           key_block=kb, stage_masks=masks)
+            check(o, lse, ro, rl, tol, ltol, f"tile {qb}x{kb} masks={masks}")
+    if w <= 64:
+        o, lse = elastic_attention_band(qd, kd, vd, lay.pattern, sc)
+        check(o, lse, ro, rl, tol, ltol, "band")
+    o, lse = elastic_attention_rows(qd, kd, vd, lay.pattern, sc)
+    check(o, lse, ro, rl, tol, ltol, "rows")
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shapes_rows_float32_any_head_dim(seed):
+    """The per-row gather in float32 at head dims the MFMA kernels do not
+    take (multiples of 4 up to 256)."""
+    r = random.Random(1000 + seed)
+    H = r.choice([1, 2, 4, 8])
+    Hkv = r.choice([d for d in range(1, H + 1) if H % d == 0])
+    L = r.randint(5, 900)
+    Lq = L if r.random() < 0.5 else r.randint(1, L)
+    nl = r.choice([1, 4, 8])
+    layer = r.randrange(nl)
+    w = r.choice([8, 32, 64, 100])
+    D = r.choice([4, 32, 60, 96, 160, 256])
+    B = r.choice([1, 3])
+    print(f"rows fp32 seed={seed} B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} nl={nl} "
+          f"layer={layer} w={w}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.float32, seed=200 + seed, Lq=Lq)
+    idx, msk = elastic_indices(L, layer, nl, H, w)
+    pi, pm = prepared_rows(idx, msk, Lq, L, L)
+    sc = scaling_for(D)
+    ro, rl = forward_fp32(q, k, v, pi, pm, sc, H // Hkv)
+    lay_pattern = make_pattern(L, w, layer, nl, H)
+    o, lse = elastic_attention_rows(q.to(DEV), k.to(DEV), v.to(DEV), lay_pattern, sc)
+    check(o, lse, ro, rl, 1e-4, 1e-4, "rows fp32")
+
+
+def rel_err(got, ref):
+    return ((got.float().cpu() - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shapes_backward(seed):
+    B, H, Hkv, L, Lq, D, nl, layer, w, dtype, scale = draw(500 + seed)
+    print(f"bwd seed={seed} B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} nl={nl} layer={layer} "
+          f"w={w} {dtype} scale={scale:.3f}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, dtype, seed=300 + seed, scale=scale, Lq=Lq)
+    idx, msk = elastic_indices(L, layer, nl, H, w)
+    pi, pm = prepared_rows(idx, msk, Lq, L, L)
+    sc = scaling_for(D)
+    g = torch.randn(B, H, Lq, D, generator=torch.Generator().manual_seed(seed)).to(dtype)
+    qf, kf, vf = (t.float().requires_grad_() for t in (q, k, v))
+    ro, _ = forward_fp32(qf, kf, vf, pi, pm, sc, H // Hkv, chunk_rows=512)
+    (ro * g.float()).sum().backward()
+    refs = (qf.grad, kf.grad, vf.grad)
+    lay = ElasticLayout(make_pattern(L, w, layer, nl, H), DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    o, lse = elastic_attention_fwd(qd, kd, vd, lay, sc, kernel="tile")
+    do = g.to(DEV).permute(0, 2, 1, 3).contiguous()
+    pairs = [("tile", "tile")]
+    if w <= 64:
+        pairs += [("band", "band"), ("band", "tile"), ("tile", "band")]
+    for dqk, dkvk in pairs:
+        got = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel=dqk,
+                                    dkdv_kernel=dkvk)
+        errs = [rel_err(x, r) for x, r in zip(got, refs)]
+        print(f"  {dqk}/{dkvk} rel err dq {errs[0]:.2e} dk {errs[1]:.2e} dv {errs[2]:.2e}",
+              flush=True)
+        assert max(errs) <= 2e-2, (dqk, dkvk, errs)
+        again = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel=dqk,
+                                      dkdv_kernel=dkvk)
+        assert all(torch.equal(x, y) for x, y in zip(got, again))
