@@ -138,3 +138,37 @@ def test_random_shapes_backward(seed):
         again = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel=dqk,
                                       dkdv_kernel=dkvk)
         assert all(torch.equal(x, y) for x, y in zip(got, again))
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_decode_positions_through_module(seed):
+    """The module's cache_position branch (the per-row gather) at random
+    positions, negative ones included, with GQA, bf16 / fp16 / float32 and
+    any head dim the gather takes, against the oracle's rows at those
+    positions."""
+    from elastic_sparse_attention import ElasticSparseAttention
+    r = random.Random(2000 + seed)
+    H = r.choice([2, 4, 8])
+    Hkv = r.choice([d for d in range(1, H + 1) if H % d == 0])
+    L = r.randint(40, 1200)
+    max_len = L + r.choice([0, 17, 300])
+    nq = r.choice([1, 1, 3, 8])
+    nl = r.choice([2, 8, 12])
+    layer = r.randrange(nl)
+    w = r.choice([16, 64, 100])
+    D = r.choice([64, 128, 96])
+    dtype = r.choice([torch.bfloat16, torch.float16, torch.float32])
+    B = r.choice([1, 4])
+    pos = torch.tensor([r.randrange(-L, L) for _ in range(nq)], dtype=torch.int64)
+    print(f"decode seed={seed} B={B} H={H} Hkv={Hkv} L={L} max={max_len} rows={nq} D={D} "
+          f"nl={nl} layer={layer} w={w} {dtype} pos={pos.tolist()}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, dtype, seed=400 + seed, scale=D ** -0.25, Lq=nq)
+    idx, msk = elastic_indices(max_len, layer, nl, H, w)
+    pi, pm = prepared_rows(idx, msk, nq, L, max_len, cache_position=pos)
+    m = ElasticSparseAttention(layer, nl, H, D, w, max_len, num_key_value_heads=Hkv)
+    ro, _ = forward_fp32(q, k, v, pi, pm, m.scaling, H // Hkv)
+    out, _ = m(q.to(DEV), k.to(DEV), v.to(DEV), cache_position=pos.to(DEV))
+    ref = ro.transpose(1, 2).reshape(B, nq, H * D)
+    tol = TOL[dtype][0]
+    err = (out.float().cpu() - ref).abs().max().item()
+    assert err <= tol, err
