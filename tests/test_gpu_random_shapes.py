@@ -172,3 +172,32 @@ def test_random_decode_positions_through_module(seed):
     tol = TOL[dtype][0]
     err = (out.float().cpu() - ref).abs().max().item()
     assert err <= tol, err
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_strided_inputs_same_bits(seed):
+    """q, k, v as the [B, L, H, D] tensors attention layers hold, seen as
+    [B, H, L, D] through transpose(1, 2) (the kernels take the strides, no
+    copy): every forward kernel gives the same bits as on contiguous
+    inputs."""
+    B, H, Hkv, L, Lq, D, nl, layer, w, dtype, scale = draw(700 + seed)
+    print(f"strided seed={seed} B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} nl={nl} "
+          f"layer={layer} w={w} {dtype}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, dtype, seed=600 + seed, scale=scale, Lq=Lq)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    qs, ks, vs = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (qd, kd, vd))
+    assert torch.equal(qs, qd)
+    if H > 1 and Lq > 1:
+        assert qs.stride(2) > qs.stride(1)  # heads inside a row
+    lay = ElasticLayout(make_pattern(L, w, layer, nl, H), DEV)
+    sc = scaling_for(D)
+    runs = [lambda a, b, c: elastic_attention_fwd(a, b, c, lay, sc, kernel="tile"),
+            lambda a, b, c: elastic_attention_fwd(a, b, c, lay, sc, kernel="tile",
+                                                  query_block=64, key_block=32),
+            lambda a, b, c: elastic_attention_rows(a, b, c, lay.pattern, sc)]
+    if w <= 64:
+        runs.append(lambda a, b, c: elastic_attention_band(a, b, c, lay.pattern, sc))
+    for run in runs:
+        o1, l1 = run(qd, kd, vd)
+        o2, l2 = run(qs, ks, vs)
+        assert torch.equal(o1, o2) and torch.equal(l1, l2)
