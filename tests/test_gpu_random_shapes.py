@@ -201,3 +201,55 @@ def test_random_strided_inputs_same_bits(seed):
         o1, l1 = run(qd, kd, vd)
         o2, l2 = run(qs, ks, vs)
         assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_operator_explicit_indices(seed):
+    """The reference operator (ElasticSparseAttentionFunction, :241-339) on
+    random explicit index lists (duplicates, entries below 0 and past kv_len,
+    rows with no valid entry, q_len below kv_len) at random shapes, dtypes
+    and head dims: forward and gradients against autograd through the
+    oracle, out-of-range entries reading a zero K / V row as the Triton
+    gather mask makes them (:131-133)."""
+    from elastic_sparse_attention import ElasticSparseAttentionFunction
+    r = random.Random(3000 + seed)
+    H = r.choice([1, 2, 4, 6])
+    Hkv = r.choice([d for d in range(1, H + 1) if H % d == 0])
+    L = r.randint(8, 700)
+    Lq = L if r.random() < 0.5 else r.randint(1, L)
+    w = r.choice([1, 5, 16, 33, 64, 90])
+    D = r.choice([32, 64, 96, 128])
+    dtype = r.choice([torch.float32, torch.bfloat16, torch.float16])
+    B = r.choice([1, 2])
+    print(f"operator seed={seed} B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} w={w} D={D} {dtype}",
+          flush=True)
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, dtype, seed=900 + seed, Lq=Lq)
+    idx = torch.randint(-3, L + 3, (H, Lq, w), generator=g)
+    if w > 1:
+        idx[:, :, 1] = idx[:, :, 0]  # duplicates
+    msk = (torch.rand(H, Lq, w, generator=g) > 0.25).long()
+    msk[:, Lq // 2] = 0  # a row with no valid entry
+    oor = (idx < 0) | (idx >= L)
+    z = torch.zeros(B, Hkv, 1, D, dtype=dtype)
+    k2, v2 = torch.cat([k, z], dim=2), torch.cat([v, z], dim=2)
+    idx2 = torch.where(oor, torch.full_like(idx, L), idx)
+    sc = D ** -0.5
+    gout = torch.randn(B, H, Lq, D, generator=torch.Generator().manual_seed(7 + seed))
+    qf, kf, vf = (t.detach().float().clone().requires_grad_() for t in (q, k2, v2))
+    ro, _ = forward_fp32(qf, kf, vf, idx2, msk, sc, H // Hkv, chunk_rows=512)
+    (ro * gout).sum().backward()
+    rq, rk, rv = qf.grad, kf.grad[:, :, :L], vf.grad[:, :, :L]
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    o = ElasticSparseAttentionFunction.apply(qd, kd, vd, idx.to(DEV), msk.to(DEV), sc, H // Hkv)
+    o.backward(gout.to(dtype).to(DEV))
+    tol = TOL[dtype][0] if dtype != torch.float32 else 1e-4
+    assert (o.detach().float().cpu() - ro.detach()).abs().max().item() <= tol
+    # errors relative to each gradient's largest entry, or to 1% of dV's
+    # where that is smaller: with one valid key per row (w = 1) p = 1, so
+    # dS = p (dP - delta) and with it dQ and dK are exactly 0, and what the
+    # kernel returns is the rounding of dP - delta
+    floor = 1e-2 * rv.abs().max().item()
+    e = [(x.float().cpu() - y).abs().max().item() / max(y.abs().max().item(), floor, 1e-30)
+         for x, y in zip((qd.grad, kd.grad, vd.grad), (rq, rk, rv))]
+    assert max(e) <= (2e-2 if dtype != torch.float32 else 1e-4), e
