@@ -43,3 +43,26 @@ def test_noalloc_matches_allocating_backward(kernels):
         for r, x in zip(ref, got):
             assert torch.equal(r, x)
             assert bool(torch.isfinite(x.float()).all())
+
+
+def test_noalloc_random_sequence_of_calls():
+    """A run of noalloc backward calls at seeded random shapes (every kernel
+    pair, GQA, ragged lengths, decreasing and increasing sizes), each against
+    the allocating entry point bit for bit: whatever one call leaves in the
+    library's array, the next call's results do not depend on it."""
+    import random
+    r = random.Random(77)
+    for step in range(12):
+        H = r.choice([2, 4, 8])
+        Hkv = r.choice([d for d in range(1, H + 1) if H % d == 0])
+        L = r.randint(100, 2500)
+        D = r.choice([64, 128])
+        layer = r.randrange(8)
+        kernels = r.choice([("band", "band"), ("tile", "tile"), ("band", "tile"),
+                            ("tile", "band")])
+        B = r.choice([1, 2])
+        print(f"noalloc step {step} {kernels} B={B} H={H} Hkv={Hkv} L={L} D={D} layer={layer}",
+              flush=True)
+        ref, got = grads(B, H, Hkv, L, D, layer, kernels, 100 + step)
+        for a, b in zip(ref, got):
+            assert torch.equal(a, b)
