@@ -55,30 +55,39 @@ __device__ __forceinline__ float row4_max(float v) {
 }
 
 // min / max over the 16 lanes of a lane group (DPP row rotations)
+// (a row rotation writes every lane, so the moves carry no old value and
+// fold into the min / max as DPP operands)
 __device__ __forceinline__ int row16_min(int v) {
-  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));
-  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xf, 0xf, false));
-  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x122, 0xf, 0xf, false));
-  v = min(v, __builtin_amdgcn_update_dpp(v, v, 0x121, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_mov_dpp(v, 0x128, 0xf, 0xf, true));
+  v = min(v, __builtin_amdgcn_mov_dpp(v, 0x124, 0xf, 0xf, true));
+  v = min(v, __builtin_amdgcn_mov_dpp(v, 0x122, 0xf, 0xf, true));
+  v = min(v, __builtin_amdgcn_mov_dpp(v, 0x121, 0xf, 0xf, true));
   return v;
 }
 __device__ __forceinline__ int row16_max(int v) {
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x128, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x124, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x122, 0xf, 0xf, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x121, 0xf, 0xf, false));
+  v = max(v, __builtin_amdgcn_mov_dpp(v, 0x128, 0xf, 0xf, true));
+  v = max(v, __builtin_amdgcn_mov_dpp(v, 0x124, 0xf, 0xf, true));
+  v = max(v, __builtin_amdgcn_mov_dpp(v, 0x122, 0xf, 0xf, true));
+  v = max(v, __builtin_amdgcn_mov_dpp(v, 0x121, 0xf, 0xf, true));
   return v;
 }
 
-
 // This lane's row i (of a 16-row group): slot (q, r), r = 0..15 of lane
 // group q, holds entry j = (16 q + r + rot) mod 64, so a wave walking the
-// slots in order visits the entries from entry rot on.  kreg[r] = the row's
-// key of that entry, or -1 when the entry is masked (j >= w, idx > i) or the
-// row is past q_len; and, the same in every lane of group q, the group's
-// band descriptors info[r] = lo | W << 24, with lo / lo + W - 1 the smallest
-// / largest valid key of the slot's entry over the group's rows (W = 0: no
-// row uses it).  lo < 2^24 (host check).
+// slots in order visits the entries from entry rot on.  The row's key of
+// that entry is -1 when the entry is masked (j >= w, idx > i) or the row is
+// past q_len; the group's band descriptor of the slot is lo | W << 24, with
+// lo / lo + W - 1 the smallest / largest valid key of the slot's entry over
+// the group's rows (W = 0: no row uses it; W capped at 255); lo < 2^24 (host
+// check).  Both come packed into 5 registers:
+//   kd[r / 4], byte r % 4: the row's key of slot (q, r) minus the slot's lo,
+//     0xFF for no key.  A band spans at most 31 keys over 16 rows (keys move
+//     by at most 2 per row); an offset past 254 would read as no key, as a
+//     tail pass bounded by the capped W would drop it.
+//   info1: lane (n, q) holds the descriptor of slot (q, n), so slot (q, r)'s
+//     is readlane(info1, 16 q + r).
+// o_j is formed once per entry: entry j_r + 1 is j_{r+1} = (16 q + r + 1 +
+// rot) mod 64 except at j_r = 63, whose o_64 is formed once.
 //
 // The rotation is the L2 schedule: groups are dispatched one after another
 // onto an XCD's resident waves, each walking its 64 entries in the same
@@ -91,21 +100,35 @@ __device__ __forceinline__ int row16_max(int v) {
 // resident waves) at B=1 H=32 L=32768 layer 4 puts the hit rate at 0.79
 // without and 0.94 with the rotation.
 __device__ __forceinline__ void band_rows(const PatternConsts& pc, int h, int i, bool row_ok,
-                                          int q, int rot, int (&kreg)[16], int (&info)[16]) {
+                                          int q, int n, int rot, uint32_t (&kd)[4],
+                                          int& info1) {
   const HeadWeights hw = head_weights(pc, h);
   const RowParams rp = row_params(pc, i);
+  int ov[17];
+#pragma unroll
+  for (int r = 0; r < 17; ++r) ov[r] = oversized(rp, (16 * q + r + rot) & 63);
+  const int o64 = oversized(rp, 64);
+  int kreg[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int j = (16 * q + r + rot) & 63;
-    const int idx = interp_index(oversized(rp, j), oversized(rp, j + 1), hw);
+    const int idx = interp_index(ov[r], j == 63 ? o64 : ov[r + 1], hw);
     kreg[r] = (row_ok && j < pc.w && idx <= i) ? idx : -1;
   }
+  info1 = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) kd[w] = 0u;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int lo = row16_min(kreg[r] < 0 ? 0x7fffffff : kreg[r]);
     const int hi = row16_max(kreg[r]);
     const int wdt = hi >= 0 ? min(hi - lo + 1, 255) : 0;
-    info[r] = hi >= 0 ? (lo | (wdt << 24)) : 0;
+    const int desc = hi >= 0 ? (lo | (wdt << 24)) : 0;
+    info1 = n == r ? desc : info1;
+    // kreg[r] - lo is in 0 .. 254 for a key in reach, and for no key
+    // (kreg[r] = -1 <= lo - 1) wraps past 255 as unsigned
+    const uint32_t db = min((uint32_t)(kreg[r] - lo), 0xFFu);
+    kd[r >> 2] |= db << (8 * (r & 3));
   }
 }
 

@@ -151,16 +151,17 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
     }
   }
 
-  int kreg[16], info[16];
+  uint32_t kd[4];  // the row's key offsets (band_rows)
+  int info1;       // slot (q, r)'s descriptor in lane 16 q + r
   // entry rotation, in 64ths of an entry per group dispatched on the XCD: a
   // little ahead of the dispatch rate, 64 / (resident waves per XCD) = 16/64
-  // at D = 128 (256 resident) and 10.7/64 at D = 64 (384), as in the
-  // forward; measured 1-4% faster than 16/64 at B=1 H=8 L=131072 layers 4
-  // and 7, unchanged at B=1 H=32 L=32768
+  // at D = 128 (256 resident) and 8/64 at D = 64 (512), as in the forward;
+  // measured 1-4% faster than 16/64 at B=1 H=8 L=131072 layers 4 and 7,
+  // unchanged at B=1 H=32 L=32768 (and 9/64 at D = 64 within 1% of 12/64)
   // (unsigned: the product wraps for grids near 2^31 blocks; only the value
   // mod 64 matters)
-  band_rows(A.pc, h, i, row_ok, q,
-            (int)(((unsigned)(bid >> 3) * (D == 128 ? 19u : 12u) / 64u) & 63u), kreg, info);
+  band_rows(A.pc, h, i, row_ok, q, n,
+            (int)(((unsigned)(bid >> 3) * (D == 128 ? 19u : 12u) / 64u) & 63u), kd, info1);
 
   const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
   const char* const vbase = (const char*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh);
@@ -251,9 +252,11 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   const float scale2 = A.scale_log2;
   // dS of this row's key in chunk [c0, c0 + 16) of a band, as bf16 at the
   // key's register slot of the lane holding it (0 elsewhere)
-  auto ds_word = [&](const f32x4& sacc, const f32x4& pacc, int key, int c0) -> uint64_t {
-    const int d = key - c0;
-    const bool has = key >= 0 && (uint32_t)d < 16u && (d >> 2) == q;
+  // d = the row's key minus the chunk's first key (no key in the chunk: d <
+  // 0 or d >= 16); this lane holds the key when d >> 2 == q (an arithmetic
+  // shift keeping d < 0 out)
+  auto ds_word = [&](const f32x4& sacc, const f32x4& pacc, int d) -> uint64_t {
+    const bool has = (d >> 2) == q;
     const int e = d & 3;
     const float s01 = (e & 1) ? sacc[1] : sacc[0];
     const float s23 = (e & 1) ? sacc[3] : sacc[2];
@@ -290,8 +293,8 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   constexpr int kWaitLds = 0xC07F;                           // lgkmcnt(0)
   const int lane_key = 4 * n;
   {
-    const int i0 = __builtin_amdgcn_readlane(info[0], 0);
-    const int i1 = __builtin_amdgcn_readlane(info[1], 0);
+    const int i0 = __builtin_amdgcn_readlane(info1, 0);
+    const int i1 = __builtin_amdgcn_readlane(info1, 1);
     __builtin_amdgcn_s_waitcnt(kWaitLds);  // the slot zeros are in LDS
     load_k(i0, lk0);
     load_k(i1, lk1);
@@ -303,15 +306,13 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
 #pragma unroll
     for (int rp = 0; rp < 8; ++rp) {
       const int ra = 2 * rp, rb = 2 * rp + 1;
-      const int ia = __builtin_amdgcn_readlane(info[ra], 16 * qj);
-      const int ib = __builtin_amdgcn_readlane(info[rb], 16 * qj);
-      int na, nb;
-      if (rp < 7) {
-        na = __builtin_amdgcn_readlane(info[ra + 2], 16 * qj);
-        nb = __builtin_amdgcn_readlane(info[rb + 2], 16 * qj);
-      } else {
-        na = more ? __builtin_amdgcn_readlane(info[0], 16 * qj + 16) : 0;
-        nb = more ? __builtin_amdgcn_readlane(info[1], 16 * qj + 16) : 0;
+      const int ia = __builtin_amdgcn_readlane(info1, 16 * qj + ra);
+      const int ib = __builtin_amdgcn_readlane(info1, 16 * qj + rb);
+      // next pair's (at rp = 7 slots 0 and 1 of lane group qj + 1)
+      int na = 0, nb = 0;
+      if (rp < 7 || more) {
+        na = __builtin_amdgcn_readlane(info1, 16 * qj + ra + 2);
+        nb = __builtin_amdgcn_readlane(info1, 16 * qj + rb + 2);
       }
       const bool live = (ia | ib) != 0;
       // this pair's K is in LDS
@@ -348,11 +349,11 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
       if (live) {
         const f32x4 pa = product(va, dop);
         const f32x4 pb = product(vb, dop);
-        const int addr = lane_key + 64 * qj;
-        const int keya = __builtin_amdgcn_ds_bpermute(addr, kreg[ra]);
-        const int keyb = __builtin_amdgcn_ds_bpermute(addr, kreg[rb]);
-        const uint64_t wa = ds_word(sa, pa, keya, ia & 0xffffff);
-        const uint64_t wb = ds_word(sb, pb, keyb, ib & 0xffffff);
+        // both bands' key offsets: bytes ra % 4, rb % 4 of word rp / 2
+        const uint32_t dw =
+            (uint32_t)__builtin_amdgcn_ds_bpermute(lane_key + 64 * qj, (int)kd[rp >> 1]);
+        const uint64_t wa = ds_word(sa, pa, (int)((dw >> (16 * (rp & 1))) & 0xFFu));
+        const uint64_t wb = ds_word(sb, pb, (int)((dw >> (16 * (rp & 1) + 8)) & 0xFFu));
         dq_step(ta, tb, wa, wb);
       }
     }
@@ -361,19 +362,13 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   // ---- tail: keys of bands wider than 16, one 16-key chunk at a time (the
   // pair's second half is ks1 with dS = 0; ks1 holds finite rows)
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  int wmax = 0;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) wmax = max(wmax, (int)((uint32_t)info[r] >> 24));
-  for (int j = 0; j < 64 && wave_any(wmax > 16); ++j) {
-    const int qj = j >> 4;
-    int bi = 0, key = -1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      if ((j & 15) == r) {
-        bi = __builtin_amdgcn_readlane(info[r], 16 * qj);
-        key = __builtin_amdgcn_ds_bpermute(lane_key + 64 * qj, kreg[r]);
-      }
-    }
+  const bool wide = wave_any(((uint32_t)info1 >> 24) > 16u);  // some slot's band
+  for (int j = 0; j < 64 && wide; ++j) {
+    const int qj = j >> 4, r = j & 15;
+    const int bi = __builtin_amdgcn_readlane(info1, j);  // slot (qj, r)
+    const uint32_t w4 = r < 8 ? (r < 4 ? kd[0] : kd[1]) : (r < 12 ? kd[2] : kd[3]);
+    const uint32_t dw = (uint32_t)__builtin_amdgcn_ds_bpermute(lane_key + 64 * qj, (int)w4);
+    const int d = (int)((dw >> (8 * (r & 3))) & 0xFFu);  // 0xFF: no key
     const int lo = bi & 0xffffff, wdt = (int)((uint32_t)bi >> 24);
     for (int c0 = lo + 16; c0 < lo + wdt; c0 += 16) {
       const int ci = c0 | (min(lo + wdt - c0, 16) << 24);
@@ -389,7 +384,7 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
       read_tr(ks1, tz);
       const f32x4 st = product(kt, qop);
       const f32x4 pt = product(vt, dop);
-      dq_step(tt, tz, ds_word(st, pt, key, c0), 0ull);
+      dq_step(tt, tz, ds_word(st, pt, d == 0xFF ? -1 : d - (c0 - lo)), 0ull);
     }
   }
 

@@ -99,22 +99,24 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     }
   }
 
-  // ---- this row's keys of bands 16 q .. 16 q + 15 (-1: no key), and the
-  // group's band descriptors for the same bands (every lane of group q)
-  int kreg[16], info[16];
+  // ---- this row's keys of bands 16 q .. 16 q + 15 as offsets from the
+  // bands' first keys (kd, byte r of word r / 4; 0xFF: no key), and the
+  // group's band descriptors (slot (q, r)'s in lane 16 q + r of info1)
+  uint32_t kd[4];
+  int info1;
   // entry rotation, in 64ths of an entry per group dispatched on the XCD:
-  // an XCD keeps 320 waves resident at D = 128 (ten per CU, by LDS) and 512
-  // at D = 64 (sixteen, by registers), so a group is dispatched about every
-  // 64 / 320 = 12.8/64 or 64 / 512 = 8/64 of a wave's walk; the rotation
-  // leads that by a little.  Measured rates per 64th: 15 and 9 are the best
+  // an XCD keeps 320 waves resident at D = 128 (ten per CU, by LDS) and 640
+  // at D = 64 (twenty, by LDS and registers alike), so a group is dispatched
+  // about every 64 / 320 = 12.8/64 or 64 / 640 = 6.4/64 of a wave's walk;
+  // the rotation leads that.  Measured rates per 64th: 15 and 9 are the best
   // or within 2% of it at every layer of B=1 H=8 L=131072, where an XCD's L2
   // cannot hold the resident groups' rows across entries (12/64 there was
   // 8-11% slower at D = 128 layers 4-7 and 17-22% at D = 64), and shapes up
-  // to L=32768 do not move with the rate.
+  // to L=32768 do not move with the rate (7 and 8 at D = 64 within 1% of 9).
   // (unsigned: the product wraps for grids near 2^31 blocks; only the value
   // mod 64 matters)
-  band_rows(A.pc, h, i, row_ok, q,
-            (int)(((unsigned)(bid >> 3) * (D == 128 ? 15u : 9u) / 64u) & 63u), kreg, info);
+  band_rows(A.pc, h, i, row_ok, q, n,
+            (int)(((unsigned)(bid >> 3) * (D == 128 ? 15u : 9u) / 64u) & 63u), kd, info1);
 
   const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
   const char* const vbase = (const char*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh);
@@ -203,13 +205,13 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
 #pragma unroll
   for (int s = 0; s < C::NV; ++s) oacc[s] = f32x4{};
 
-  // This row's scaled score (log2 units) in chunk [c0, c0 + 16) of a band
-  // (key = the row's key of the band, -1 for none), the same in the row's 4
-  // lanes; -inf when the row has no key there.  has / e: this lane holds the
-  // key, at register e.
-  auto pick = [&](const f32x4& sacc, int key, int c0, bool& has, int& e) -> float {
-    const int d = key - c0;
-    has = key >= 0 && (uint32_t)d < 16u && (d >> 2) == q;
+  // This row's scaled score (log2 units) in a 16-key chunk of a band (d =
+  // the row's key minus the chunk's first key; no key in the chunk: d < 0 or
+  // d >= 16), the same in the row's 4 lanes; -inf when the row has no key
+  // there.  has / e: this lane holds the key, at register e (d >> 2 == q
+  // only for d in 4 q .. 4 q + 3, an arithmetic shift keeping d < 0 out).
+  auto pick = [&](const f32x4& sacc, int d, bool& has, int& e) -> float {
+    has = (d >> 2) == q;
     e = d & 3;
     const float s01 = (e & 1) ? sacc[1] : sacc[0];
     const float s23 = (e & 1) ? sacc[3] : sacc[2];
@@ -291,8 +293,8 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   constexpr int kWaitLds = 0xC07F;                           // lgkmcnt(0)
   const int lane_key = 4 * n;  // ds_bpermute byte address of row n in group 0
   {
-    const int i0 = __builtin_amdgcn_readlane(info[0], 0);
-    const int i1 = __builtin_amdgcn_readlane(info[1], 0);
+    const int i0 = __builtin_amdgcn_readlane(info1, 0);
+    const int i1 = __builtin_amdgcn_readlane(info1, 1);
     __builtin_amdgcn_s_waitcnt(kWaitLds);  // the slot zeros are in LDS
     load_k(i0, lk0);
     load_k(i1, lk1);
@@ -304,16 +306,14 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
 #pragma unroll
     for (int rp = 0; rp < 8; ++rp) {
       const int ra = 2 * rp, rb = 2 * rp + 1;
-      const int ia = __builtin_amdgcn_readlane(info[ra], 16 * qj);
-      const int ib = __builtin_amdgcn_readlane(info[rb], 16 * qj);
-      // next pair's descriptors
-      int na, nb;
-      if (rp < 7) {
-        na = __builtin_amdgcn_readlane(info[ra + 2], 16 * qj);
-        nb = __builtin_amdgcn_readlane(info[rb + 2], 16 * qj);
-      } else {
-        na = more ? __builtin_amdgcn_readlane(info[0], 16 * qj + 16) : 0;
-        nb = more ? __builtin_amdgcn_readlane(info[1], 16 * qj + 16) : 0;
+      const int ia = __builtin_amdgcn_readlane(info1, 16 * qj + ra);
+      const int ib = __builtin_amdgcn_readlane(info1, 16 * qj + rb);
+      // next pair's descriptors (slots 16 qj + ra + 2, + rb + 2: at rp = 7
+      // slots 0 and 1 of lane group qj + 1)
+      int na = 0, nb = 0;
+      if (rp < 7 || more) {
+        na = __builtin_amdgcn_readlane(info1, 16 * qj + ra + 2);
+        nb = __builtin_amdgcn_readlane(info1, 16 * qj + rb + 2);
       }
       const bool live = (ia | ib) != 0;  // some row of the group uses a band
       const int n_nxt = KSKIP ? n_loads(na) + n_loads(nb) : 2 * C::VLOADS;  // next K DMAs
@@ -327,15 +327,18 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
       load_k(na, lk0);
       load_k(nb, lk1);
       if (live) {
-        const int addr = lane_key + 64 * qj;
-        const int keya = __builtin_amdgcn_ds_bpermute(addr, kreg[ra]);
-        const int keyb = __builtin_amdgcn_ds_bpermute(addr, kreg[rb]);
+        // the row's key offsets of both bands: bytes ra % 4, rb % 4 of word
+        // rp / 2 (the same word for the pair)
+        const uint32_t dw =
+            (uint32_t)__builtin_amdgcn_ds_bpermute(lane_key + 64 * qj, (int)kd[rp >> 1]);
+        const int da = (int)((dw >> (16 * (rp & 1))) & 0xFFu);
+        const int db = (int)((dw >> (16 * (rp & 1) + 8)) & 0xFFu);
         const f32x4 sa = scores(kopa);
         const f32x4 sb = scores(kopb);
         bool ha, hb;
         int ea, eb;
-        const float xa = pick(sa, keya, ia & 0xffffff, ha, ea);
-        const float xb = pick(sb, keyb, ib & 0xffffff, hb, eb);
+        const float xa = pick(sa, da, ha, ea);
+        const float xb = pick(sb, db, hb, eb);
         uint64_t pa, pbw;
         pair_softmax(xa, ha, ea, xb, hb, eb, pa, pbw);
         // this pair's V is in LDS
@@ -359,19 +362,13 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
 
   // ---- tail: keys of bands wider than 16, one 16-key chunk at a time
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  int wmax = 0;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) wmax = max(wmax, (int)((uint32_t)info[r] >> 24));
-  for (int j = 0; j < 64 && wave_any(wmax > 16); ++j) {
-    const int qj = j >> 4;
-    int bi = 0, key = -1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      if ((j & 15) == r) {
-        bi = __builtin_amdgcn_readlane(info[r], 16 * qj);
-        key = __builtin_amdgcn_ds_bpermute(lane_key + 64 * qj, kreg[r]);
-      }
-    }
+  const bool wide = wave_any(((uint32_t)info1 >> 24) > 16u);  // some slot's band
+  for (int j = 0; j < 64 && wide; ++j) {
+    const int qj = j >> 4, r = j & 15;
+    const int bi = __builtin_amdgcn_readlane(info1, j);  // slot (qj, r)
+    const uint32_t w4 = r < 8 ? (r < 4 ? kd[0] : kd[1]) : (r < 12 ? kd[2] : kd[3]);
+    const uint32_t dw = (uint32_t)__builtin_amdgcn_ds_bpermute(lane_key + 64 * qj, (int)w4);
+    const int d = (int)((dw >> (8 * (r & 3))) & 0xFFu);  // 0xFF: no key
     const int lo = bi & 0xffffff, wdt = (int)((uint32_t)bi >> 24);
     for (int c0 = lo + 16; c0 < lo + wdt; c0 += 16) {
       const int rem = lo + wdt - c0;
@@ -385,7 +382,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
       const f32x4 st = scores(kt);
       bool ht;
       int et;
-      const float xt = pick(st, key, c0, ht, et);
+      const float xt = pick(st, d == 0xFF ? -1 : d - (c0 - lo), ht, et);
       uint64_t pt, pz;
       pair_softmax(xt, ht, et, -INFINITY, false, 0, pt, pz);
       // the second band of the pair contributes p = 0 (vs1 holds finite rows)
