@@ -36,9 +36,9 @@
 // K and V rows reach LDS by buffer_load ... lds, whole rows per 16 lanes:
 // the L1 spends about a clock per (16-lane pass, cache line), so loading the
 // MFMA operand straight into registers (16 key rows per pass) would cost 8x
-// the L1 time.  Two K and two V slots per wave: the next pair's K is
-// requested once this pair's K operands are in registers, its V once this
-// pair's PV has read V.
+// the L1 time.  Two K and two V slots per wave: once a pair's K and V^T
+// operands are in registers, the next pair's K and V are requested together,
+// so both have the whole pair's scores, softmax and PV to land.
 //
 // Operand layouts: esa_band.hpp.
 #include "esa_band.hpp"
@@ -144,7 +144,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   // with KSKIP only the ceil(W / RPI) that reach a band row (each DMA costs
   // the texture unit a full 64-lane transfer, rows past W included): K rows
   // past the band then keep older finite contents, whose scores belong to
-  // keys no row picks.  The vmcnt waits below count the DMAs issued.
+  // keys no row picks.
   constexpr int RPI = 64 / C::CPR;  // slot rows per DMA
   auto n_loads = [&](int bi) { return (min((int)((uint32_t)bi >> 24), 16) + RPI - 1) / RPI; };
   auto load_rows = [&](const char* base, int ss2, const int* ofs, int bi, lds_u16* dst,
@@ -163,21 +163,6 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   };
   auto load_k = [&](int bi, lds_u16* dst) { load_rows(kbase, kss2, kofs, bi, dst, !KSKIP); };
   auto load_v = [&](int bi, lds_u16* dst) { load_rows(vbase, vss2, vofs, bi, dst, true); };
-  // s_waitcnt vmcnt(n) for a count known only at run time (0 .. 8)
-  auto wait_vm = [&](int n) {
-    switch (n) {
-      case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-      case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
-      case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
-      case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
-      case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
-      case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
-      case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-      case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
-      default: __builtin_amdgcn_s_waitcnt(0x0F78); break;
-    }
-  };
-  static_assert(2 * C::VLOADS <= 8, "wait_vm covers at most 8 DMAs in flight");
 
   // K operand read addresses (bytes within a slot) for k-step s: lane
   // (m = n, q) reads key row n, dims 32 s + 8 q .. + 8
@@ -262,18 +247,20 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     return sacc;
   };
 
-  // O^T += V^T P^T over two bands held in ring slots va, vb with P words
-  // pa, pb (k-slots 8 q .. 8 q + 3: band a keys 4 q .. 4 q + 3; 8 q + 4 ..
-  // 8 q + 7: band b's)
-  auto pv = [&](const uint16_t* va, const uint16_t* vb, uint64_t pa, uint64_t pb) {
-    s16x4 ta[C::NV], tb[C::NV];
+  // V^T operands of two bands from slots va, vb (ds_read_b64_tr_b16)
+  auto read_vt = [&](const uint16_t* va, const uint16_t* vb, s16x4 (&ta)[C::NV],
+                     s16x4 (&tb)[C::NV]) {
 #pragma unroll
     for (int s = 0; s < C::NV; ++s) {
-      ta[s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_s16x4*)((const char*)va + vrd[s]));
-      tb[s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_s16x4*)((const char*)vb + vrd[s]));
+      ta[s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((const char*)va + vrd[s]));
+      tb[s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((const char*)vb + vrd[s]));
     }
+  };
+  // O^T += V^T P^T over two bands' V^T operands ta, tb with P words pa, pb
+  // (k-slots 8 q .. 8 q + 3: band a keys 4 q .. 4 q + 3; 8 q + 4 .. 8 q + 7:
+  // band b's)
+  auto pv = [&](const s16x4 (&ta)[C::NV], const s16x4 (&tb)[C::NV], uint64_t pa,
+                uint64_t pb) {
     const u32x4 pq = {(uint32_t)pa, (uint32_t)(pa >> 32), (uint32_t)pb, (uint32_t)(pb >> 32)};
     const V8 pop = __builtin_bit_cast(V8, pq);
 #pragma unroll
@@ -283,15 +270,12 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     }
   };
 
-  // ---- main loop: band pairs (2 p, 2 p + 1).  Load order per pair: K of
-  // the next pair (after this pair's K reads), then V of the next pair (after
-  // this pair's PV).  So before the K wait exactly this pair's 2 VLOADS V
-  // DMAs may be newer, and before the V wait the next pair's K DMAs (2 VLOADS
-  // of them, or with KSKIP as many as load_k issued).
-  constexpr int kWaitPair = (0xF70 & ~0xF) | ((2 * C::VLOADS) & 0xF) |
-                            (((2 * C::VLOADS) >> 4) << 14);  // vmcnt(2 VLOADS)
-  constexpr int kWaitLds = 0xC07F;                           // lgkmcnt(0)
-  const int lane_key = 4 * n;  // ds_bpermute byte address of row n in group 0
+  // ---- main loop: band pairs (2 p, 2 p + 1).  Per pair: wait for its K
+  // and V DMAs (the only ones outstanding), read the K and V^T operands,
+  // then request the next pair's K and V into the same slots, and compute
+  // from registers: scores, select, softmax, PV.
+  constexpr int kWaitLds = 0xC07F;  // lgkmcnt(0)
+  const int lane_key = 4 * n;       // ds_bpermute byte address of row n in group 0
   {
     const int i0 = __builtin_amdgcn_readlane(info1, 0);
     const int i1 = __builtin_amdgcn_readlane(info1, 1);
@@ -316,16 +300,19 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
         nb = __builtin_amdgcn_readlane(info1, 16 * qj + rb + 2);
       }
       const bool live = (ia | ib) != 0;  // some row of the group uses a band
-      const int n_nxt = KSKIP ? n_loads(na) + n_loads(nb) : 2 * C::VLOADS;  // next K DMAs
-      __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's K is in LDS
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this pair's K and V are in LDS
       V8 kopa[C::NS], kopb[C::NS];
+      s16x4 ta[C::NV], tb[C::NV];
       if (live) {
         read_k(ks0, kopa);
         read_k(ks1, kopb);
+        read_vt(vs0, vs1, ta, tb);
       }
-      __builtin_amdgcn_s_waitcnt(kWaitLds);  // K slots read: refill them
+      __builtin_amdgcn_s_waitcnt(kWaitLds);  // slots read: refill them
       load_k(na, lk0);
       load_k(nb, lk1);
+      load_v(na, lv0);
+      load_v(nb, lv1);
       if (live) {
         // the row's key offsets of both bands: bytes ra % 4, rb % 4 of word
         // rp / 2 (the same word for the pair)
@@ -341,22 +328,8 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
         const float xb = pick(sb, db, hb, eb);
         uint64_t pa, pbw;
         pair_softmax(xa, ha, ea, xb, hb, eb, pa, pbw);
-        // this pair's V is in LDS
-        if constexpr (KSKIP)
-          wait_vm(n_nxt);
-        else
-          __builtin_amdgcn_s_waitcnt(kWaitPair);
-        pv(vs0, vs1, pa, pbw);
+        pv(ta, tb, pa, pbw);
       }
-      // this pair's V has landed (and been read): refill the V slots
-      if constexpr (KSKIP) {
-        wait_vm(n_nxt);
-        __builtin_amdgcn_s_waitcnt(kWaitLds);
-      } else {
-        __builtin_amdgcn_s_waitcnt(kWaitPair & kWaitLds);
-      }
-      load_v(na, lv0);
-      load_v(nb, lv1);
     }
   }
 
@@ -386,7 +359,9 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
       uint64_t pt, pz;
       pair_softmax(xt, ht, et, -INFINITY, false, 0, pt, pz);
       // the second band of the pair contributes p = 0 (vs1 holds finite rows)
-      pv(vs0, vs1, pt, 0ull);
+      s16x4 ta[C::NV], tb[C::NV];
+      read_vt(vs0, vs1, ta, tb);
+      pv(ta, tb, pt, 0ull);
     }
   }
 
