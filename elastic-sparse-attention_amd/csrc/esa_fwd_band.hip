@@ -36,9 +36,13 @@
 // K and V rows reach LDS by buffer_load ... lds, whole rows per 16 lanes:
 // the L1 spends about a clock per (16-lane pass, cache line), so loading the
 // MFMA operand straight into registers (16 key rows per pass) would cost 8x
-// the L1 time.  Two K and two V slots per wave: once a pair's K and V^T
-// operands are in registers, the next pair's K and V are requested together,
-// so both have the whole pair's scores, softmax and PV to land.
+// the L1 time.  Two K and two V slots per wave, refilled in one of two
+// orders (VEARLY, picked by the host):
+//   VEARLY    once a pair's K and V^T operands are in registers, the next
+//             pair's K and V are requested together, so both have the whole
+//             pair's scores, softmax and PV to land;
+//   otherwise the next pair's K is requested once this pair's K operands are
+//             in registers, its V once this pair's PV has read V.
 //
 // Operand layouts: esa_band.hpp.
 #include "esa_band.hpp"
@@ -52,7 +56,7 @@ namespace esa {
 // where many bands are narrower than 16 keys (the dilated, late layers);
 // where nearly every band is 16 keys wide the run-time waits cost more than
 // the DMAs saved, so the host picks it by the pattern's interpolation weight.
-template <int D, bool KSKIP, Elem E>
+template <int D, bool KSKIP, bool VEARLY, Elem E>
 __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   using C = BandCfg<D>;
   using M = MmaT<E>;
@@ -163,6 +167,21 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   };
   auto load_k = [&](int bi, lds_u16* dst) { load_rows(kbase, kss2, kofs, bi, dst, !KSKIP); };
   auto load_v = [&](int bi, lds_u16* dst) { load_rows(vbase, vss2, vofs, bi, dst, true); };
+  // s_waitcnt vmcnt(n) for a count known only at run time (0 .. 8)
+  auto wait_vm = [&](int n) {
+    switch (n) {
+      case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+      case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+      case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+      case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+      case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+      case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+      case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+      case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+      default: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+    }
+  };
+  static_assert(2 * C::VLOADS <= 8, "wait_vm covers at most 8 DMAs in flight");
 
   // K operand read addresses (bytes within a slot) for k-step s: lane
   // (m = n, q) reads key row n, dims 32 s + 8 q .. + 8
@@ -270,12 +289,17 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     }
   };
 
-  // ---- main loop: band pairs (2 p, 2 p + 1).  Per pair: wait for its K
-  // and V DMAs (the only ones outstanding), read the K and V^T operands,
-  // then request the next pair's K and V into the same slots, and compute
-  // from registers: scores, select, softmax, PV.
-  constexpr int kWaitLds = 0xC07F;  // lgkmcnt(0)
-  const int lane_key = 4 * n;       // ds_bpermute byte address of row n in group 0
+  // ---- main loop: band pairs (2 p, 2 p + 1).
+  //   VEARLY: wait for the pair's K and V DMAs (the only ones outstanding),
+  //   read the K and V^T operands, request the next pair's K and V into the
+  //   same slots, then compute from registers.
+  //   Otherwise: before the K wait exactly this pair's 2 VLOADS V DMAs may be
+  //   newer; before the V wait the next pair's K DMAs (2 VLOADS of them, or
+  //   with KSKIP as many as load_k issued).
+  constexpr int kWaitPair = (0xF70 & ~0xF) | ((2 * C::VLOADS) & 0xF) |
+                            (((2 * C::VLOADS) >> 4) << 14);  // vmcnt(2 VLOADS)
+  constexpr int kWaitLds = 0xC07F;                           // lgkmcnt(0)
+  const int lane_key = 4 * n;  // ds_bpermute byte address of row n in group 0
   {
     const int i0 = __builtin_amdgcn_readlane(info1, 0);
     const int i1 = __builtin_amdgcn_readlane(info1, 1);
@@ -300,19 +324,31 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
         nb = __builtin_amdgcn_readlane(info1, 16 * qj + rb + 2);
       }
       const bool live = (ia | ib) != 0;  // some row of the group uses a band
-      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this pair's K and V are in LDS
+      const int n_nxt = KSKIP ? n_loads(na) + n_loads(nb) : 2 * C::VLOADS;  // next K DMAs
       V8 kopa[C::NS], kopb[C::NS];
       s16x4 ta[C::NV], tb[C::NV];
-      if (live) {
-        read_k(ks0, kopa);
-        read_k(ks1, kopb);
-        read_vt(vs0, vs1, ta, tb);
+      if constexpr (VEARLY) {
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this pair's K and V are in LDS
+        if (live) {
+          read_k(ks0, kopa);
+          read_k(ks1, kopb);
+          read_vt(vs0, vs1, ta, tb);
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitLds);  // slots read: refill them
+        load_k(na, lk0);
+        load_k(nb, lk1);
+        load_v(na, lv0);
+        load_v(nb, lv1);
+      } else {
+        __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's K is in LDS
+        if (live) {
+          read_k(ks0, kopa);
+          read_k(ks1, kopb);
+        }
+        __builtin_amdgcn_s_waitcnt(kWaitLds);  // K slots read: refill them
+        load_k(na, lk0);
+        load_k(nb, lk1);
       }
-      __builtin_amdgcn_s_waitcnt(kWaitLds);  // slots read: refill them
-      load_k(na, lk0);
-      load_k(nb, lk1);
-      load_v(na, lv0);
-      load_v(nb, lv1);
       if (live) {
         // the row's key offsets of both bands: bytes ra % 4, rb % 4 of word
         // rp / 2 (the same word for the pair)
@@ -328,7 +364,26 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
         const float xb = pick(sb, db, hb, eb);
         uint64_t pa, pbw;
         pair_softmax(xa, ha, ea, xb, hb, eb, pa, pbw);
+        if constexpr (!VEARLY) {
+          // this pair's V is in LDS
+          if constexpr (KSKIP)
+            wait_vm(n_nxt);
+          else
+            __builtin_amdgcn_s_waitcnt(kWaitPair);
+          read_vt(vs0, vs1, ta, tb);
+        }
         pv(ta, tb, pa, pbw);
+      }
+      if constexpr (!VEARLY) {
+        // this pair's V has landed (and been read): refill the V slots
+        if constexpr (KSKIP) {
+          wait_vm(n_nxt);
+          __builtin_amdgcn_s_waitcnt(kWaitLds);
+        } else {
+          __builtin_amdgcn_s_waitcnt(kWaitPair & kWaitLds);
+        }
+        load_v(na, lv0);
+        load_v(nb, lv1);
       }
     }
   }
@@ -388,20 +443,28 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   }
 }
 
-template <Elem E>
-void launch_band_elem(const BandArgs& a, int head_dim, dim3 grid, bool kskip,
-                      hipStream_t stream) {
-  if (head_dim == 128) {
-    if (kskip)
-      band_fwd_kernel<128, true, E><<<grid, 64, 0, stream>>>(a);
+template <int D, Elem E>
+void launch_band_d(const BandArgs& a, dim3 grid, bool kskip, bool vearly, hipStream_t stream) {
+  if (kskip) {
+    if (vearly)
+      band_fwd_kernel<D, true, true, E><<<grid, 64, 0, stream>>>(a);
     else
-      band_fwd_kernel<128, false, E><<<grid, 64, 0, stream>>>(a);
+      band_fwd_kernel<D, true, false, E><<<grid, 64, 0, stream>>>(a);
   } else {
-    if (kskip)
-      band_fwd_kernel<64, true, E><<<grid, 64, 0, stream>>>(a);
+    if (vearly)
+      band_fwd_kernel<D, false, true, E><<<grid, 64, 0, stream>>>(a);
     else
-      band_fwd_kernel<64, false, E><<<grid, 64, 0, stream>>>(a);
+      band_fwd_kernel<D, false, false, E><<<grid, 64, 0, stream>>>(a);
   }
+}
+
+template <Elem E>
+void launch_band_elem(const BandArgs& a, int head_dim, dim3 grid, bool kskip, bool vearly,
+                      hipStream_t stream) {
+  if (head_dim == 128)
+    launch_band_d<128, E>(a, grid, kskip, vearly, stream);
+  else
+    launch_band_d<64, E>(a, grid, kskip, vearly, stream);
 }
 
 hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) {
@@ -411,10 +474,19 @@ hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) 
   // L=32768, D=128, w=64 over 8 layers: 1-7% faster at weights 4/7 .. 1,
   // even at 3/7, 3-4% slower at 1/7 and 2/7
   const bool kskip = a.pc.a >= 0.5f;
+  // The refill order by the entry spacing at the last row, (q_len a + c) / w
+  // query rows between one entry's keys and the next's: at B=1 H=8 L=131072
+  // D=128 the early V requests were 9-11% faster at spacings 586 and 878
+  // (layers 2, 3) and 3-12% slower at 1171 .. 2048 (layers 4-7), where the
+  // L2 hit rate fell from 0.73 to 0.64 (layer 4) and HBM misses bound the
+  // kernel; at the shapes up to L = 32768 (spacings up to 512) they were
+  // faster or within 3.5%.
+  const float spacing = ((float)a.q_len * a.pc.a + a.pc.c) / (float)a.pc.w;
+  const bool vearly = spacing < 1000.0f;
   if (a.elem == (int)Elem::f16)
-    launch_band_elem<Elem::f16>(a, head_dim, grid, kskip, stream);
+    launch_band_elem<Elem::f16>(a, head_dim, grid, kskip, vearly, stream);
   else
-    launch_band_elem<Elem::bf16>(a, head_dim, grid, kskip, stream);
+    launch_band_elem<Elem::bf16>(a, head_dim, grid, kskip, vearly, stream);
   return hipGetLastError();
 }
 

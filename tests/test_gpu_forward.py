@@ -293,6 +293,10 @@ def test_band_all_layers(D):
     (1, 3, 3, 1024, 1024, 128, 4, 48, 6),   # w = 48, wide bands
     (1, 4, 4, 1024, 1024, 128, 2, 17, 4),   # w = 17
     (1, 1, 1, 1024, 1024, 128, 5, 32, 8),   # one head (t = 0)
+    # entry spacing (q_len + 0) / w >= 1000 at the last layer: the kernel
+    # that requests V after PV (the other refill order)
+    (1, 3, 3, 16384, 16384, 64, 7, 16, 8),  # odd head count, D = 64
+    (2, 2, 1, 12000, 12000, 128, 7, 12, 8),  # GQA, D = 128, spacing exactly 1000
 ])
 def test_band_shapes(B, H, Hkv, L, Lq, D, layer, w, nl):
     print(f"band shape B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} layer={layer} w={w} nl={nl}",
