@@ -400,21 +400,20 @@ MFMA_DTYPES = (torch.bfloat16, torch.float16)
 # kernels about the same per staged 64 x 32 block, and the band kernel is the
 # faster one once a group's rows stage more than this many blocks.  Forward
 # (tile kernel with per-stage masks, 128 x 64 stages), over every dilated
-# layer of B=1 H=32 L=8192 and 16384, B=4 H=32 L=4096, B=8 H=16 L=4096 and
-# B=2 H=16 L=16384: at D = 128 the tile kernel is faster up to 14.4 blocks
-# per group, the band kernel from 21.8; in between, interleaved same-process
-# runs put the band kernel 3.5% ahead at 18.7 (L=8192 layer 4) and the tile
-# kernel 3% ahead at 19.0 (L=16384 layer 2).  At D = 64 the tile kernel is
-# faster up to 14.0 (L=4096 layer 6, by 1%), the band kernel from 15.5 (by
-# 6%).  Backward, each half on its own (all four dQ / dK-dV pairs timed at
-# every dilated layer of B=1 H=32 L=8192 with 32 and 8 kv heads, B=8 H=16
-# L=4096, B=4 H=32/8 L=4096, B=4 H=16 L=8192 with 16 and 4 kv heads and B=2
-# H=16 L=16384): at D = 128 both halves switch between 14.4 and 18.7; at
-# D = 64 the tile dQ is faster up to 14.0 (by 1.3%) and even at 14.4, the
-# band dQ from 15.5; the tile dK/dV up to 15.5 (by 6-17%), the band dK/dV
-# from 18.7.
-BAND_CROSSOVER = {128: 18.5, 64: 14.75}
-BWD_DQ_CROSSOVER = {128: 16.5, 64: 14.5}
+# layer of B=1 H=32 L=8192 and 16384, B=4 H=32 L=4096, B=8 H=16 L=4096,
+# B=2 H=16 L=16384 and, at D = 64, B=4 H=16 L=8192 and B=4 H=32 L=4096: at
+# D = 128 the tile kernel is faster up to 15.5 blocks per group (by 5%), the
+# band kernel at 18.7 (by 6%), the two within 2% at 19.0 (L=16384 layer 2);
+# at D = 64 the tile kernel is faster up to 11.9 (by 10%), the band kernel
+# from 14.0 (by 4-5%; tied at 14.4).  Backward, each half on its own (all
+# four dQ / dK-dV pairs timed at every dilated layer of B=1 H=32 L=8192 with
+# 32 and 8 kv heads, B=8 H=16 L=4096, B=4 H=32/8 L=4096, B=4 H=16 L=8192
+# with 16 and 4 kv heads and B=2 H=16 L=16384): at D = 128 both halves
+# switch between 14.4 and 18.7; at D = 64 the tile dQ is faster up to 11.9
+# (within 1% with 8 kv heads), the band dQ from 14.0 (by 3-5%); the tile
+# dK/dV up to 15.5 (by 6-17%), the band dK/dV from 18.7.
+BAND_CROSSOVER = {128: 18.5, 64: 13.0}
+BWD_DQ_CROSSOVER = {128: 16.5, 64: 13.0}
 BWD_DKDV_CROSSOVER = {128: 16.5, 64: 17.0}
 
 

@@ -328,9 +328,10 @@ def test_band_sharp_softmax_outliers():
     (32768, 32, 1, 128, 4, "band", "band/band"), (32768, 32, 1, 128, 0, "tile", "tile/tile"),
     (8192, 32, 1, 128, 3, "tile", "tile/tile"), (8192, 32, 1, 128, 4, "band", "band/band"),
     (4096, 32, 4, 128, 7, "tile", "tile/tile"),
-    (8192, 32, 1, 128, 5, "band", "band/band"), (4096, 16, 8, 64, 6, "tile", "tile/tile"),
+    (8192, 32, 1, 128, 5, "band", "band/band"), (4096, 16, 8, 64, 6, "band", "band/tile"),
     (4096, 16, 8, 64, 7, "band", "band/tile"), (4096, 16, 8, 64, 4, "tile", "tile/tile"),
-    (8192, 16, 4, 64, 3, "tile", "tile/tile"), (8192, 16, 4, 64, 4, "band", "band/band"),
+    (4096, 16, 8, 64, 5, "tile", "tile/tile"),
+    (8192, 16, 4, 64, 3, "band", "band/tile"), (8192, 16, 4, 64, 4, "band", "band/band"),
     (16384, 16, 2, 64, 3, "band", "band/band"),
 ])
 def test_prefill_kernel_choice(L, H, B, D, layer, want, want_bwd):
