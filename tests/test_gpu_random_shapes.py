@@ -253,3 +253,40 @@ def test_random_operator_explicit_indices(seed):
     e = [(x.float().cpu() - y).abs().max().item() / max(y.abs().max().item(), floor, 1e-30)
          for x, y in zip((qd.grad, kd.grad, vd.grad), (rq, rk, rv))]
     assert max(e) <= (2e-2 if dtype != torch.float32 else 1e-4), e
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_band_late_refill_order(seed):
+    """The band forward's other refill order (V requested after PV), which
+    the host picks where the entry spacing at the last row, (q_len a + w (1 -
+    a)) / w query rows, is 1000 or more: drawn here with short attention
+    lengths at the last layers, against the oracle."""
+    r = random.Random(7000 + seed)
+    H = r.choice([1, 2, 3, 5])
+    Hkv = r.choice([d for d in range(1, H + 1) if H % d == 0])
+    w = r.choice([2, 3, 4, 6, 8])
+    nl = r.choice([2, 4, 8])
+    layer = nl - 1 if r.random() < 0.7 else nl - 2
+    a = layer / max(nl - 1, 1)
+    need = int((1000 * w - w * (1 - a)) / max(a, 1e-9)) + 1 if a > 0 else None
+    if need is None:
+        layer, a = nl - 1, 1.0
+        need = 1000 * w + 1
+    L = need + r.randint(0, 2500)
+    D = r.choice([64, 128])
+    dtype = r.choice([torch.bfloat16, torch.float16])
+    B = r.choice([1, 2])
+    spacing = (torch.tensor(L, dtype=torch.float32) * torch.tensor(a, dtype=torch.float32)
+               + torch.tensor(w * (1 - a), dtype=torch.float32)) / w
+    assert spacing.item() >= 1000.0
+    print(f"seed={seed} B={B} H={H} Hkv={Hkv} L={L} D={D} nl={nl} layer={layer} w={w} {dtype} "
+          f"spacing={spacing.item():.1f}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, dtype, seed=200 + seed, scale=D ** -0.25)
+    idx, msk = elastic_indices(L, layer, nl, H, w)
+    pi, pm = prepared_rows(idx, msk, L, L, L)
+    sc = scaling_for(D)
+    ro, rl = forward_fp32(q, k, v, pi, pm, sc, H // Hkv)
+    tol, ltol = TOL[dtype]
+    o, lse = elastic_attention_band(q.to(DEV), k.to(DEV), v.to(DEV),
+                                    make_pattern(L, w, layer, nl, H), sc)
+    check(o, lse, ro, rl, tol, ltol, "band, V after PV")
