@@ -334,6 +334,23 @@ esa_status esa_build_indices(const esa_pattern* p, int32_t row0, int32_t nrows, 
                                    (hipStream_t)stream));
 }
 
+esa_status esa_build_dense_mask(const esa_pattern* p, int32_t row0, int32_t nrows,
+                                int32_t ncols, uint8_t* mask, int64_t stride_h,
+                                int64_t stride_s, void* stream) {
+  esa_status s = check_pattern(p);
+  if (s != ESA_OK) return s;
+  if (!mask) return ESA_ERR_NULL;
+  if (row0 < 0 || nrows < 0 || (int64_t)row0 + nrows > p->seq_len || ncols < 1)
+    return ESA_ERR_SHAPE;
+  if (p->num_heads > 65535) return ESA_ERR_UNSUPPORTED;  // grid.y
+  // a row's bytes and the rows / heads must not overlap
+  if (stride_s < ncols || (p->num_heads > 1 && stride_h < (int64_t)nrows * stride_s))
+    return ESA_ERR_SHAPE;
+  if (nrows == 0) return ESA_OK;
+  return hip_status(launch_dense_mask(make_consts(*p), row0, nrows, ncols, mask, stride_h,
+                                      stride_s, (hipStream_t)stream));
+}
+
 esa_status esa_build_layout(const esa_pattern* p, int32_t* row_ptr, int32_t* col_idx,
                             int64_t col_capacity, void* workspace, size_t workspace_bytes,
                             void* stream) {
@@ -372,7 +389,8 @@ esa_status esa_plan_schedule(const esa_pattern* p, const int32_t* row_ptr_host, 
 }
 
 esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const int32_t* row_ptr,
-                           const int32_t* col_idx, const uint32_t* stage_masks,
+                           const int32_t* col_idx, const int32_t* row_ptr_host,
+                           const uint32_t* stage_masks, int64_t stage_mask_words,
                            const int32_t* items, int64_t num_items, void* stream) {
   esa_status s = check_fwd_common(a);
   if (s != ESA_OK) return s;
@@ -389,6 +407,15 @@ esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p, const in
   // stage masks exist for layouts whose key blocks are the stages
   if (stage_masks && p->block_n == 128) return ESA_ERR_UNSUPPORTED;
   if (stage_masks && !aligned(stage_masks, 8)) return ESA_ERR_ALIGN;
+  if (stage_masks) {
+    // the kernel reads the masks of every tile of the layout it walks: the
+    // buffer must hold them all (sized from the host copy of row_ptr)
+    if (!row_ptr_host) return ESA_ERR_NULL;
+    int64_t need = 0;
+    s = esa_stage_masks_size(p, row_ptr_host, &need);
+    if (s != ESA_OK) return s;
+    if (stage_mask_words < need) return ESA_ERR_CAPACITY;
+  }
   // The per-tile key masks assume strictly rising indices, which holds for
   // 0 <= alpha <= 1.
   if (p->layer_idx < 0 || p->layer_idx > std::max(p->num_hidden_layers - 1, 0))
@@ -733,16 +760,16 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of `scratch` on the device `stream` belongs to.
-esa_status scratch_of(hipStream_t stream, void** out) {
-  int dev = 0, cur = 0;
-  if (hipGetDevice(&cur) != hipSuccess) return ESA_ERR_HIP;
-  dev = cur;
-  if (stream && hipStreamGetDevice(stream, &dev) != hipSuccess) return ESA_ERR_HIP;
+// Looks up `scratch`'s device address on device dev once (with dev
+// current; the caller's device is restored) and keeps it.  esa_init_device
+// calls this at set-up, outside any graph capture; a call of the entry point
+// on a device nobody initialised does it on its first call.
+esa_status scratch_on(int dev, void** out = nullptr) {
   if (dev < 0 || dev >= kMaxDevices) return ESA_ERR_UNSUPPORTED;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
-    // the symbol's address on a device is looked up with that device current
+    int cur = 0;
+    if (hipGetDevice(&cur) != hipSuccess) return ESA_ERR_HIP;
     if (dev != cur && hipSetDevice(dev) != hipSuccess) return ESA_ERR_HIP;
     void* ptr = nullptr;
     const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
@@ -750,20 +777,29 @@ esa_status scratch_of(hipStream_t stream, void** out) {
     if (e != hipSuccess || !ptr) return ESA_ERR_HIP;
     g_scratch_ptr[dev] = ptr;
   }
-  *out = g_scratch_ptr[dev];
+  if (out) *out = g_scratch_ptr[dev];
   return ESA_OK;
+}
+
+// Device address of `scratch` on the device `stream` belongs to.
+esa_status scratch_of(hipStream_t stream, void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return ESA_ERR_HIP;
+  if (stream && hipStreamGetDevice(stream, &dev) != hipSuccess) return ESA_ERR_HIP;
+  return scratch_on(dev, out);
 }
 
 // The backward's argument checks and launches; `workspace` is the caller's
 // buffer (esa_elastic_bwd) or the device's scratch array
 // (esa_elastic_bwd_noalloc, workspace NULL until the checks pass).
 esa_status elastic_bwd_impl(const esa_bwd_args* a, const esa_pattern* p, const int32_t* row_ptr,
-                            const int32_t* col_idx, const int32_t* q_items, int64_t num_q_items,
+                            const int32_t* col_idx, const int32_t* row_ptr_host,
+                            const int32_t* q_items, int64_t num_q_items,
                             const int32_t* tile_row, const int32_t* kv_ptr,
                             const int32_t* kv_tiles, const int32_t* kv_items,
-                            int64_t num_kv_items, const uint32_t* mask_t,
-                            const uint32_t* q_masks, void* workspace, size_t workspace_bytes,
-                            bool static_ws, void* stream) {
+                            int64_t num_kv_items, const uint32_t* mask_t, int64_t mask_t_words,
+                            const uint32_t* q_masks, int64_t q_mask_words, void* workspace,
+                            size_t workspace_bytes, bool static_ws, void* stream) {
   if (!a || !a->q || !a->k || !a->v || !a->o || !a->dout || !a->dq || !a->dk || !a->dv || !a->lse)
     return ESA_ERR_NULL;
   esa_status s = check_pattern(p);
@@ -816,6 +852,20 @@ esa_status elastic_bwd_impl(const esa_bwd_args* a, const esa_pattern* p, const i
   if (q_masks && !aligned(q_masks, 16)) return ESA_ERR_ALIGN;
   const LayoutDims d = dims_of(*p);
   const int nq = (a->q_len + 127) / 128;
+  // the masks are read by tile id: each buffer must hold every tile the
+  // kernels reach, sized from the host copy of row_ptr
+  if ((q_masks || !band_dkdv) && !row_ptr_host) return ESA_ERR_NULL;
+  if (q_masks) {
+    int64_t need = 0;
+    s = esa_stage_masks_size(p, row_ptr_host, &need);
+    if (s != ESA_OK) return s;
+    if (q_mask_words < need) return ESA_ERR_CAPACITY;
+  }
+  if (!band_dkdv) {
+    const int64_t tiles = row_ptr_host[(int64_t)(p->num_heads - 1) * d.nqb + nq];
+    if (tiles < 0) return ESA_ERR_SHAPE;
+    if (mask_t_words < tiles * 512) return ESA_ERR_CAPACITY;
+  }
   const int64_t n_real = (int64_t)a->batch * a->num_heads * nq;
   if (!band_dq && (num_q_items < n_real || num_q_items > 8 * std::max<int64_t>(n_real, 1)))
     return ESA_ERR_SHAPE;
@@ -887,29 +937,39 @@ esa_status elastic_bwd_impl(const esa_bwd_args* a, const esa_pattern* p, const i
 extern "C" {
 
 esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p, const int32_t* row_ptr,
-                           const int32_t* col_idx, const int32_t* q_items, int64_t num_q_items,
+                           const int32_t* col_idx, const int32_t* row_ptr_host,
+                           const int32_t* q_items, int64_t num_q_items,
                            const int32_t* tile_row, const int32_t* kv_ptr,
                            const int32_t* kv_tiles, const int32_t* kv_items,
-                           int64_t num_kv_items, const uint32_t* mask_t,
-                           const uint32_t* q_masks, void* workspace, size_t workspace_bytes,
-                           void* stream) {
-  return elastic_bwd_impl(a, p, row_ptr, col_idx, q_items, num_q_items, tile_row, kv_ptr,
-                          kv_tiles, kv_items, num_kv_items, mask_t, q_masks, workspace,
-                          workspace_bytes, false, stream);
+                           int64_t num_kv_items, const uint32_t* mask_t, int64_t mask_t_words,
+                           const uint32_t* q_masks, int64_t q_mask_words, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  return elastic_bwd_impl(a, p, row_ptr, col_idx, row_ptr_host, q_items, num_q_items, tile_row,
+                          kv_ptr, kv_tiles, kv_items, num_kv_items, mask_t, mask_t_words,
+                          q_masks, q_mask_words, workspace, workspace_bytes, false, stream);
 }
 
 size_t esa_bwd_noalloc_max_workspace(void) { return kScratchBytes; }
 
 esa_status esa_elastic_bwd_noalloc(const esa_bwd_args* a, const esa_pattern* p,
                                    const int32_t* row_ptr, const int32_t* col_idx,
-                                   const int32_t* q_items, int64_t num_q_items,
-                                   const int32_t* tile_row, const int32_t* kv_ptr,
-                                   const int32_t* kv_tiles, const int32_t* kv_items,
-                                   int64_t num_kv_items, const uint32_t* mask_t,
-                                   const uint32_t* q_masks, void* stream) {
-  return elastic_bwd_impl(a, p, row_ptr, col_idx, q_items, num_q_items, tile_row, kv_ptr,
-                          kv_tiles, kv_items, num_kv_items, mask_t, q_masks, nullptr,
-                          kScratchBytes, true, stream);
+                                   const int32_t* row_ptr_host, const int32_t* q_items,
+                                   int64_t num_q_items, const int32_t* tile_row,
+                                   const int32_t* kv_ptr, const int32_t* kv_tiles,
+                                   const int32_t* kv_items, int64_t num_kv_items,
+                                   const uint32_t* mask_t, int64_t mask_t_words,
+                                   const uint32_t* q_masks, int64_t q_mask_words,
+                                   void* stream) {
+  return elastic_bwd_impl(a, p, row_ptr, col_idx, row_ptr_host, q_items, num_q_items, tile_row,
+                          kv_ptr, kv_tiles, kv_items, num_kv_items, mask_t, mask_t_words,
+                          q_masks, q_mask_words, nullptr, kScratchBytes, true, stream);
+}
+
+esa_status esa_init_device(int32_t device) {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess) return ESA_ERR_HIP;
+  if (device < 0 || device >= count) return ESA_ERR_SHAPE;
+  return scratch_on(device);
 }
 
 esa_status esa_gather_bwd_workspace_size(const esa_bwd_args* a, int32_t attn_length,

@@ -203,6 +203,9 @@ struct BwdArgs {
 
 hipError_t launch_indices(const PatternConsts& pc, int row0, int nrows, void* indices, void* mask,
                           int elem_bytes, hipStream_t stream);
+hipError_t launch_dense_mask(const PatternConsts& pc, int row0, int nrows, int ncols,
+                             uint8_t* mask, int64_t stride_h, int64_t stride_s,
+                             hipStream_t stream);
 hipError_t launch_layout(const PatternConsts& pc, const LayoutDims& ld, int32_t* row_ptr,
                          int32_t* col_idx, void* workspace, hipStream_t stream);
 // per-stage row masks of a 64 x 32 or 128 x 64 layout: num_tiles x block_m x

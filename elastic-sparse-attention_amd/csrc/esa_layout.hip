@@ -30,6 +30,32 @@ __global__ __launch_bounds__(256) void indices_kernel(PatternConsts pc, int row0
   if (mask) mask[off] = (IdxT)(valid ? 1 : 0);
 }
 
+// One workgroup per (row, head) of the dense mask <- _create_full_sparse_mask
+// (elastic_sparse_attention.py:537-572): the row's ncols bytes are cleared
+// (16 bytes per store where the row allows), then every valid entry sets
+// the byte of its index, clamped to [0, ncols - 1] as :556 clamps it.  The
+// barrier orders the clearing stores before the setting ones.
+__global__ __launch_bounds__(256) void dense_mask_kernel(PatternConsts pc, int row0, int ncols,
+                                                         uint8_t* __restrict__ mask,
+                                                         int64_t stride_h, int64_t stride_s) {
+  const int r = blockIdx.x, h = blockIdx.y;
+  const int i = row0 + r;
+  uint8_t* row = mask + (int64_t)h * stride_h + (int64_t)r * stride_s;
+  if (((uintptr_t)row & 15) == 0 && (ncols & 15) == 0) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    for (int c = 16 * threadIdx.x; c < ncols; c += 16 * blockDim.x) *(u32x4*)(row + c) = z;
+  } else {
+    for (int c = threadIdx.x; c < ncols; c += blockDim.x) row[c] = 0;
+  }
+  __syncthreads();
+  const HeadWeights hw = head_weights(pc, h);
+  const RowParams rp = row_params(pc, i);
+  for (int j = threadIdx.x; j < pc.w; j += blockDim.x) {
+    const int idx = interp_index(oversized(rp, j), oversized(rp, j + 1), hw);
+    if (idx <= i) row[min(max(idx, 0), ncols - 1)] = 1;
+  }
+}
+
 // One workgroup per (query block, head): marks the key tiles the block's
 // valid entries fall in, in an LDS bitmap, then stores the bitmap and its
 // population count.
@@ -142,6 +168,14 @@ hipError_t launch_indices(const PatternConsts& pc, int row0, int nrows, void* in
   else
     indices_kernel<int32_t><<<grid, 256, 0, stream>>>(pc, row0, nrows, (int32_t*)indices,
                                                       (int32_t*)mask);
+  return hipGetLastError();
+}
+
+hipError_t launch_dense_mask(const PatternConsts& pc, int row0, int nrows, int ncols,
+                             uint8_t* mask, int64_t stride_h, int64_t stride_s,
+                             hipStream_t stream) {
+  dim3 grid((unsigned)nrows, (unsigned)pc.H);
+  dense_mask_kernel<<<grid, 256, 0, stream>>>(pc, row0, ncols, mask, stride_h, stride_s);
   return hipGetLastError();
 }
 

@@ -56,6 +56,7 @@ from __future__ import annotations
 
 import ctypes
 import logging
+from collections import OrderedDict
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -84,6 +85,7 @@ __all__ = [
     "elastic_attention_rows",
     "sparse_attention_fwd",
     "elastic_attention_bwd",
+    "init_device",
 ]
 
 
@@ -101,6 +103,23 @@ def _stream(device: torch.device) -> ctypes.c_void_p:
         index = device.index if device.index is not None else torch.cuda.current_device()
         return ctypes.c_void_p(_RAW_STREAM(index))
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+_INITIALISED = set()
+
+
+def init_device(device: torch.device) -> None:
+    """esa_init_device on ``device``, once per process: looks up the device
+    address of the allocation-free backward's workspace array there (and
+    loads the library's kernels), so a later first call of
+    ``elastic_attention_bwd(noalloc=True)`` may be captured into a HIP
+    graph."""
+    device = torch.device(device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if index in _INITIALISED:
+        return
+    check(load().esa_init_device(index), "esa_init_device")
+    _INITIALISED.add(index)
 
 
 def _dtype_code(dt: torch.dtype) -> int:
@@ -162,6 +181,28 @@ def build_indices(pattern: EsaPattern, device: torch.device, dtype: torch.dtype 
     return idx, msk
 
 
+class _LRU(OrderedDict):
+    """A dict that keeps its ``capacity`` most recently used entries: the
+    per-shape caches of a layout stay bounded when a training run feeds many
+    distinct sequence lengths or batch sizes."""
+
+    def __init__(self, capacity: int):
+        super().__init__()
+        self.capacity = int(capacity)
+
+    def get(self, key, default=None):
+        if key in self:
+            self.move_to_end(key)
+            return self[key]
+        return default
+
+    def __setitem__(self, key, value):
+        super().__setitem__(key, value)
+        self.move_to_end(key)
+        while len(self) > self.capacity:
+            self.popitem(last=False)
+
+
 class ElasticLayout:
     """Block layout of one elastic pattern on one device.
 
@@ -198,13 +239,23 @@ class ElasticLayout:
         # col_idx was sized by the bound; keep only the tiles the layout holds
         if self.col_idx.numel() > max(1, self.num_tiles):
             self.col_idx = self.col_idx[:max(1, self.num_tiles)].clone()
-        self._schedules: Dict[Tuple[int, int], Tuple[torch.Tensor, int]] = {}
+        # per-shape caches, each keeping its most recently used entries
+        self._schedules = _LRU(self.SCHEDULE_CACHE)   # (q_len, batch) -> work list
         self._col_idx_host: Optional[torch.Tensor] = None
-        self._bwd_plans: Dict[Tuple[int, int, int], Tuple[torch.Tensor, ...]] = {}
-        self._masks: Dict[int, torch.Tensor] = {}
-        self._stages: Dict[Tuple[int, int], "ElasticLayout"] = {}
+        self._bwd_plans = _LRU(self.PLAN_CACHE)       # (q_len, batch, kv heads) -> plan
+        self._masks = _LRU(self.MASK_CACHE)           # q_len -> key-major tile masks
+        self._stages = _LRU(self.STAGE_CACHE)         # (block_m, block_n) -> layout
         self._stage_masks = None  # tensor, False (none: over budget), or unbuilt
-        self._tiles_for: Dict[int, int] = {}
+        self._tiles_for = _LRU(self.COUNT_CACHE)      # q_len -> active tiles
+
+    # cache capacities: work lists and backward plans are device arrays sized
+    # by the batch and the tile count (about 563K tiles at H=32 L=32768 layer
+    # 4), tile masks 2 KB per tile; tile counts are integers
+    SCHEDULE_CACHE = 8
+    PLAN_CACHE = 4
+    MASK_CACHE = 2
+    STAGE_CACHE = 3
+    COUNT_CACHE = 256
 
     def stages(self, block_n: int = 32, block_m: Optional[int] = 64) -> "ElasticLayout":
         """The same pattern's layout at ``block_m`` x ``block_n`` blocks, the
@@ -321,9 +372,6 @@ class ElasticLayout:
         self._bwd_plans[key] = got
         return got
 
-    # tile masks kept for this many distinct q_len values (oldest dropped)
-    MASK_CACHE = 2
-
     def mask_tiles(self, q_len: int) -> int:
         """Tiles whose masks a backward over q_len rows reads: the end of the
         last head's tiles among the query blocks below ceil(q_len / 128)."""
@@ -345,8 +393,6 @@ class ElasticLayout:
                                           ctypes.c_void_p(self.row_ptr_host.data_ptr()), q_len,
                                           ctypes.c_void_p(masks.data_ptr()), n,
                                           _stream(self.device)), "esa_build_tile_masks")
-        while len(self._masks) >= self.MASK_CACHE:
-            self._masks.pop(next(iter(self._masks)))
         self._masks[int(q_len)] = masks
         return masks
 
@@ -512,7 +558,9 @@ def _prefill_fwd(q, k, v, layout, scaling, return_lse, out, key_block, query_blo
     check(load().esa_elastic_fwd(ctypes.byref(a), ctypes.byref(st.pattern),
                                  ctypes.c_void_p(st.row_ptr.data_ptr()),
                                  ctypes.c_void_p(st.col_idx.data_ptr()),
+                                 ctypes.c_void_p(st.row_ptr_host.data_ptr()),
                                  ctypes.c_void_p(masks.data_ptr() if masks is not None else None),
+                                 masks.numel() if masks is not None else 0,
                                  ctypes.c_void_p(items.data_ptr()), n, _stream(q.device)),
           "esa_elastic_fwd")
     return o, lse
@@ -778,7 +826,9 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
                   (dout.stride(0), dout.stride(2), dout.stride(1)), dq, dk, dv, scaling)
     lib = load()
     work = None
-    if not noalloc:
+    if noalloc:
+        init_device(q.device)
+    else:
         ws = ctypes.c_size_t()
         check(lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(ws)),
               "esa_bwd_workspace_size")
@@ -803,19 +853,24 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
     else:
         tile_row, kv_ptr, kv_tiles, kv_items, n_kv = layout.bwd_plan(Lq, B, Hkv)
         masks = layout.tile_masks(Lq)
+    def words(t):
+        return t.numel() if t is not None else 0
+
     if noalloc:
         check(lib.esa_elastic_bwd_noalloc(ctypes.byref(a), ctypes.byref(layout.pattern),
-                                          ptr(layout.row_ptr), ptr(layout.col_idx), ptr(items),
-                                          n_items, ptr(tile_row), ptr(kv_ptr), ptr(kv_tiles),
-                                          ptr(kv_items), n_kv, ptr(masks), ptr(q_masks),
-                                          _stream(q.device)),
+                                          ptr(layout.row_ptr), ptr(layout.col_idx),
+                                          ptr(layout.row_ptr_host), ptr(items), n_items,
+                                          ptr(tile_row), ptr(kv_ptr), ptr(kv_tiles),
+                                          ptr(kv_items), n_kv, ptr(masks), words(masks),
+                                          ptr(q_masks), words(q_masks), _stream(q.device)),
               "esa_elastic_bwd_noalloc")
     else:
         check(lib.esa_elastic_bwd(ctypes.byref(a), ctypes.byref(layout.pattern),
-                                  ptr(layout.row_ptr), ptr(layout.col_idx), ptr(items), n_items,
-                                  ptr(tile_row), ptr(kv_ptr), ptr(kv_tiles), ptr(kv_items), n_kv,
-                                  ptr(masks), ptr(q_masks), ptr(work), work.numel() * 4,
-                                  _stream(q.device)),
+                                  ptr(layout.row_ptr), ptr(layout.col_idx),
+                                  ptr(layout.row_ptr_host), ptr(items), n_items, ptr(tile_row),
+                                  ptr(kv_ptr), ptr(kv_tiles), ptr(kv_items), n_kv, ptr(masks),
+                                  words(masks), ptr(q_masks), words(q_masks), ptr(work),
+                                  work.numel() * 4, _stream(q.device)),
               "esa_elastic_bwd")
     return dq, dk, dv
 
@@ -924,28 +979,88 @@ class ElasticSparseAttention(nn.Module):
         self.pattern = make_pattern(max_seq_len, attention_length, layer_idx,
                                     num_hidden_layers, num_attention_heads)
         self._layouts: Dict[torch.device, ElasticLayout] = {}
-        self._index_cache: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
-        self._last_device: Optional[torch.device] = None
-        self.full_attention_mask = None
+        # The reference's cached index buffers (:454-468), registered the same
+        # way (non-persistent, so they follow module.to() and stay out of the
+        # state dict).  The kernels regenerate indices and never read them, so
+        # they start out None and are built on first access, by the HIP
+        # builders, on the device the module lives on: "dense" gets
+        # full_attention_mask, the others the index set and its mask, as the
+        # reference registers them.  An empty anchor buffer records that
+        # device.
+        self.register_buffer("_anchor", torch.empty(0), persistent=False)
+        self.register_buffer("sparse_attention_indices", None, persistent=False)
+        self.register_buffer("sparse_causal_mask", None, persistent=False)
+        self.register_buffer("full_attention_mask", None, persistent=False)
         # bf16 prefill kernel: "auto" (the faster for the shape), "band" or "tile"
         self.prefill_kernel = "auto"
 
-    # -- the reference's cached buffers, built on the GPU on first access --
-    def _indices(self) -> Tuple[torch.Tensor, torch.Tensor]:
-        dev = self._last_device or torch.device("cuda", torch.cuda.current_device())
-        if self._index_cache is None or self._index_cache[0].device != dev:
-            self._index_cache = build_indices(self.pattern, dev, torch.int64)
-        return self._index_cache
+    _LAZY_BUFFERS = ("sparse_attention_indices", "sparse_causal_mask", "full_attention_mask")
 
-    @property
-    def sparse_attention_indices(self) -> torch.Tensor:
-        """int64 ``[H, max_seq_len, w]``, as the reference caches (:465-466)."""
-        return self._indices()[0]
+    def __getattr__(self, name: str):
+        buffers = self.__dict__.get("_buffers", {})
+        if name in ElasticSparseAttention._LAZY_BUFFERS and name in buffers:
+            if buffers[name] is None:
+                self._materialise(name)
+            return buffers[name]
+        return super().__getattr__(name)
 
-    @property
-    def sparse_causal_mask(self) -> torch.Tensor:
-        """int64 ``[H, max_seq_len, w]`` 0/1, as the reference caches (:465-467)."""
-        return self._indices()[1]
+    def _materialise(self, name: str) -> None:
+        """Builds the reference's buffer ``name`` on the module's device, if
+        this implementation registers it (:454-468); leaves it None
+        otherwise."""
+        buffers = self.__dict__["_buffers"]
+        device = buffers["_anchor"].device
+        L = self.max_seq_len
+        if self.implementation == "dense":
+            if name == "full_attention_mask":
+                buffers[name] = self._create_full_sparse_mask(L, device)
+        elif name != "full_attention_mask":
+            idx, msk = self._create_elastic_sparse_indices(L, device)
+            buffers["sparse_attention_indices"] = idx
+            buffers["sparse_causal_mask"] = msk
+
+    @staticmethod
+    def _builder_device(device: torch.device) -> torch.device:
+        """The GPU the HIP builders run on for a buffer wanted on ``device``
+        (the current GPU for a CPU-resident module: the product has no CPU
+        path, so the result is copied there)."""
+        device = torch.device(device)
+        if device.type == "cuda":
+            return device if device.index is not None else torch.device(
+                "cuda", torch.cuda.current_device())
+        if not torch.cuda.is_available():
+            raise RuntimeError("the elastic index builders run on the GPU through libesa.so "
+                               "(HIP); no GPU is available")
+        return torch.device("cuda", torch.cuda.current_device())
+
+    def _create_elastic_sparse_indices(self, seq_len: int, device: torch.device
+                                       ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """``(indices, mask)``, int64 ``[H, seq_len, w]`` on ``device``, as the
+        reference's method of this name returns them (:470-535): masked
+        entries have index 0 and mask 0.  Built by the HIP index builder
+        (esa_build_indices, bit-exact)."""
+        dev = self._builder_device(device)
+        pat = make_pattern(seq_len, self.attention_length, self.layer_idx,
+                           self.num_hidden_layers, self.num_attention_heads)
+        idx, msk = build_indices(pat, dev, torch.int64)
+        return idx.to(device), msk.to(device)
+
+    def _create_full_sparse_mask(self, seq_len: int, device: torch.device) -> torch.Tensor:
+        """bool ``[1, H, seq_len, seq_len]`` on ``device``: True where the
+        query row lists the key among its valid entries, as the reference's
+        method of this name returns it (:537-572).  Built by the HIP
+        dense-mask builder (esa_build_dense_mask) from the same index set."""
+        dev = self._builder_device(device)
+        pat = make_pattern(seq_len, self.attention_length, self.layer_idx,
+                           self.num_hidden_layers, self.num_attention_heads)
+        H = self.num_attention_heads
+        mask = torch.empty(1, H, seq_len, seq_len, dtype=torch.bool, device=dev)
+        if seq_len > 0:
+            check(load().esa_build_dense_mask(ctypes.byref(pat), 0, seq_len, seq_len,
+                                              ctypes.c_void_p(mask.data_ptr()), mask.stride(1),
+                                              mask.stride(2), _stream(dev)),
+                  "esa_build_dense_mask")
+        return mask.to(device)
 
     def layout(self, device: torch.device) -> ElasticLayout:
         """The block layout on ``device`` (built once, cached)."""
@@ -964,7 +1079,11 @@ class ElasticSparseAttention(nn.Module):
             raise ValueError(
                 f"Input sequence length ({kv_seq_len}) exceeds the maximum length initialized "
                 f"in the module ({self.max_seq_len}).")
-        idx, msk = self._indices()
+        idx, msk = self.sparse_attention_indices, self.sparse_causal_mask
+        if idx is None:
+            # ("dense" registers no index buffers, as the reference's does not)
+            idx, msk = self._create_elastic_sparse_indices(self.max_seq_len,
+                                                           self._anchor.device)
         return idx[:, :kv_seq_len, :], msk[:, :kv_seq_len, :]
 
     @staticmethod
@@ -1006,7 +1125,6 @@ class ElasticSparseAttention(nn.Module):
             raise ValueError(
                 f"expected {self.num_attention_heads} query heads and "
                 f"{self.num_key_value_heads} key/value heads; got {H} and {k.shape[1]}")
-        self._last_device = q.device
         pos = None
         if cache_position is None:
             if Lq > kv_len:

@@ -34,6 +34,7 @@ EXPORTED = (
     "esa_elastic_fwd_rows",
     "esa_sparse_fwd", "esa_plan_bwd", "esa_build_tile_masks", "esa_bwd_workspace_size",
     "esa_elastic_bwd", "esa_elastic_bwd_noalloc", "esa_bwd_noalloc_max_workspace",
+    "esa_init_device", "esa_build_dense_mask",
     "esa_elastic_fwd_naive", "esa_gather_bwd_workspace_size", "esa_sparse_bwd",
     "esa_elastic_bwd_rows", "esa_reachability",
 )
@@ -128,6 +129,9 @@ def load() -> ctypes.CDLL:
     lib.esa_build_indices.restype = st
     lib.esa_build_indices.argtypes = [P(EsaPattern), ctypes.c_int32, ctypes.c_int32, vp, vp,
                                       ctypes.c_int32, vp]
+    lib.esa_build_dense_mask.restype = st
+    lib.esa_build_dense_mask.argtypes = [P(EsaPattern), ctypes.c_int32, ctypes.c_int32,
+                                         ctypes.c_int32, vp, ctypes.c_int64, ctypes.c_int64, vp]
     lib.esa_build_layout.restype = st
     lib.esa_build_layout.argtypes = [P(EsaPattern), vp, vp, ctypes.c_int64, vp, ctypes.c_size_t,
                                      vp]
@@ -136,7 +140,7 @@ def load() -> ctypes.CDLL:
                                       ctypes.c_int64, P(ctypes.c_int64)]
     lib.esa_elastic_fwd.restype = st
     lib.esa_elastic_fwd.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp, vp, vp, vp, ctypes.c_int64,
-                                    vp]
+                                    vp, ctypes.c_int64, vp]
     lib.esa_stage_masks_size.restype = st
     lib.esa_stage_masks_size.argtypes = [P(EsaPattern), vp, P(ctypes.c_int64)]
     lib.esa_build_stage_masks.restype = st
@@ -158,11 +162,13 @@ def load() -> ctypes.CDLL:
     lib.esa_bwd_workspace_size.restype = st
     lib.esa_bwd_workspace_size.argtypes = [P(EsaBwdArgs), P(ctypes.c_size_t)]
     lib.esa_elastic_bwd.restype = st
-    lib.esa_elastic_bwd.argtypes = [P(EsaBwdArgs), P(EsaPattern), vp, vp, vp, i64, vp, vp, vp, vp,
-                                    i64, vp, vp, vp, ctypes.c_size_t, vp]
+    lib.esa_elastic_bwd.argtypes = [P(EsaBwdArgs), P(EsaPattern), vp, vp, vp, vp, i64, vp, vp, vp,
+                                    vp, i64, vp, i64, vp, i64, vp, ctypes.c_size_t, vp]
     lib.esa_elastic_bwd_noalloc.restype = st
-    lib.esa_elastic_bwd_noalloc.argtypes = [P(EsaBwdArgs), P(EsaPattern), vp, vp, vp, i64, vp, vp,
-                                            vp, vp, i64, vp, vp, vp]
+    lib.esa_elastic_bwd_noalloc.argtypes = [P(EsaBwdArgs), P(EsaPattern), vp, vp, vp, vp, i64, vp,
+                                            vp, vp, vp, i64, vp, i64, vp, i64, vp]
+    lib.esa_init_device.restype = st
+    lib.esa_init_device.argtypes = [i32]
     lib.esa_bwd_noalloc_max_workspace.restype = ctypes.c_size_t
     lib.esa_bwd_noalloc_max_workspace.argtypes = []
     lib.esa_elastic_fwd_naive.restype = st

@@ -7,8 +7,11 @@
  *   - Every function returns an esa_status; 0 (ESA_OK) means success.  Invalid
  *     arguments are rejected on the host before anything is launched.
  *   - Device pointers are plain addresses of device memory the caller owns.
- *     The library never allocates device memory and keeps no mutable global
- *     state, so calls on different streams may run concurrently.
+ *     The library never allocates device memory.  Its one piece of mutable
+ *     global state is the per-device workspace array of
+ *     esa_elastic_bwd_noalloc: calls of that entry point that overlap in
+ *     time on one device race on it.  Every other call may run concurrently
+ *     with any other on different streams.
  *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
  *     Launch functions are asynchronous and never synchronise the host.
  *   - Strides are in elements.  The innermost (head_dim / w) dimension of
@@ -77,6 +80,17 @@ typedef struct esa_fwd_args {
   float sm_scale; /* the module's scaling = head_dim ** -0.5 (:444) */
 } esa_fwd_args;
 
+/* Host only.  Set-up of the library on one device (an index below
+ * hipGetDeviceCount): looks up, with that device current, the device address
+ * of the array esa_elastic_bwd_noalloc uses as its workspace
+ * (hipGetSymbolAddress, which also loads the library's code object there),
+ * and keeps it; the caller's current device is restored.  Allocates nothing.
+ * Call it once per device before capturing esa_elastic_bwd_noalloc into a
+ * HIP graph: without it, the entry point's first call on a device does the
+ * lookup, which must not happen under capture.  Calling it again is
+ * harmless.  No reference counterpart. */
+esa_status esa_init_device(int32_t device);
+
 /* Human-readable name of a status code. */
 const char* esa_status_string(esa_status s);
 
@@ -102,6 +116,20 @@ esa_status esa_layout_sizes(const esa_pattern* p, int32_t* num_qblocks,
 esa_status esa_build_indices(const esa_pattern* p, int32_t row0, int32_t nrows,
                              void* indices, void* mask, int32_t elem_bytes,
                              void* stream);
+
+/* Replaces ElasticSparseAttention._create_full_sparse_mask
+ * (elastic_sparse_attention.py:537-572), the dense boolean mask the
+ * reference's "dense" implementation hands to SDPA: for rows
+ * [row0, row0 + nrows) of the index set and every head h, writes the bytes
+ * mask[h * stride_h + r * stride_s + c], c in [0, ncols): 1 where row
+ * row0 + r has a valid entry with index c (indices clamped to
+ * [0, ncols - 1], :556), else 0.  Every byte of each row's ncols is
+ * written, none between rows.  stride_s >= ncols, stride_h >= nrows *
+ * stride_s (for more than one head).  Bit-exact with the reference's mask,
+ * which is built from the same index set. */
+esa_status esa_build_dense_mask(const esa_pattern* p, int32_t row0, int32_t nrows,
+                                int32_t ncols, uint8_t* mask, int64_t stride_h,
+                                int64_t stride_s, void* stream);
 
 /* Block layout builder (derived from :470-535; no reference counterpart).
  * For every (head h, query block qb) writes the ascending list of active key
@@ -149,11 +177,17 @@ esa_status esa_plan_schedule(const esa_pattern* p, const int32_t* row_ptr_host,
  * are skipped.  stage_masks: NULL (each row's valid keys per stage are
  * computed in the kernel from the pattern), or, for a 64 x 32 or 128 x 64
  * layout, the masks esa_build_stage_masks wrote for this layout (8-byte
- * aligned); same output bit for bit, without the per-row index walk. */
+ * aligned); same output bit for bit, without the per-row index walk.  With
+ * stage_masks, stage_mask_words is their length in 32-bit words and
+ * row_ptr_host the host copy of row_ptr: a buffer shorter than
+ * esa_stage_masks_size(p, row_ptr_host) is rejected (ESA_ERR_CAPACITY), a
+ * NULL row_ptr_host too (ESA_ERR_NULL); without stage_masks both are
+ * ignored. */
 esa_status esa_elastic_fwd(const esa_fwd_args* a, const esa_pattern* p,
                            const int32_t* row_ptr, const int32_t* col_idx,
-                           const uint32_t* stage_masks, const int32_t* items,
-                           int64_t num_items, void* stream);
+                           const int32_t* row_ptr_host,
+                           const uint32_t* stage_masks, int64_t stage_mask_words,
+                           const int32_t* items, int64_t num_items, void* stream);
 
 /* Host only.  32-bit words of the stage masks of a 64 x 32, 128 x 64 or
  * 128 x 128 layout (block_m x block_n of p): num_tiles x block_m x
@@ -342,16 +376,23 @@ esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes
  * per tile from the pattern), or esa_build_stage_masks' masks of this 128 x
  * 128 layout (16-byte aligned; only with q_items, ESA_ERR_UNSUPPORTED
  * otherwise): same results bit for bit, without the per-row index walk.
- * All lists and masks are device memory.
+ * All lists and masks are device memory.  mask_t_words and q_mask_words are
+ * the lengths of mask_t and q_masks in 32-bit words, checked on the host
+ * against what the kernels read (mask_t: esa_build_tile_masks' size for
+ * q_len; q_masks: esa_stage_masks_size) from row_ptr_host, the host copy of
+ * row_ptr, which is required (ESA_ERR_NULL) whenever mask_t or q_masks is
+ * read; a shorter buffer is rejected (ESA_ERR_CAPACITY).
  * Requires dtype ESA_BF16 or ESA_F16, head_dim 64 or 128, block 128 x 128, a finite
  * sm_scale > 0, q_len <= kv_len, 16-byte aligned rows. */
 esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p,
                            const int32_t* row_ptr, const int32_t* col_idx,
+                           const int32_t* row_ptr_host,
                            const int32_t* q_items, int64_t num_q_items,
                            const int32_t* tile_row, const int32_t* kv_ptr,
                            const int32_t* kv_tiles, const int32_t* kv_items,
                            int64_t num_kv_items, const uint32_t* mask_t,
-                           const uint32_t* q_masks, void* workspace,
+                           int64_t mask_t_words, const uint32_t* q_masks,
+                           int64_t q_mask_words, void* workspace,
                            size_t workspace_bytes, void* stream);
 
 /* Host only.  Bytes of workspace esa_sparse_bwd and esa_elastic_bwd_rows
@@ -407,14 +448,19 @@ esa_status esa_elastic_bwd_rows(const esa_bwd_args* a, const esa_pattern* p,
  * counters).  Every call on one device shares that device's array, so calls
  * that overlap in time on one device (different streams, or host threads)
  * race on it and must be serialised by the caller; consecutive calls on one
- * stream are safe.  Results are bit-identical to esa_elastic_bwd's. */
+ * stream are safe.  Results are bit-identical to esa_elastic_bwd's.  The
+ * array's device address is looked up once per device, by esa_init_device
+ * or else on the entry point's first call there: a caller that captures its
+ * first call into a HIP graph calls esa_init_device before the capture. */
 esa_status esa_elastic_bwd_noalloc(const esa_bwd_args* a, const esa_pattern* p,
                                    const int32_t* row_ptr, const int32_t* col_idx,
+                                   const int32_t* row_ptr_host,
                                    const int32_t* q_items, int64_t num_q_items,
                                    const int32_t* tile_row, const int32_t* kv_ptr,
                                    const int32_t* kv_tiles, const int32_t* kv_items,
                                    int64_t num_kv_items, const uint32_t* mask_t,
-                                   const uint32_t* q_masks, void* stream);
+                                   int64_t mask_t_words, const uint32_t* q_masks,
+                                   int64_t q_mask_words, void* stream);
 
 /* Bytes of the per-device array esa_elastic_bwd_noalloc uses as its
  * workspace (the largest esa_bwd_workspace_size it accepts).  Host only. */

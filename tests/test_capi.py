@@ -6,6 +6,7 @@ import ctypes
 import os
 import re
 
+import numpy as np
 import pytest
 import torch
 
@@ -132,9 +133,14 @@ def test_forward_entry_points_reject_bad_arguments():
     fake = ctypes.c_void_p(4096)
     n = 4 * 2
 
-    def call(a, pp=p, items=n, masks=None):
-        return lib.esa_elastic_fwd(ctypes.byref(a), ctypes.byref(pp), fake, fake, masks, fake,
-                                   items, None)
+    # host copy of a 64 x 32 layout's row_ptr (16 query blocks x 4 heads, 3
+    # stages each): the stage masks need 192 stages x 64 rows x 1 word
+    rp64 = (np.arange(4 * 16 + 1, dtype=np.int32) * 3)
+    rph = ctypes.c_void_p(rp64.ctypes.data)
+
+    def call(a, pp=p, items=n, masks=None, words=1 << 20, row_ptr_host=rph):
+        return lib.esa_elastic_fwd(ctypes.byref(a), ctypes.byref(pp), fake, fake, row_ptr_host,
+                                   masks, words, fake, items, None)
 
     a = fwd_args()
     a.q = None
@@ -170,6 +176,17 @@ def test_forward_entry_points_reject_bad_arguments():
     assert call(fwd_args(), masks=fake) == en.ESA_ERR_UNSUPPORTED
     assert call(fwd_args(), pp=pat(L=1024, H=4, bm=64, bn=32), items=4 * 16,
                 masks=ctypes.c_void_p(4100)) == en.ESA_ERR_ALIGN
+    # stage masks are sized on the host from row_ptr_host: a short buffer, or
+    # no host row_ptr to size them by, is rejected before any launch
+    p64 = pat(L=1024, H=4, bm=64, bn=32)
+    words = ctypes.c_int64()
+    assert lib.esa_stage_masks_size(ctypes.byref(p64), rph, ctypes.byref(words)) == en.ESA_OK
+    assert words.value == 192 * 64
+    assert call(fwd_args(), pp=p64, items=4 * 16, masks=fake, words=words.value - 1) \
+        == en.ESA_ERR_CAPACITY
+    assert call(fwd_args(), pp=p64, items=4 * 16, masks=fake, words=0) == en.ESA_ERR_CAPACITY
+    assert call(fwd_args(), pp=p64, items=4 * 16, masks=fake, row_ptr_host=None) \
+        == en.ESA_ERR_NULL
 
     assert lib.esa_elastic_fwd_rows(ctypes.byref(fwd_args(D=258)), ctypes.byref(p), None, None) \
         == en.ESA_ERR_UNSUPPORTED
@@ -357,11 +374,19 @@ def test_bwd_entry_points_reject_bad_arguments():
     assert lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(ws)) == en.ESA_OK
     assert ws.value == 2 * 1 * 4 * (256 + 32) * 4   # rows padded to 32, + 32
 
+    # host copy of the 128 x 128 layout's row_ptr (8 query blocks x 4 heads,
+    # 3 tiles each)
+    rp128 = (np.arange(4 * 8 + 1, dtype=np.int32) * 3)
+    rph = ctypes.c_void_p(rp128.ctypes.data)
+    big = 1 << 24
+
     def call(args, items=8, kv_items=64, wsb=ws.value, pat_=p, layout=fake, q_list=fake,
-             kv_lists=fake, kv_list=fake, masks=fake, q_masks=None):
-        return lib.esa_elastic_bwd(ctypes.byref(args), ctypes.byref(pat_), layout, layout, q_list,
-                                   items, kv_lists, kv_lists, kv_lists, kv_list, kv_items, masks,
-                                   q_masks, fake, wsb, None)
+             kv_lists=fake, kv_list=fake, masks=fake, q_masks=None, row_ptr_host=rph,
+             mask_words=big, q_mask_words=big):
+        return lib.esa_elastic_bwd(ctypes.byref(args), ctypes.byref(pat_), layout, layout,
+                                   row_ptr_host, q_list, items, kv_lists, kv_lists, kv_lists,
+                                   kv_list, kv_items, masks, mask_words, q_masks, q_mask_words,
+                                   fake, wsb, None)
 
     # the block-sparse halves need their layout, lists and masks; the band
     # halves need none of them, and attention_length <= 64
@@ -376,6 +401,16 @@ def test_bwd_entry_points_reject_bad_arguments():
     # row masks serve the block-sparse dQ only, 16-byte aligned
     assert call(a, q_list=None, q_masks=fake) == en.ESA_ERR_UNSUPPORTED
     assert call(a, q_masks=ctypes.c_void_p(4104)) == en.ESA_ERR_ALIGN
+    # both mask buffers are sized on the host from row_ptr_host: the key-major
+    # masks of the tiles of query blocks 0, 1 of every head (up to the last
+    # head's block 1 end, tile 3 * (3 * 8 + 2) = 78) and the row masks of all
+    # 96 tiles; shorter buffers, or no host row_ptr, are rejected
+    assert call(a, row_ptr_host=None) == en.ESA_ERR_NULL
+    assert call(a, q_masks=fake, kv_list=None, masks=None, row_ptr_host=None) == en.ESA_ERR_NULL
+    assert call(a, mask_words=78 * 512 - 1) == en.ESA_ERR_CAPACITY
+    assert call(a, q_masks=fake, q_mask_words=96 * 128 * 4 - 1) == en.ESA_ERR_CAPACITY
+    # (a band dK/dV reads no key-major masks: their size is not checked)
+    assert call(a, kv_list=None, masks=None, mask_words=0, items=7) == en.ESA_ERR_SHAPE
 
     assert call(a, wsb=16) == en.ESA_ERR_CAPACITY
     assert call(a, items=7) == en.ESA_ERR_SHAPE
@@ -499,8 +534,8 @@ def test_noalloc_rejects_oversized_workspace():
     a.lse_stride_b, a.lse_stride_h = 32 * 32768, 32768
     a.sm_scale = 128 ** -0.5
     p = en.EsaPattern(32768, 64, 4, 8, 32, 128, 128)
-    st = lib.esa_elastic_bwd_noalloc(ctypes.byref(a), ctypes.byref(p), None, None, None, 0, None,
-                                     None, None, None, 0, None, None, None)
+    st = lib.esa_elastic_bwd_noalloc(ctypes.byref(a), ctypes.byref(p), None, None, None, None, 0,
+                                     None, None, None, None, 0, None, 0, None, 0, None)
     assert st == en.ESA_ERR_CAPACITY
 
 

@@ -3,8 +3,9 @@
 The module's prefill forward (band and tile kernels) and the allocation-free
 backward entry point (esa_elastic_bwd_noalloc, for callers that record
 graphs) are recorded in a torch.cuda.CUDAGraph after eager warm-up calls
-(which build the layout, work lists, stage masks, backward plans and the
-library's per-device workspace address), then replayed.  Each replay runs on
+(which build the layout, work lists, stage masks and backward plans; the
+library's per-device workspace address is looked up by esa_init_device),
+then replayed.  Each replay runs on
 new input contents written into the recorded (static) tensors, with eager
 work and synchronisations between replays, and must give the same bits as an
 eager call on the same inputs: every kernel on these paths is deterministic,
@@ -16,7 +17,7 @@ import torch
 
 from esa_oracle import scaling_for, seeded_inputs
 from elastic_sparse_attention import (ElasticLayout, ElasticSparseAttention, elastic_attention_bwd,
-                                      elastic_attention_fwd, make_pattern)
+                                      elastic_attention_fwd, init_device, make_pattern)
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
@@ -63,6 +64,39 @@ def test_module_forward_graph_replays(kernel, layer, L, H, D):
             ref, _ = m(nq, nk, nv)
             torch.cuda.synchronize()
             assert torch.equal(out, ref), rep
+
+
+def test_noalloc_first_call_captured_after_init():
+    """esa_init_device at set-up, then the process's first allocation-free
+    backward is itself captured (no eager noalloc call before it: the
+    eager warm-up below uses the allocating entry point, which builds the
+    plans and masks).  Runs before every other noalloc test of the suite (the
+    test files run in name order and this is the first noalloc test here), so
+    the capture holds the entry point's first call on the device."""
+    print("graph noalloc first call after esa_init_device", flush=True)
+    B, H, Hkv, L, D, layer = 1, 4, 4, 1024, 128, 5
+    sc = scaling_for(D)
+    init_device(DEV)
+    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+    q, k, v = inputs(B, H, Hkv, L, D, seed=41)
+    gen = torch.Generator(device="cpu").manual_seed(41)
+    do = torch.randn(B, L, H, D, generator=gen).to(torch.bfloat16).to(DEV)
+    o, lse = elastic_attention_fwd(q, k, v, lay, sc, kernel="tile")
+
+    def bwd(noalloc):
+        return elastic_attention_bwd(q, k, v, o, lse, do, lay, sc, dq_kernel="tile",
+                                     dkdv_kernel="tile", noalloc=noalloc)
+
+    warm_up(lambda: bwd(False))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        dq, dk, dv = bwd(True)
+    for rep in range(2):
+        g.replay()
+        torch.cuda.synchronize()
+        rq, rk, rv = bwd(False)
+        torch.cuda.synchronize()
+        assert torch.equal(dq, rq) and torch.equal(dk, rk) and torch.equal(dv, rv), rep
 
 
 @pytest.mark.parametrize("kernel,layer,L,H,Hkv,D", [("band", 4, 2048, 8, 8, 128),

@@ -97,3 +97,48 @@ def test_long_context_layout_full_size():
         assert torch.equal(lay.row_ptr.cpu(), rp)
         assert torch.equal(lay.col_idx[:lay.num_tiles].cpu(), ci)
         del idx, msk
+
+
+@pytest.mark.parametrize("L,H,w,nl,layer", [(700, 4, 64, 8, 0), (700, 4, 64, 8, 4),
+                                            (513, 3, 33, 6, 5), (300, 1, 16, 4, 3)])
+def test_module_index_buffers_and_dense_mask(L, H, w, nl, layer):
+    """The reference's module surface (:454-468, :470-572): the index buffers
+    are non-persistent buffers built by the HIP builders on the module's
+    device, follow module.to(), and match the oracle bit for bit; the dense
+    mask of implementation="dense" matches the oracle's
+    _create_full_sparse_mask restatement."""
+    from elastic_sparse_attention import ElasticSparseAttention
+    from esa_oracle import dense_mask
+    print(f"module buffers L={L} H={H} w={w} nl={nl} layer={layer}", flush=True)
+    ref_i, ref_m = elastic_indices(L, layer, nl, H, w)
+    m = ElasticSparseAttention(layer, nl, H, 64, w, L).to(DEV)
+    assert m.state_dict() == {}
+    gi, gm = m.sparse_attention_indices, m.sparse_causal_mask
+    assert gi.device == DEV and gi.dtype == torch.int64 and gm.dtype == torch.int64
+    assert torch.equal(gi.cpu(), ref_i) and torch.equal(gm.cpu(), ref_m)
+    assert m.full_attention_mask is None
+    m.to("cpu")  # built buffers follow the module
+    assert m.sparse_attention_indices.device.type == "cpu"
+    assert torch.equal(m.sparse_attention_indices, ref_i)
+    ci, cm = m._create_elastic_sparse_indices(L - 7, torch.device("cpu"))
+    assert torch.equal(ci, ref_i[:, :L - 7]) and torch.equal(cm, ref_m[:, :L - 7])
+    pi, pm = m._get_prepared_indices_and_mask(L // 2)
+    assert torch.equal(pi, ref_i[:, :L // 2]) and torch.equal(pm, ref_m[:, :L // 2])
+
+    d = ElasticSparseAttention(layer, nl, H, 64, w, L, implementation="dense").to(DEV)
+    assert d.sparse_attention_indices is None and d.sparse_causal_mask is None
+    full = d.full_attention_mask
+    assert full.shape == (1, H, L, L) and full.dtype == torch.bool and full.device == DEV
+    assert torch.equal(full[0].cpu(), dense_mask(ref_i, ref_m))
+    # a padded row stride: the bytes between rows are left alone
+    pat = make_pattern(L, w, layer, nl, H)
+    import ctypes
+    from esa_native import check, load
+    buf = torch.full((H, 40, L + 9), 7, dtype=torch.uint8, device=DEV)
+    check(load().esa_build_dense_mask(ctypes.byref(pat), 100, 40, L,
+                                      ctypes.c_void_p(buf.data_ptr()), buf.stride(0),
+                                      buf.stride(1), None), "esa_build_dense_mask")
+    torch.cuda.synchronize()
+    b = buf.cpu()
+    assert torch.equal(b[..., :L].bool(), dense_mask(ref_i, ref_m)[:, 100:140])
+    assert bool((b[..., :L] <= 1).all()) and bool((b[..., L:] == 7).all())

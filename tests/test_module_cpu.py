@@ -34,3 +34,24 @@ def test_cpu_tensors_raise():
     q = torch.randn(1, 4, 16, 64)
     with pytest.raises(RuntimeError, match="GPU"):
         m(q, q, q)
+
+
+def test_index_buffers_registered_like_the_reference():
+    """The reference registers its index buffers as non-persistent buffers
+    (:454-468): here too, so they stay out of the state dict and follow
+    module.to(); they are None until first read (the kernels never read
+    them), and "dense" registers full_attention_mask instead."""
+    m = ElasticSparseAttention(4, 8, 4, 64, 64, 1024)
+    names = set(m._buffers)
+    assert {"sparse_attention_indices", "sparse_causal_mask", "full_attention_mask"} <= names
+    assert m._buffers["sparse_attention_indices"] is None
+    assert m.state_dict() == {}
+    assert m.to(torch.float32) is m
+    if not torch.cuda.is_available():
+        # the builders are HIP kernels: no CPU path to fall back to
+        with pytest.raises(RuntimeError, match="GPU"):
+            m.sparse_attention_indices
+        d = ElasticSparseAttention(4, 8, 4, 64, 64, 1024, implementation="dense")
+        assert d.sparse_attention_indices is None
+        with pytest.raises(RuntimeError, match="GPU"):
+            d.full_attention_mask
