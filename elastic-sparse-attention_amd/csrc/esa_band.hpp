@@ -44,14 +44,16 @@ __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const 
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-// max over the 4 lanes l, l^16, l^32, l^48 (one row's lanes)
+// max over the 4 lanes l, l^16, l^32, l^48 (one row's lanes), NaN if one of
+// them is NaN (v_maximum3_f32: a row's NaN score, from a non-finite key it
+// lists, must reach the row's softmax as the reference's does)
 __device__ __forceinline__ float row4_max(float v) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
                                                   false);
-  const float m1 = max_nq(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const float m1 = __builtin_elementwise_maximum(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(m1), __float_as_uint(m1),
                                                   false, false);
-  return max_nq(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return __builtin_elementwise_maximum(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 // min / max over the 16 lanes of a lane group (DPP row rotations)

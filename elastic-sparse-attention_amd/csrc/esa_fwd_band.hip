@@ -266,13 +266,28 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     return sacc;
   };
 
-  // V^T operands of two bands from slots va, vb (ds_read_b64_tr_b16)
-  auto read_vt = [&](const uint16_t* va, const uint16_t* vb, s16x4 (&ta)[C::NV],
+  // V^T operands of two bands from slots va, vb (ds_read_b64_tr_b16); with
+  // san, non-finite values become +0 (the rerun of a group whose output met
+  // a non-finite value)
+  auto read_vt = [&](auto san, const uint16_t* va, const uint16_t* vb, s16x4 (&ta)[C::NV],
                      s16x4 (&tb)[C::NV]) {
 #pragma unroll
     for (int s = 0; s < C::NV; ++s) {
       ta[s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((const char*)va + vrd[s]));
       tb[s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((const char*)vb + vrd[s]));
+    }
+    if constexpr (decltype(san)::value) {
+#pragma unroll
+      for (int s = 0; s < C::NV; ++s) {
+        u32x2 a = __builtin_bit_cast(u32x2, ta[s]), c = __builtin_bit_cast(u32x2, tb[s]);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          a[e] = sanitize2<E>(a[e]);
+          c[e] = sanitize2<E>(c[e]);
+        }
+        ta[s] = __builtin_bit_cast(s16x4, a);
+        tb[s] = __builtin_bit_cast(s16x4, c);
+      }
     }
   };
   // O^T += V^T P^T over two bands' V^T operands ta, tb with P words pa, pb
@@ -289,135 +304,155 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     }
   };
 
-  // ---- main loop: band pairs (2 p, 2 p + 1).
-  //   VEARLY: wait for the pair's K and V DMAs (the only ones outstanding),
-  //   read the K and V^T operands, request the next pair's K and V into the
-  //   same slots, then compute from registers.
-  //   Otherwise: before the K wait exactly this pair's 2 VLOADS V DMAs may be
-  //   newer; before the V wait the next pair's K DMAs (2 VLOADS of them, or
-  //   with KSKIP as many as load_k issued).
-  constexpr int kWaitPair = (0xF70 & ~0xF) | ((2 * C::VLOADS) & 0xF) |
-                            (((2 * C::VLOADS) >> 4) << 14);  // vmcnt(2 VLOADS)
-  constexpr int kWaitLds = 0xC07F;                           // lgkmcnt(0)
-  const int lane_key = 4 * n;  // ds_bpermute byte address of row n in group 0
-  {
-    const int i0 = __builtin_amdgcn_readlane(info1, 0);
-    const int i1 = __builtin_amdgcn_readlane(info1, 1);
-    __builtin_amdgcn_s_waitcnt(kWaitLds);  // the slot zeros are in LDS
-    load_k(i0, lk0);
-    load_k(i1, lk1);
-    load_v(i0, lv0);
-    load_v(i1, lv1);
-  }
-  for (int qj = 0; qj < 4; ++qj) {
-    const bool more = qj < 3;
-#pragma unroll
-    for (int rp = 0; rp < 8; ++rp) {
-      const int ra = 2 * rp, rb = 2 * rp + 1;
-      const int ia = __builtin_amdgcn_readlane(info1, 16 * qj + ra);
-      const int ib = __builtin_amdgcn_readlane(info1, 16 * qj + rb);
-      // next pair's descriptors (slots 16 qj + ra + 2, + rb + 2: at rp = 7
-      // slots 0 and 1 of lane group qj + 1)
-      int na = 0, nb = 0;
-      if (rp < 7 || more) {
-        na = __builtin_amdgcn_readlane(info1, 16 * qj + ra + 2);
-        nb = __builtin_amdgcn_readlane(info1, 16 * qj + rb + 2);
-      }
-      const bool live = (ia | ib) != 0;  // some row of the group uses a band
-      const int n_nxt = KSKIP ? n_loads(na) + n_loads(nb) : 2 * C::VLOADS;  // next K DMAs
-      V8 kopa[C::NS], kopb[C::NS];
-      s16x4 ta[C::NV], tb[C::NV];
-      if constexpr (VEARLY) {
-        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this pair's K and V are in LDS
-        if (live) {
-          read_k(ks0, kopa);
-          read_k(ks1, kopb);
-          read_vt(vs0, vs1, ta, tb);
+  // ---- the bands: the main loop over band pairs, then the tail.  san: the
+  // rerun with sanitised V operands (see below).
+  auto run_bands = [&](auto san) {
+    // ---- main loop: band pairs (2 p, 2 p + 1).
+    //   VEARLY: wait for the pair's K and V DMAs (the only ones outstanding),
+    //   read the K and V^T operands, request the next pair's K and V into the
+    //   same slots, then compute from registers.
+    //   Otherwise: before the K wait exactly this pair's 2 VLOADS V DMAs may be
+    //   newer; before the V wait the next pair's K DMAs (2 VLOADS of them, or
+    //   with KSKIP as many as load_k issued).
+    constexpr int kWaitPair = (0xF70 & ~0xF) | ((2 * C::VLOADS) & 0xF) |
+                              (((2 * C::VLOADS) >> 4) << 14);  // vmcnt(2 VLOADS)
+    constexpr int kWaitLds = 0xC07F;                           // lgkmcnt(0)
+    const int lane_key = 4 * n;  // ds_bpermute byte address of row n in group 0
+    {
+      const int i0 = __builtin_amdgcn_readlane(info1, 0);
+      const int i1 = __builtin_amdgcn_readlane(info1, 1);
+      __builtin_amdgcn_s_waitcnt(kWaitLds);  // the slot zeros are in LDS
+      load_k(i0, lk0);
+      load_k(i1, lk1);
+      load_v(i0, lv0);
+      load_v(i1, lv1);
+    }
+    for (int qj = 0; qj < 4; ++qj) {
+      const bool more = qj < 3;
+  #pragma unroll
+      for (int rp = 0; rp < 8; ++rp) {
+        const int ra = 2 * rp, rb = 2 * rp + 1;
+        const int ia = __builtin_amdgcn_readlane(info1, 16 * qj + ra);
+        const int ib = __builtin_amdgcn_readlane(info1, 16 * qj + rb);
+        // next pair's descriptors (slots 16 qj + ra + 2, + rb + 2: at rp = 7
+        // slots 0 and 1 of lane group qj + 1)
+        int na = 0, nb = 0;
+        if (rp < 7 || more) {
+          na = __builtin_amdgcn_readlane(info1, 16 * qj + ra + 2);
+          nb = __builtin_amdgcn_readlane(info1, 16 * qj + rb + 2);
         }
-        __builtin_amdgcn_s_waitcnt(kWaitLds);  // slots read: refill them
-        load_k(na, lk0);
-        load_k(nb, lk1);
-        load_v(na, lv0);
-        load_v(nb, lv1);
-      } else {
-        __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's K is in LDS
-        if (live) {
-          read_k(ks0, kopa);
-          read_k(ks1, kopb);
-        }
-        __builtin_amdgcn_s_waitcnt(kWaitLds);  // K slots read: refill them
-        load_k(na, lk0);
-        load_k(nb, lk1);
-      }
-      if (live) {
-        // the row's key offsets of both bands: bytes ra % 4, rb % 4 of word
-        // rp / 2 (the same word for the pair)
-        const uint32_t dw =
-            (uint32_t)__builtin_amdgcn_ds_bpermute(lane_key + 64 * qj, (int)kd[rp >> 1]);
-        const int da = (int)((dw >> (16 * (rp & 1))) & 0xFFu);
-        const int db = (int)((dw >> (16 * (rp & 1) + 8)) & 0xFFu);
-        const f32x4 sa = scores(kopa);
-        const f32x4 sb = scores(kopb);
-        bool ha, hb;
-        int ea, eb;
-        const float xa = pick(sa, da, ha, ea);
-        const float xb = pick(sb, db, hb, eb);
-        uint64_t pa, pbw;
-        pair_softmax(xa, ha, ea, xb, hb, eb, pa, pbw);
-        if constexpr (!VEARLY) {
-          // this pair's V is in LDS
-          if constexpr (KSKIP)
-            wait_vm(n_nxt);
-          else
-            __builtin_amdgcn_s_waitcnt(kWaitPair);
-          read_vt(vs0, vs1, ta, tb);
-        }
-        pv(ta, tb, pa, pbw);
-      }
-      if constexpr (!VEARLY) {
-        // this pair's V has landed (and been read): refill the V slots
-        if constexpr (KSKIP) {
-          wait_vm(n_nxt);
-          __builtin_amdgcn_s_waitcnt(kWaitLds);
+        const bool live = (ia | ib) != 0;  // some row of the group uses a band
+        const int n_nxt = KSKIP ? n_loads(na) + n_loads(nb) : 2 * C::VLOADS;  // next K DMAs
+        V8 kopa[C::NS], kopb[C::NS];
+        s16x4 ta[C::NV], tb[C::NV];
+        if constexpr (VEARLY) {
+          __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this pair's K and V are in LDS
+          if (live) {
+            read_k(ks0, kopa);
+            read_k(ks1, kopb);
+            read_vt(san, vs0, vs1, ta, tb);
+          }
+          __builtin_amdgcn_s_waitcnt(kWaitLds);  // slots read: refill them
+          load_k(na, lk0);
+          load_k(nb, lk1);
+          load_v(na, lv0);
+          load_v(nb, lv1);
         } else {
-          __builtin_amdgcn_s_waitcnt(kWaitPair & kWaitLds);
+          __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's K is in LDS
+          if (live) {
+            read_k(ks0, kopa);
+            read_k(ks1, kopb);
+          }
+          __builtin_amdgcn_s_waitcnt(kWaitLds);  // K slots read: refill them
+          load_k(na, lk0);
+          load_k(nb, lk1);
         }
-        load_v(na, lv0);
-        load_v(nb, lv1);
+        if (live) {
+          // the row's key offsets of both bands: bytes ra % 4, rb % 4 of word
+          // rp / 2 (the same word for the pair)
+          const uint32_t dw =
+              (uint32_t)__builtin_amdgcn_ds_bpermute(lane_key + 64 * qj, (int)kd[rp >> 1]);
+          const int da = (int)((dw >> (16 * (rp & 1))) & 0xFFu);
+          const int db = (int)((dw >> (16 * (rp & 1) + 8)) & 0xFFu);
+          const f32x4 sa = scores(kopa);
+          const f32x4 sb = scores(kopb);
+          bool ha, hb;
+          int ea, eb;
+          const float xa = pick(sa, da, ha, ea);
+          const float xb = pick(sb, db, hb, eb);
+          uint64_t pa, pbw;
+          pair_softmax(xa, ha, ea, xb, hb, eb, pa, pbw);
+          if constexpr (!VEARLY) {
+            // this pair's V is in LDS
+            if constexpr (KSKIP)
+              wait_vm(n_nxt);
+            else
+              __builtin_amdgcn_s_waitcnt(kWaitPair);
+            read_vt(san, vs0, vs1, ta, tb);
+          }
+          pv(ta, tb, pa, pbw);
+        }
+        if constexpr (!VEARLY) {
+          // this pair's V has landed (and been read): refill the V slots
+          if constexpr (KSKIP) {
+            wait_vm(n_nxt);
+            __builtin_amdgcn_s_waitcnt(kWaitLds);
+          } else {
+            __builtin_amdgcn_s_waitcnt(kWaitPair & kWaitLds);
+          }
+          load_v(na, lv0);
+          load_v(nb, lv1);
+        }
       }
     }
-  }
 
-  // ---- tail: keys of bands wider than 16, one 16-key chunk at a time
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  const bool wide = wave_any(((uint32_t)info1 >> 24) > 16u);  // some slot's band
-  for (int j = 0; j < 64 && wide; ++j) {
-    const int qj = j >> 4, r = j & 15;
-    const int bi = __builtin_amdgcn_readlane(info1, j);  // slot (qj, r)
-    const uint32_t w4 = r < 8 ? (r < 4 ? kd[0] : kd[1]) : (r < 12 ? kd[2] : kd[3]);
-    const uint32_t dw = (uint32_t)__builtin_amdgcn_ds_bpermute(lane_key + 64 * qj, (int)w4);
-    const int d = (int)((dw >> (8 * (r & 3))) & 0xFFu);  // 0xFF: no key
-    const int lo = bi & 0xffffff, wdt = (int)((uint32_t)bi >> 24);
-    for (int c0 = lo + 16; c0 < lo + wdt; c0 += 16) {
-      const int rem = lo + wdt - c0;
-      const int ci = c0 | (min(rem, 16) << 24);
-      __builtin_amdgcn_s_waitcnt(kWaitLds);  // earlier reads of slots 0 done
-      load_k(ci, lk0);
-      load_v(ci, lv0);
-      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-      V8 kt[C::NS];
-      read_k(ks0, kt);
-      const f32x4 st = scores(kt);
-      bool ht;
-      int et;
-      const float xt = pick(st, d == 0xFF ? -1 : d - (c0 - lo), ht, et);
-      uint64_t pt, pz;
-      pair_softmax(xt, ht, et, -INFINITY, false, 0, pt, pz);
-      // the second band of the pair contributes p = 0 (vs1 holds finite rows)
-      s16x4 ta[C::NV], tb[C::NV];
-      read_vt(vs0, vs1, ta, tb);
-      pv(ta, tb, pt, 0ull);
+    // ---- tail: keys of bands wider than 16, one 16-key chunk at a time
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    const bool wide = wave_any(((uint32_t)info1 >> 24) > 16u);  // some slot's band
+    for (int j = 0; j < 64 && wide; ++j) {
+      const int qj = j >> 4, r = j & 15;
+      const int bi = __builtin_amdgcn_readlane(info1, j);  // slot (qj, r)
+      const uint32_t w4 = r < 8 ? (r < 4 ? kd[0] : kd[1]) : (r < 12 ? kd[2] : kd[3]);
+      const uint32_t dw = (uint32_t)__builtin_amdgcn_ds_bpermute(lane_key + 64 * qj, (int)w4);
+      const int d = (int)((dw >> (8 * (r & 3))) & 0xFFu);  // 0xFF: no key
+      const int lo = bi & 0xffffff, wdt = (int)((uint32_t)bi >> 24);
+      for (int c0 = lo + 16; c0 < lo + wdt; c0 += 16) {
+        const int rem = lo + wdt - c0;
+        const int ci = c0 | (min(rem, 16) << 24);
+        __builtin_amdgcn_s_waitcnt(kWaitLds);  // earlier reads of slots 0 done
+        load_k(ci, lk0);
+        load_v(ci, lv0);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        V8 kt[C::NS];
+        read_k(ks0, kt);
+        const f32x4 st = scores(kt);
+        bool ht;
+        int et;
+        const float xt = pick(st, d == 0xFF ? -1 : d - (c0 - lo), ht, et);
+        uint64_t pt, pz;
+        pair_softmax(xt, ht, et, -INFINITY, false, 0, pt, pz);
+        // the second band of the pair contributes p = 0 (vs1 holds finite rows)
+        s16x4 ta[C::NV], tb[C::NV];
+        read_vt(san, vs0, vs1, ta, tb);
+        pv(ta, tb, pt, 0ull);
+      }
     }
+  };
+
+  run_bands(std::integral_constant<bool, false>{});
+  // A group whose outputs met a non-finite value (an Inf or NaN in V, staged
+  // with a band, can reach rows that do not list it through 0 * Inf in PV)
+  // runs again with the V operands sanitised: rows whose entries bring no
+  // non-finite value then get exactly the bits a run without it gives, and
+  // the reference's non-finite values go back in below.
+  const bool rerun = wave_any(!sum_finite(oacc));
+  if (rerun) {
+    m_run = -INFINITY;
+    l_run = 0.f;
+    n_run = 0.f;
+#pragma unroll
+    for (int s = 0; s < C::NV; ++s) oacc[s] = f32x4{};
+    run_bands(std::integral_constant<bool, true>{});
   }
 
   // ---- epilogue: lane (n, q) holds O^T[dim][row n] for dims CW q .. CW q + CW
@@ -439,6 +474,20 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
       const float lse = l_run > 0.f ? (m_run + __log2f(l_run)) * 0.69314718055994530942f
                                     : -INFINITY;
       A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + i] = lse;
+    }
+    // after a rerun: the dims where the row's own entries bring an Inf or NaN
+    // of V take the reference's value (this lane's dims CW q .. CW q + CW)
+    if (rerun) {
+      int dim0[C::CW / 4];
+#pragma unroll
+      for (int g = 0; g < C::CW / 4; ++g) dim0[g] = C::CW * q + 4 * g;
+      uint64_t pos, neg, nan;
+      nonfinite_v<E>(A.pc, h, i, A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh, A.vss, dim0,
+                     pos, neg, nan);
+      for (uint64_t any = pos | neg | nan; any != 0ull; any &= any - 1ull) {
+        const int bit = __builtin_ctzll(any);
+        orow[C::CW * q + bit] = nonfinite_value<E>(pos, neg, nan, bit);
+      }
     }
   }
 }

@@ -83,7 +83,7 @@ struct TileCfg {
 // the index walk, which at dilated layers costs about a third of the
 // kernel's VALU work and is the same for every batch element.
 template <int D, int BMQ, Elem E, bool PRE>
-__global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
+__global__ __launch_bounds__(BMQ * 2, D == 64 ? 4 : 2) void tile_fwd_kernel(TileArgs A) {
   using C = TileCfg<D, BMQ>;
   // stage buffers (HALF rows x D, rows unpadded, chunks swizzled); separate
   // objects, so the compiler can tell reads of one buffer from the direct
@@ -92,6 +92,7 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
   __shared__ __attribute__((aligned(1024))) uint16_t v_st0[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint16_t k_st1[C::STAGE];
   __shared__ __attribute__((aligned(1024))) uint16_t v_st1[C::STAGE];
+  __shared__ uint32_t wave_met[C::W];  // each wave's non-finite flag (below)
   // the layout and the work list are read-only here: scalar loads
   const cptr_i32 items = (cptr_i32)A.items;
   const cptr_i32 row_ptr = (cptr_i32)A.row_ptr;
@@ -107,123 +108,174 @@ __global__ __launch_bounds__(BMQ * 2, 2) void tile_fwd_kernel(TileArgs A) {
   const int b = bh / A.H;
   const int kvh = h / A.groups;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l32 = lane & 31;
+  // ---- the item: set-up, the stages, the store.  An item whose outputs met
+  // a non-finite value (an Inf or NaN in V, staged with a 32-key block, can
+  // reach rows that do not list it through 0 * Inf in PV) runs again, every
+  // wave of the workgroup together, with the V operands sanitised (SAN):
+  // rows whose entries bring no non-finite value then get exactly the bits a
+  // run without it gives, and the reference's non-finite values go back in
+  // after the store.  Each run sets itself up from the kernel arguments, so
+  // nothing but the flag is live from one to the other, and the second costs
+  // the first no registers.
+  auto run_item = [&](auto san_tag) -> bool {
+    constexpr bool SAN = decltype(san_tag)::value;
+    // (the lane id passes through an empty asm, so the compiler cannot share
+    // the runs' per-lane set-up and keep it live from one to the other)
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31;
 
-  const int i = qb * C::BM + wave * 32 + l32;  // this lane's query row = position
-  const bool row_ok = i < A.q_len;
+    const int i = qb * C::BM + wave * 32 + l32;  // this lane's query row = position
+    const bool row_ok = i < A.q_len;
 
-  Rows32<D, E> rows;
-  rows.init(lane, A.scale_log2);  // scale > 0 (checked on the host)
-  rows.load_q(A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)i * A.qss, row_ok);
+    Rows32<D, E> rows;
+    rows.init(lane, A.scale_log2);  // scale > 0 (checked on the host)
+    rows.load_q(A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)i * A.qss, row_ok);
 
-  // ---- this row's index list
-  RowWalker walk;
-  if constexpr (!PRE) walk.init(A.pc, h, i, row_ok);
+    // ---- this row's index list
+    RowWalker walk;
+    if constexpr (!PRE) walk.init(A.pc, h, i, row_ok);
 
-  // ---- staging: buffer resources over this (batch, kv head)'s rows; keys at
-  // or past kv_len are outside num_records and load as zeros (the host keeps
-  // kv_len * row stride * 2 below 2^31)
-  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh), (short)0,
-      (int)((int64_t)A.kv_len * A.kss * 2), 0x00020000);
-  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh), (short)0,
-      (int)((int64_t)A.kv_len * A.vss * 2), 0x00020000);
-  auto block = [&](const uint16_t* Kb, const uint16_t* Vb, int kbl, uint32_t mbits) {
-    rows.block(Kb, Vb, kbl, mbits);
-  };
+    // ---- staging: buffer resources over this (batch, kv head)'s rows; keys at
+    // or past kv_len are outside num_records and load as zeros (the host keeps
+    // kv_len * row stride * 2 below 2^31)
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh), (short)0,
+        (int)((int64_t)A.kv_len * A.kss * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh), (short)0,
+        (int)((int64_t)A.kv_len * A.vss * 2), 0x00020000);
 
-  const int64_t lrow = (int64_t)h * A.nqb + qb;
-  // ---- the item's 64-key stages: layout key blocks of 64 keys are one stage
-  // each; 128-key blocks are two (stage s is half s & 1 of block s >> 1)
-  const int sh = A.stage_shift;
-  const int s0 = row_ptr[lrow] << sh, s1 = row_ptr[lrow + 1] << sh;
+    const int64_t lrow = (int64_t)h * A.nqb + qb;
+    // ---- the item's 64-key stages: layout key blocks of 64 keys are one stage
+    // each; 128-key blocks are two (stage s is half s & 1 of block s >> 1)
+    const int sh = A.stage_shift;
+    const int s0 = row_ptr[lrow] << sh, s1 = row_ptr[lrow + 1] << sh;
 
-  // load j of this lane fills chunk slot (LOADS wave + j) * 64 + lane of a
-  // stage buffer: row slot / CPR, physical chunk slot % CPR
-  int koff[C::LOADS], voff[C::LOADS];
-#pragma unroll
-  for (int j = 0; j < C::LOADS; ++j) {
-    const int slot = (C::LOADS * wave + j) * 64 + lane;
-    const int row = slot / C::CPR, pc = slot % C::CPR;
-    koff[j] = (row * (int)A.kss + 8 * (pc ^ swz_k<D>(row))) * 2;
-    voff[j] = (row * (int)A.vss + 8 * (pc ^ swz_v<D>(row))) * 2;
-  }
-  auto stage_key0 = [&](int st) {
-    return (col_idx[st >> sh] << (C::LOG_HALF + sh)) + ((st & sh) << C::LOG_HALF);
-  };
-  // the HALF keys from key0 -> buffers (kd, vd)
-  auto issue = [&](int key0, uint16_t* kd, uint16_t* vd) {
-    const int ks = key0 * (int)A.kss * 2, vs = key0 * (int)A.vss * 2;
+    // load j of this lane fills chunk slot (LOADS wave + j) * 64 + lane of a
+    // stage buffer: row slot / CPR, physical chunk slot % CPR
+    int koff[C::LOADS], voff[C::LOADS];
+  #pragma unroll
+    for (int j = 0; j < C::LOADS; ++j) {
+      const int slot = (C::LOADS * wave + j) * 64 + lane;
+      const int row = slot / C::CPR, pc = slot % C::CPR;
+      koff[j] = (row * (int)A.kss + 8 * (pc ^ swz_k<D>(row))) * 2;
+      voff[j] = (row * (int)A.vss + 8 * (pc ^ swz_v<D>(row))) * 2;
+    }
+    auto stage_key0 = [&](int st) {
+      return (col_idx[st >> sh] << (C::LOG_HALF + sh)) + ((st & sh) << C::LOG_HALF);
+    };
+    // the HALF keys from key0 -> buffers (kd, vd)
+    auto issue = [&](int key0, uint16_t* kd, uint16_t* vd) {
+      const int ks = key0 * (int)A.kss * 2, vs = key0 * (int)A.vss * 2;
+  #pragma unroll
+      for (int j = 0; j < C::LOADS; ++j) {
+        // each load writes 64 lanes x 16 bytes = 512 elements
+        load_lds16(krs, kd + (C::LOADS * wave + j) * 512, koff[j], ks);
+        load_lds16(vrs, vd + (C::LOADS * wave + j) * 512, voff[j], vs);
+      }
+    };
+
+    // the rerun: this lane's 16-byte chunks of a landed V stage (the ones its
+  // DMAs wrote) with non-finite values replaced by +0, before the barrier
+  // that hands the stage to the blocks
+  auto sanitize_stage = [&](uint16_t* vd) {
 #pragma unroll
     for (int j = 0; j < C::LOADS; ++j) {
-      // each load writes 64 lanes x 16 bytes = 512 elements
-      load_lds16(krs, kd + (C::LOADS * wave + j) * 512, koff[j], ks);
-      load_lds16(vrs, vd + (C::LOADS * wave + j) * 512, voff[j], vs);
+      u32x4* p = (u32x4*)(vd + (C::LOADS * wave + j) * 512) + lane;
+      u32x4 x = *p;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = sanitize2<E>(x[e]);
+      *p = x;
     }
   };
 
   // PRE: this row's mask words of stages st (and st + 1 if has_b) -> mb;
-  // zeros for rows past q_len, as the walk gives them
-  const int64_t mrow = (int64_t)(wave * 32 + l32) * C::NB;
-  auto load_masks = [&](int st, bool has_b, uint32_t (&mb)[2 * C::NB]) {
-    const uint32_t* m0 = A.smask + (int64_t)st * (C::BM * C::NB) + mrow;
-#pragma unroll
-    for (int j = 0; j < C::NB; ++j) {
-      mb[j] = row_ok ? m0[j] : 0u;
-      mb[C::NB + j] = row_ok && has_b ? m0[C::BM * C::NB + j] : 0u;
+    // zeros for rows past q_len, as the walk gives them
+    const int64_t mrow = (int64_t)(wave * 32 + l32) * C::NB;
+    auto load_masks = [&](int st, bool has_b, uint32_t (&mb)[2 * C::NB]) {
+      const uint32_t* m0 = A.smask + (int64_t)st * (C::BM * C::NB) + mrow;
+  #pragma unroll
+      for (int j = 0; j < C::NB; ++j) {
+        mb[j] = row_ok ? m0[j] : 0u;
+        mb[C::NB + j] = row_ok && has_b ? m0[C::BM * C::NB + j] : 0u;
+      }
+    };
+    // ---- the item's stages
+    uint32_t mnext[2 * C::NB];
+    if constexpr (PRE) {
+      if (s0 < s1) load_masks(s0, s0 + 1 < s1, mnext);
     }
+    // ---- two stage buffers, one stage ahead: each barrier retires every
+    // wave's reads of the other buffer before the next stage is loaded into it.
+    // Stages go in pairs (buffer 0, buffer 1); this row's valid keys of both
+    // are walked first (or, with PRE, were loaded during the previous pair).
+    // The next two stage keys are read together at the top of a pair (clamped
+    // indices: unconditional scalar loads, one wait).
+    int ka = s0 < s1 ? stage_key0(s0) : 0;
+    if (s0 < s1) issue(ka, k_st0, v_st0);
+    for (int st = s0; st < s1; st += 2) {
+      const bool has_b = st + 1 < s1, has_c = st + 2 < s1;
+      const int kb = stage_key0(min(st + 1, s1 - 1));
+      const int kc = stage_key0(min(st + 2, s1 - 1));
+      uint32_t mb[2 * C::NB];
+      if constexpr (PRE) {
+  #pragma unroll
+        for (int j = 0; j < 2 * C::NB; ++j) mb[j] = mnext[j];
+      } else {
+        walk.stage_pair<C::NB>(ka, kb, has_b, mb);
+      }
+
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      if constexpr (SAN) {
+        sanitize_stage(v_st0);  // (this wave's own DMAs have landed)
+        __builtin_amdgcn_s_waitcnt(0);
+      }
+      __syncthreads();
+      if (has_b) issue(kb, k_st1, v_st1);
+      // the next pair's masks, in flight during this pair's blocks (the waits
+      // above the next barriers cover them)
+      if constexpr (PRE) {
+        if (has_c) load_masks(st + 2, st + 3 < s1, mnext);
+      }
+  #pragma unroll
+      for (int j = 0; j < C::NB; ++j) rows.template block<SAN>(k_st0, v_st0, j, mb[j]);
+      if (!has_b) break;
+
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+      if constexpr (SAN) {
+        sanitize_stage(v_st1);
+        __builtin_amdgcn_s_waitcnt(0);
+      }
+      __syncthreads();
+      if (has_c) issue(kc, k_st0, v_st0);
+  #pragma unroll
+      for (int j = 0; j < C::NB; ++j) rows.template block<SAN>(k_st1, v_st1, j, mb[C::NB + j]);
+      ka = kc;
+    }
+
+    // ---- epilogue: normalise and store O rows and the log-sum-exp
+    const bool met_nonfinite = !SAN && !sum_finite(rows.oacc);
+    uint16_t* const orow = A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)i * A.oss;
+    rows.store(orow, A.lse ? A.lse + (int64_t)b * A.lsb + (int64_t)h * A.lsh + i : nullptr,
+               row_ok);
+    if (SAN && row_ok)
+      rows.put_nonfinite(orow, A.pc, h, i, A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh, A.vss);
+    return met_nonfinite;
   };
-  uint32_t mnext[2 * C::NB];
-  if constexpr (PRE) {
-    if (s0 < s1) load_masks(s0, s0 + 1 < s1, mnext);
-  }
-
-  // ---- two stage buffers, one stage ahead: each barrier retires every
-  // wave's reads of the other buffer before the next stage is loaded into it.
-  // Stages go in pairs (buffer 0, buffer 1); this row's valid keys of both
-  // are walked first (or, with PRE, were loaded during the previous pair).
-  // The next two stage keys are read together at the top of a pair (clamped
-  // indices: unconditional scalar loads, one wait).
-  int ka = s0 < s1 ? stage_key0(s0) : 0;
-  if (s0 < s1) issue(ka, k_st0, v_st0);
-  for (int st = s0; st < s1; st += 2) {
-    const bool has_b = st + 1 < s1, has_c = st + 2 < s1;
-    const int kb = stage_key0(min(st + 1, s1 - 1));
-    const int kc = stage_key0(min(st + 2, s1 - 1));
-    uint32_t mb[2 * C::NB];
-    if constexpr (PRE) {
+  const bool met = run_item(std::integral_constant<bool, false>{});
+  // every wave's flag through its own LDS word and one barrier (which also
+  // retires every wave's reads of the stage buffers before a rerun refills
+  // them)
+  const uint32_t wmet = wave_any(met) ? 1u : 0u;
+  if ((threadIdx.x & 63) == 0) wave_met[threadIdx.x >> 6] = wmet;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  uint32_t any = 0u;
 #pragma unroll
-      for (int j = 0; j < 2 * C::NB; ++j) mb[j] = mnext[j];
-    } else {
-      walk.stage_pair<C::NB>(ka, kb, has_b, mb);
-    }
-
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    __syncthreads();
-    if (has_b) issue(kb, k_st1, v_st1);
-    // the next pair's masks, in flight during this pair's blocks (the waits
-    // above the next barriers cover them)
-    if constexpr (PRE) {
-      if (has_c) load_masks(st + 2, st + 3 < s1, mnext);
-    }
-#pragma unroll
-    for (int j = 0; j < C::NB; ++j) block(k_st0, v_st0, j, mb[j]);
-    if (!has_b) break;
-
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    __syncthreads();
-    if (has_c) issue(kc, k_st0, v_st0);
-#pragma unroll
-    for (int j = 0; j < C::NB; ++j) block(k_st1, v_st1, j, mb[C::NB + j]);
-    ka = kc;
-  }
-
-  // ---- epilogue: normalise and store O rows and the log-sum-exp
-  rows.store(A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)i * A.oss,
-             A.lse ? A.lse + (int64_t)b * A.lsb + (int64_t)h * A.lsh + i : nullptr, row_ok);
+  for (int w = 0; w < C::W; ++w) any |= wave_met[w];
+  if (any) run_item(std::integral_constant<bool, true>{});
 }
 
 template <Elem E, bool PRE>

@@ -89,6 +89,28 @@ __device__ __forceinline__ void mask_init(f32x16& s, uint32_t nmk) {
   }
 }
 
+// Per-register select masks from a lane's valid-key bits mk (bit
+// 8 (r / 4) + r % 4 for register r): -1 for a valid key, 0 for a masked one,
+// one v_bfe_i32 each (inline asm on mk only, which is no MFMA result).
+template <int R>
+__device__ __forceinline__ void key_masks(uint32_t (&m)[16], uint32_t mk) {
+  if constexpr (R < 16) {
+    asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(m[R]) : "v"(mk), "i"(8 * (R / 4) + R % 4));
+    key_masks<R + 1>(m, mk);
+  }
+}
+
+// Scores of masked keys to -inf after the MFMA: one v_bfi_b32 per register
+// (written in C, not asm, so the compiler keeps the wait states between the
+// MFMA that writes s and this VALU read of it).  A select rather than an
+// additive mask, so a non-finite key row never reaches the score of a row
+// that does not list it (-inf + Inf would be NaN).
+__device__ __forceinline__ void mask_select(f32x16& s, const uint32_t (&m)[16]) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    s[r] = __uint_as_float((m[r] & __float_as_uint(s[r])) | (~m[r] & 0xff800000u));
+}
+
 __device__ __forceinline__ bool wave_any(bool p) {
   return __builtin_amdgcn_ballot_w64(p) != 0;
 }
@@ -261,6 +283,12 @@ struct Rows32 {
 
   // One 32-key block: keys 32 kbl .. 32 kbl + 31 of the LDS buffers (Kb, Vb),
   // whose valid-key bits for this lane's row are mbits (bit k: key k).
+  // SAN: the rerun of an item whose output met a non-finite value: masked
+  // scores are selected to -inf after the MFMA (instead of entering as the
+  // accumulator's -inf start, where a non-finite K value would make NaN of
+  // them); the caller has sanitised the staged V rows.  For finite inputs
+  // both give the same bits.
+  template <bool SAN>
   __device__ __forceinline__ void block(const uint16_t* Kb, const uint16_t* Vb, int kbl,
                                         uint32_t mbits) {
     // lane half hf holds keys 8*(r/4) + 4*hf + r%4 of the block
@@ -274,13 +302,26 @@ struct Rows32 {
     V8 ka[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) ka[s] = *(const V8*)(Kb + kaddr[s] + 32 * kbl * D);
-    // the mask enters as the accumulator's initial value: 0 for a valid key,
-    // -inf for a masked one
     f32x16 sacc;
-    mask_init<0>(sacc, ~mk);
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (SAN) {
+      sacc = f32x16{};
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int s = 0; s < NS; ++s) sacc = M::mfma32(ka[s], qop[s], sacc);
+      for (int s = 0; s < NS; ++s) sacc = M::mfma32(ka[s], qop[s], sacc);
+      // (the masks are formed after the MFMAs, one register at a time, so the
+      // rerun holds no more registers than the first run)
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t kmask[16];
+      key_masks<0>(kmask, mk);
+      mask_select(sacc, kmask);
+    } else {
+      // the mask enters as the accumulator's initial value: 0 for a valid
+      // key, -inf for a masked one
+      mask_init<0>(sacc, ~mk);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) sacc = M::mfma32(ka[s], qop[s], sacc);
+    }
     // the V^T operands of this block, read while the softmax runs
     s16x4 va[ND][4];
 #pragma unroll
@@ -366,6 +407,24 @@ struct Rows32 {
     }
     if (lse && hf == 0)
       *lse = l_tot > 0.f ? (m_run + __log2f(l_tot)) * 0.69314718055994530942f : -INFINITY;
+  }
+
+  // After a rerun with sanitised V: the dims of this lane's output where row
+  // i's own entries bring an Inf or NaN of V take the reference's value.
+  // vrows: element 0 of key 0 of the (batch, kv head).
+  __device__ __forceinline__ void put_nonfinite(uint16_t* orow, const PatternConsts& pc, int h,
+                                                int i, const uint16_t* vrows, int64_t vss) {
+    int dim0[4 * ND];
+#pragma unroll
+    for (int d = 0; d < ND; ++d)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) dim0[4 * d + g] = 32 * d + 8 * g + 4 * hf;
+    uint64_t pos, neg, nan;
+    nonfinite_v<E>(pc, h, i, vrows, vss, dim0, pos, neg, nan);
+    for (uint64_t any = pos | neg | nan; any != 0ull; any &= any - 1ull) {
+      const int bit = __builtin_ctzll(any);
+      orow[dim0[bit >> 2] + (bit & 3)] = nonfinite_value<E>(pos, neg, nan, bit);
+    }
   }
 };
 

@@ -550,8 +550,9 @@ def _prefill_fwd(q, k, v, layout, scaling, return_lse, out, key_block, query_blo
     st = layout if (query_block, key_block) == (128, 128) else layout.stages(key_block,
                                                                              query_block)
     items, n = st.schedule(Lq, B)
-    # layer 0 rows are contiguous runs: the kernel sets them without a walk;
-    # whole-tile staging walks
+    # layer 0 rows are contiguous runs: the kernel sets them without a walk
+    # (measured: with masks 5-8% slower at B=8 H=16 L=4096 and B=1 H=32
+    # L=8192, within 2% elsewhere); whole-tile staging walks
     use = stage_masks and st.pattern.layer_idx > 0 and st.pattern.block_n != 128
     masks = st.stage_masks() if use else None
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)

@@ -1,15 +1,16 @@
-"""Non-finite values in V (GPU).
+"""Non-finite values in K and V (GPU).
 
 The reference gathers only the K/V rows a query row attends
-(elastic_sparse_attention.py:131-154), so an Inf or NaN in V row k reaches
-exactly the rows that list k.  The per-row gather kernels (decode, float32,
-the reference operator) keep that: rows that do not attend k are
-bit-identical to a clean run.  The MFMA kernels stage whole key blocks or
-bands and multiply p = 0 into the rows a query row does not attend, and
-0 * Inf is NaN: a non-finite V row can also reach rows whose staged block
-or band covers it without attending it.  That is a declared limitation
-(the reference-exact test below is skipped); what holds for them is that
-rows whose staged keys stay clear of k are bit-identical to a clean run.
+(elastic_sparse_attention.py:131-154), so an Inf or NaN in K or V row k
+reaches exactly the rows that list k.  The per-row gather kernels (decode,
+float32, the reference operator) keep that bit for bit.  The MFMA prefill
+kernels stage whole key blocks or bands: they mask scores by a select (so a
+non-finite K value never reaches a row that does not list its key), and a
+group or item whose output met a non-finite value runs again with the staged
+V operands sanitised and the reference's non-finite values put back from the
+row's own entries.  So for them too, rows that do not attend a planted key
+are bit-identical to a clean run, and rows that do are non-finite exactly
+where the per-row gather path is.
 """
 import pytest
 import torch
@@ -73,18 +74,108 @@ def test_mfma_paths_confine_nonfinite_v(kernel, layer):
     assert torch.equal(bad[far], clean[far])
 
 
-@pytest.mark.skip(reason="declared limitation: the MFMA kernels multiply p = 0 into staged V "
-                         "rows a query row does not attend, so a non-finite value there reaches "
-                         "that row; the per-row gather path keeps the reference's semantics")
-@pytest.mark.parametrize("kernel,layer", [("band", 4), ("tile", 4), ("tile", 0)])
-def test_mfma_paths_reference_semantics(kernel, layer):
-    B, H, L, D, key = 1, 4, 2048, 128, 1000
-    q, k, v, vb = planted(B, H, L, D, torch.bfloat16, key)
-    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+def rows_path(q, k, v, pat, D):
+    o, _ = elastic_attention_rows(q, k, v, pat, D ** -0.5)
+    return o
+
+
+# (kernel, layer, L, H, D, w, dtype): the band kernel's early and late V
+# refill orders (w = 2 at the last layer puts the entry spacing past 1000
+# rows), both head dims, float16, and the tile kernel's three staging shapes
+NF_CASES = [("band", 4, 2048, 4, 128, 64, torch.bfloat16),
+            ("band", 7, 2048, 4, 64, 64, torch.bfloat16),
+            ("band", 7, 2048, 4, 128, 2, torch.bfloat16),
+            ("band", 5, 1500, 3, 128, 64, torch.float16),
+            ("tile", 4, 2048, 4, 128, 64, torch.bfloat16),
+            ("tile", 0, 2048, 4, 128, 64, torch.bfloat16),
+            ("tile", 2, 1024, 4, 64, 64, torch.float16),
+            ("tile64", 3, 1024, 4, 64, 64, torch.bfloat16),
+            ("tile128", 6, 1024, 2, 128, 48, torch.bfloat16)]
+
+
+def mfma(kernel, q, k, v, lay, D):
+    if kernel == "tile64":
+        o, _ = elastic_attention_fwd(q, k, v, lay, D ** -0.5, kernel="tile", query_block=64,
+                                     key_block=32)
+    elif kernel == "tile128":
+        o, _ = elastic_attention_fwd(q, k, v, lay, D ** -0.5, kernel="tile", query_block=128,
+                                     key_block=128)
+    else:
+        o, _ = elastic_attention_fwd(q, k, v, lay, D ** -0.5, kernel=kernel)
+    return o
+
+
+def same_nonfinite(a, b):
+    """Same positions hold NaN, +Inf and -Inf in a and b."""
+    a, b = a.float(), b.float()
+    return (torch.equal(torch.isnan(a), torch.isnan(b)) and
+            torch.equal(a == float("inf"), b == float("inf")) and
+            torch.equal(a == float("-inf"), b == float("-inf")))
+
+
+@pytest.mark.parametrize("kernel,layer,L,H,D,w,dtype", NF_CASES)
+def test_mfma_paths_reference_semantics(kernel, layer, L, H, D, w, dtype):
+    """V planted with +Inf, -Inf and NaN at three keys: every output row that
+    attends none of them is bit-identical to a clean run of the same kernel,
+    and the non-finite positions (and their kind) are those of the per-row
+    gather path, which follows the reference's gather (:131-133, :152-154)."""
+    print(f"nonfinite V {kernel} layer={layer} L={L} H={H} D={D} w={w} {dtype}", flush=True)
+    q, k, v = seeded_inputs(1, H, H, L, D, dtype, seed=23, scale=1.0)
+    keys = [L // 2 + 1, L // 3, L - 5]
+    vb = v.clone()
+    vb[:, :, keys[0], 3] = float("inf")
+    vb[:, :, keys[1], D - 1] = float("nan")
+    vb[:, :, keys[2], 7] = float("-inf")
+    vb[:, :, keys[2], 8] = float("inf")
+    pat = make_pattern(L, w, layer, 8, H)
+    lay = ElasticLayout(pat, DEV)
     qd, kd = q.to(DEV), k.to(DEV)
-    clean, _ = elastic_attention_fwd(qd, kd, v.to(DEV), lay, D ** -0.5, kernel=kernel)
-    bad, _ = elastic_attention_fwd(qd, kd, vb.to(DEV), lay, D ** -0.5, kernel=kernel)
-    idx, msk = elastic_indices(L, layer, 8, H, 64)
-    hit = attends(idx, msk, key).T.unsqueeze(0).to(DEV)
+    clean = mfma(kernel, qd, kd, v.to(DEV), lay, D)
+    bad = mfma(kernel, qd, kd, vb.to(DEV), lay, D)
+    ref = rows_path(qd, kd, vb.to(DEV), pat, D)
+    idx, msk = elastic_indices(L, layer, 8, H, w)
+    hit = torch.zeros(H, L, dtype=torch.bool)
+    for key in keys:
+        hit |= attends(idx, msk, key)
+    hit = hit.T.unsqueeze(0).to(DEV)                                      # [1, L, H]
+    assert bool(hit.any()) and bool((~hit).any())
     keep = (~hit).unsqueeze(-1).expand_as(bad)
     assert torch.equal(bad[keep], clean[keep])
+    assert same_nonfinite(bad, ref)
+    # the finite outputs of rows that attend a planted key agree with the
+    # gather path to the bf16 bar (only the planted dims differ from clean)
+    fin = torch.isfinite(ref.float()) & torch.isfinite(bad.float())
+    assert float((bad.float() - ref.float())[fin].abs().max()) <= 2e-2
+
+
+@pytest.mark.parametrize("kernel,layer,L,H,D,w,dtype", NF_CASES[:2] + NF_CASES[4:8])
+def test_mfma_paths_nonfinite_k(kernel, layer, L, H, D, w, dtype):
+    """K planted with +Inf, -Inf and NaN: a row attending a planted key gets a
+    non-finite score there (NaN output, or, for a -Inf score, that key's
+    probability is 0), exactly as the per-row gather path gives it; rows that
+    attend no planted key are bit-identical to a clean run (the masked
+    scores are selected away, never added to -inf)."""
+    print(f"nonfinite K {kernel} layer={layer} L={L} H={H} D={D} w={w} {dtype}", flush=True)
+    q, k, v = seeded_inputs(1, H, H, L, D, dtype, seed=29, scale=1.0)
+    keys = [L // 2 + 3, L // 4, L - 9]
+    kb = k.clone()
+    kb[:, :, keys[0], 3] = float("inf")
+    kb[:, :, keys[1], 5] = float("nan")
+    kb[:, :, keys[2], 11] = float("-inf")
+    pat = make_pattern(L, w, layer, 8, H)
+    lay = ElasticLayout(pat, DEV)
+    qd, vd = q.to(DEV), v.to(DEV)
+    clean = mfma(kernel, qd, k.to(DEV), vd, lay, D)
+    bad = mfma(kernel, qd, kb.to(DEV), vd, lay, D)
+    ref = rows_path(qd, kb.to(DEV), vd, pat, D)
+    idx, msk = elastic_indices(L, layer, 8, H, w)
+    hit = torch.zeros(H, L, dtype=torch.bool)
+    for key in keys:
+        hit |= attends(idx, msk, key)
+    hit = hit.T.unsqueeze(0).to(DEV)
+    assert bool(hit.any()) and bool((~hit).any())
+    keep = (~hit).unsqueeze(-1).expand_as(bad)
+    assert torch.equal(bad[keep], clean[keep])
+    assert same_nonfinite(bad, ref)
+    fin = torch.isfinite(ref.float()) & torch.isfinite(bad.float())
+    assert float((bad.float() - ref.float())[fin].abs().max()) <= 2e-2
