@@ -1,7 +1,12 @@
 """Builds libesa.so (the HIP kernels and the C ABI) and libesa_probe.so (the
 rate probes bench.py --peaks runs) for gfx950 in place.
 
-    python elastic-sparse-attention_amd/build_lib.py [-v]
+    python elastic-sparse-attention_amd/build_lib.py [-v] [--sanitize]
+
+--sanitize builds libesa_san.so instead: the same sources with the host code
+under AddressSanitizer and UndefinedBehaviorSanitizer (device code is left
+alone), for running the host-side tests against (tests/test_sanitizers.py);
+esa_native loads it when ESA_LIB names it.
 
 hipcc cross-compiles without a GPU.  Each source is compiled to an object
 (in parallel) under _build/ next to this file, then the objects are linked
@@ -25,6 +30,12 @@ SOURCES = ["esa_capi.hip", "esa_layout.hip", "esa_fwd_tile.hip", "esa_fwd_band.h
 PROBE_SOURCES = ["esa_probe.hip"]
 LIB = os.path.join(HERE, "libesa.so")
 PROBE_LIB = os.path.join(HERE, "libesa_probe.so")
+SAN_LIB = os.path.join(HERE, "libesa_san.so")
+SAN_BUILD = os.path.join(HERE, "_build_san")
+# host-only sanitizers: each -fsanitize= applies to the host pass alone
+SAN_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+             "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host",
+             "-fno-omit-frame-pointer", "-g"]
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
          # packed fp32 VALU forms are kept out of every kernel
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -44,10 +55,10 @@ def _messages(res: subprocess.CompletedProcess) -> list:
             if "packed-fp32-ops" not in ln and ln.strip()]
 
 
-def _compile(src: str, verbose: bool) -> str:
-    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *FLAGS, "-I", os.path.join(HERE, "..", "include"), "-c",
-           os.path.join(CSRC, src), "-o", obj]
+def _compile(src: str, verbose: bool, san: bool = False) -> str:
+    obj = os.path.join(SAN_BUILD if san else BUILD, os.path.splitext(src)[0] + ".o")
+    cmd = [hipcc(), *FLAGS, *(SAN_FLAGS if san else []), "-I",
+           os.path.join(HERE, "..", "include"), "-c", os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -59,9 +70,11 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
-def _link(objs: list, lib: str, verbose: bool) -> None:
+def _link(objs: list, lib: str, verbose: bool, san: bool = False) -> None:
     tmp = lib + ".tmp"
-    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC",
+           *(["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+              "-shared-libsan"] if san else []), *objs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -84,5 +97,19 @@ def build(verbose: bool = False) -> str:
     return LIB
 
 
+def build_sanitized(verbose: bool = False) -> str:
+    """Compiles every library source with host-side ASan/UBSan and links
+    libesa_san.so; returns its path."""
+    os.makedirs(SAN_BUILD, exist_ok=True)
+    workers = min(len(SOURCES), max(1, min(os.cpu_count() or 1, 8)))
+    with cf.ThreadPoolExecutor(workers) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose, san=True), SOURCES))
+    _link(objs, SAN_LIB, verbose, san=True)
+    return SAN_LIB
+
+
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    if "--sanitize" in sys.argv:
+        print(build_sanitized(verbose="-v" in sys.argv))
+    else:
+        print(build(verbose="-v" in sys.argv))

@@ -11,7 +11,9 @@ import os
 from typing import Optional
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libesa.so")
+# ESA_LIB may name another build of the library (the sanitizer build the
+# host-side tests run against); by default the in-tree libesa.so
+LIB_PATH = os.environ.get("ESA_LIB") or os.path.join(HERE, "libesa.so")
 PROBE_LIB_PATH = os.path.join(HERE, "libesa_probe.so")
 
 ESA_OK = 0
