@@ -2,7 +2,7 @@
 
     python bench.py [--steps K] [--warmup W] [--config 32k|8k|batched|128k]
                     [--layer N] [--no-cpu] [--no-backward] [--no-decode]
-                    [--no-configs]
+                    [--no-configs] [--no-chunk]
     python bench.py --peaks            (only the rate probes, one JSON line)
 
 A step is one ElasticSparseAttention.forward over one batch of synthetic
@@ -40,6 +40,9 @@ configs          every configured workload (forward and backward kernel
 backward         the backward of the headline forward (dQ, dK, dV).
 decode           one decode step of 128 sequences through the module's
                  cache_position path.
+chunked_prefill  the headline's last 4096 rows as a cache_position chunk
+                 through the module (the band kernel at those positions),
+                 beside the same rows' share of the full prefill.
 cpu_baseline     the reference's PyTorch fallback (_naive_forward, restated
                  in oracle/) over the whole headline forward on the host
                  cores, in row chunks, no extrapolation.
@@ -488,6 +491,41 @@ def time_decode(torch, layer: int, steps: int, warmup: int) -> dict:
                          "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}}
 
 
+CHUNK = (28672, 4096)  # a chunked prefill of the headline shape: rows p0 .. p0 + n - 1
+
+
+def time_chunk(torch, cfg: str, layer: int, steps: int, warmup: int) -> dict:
+    """A chunked prefill through the module: the last CHUNK rows of a
+    configured sequence as query rows with cache_position = arange(p0, p0 +
+    n) on the device, against the full key/value cache (the band kernel at
+    the given positions).  Beside it, the same rows' share of a full prefill
+    (the band kernel does the same work for every 16-row group, so the share
+    is the full forward's time times n / L)."""
+    from elastic_sparse_attention import ElasticSparseAttention, elastic_attention_band
+    B, H, L, D, _, _ = CONFIGS[cfg]
+    p0, n = CHUNK
+    dev = torch.device("cuda", 0)
+    q, k, v = make_inputs(torch, cfg, dev, on_device=True)
+    m = ElasticSparseAttention(layer_idx=layer, num_hidden_layers=NL, num_attention_heads=H,
+                               head_dim=D, attention_length=W, max_seq_len=L)
+    qc = q[:, :, p0:p0 + n].contiguous()
+    pos = torch.arange(p0, p0 + n, dtype=torch.int64, device=dev)
+    with torch.no_grad():
+        chunk_ms = event_ms(torch, lambda: m(qc, k, v, cache_position=pos), steps, warmup)
+        full_ms = event_ms(torch, lambda: elastic_attention_band(q, k, v, m.pattern, m.scaling,
+                                                                 return_lse=False),
+                           steps, warmup)
+    share = full_ms * n / L
+    del q, k, v, qc
+    torch.cuda.empty_cache()
+    return {"workload": (f"chunked prefill through the module (cache_position = arange({p0}, "
+                         f"{p0 + n})), bf16 B={B} H={H} kv L={L} D={D}, w={W}, layer {layer} "
+                         f"of {NL}"),
+            "chunk_ms": round(chunk_ms, 4), "full_prefill_ms": round(full_ms, 4),
+            "prefill_rows_share_ms": round(share, 4),
+            "ratio_to_prefill_share": round(chunk_ms / share, 3)}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -504,6 +542,8 @@ def main() -> None:
                     help="skip timing one decode step of a serving batch (reported by default)")
     ap.add_argument("--no-configs", dest="configs", action="store_false",
                     help="skip the per-configuration forward/backward table")
+    ap.add_argument("--no-chunk", dest="chunk", action="store_false",
+                    help="skip timing a chunked prefill (cache_position rows) of the headline")
     ap.add_argument("--config-steps", type=int, default=20)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain device copy of known size (HBM counter scale)")
@@ -631,6 +671,11 @@ def main() -> None:
                 print(f"# configs {key}: {rows[key].get('fwd_ms')} ms", file=sys.stderr,
                       flush=True)
         out["configs"] = rows
+    if args.chunk:
+        try:
+            out["chunked_prefill"] = time_chunk(torch, "32k", args.layer, args.steps, args.warmup)
+        except Exception as exc:  # noqa: BLE001
+            out["chunked_prefill"] = {"error": f"{type(exc).__name__}: {exc}"}
     if args.decode:
         try:
             out["decode"] = time_decode(torch, args.layer, max(args.steps, 50), args.warmup)

@@ -474,7 +474,8 @@ namespace {
 
 // Checks and arguments of the band-gathered forward (16 query rows per
 // group; a band's buffer offsets reach up to 16 rows past kv_len).
-esa_status band_args_of(const esa_fwd_args* a, const esa_pattern* p, BandArgs* out) {
+esa_status band_args_of(const esa_fwd_args* a, const esa_pattern* p, const int64_t* positions,
+                        BandArgs* out) {
   constexpr int rows_per_item = 16, pad_rows = 16;
   esa_status s = check_fwd_common(a);
   if (s != ESA_OK) return s;
@@ -488,7 +489,9 @@ esa_status band_args_of(const esa_fwd_args* a, const esa_pattern* p, BandArgs* o
   if (p->layer_idx < 0 || p->layer_idx > std::max(p->num_hidden_layers - 1, 0))
     return ESA_ERR_UNSUPPORTED;
   if (p->num_heads != a->num_heads) return ESA_ERR_SHAPE;
-  if (a->q_len > a->kv_len || a->q_len > p->seq_len) return ESA_ERR_SHAPE;
+  // (with positions the rows may be any positions, as esa_elastic_fwd_rows
+  // takes them)
+  if (!positions && (a->q_len > a->kv_len || a->q_len > p->seq_len)) return ESA_ERR_SHAPE;
   if (!(a->sm_scale > 0.f) || !std::isfinite(a->sm_scale)) return ESA_ERR_UNSUPPORTED;
   // band descriptors pack the first key in 24 bits; K/V rows are addressed
   // through 32-bit buffer offsets per (batch, kv head)
@@ -525,6 +528,9 @@ esa_status band_args_of(const esa_fwd_args* a, const esa_pattern* p, BandArgs* o
   t.scale_log2 = a->sm_scale * 1.4426950408889634f;
   t.pc = make_consts(*p);
   t.elem = a->dtype;
+  t.positions = positions;
+  t.kv_len = a->kv_len;
+  t.sm_scale = a->sm_scale;
   return ESA_OK;
 }
 
@@ -532,9 +538,10 @@ esa_status band_args_of(const esa_fwd_args* a, const esa_pattern* p, BandArgs* o
 
 extern "C" {
 
-esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, void* stream) {
+esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p,
+                                const int64_t* positions, void* stream) {
   BandArgs t;
-  esa_status s = band_args_of(a, p, &t);
+  esa_status s = band_args_of(a, p, positions, &t);
   if (s != ESA_OK || t.n_groups == 0) return s;
   return hip_status(launch_band_fwd(t, a->head_dim, (hipStream_t)stream));
 }

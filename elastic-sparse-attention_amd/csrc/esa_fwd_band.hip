@@ -46,6 +46,7 @@
 //
 // Operand layouts: esa_band.hpp.
 #include "esa_band.hpp"
+#include "esa_gather.hpp"
 
 namespace esa {
 
@@ -56,7 +57,15 @@ namespace esa {
 // where many bands are narrower than 16 keys (the dilated, late layers);
 // where nearly every band is 16 keys wide the run-time waits cost more than
 // the DMAs saved, so the host picks it by the pattern's interpolation weight.
-template <int D, bool KSKIP, bool VEARLY, Elem E>
+//
+// POS: query rows at positions A.positions[r] (cache_position: a chunked
+// prefill's rows p0 .. p0 + q_len - 1, or any positions).  A group whose rows
+// sit at consecutive positions, all in [0, kv_len), runs as a prefill group
+// from its first row's position (the bands only need consecutive positions,
+// not a multiple of 16); any other group computes its rows one at a time
+// with the per-row gather (gather_one_row_any: float32, the arithmetic of
+// esa_elastic_fwd_rows).  Q, O and the log-sum-exp stay indexed by the row r.
+template <int D, bool KSKIP, bool VEARLY, Elem E, bool POS>
 __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   using C = BandCfg<D>;
   using M = MmaT<E>;
@@ -79,8 +88,38 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
 
   const int lane = threadIdx.x;
   const int n = lane & 15, q = lane >> 4;
-  const int i = gq * 16 + n;  // this lane's query row
-  const bool row_ok = i < A.q_len;
+  const int r = gq * 16 + n;  // this lane's query row (of q, o and lse)
+  const bool row_ok = r < A.q_len;
+  int i = r;  // its position
+  if constexpr (POS) {
+    int64_t p = row_ok ? A.positions[r] : 0;
+    p = p < 0 ? p + A.kv_len : p;
+    const bool in_range = p >= 0 && p < A.kv_len;
+    // row 0 of a group always exists: the group's base position
+    const int base = __builtin_amdgcn_readfirstlane((int)(in_range ? p : 0) - n);
+    if (wave_any(row_ok && !(in_range && (int)p - n == base))) {
+      // positions not consecutive (or out of range): the rows one at a time,
+      // by the per-row gather, with the first K slot as its 384-float scratch
+      // (the gather that holds few registers: this path must not raise the
+      // kernel's register count)
+      GatherArgs G{};
+      G.q = A.q; G.k = A.k; G.v = A.v; G.o = A.o; G.lse = A.lse;
+      G.qsb = A.qsb; G.qsh = A.qsh; G.qss = A.qss;
+      G.ksb = A.ksb; G.ksh = A.ksh; G.kss = A.kss;
+      G.vsb = A.vsb; G.vsh = A.vsh; G.vss = A.vss;
+      G.osb = A.osb; G.osh = A.osh; G.oss = A.oss;
+      G.lsb = A.lsb; G.lsh = A.lsh;
+      G.H = A.H; G.groups = A.groups; G.q_len = A.q_len; G.kv_len = A.kv_len; G.D = D;
+      G.sm_scale = A.sm_scale;
+      G.elem = A.elem;
+      G.src.w = A.pc.w; G.src.kv_len = A.kv_len; G.src.pc = A.pc;
+      G.src.positions = A.positions;
+      for (int rr = 0; rr < 16 && gq * 16 + rr < A.q_len; ++rr)
+        gather_one_row_any<E, true>(G, b, h, gq * 16 + rr, (float*)ks0, lane);
+      return;
+    }
+    i = base + n;
+  }
 
   // ---- slots to zeros once: rows a band does not fill keep finite values
   {
@@ -94,7 +133,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   // ---- Q as the B operand: row n, dims 32 s + 8 q .. + 8 for k-step s
   V8 qop[C::NS];
   {
-    const uint16_t* qrow = A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)i * A.qss;
+    const uint16_t* qrow = A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)r * A.qss;
 #pragma unroll
     for (int s = 0; s < C::NS; ++s) {
       u32x4 raw = {0u, 0u, 0u, 0u};
@@ -459,7 +498,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   // (slice s, reg e: dim CW q + 4 s + e)
   if (row_ok) {
     const float inv = n_run > 0.f ? 1.f / n_run : 0.f;
-    uint16_t* orow = A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)i * A.oss;
+    uint16_t* orow = A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)r * A.oss;
 #pragma unroll
     for (int t = 0; t < C::NV / 2; ++t) {
       V8 ov;
@@ -473,7 +512,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     if (A.lse && q == 0) {
       const float lse = l_run > 0.f ? (m_run + __log2f(l_run)) * 0.69314718055994530942f
                                     : -INFINITY;
-      A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + i] = lse;
+      A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + r] = lse;
     }
     // after a rerun: the dims where the row's own entries bring an Inf or NaN
     // of V take the reference's value (this lane's dims CW q .. CW q + CW)
@@ -492,28 +531,35 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   }
 }
 
-template <int D, Elem E>
+template <int D, Elem E, bool POS>
 void launch_band_d(const BandArgs& a, dim3 grid, bool kskip, bool vearly, hipStream_t stream) {
   if (kskip) {
     if (vearly)
-      band_fwd_kernel<D, true, true, E><<<grid, 64, 0, stream>>>(a);
+      band_fwd_kernel<D, true, true, E, POS><<<grid, 64, 0, stream>>>(a);
     else
-      band_fwd_kernel<D, true, false, E><<<grid, 64, 0, stream>>>(a);
+      band_fwd_kernel<D, true, false, E, POS><<<grid, 64, 0, stream>>>(a);
   } else {
     if (vearly)
-      band_fwd_kernel<D, false, true, E><<<grid, 64, 0, stream>>>(a);
+      band_fwd_kernel<D, false, true, E, POS><<<grid, 64, 0, stream>>>(a);
     else
-      band_fwd_kernel<D, false, false, E><<<grid, 64, 0, stream>>>(a);
+      band_fwd_kernel<D, false, false, E, POS><<<grid, 64, 0, stream>>>(a);
   }
 }
 
 template <Elem E>
 void launch_band_elem(const BandArgs& a, int head_dim, dim3 grid, bool kskip, bool vearly,
                       hipStream_t stream) {
-  if (head_dim == 128)
-    launch_band_d<128, E>(a, grid, kskip, vearly, stream);
-  else
-    launch_band_d<64, E>(a, grid, kskip, vearly, stream);
+  if (a.positions) {
+    if (head_dim == 128)
+      launch_band_d<128, E, true>(a, grid, kskip, vearly, stream);
+    else
+      launch_band_d<64, E, true>(a, grid, kskip, vearly, stream);
+  } else {
+    if (head_dim == 128)
+      launch_band_d<128, E, false>(a, grid, kskip, vearly, stream);
+    else
+      launch_band_d<64, E, false>(a, grid, kskip, vearly, stream);
+  }
 }
 
 hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) {
@@ -530,7 +576,9 @@ hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) 
   // L2 hit rate fell from 0.73 to 0.64 (layer 4) and HBM misses bound the
   // kernel; at the shapes up to L = 32768 (spacings up to 512) they were
   // faster or within 3.5%.
-  const float spacing = ((float)a.q_len * a.pc.a + a.pc.c) / (float)a.pc.w;
+  // (with positions, the last row sits near kv_len)
+  const float last = (float)(a.positions ? a.kv_len : a.q_len);
+  const float spacing = (last * a.pc.a + a.pc.c) / (float)a.pc.w;
   const bool vearly = spacing < 1000.0f;
   if (a.elem == (int)Elem::f16)
     launch_band_elem<Elem::f16>(a, head_dim, grid, kskip, vearly, stream);

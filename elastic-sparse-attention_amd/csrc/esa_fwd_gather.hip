@@ -30,107 +30,14 @@ namespace esa {
 
 namespace {
 
-// dot(q, k_row) over D (D % 4 == 0); q in LDS as float
-template <Elem E>
-__device__ __forceinline__ float row_dot(const float* __restrict__ qs,
-                                         const typename ElemT<E>::T* __restrict__ kr, int D) {
-  float acc = 0.f;
-  if constexpr (E == Elem::f32) {
-    for (int d = 0; d < D; d += 4) {
-      const f32x4 kv = *(const f32x4*)(kr + d);
-      acc += qs[d] * kv[0];
-      acc += qs[d + 1] * kv[1];
-      acc += qs[d + 2] * kv[2];
-      acc += qs[d + 3] * kv[3];
-    }
-  } else {
-    for (int d = 0; d < D; d += 4) {
-      const u32x2 kv = *(const u32x2*)(kr + d);
-      const u32x4 raw = {kv[0], kv[1], 0u, 0u};
-      acc += qs[d] * ElemT<E>::chunk(raw, 0);
-      acc += qs[d + 1] * ElemT<E>::chunk(raw, 1);
-      acc += qs[d + 2] * ElemT<E>::chunk(raw, 2);
-      acc += qs[d + 3] * ElemT<E>::chunk(raw, 3);
-    }
-  }
-  return acc;
-}
-
 template <Elem E, bool PATTERN>
 __global__ __launch_bounds__(256) void gather_fwd_kernel(GatherArgs A) {
-  using T = typename ElemT<E>::T;
-  __shared__ float qs_all[4][256];
-  __shared__ float ps_all[4][64];
-  __shared__ int ks_all[4][64];
+  __shared__ float scratch_all[4][384];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = blockIdx.x * 4 + wave;
   const int h = blockIdx.y, b = blockIdx.z;
   if (r >= A.q_len) return;  // whole wave leaves; no block-level barrier below
-  const int kvh = h / A.groups;
-  const int D = A.D;
-  float* qs = qs_all[wave];
-  float* ps = ps_all[wave];
-  int* ks = ks_all[wave];
-
-  const T* qrow = (const T*)A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)r * A.qss;
-  for (int d = lane; d < D; d += 64) qs[d] = ElemT<E>::load(qrow + d);
-  wave_sync_lds();
-
-  const T* kbase = (const T*)A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh;
-  const T* vbase = (const T*)A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh;
-  RowEntries row;
-  row.init<PATTERN>(A.src, h, r);
-
-  float m = -INFINITY, l = 0.f;
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  const int w = A.src.w;
-  for (int c0 = 0; c0 < w; c0 += 64) {
-    const int j = c0 + lane;
-    bool valid = false;
-    int64_t key = 0;
-    if (j < w) row.entry<PATTERN>(A.src, h, r, j, valid, key);
-    const bool in_range = key >= 0 && key < A.kv_len;
-    float s = -INFINITY;
-    if (valid) s = in_range ? row_dot<E>(qs, kbase + key * A.kss, D) * A.sm_scale : 0.f;
-    const float cmax = wave_max(s);
-    const float m_new = fmaxf(m, cmax);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float p = valid ? expf(s - m_use) : 0.f;
-    const float alpha = expf(m - m_use);
-    l = l * alpha + wave_sum(p);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) acc[e] *= alpha;
-    m = m_new;
-    const float keep = j < w ? drop_factor(A.drop, b, h, r, j, A.H, A.q_len, w) : 0.f;
-    ps[lane] = p * keep;
-    ks[lane] = (valid && in_range) ? (int)key : -1;
-    wave_sync_lds();
-    const int nj = min(64, w - c0);
-    for (int jj = 0; jj < nj; ++jj) {
-      const float pj = ps[jj];
-      const int kj = ks[jj];
-      if (kj >= 0 && pj != 0.f) {
-        const T* vr = vbase + (int64_t)kj * A.vss;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int d = lane + 64 * e;
-          if (d < D) acc[e] += pj * ElemT<E>::load(vr + d);
-        }
-      }
-    }
-    wave_sync_lds();
-  }
-
-  const float inv = row.bad_pos ? __builtin_nanf("") : (l > 0.f ? 1.f / l : 0.f);
-  T* orow = (T*)A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)r * A.oss;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int d = lane + 64 * e;
-    if (d < D) ElemT<E>::store(orow + d, acc[e] * inv);
-  }
-  if (A.lse && lane == 0)
-    A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + r] =
-        row.bad_pos ? __builtin_nanf("") : (l > 0.f ? m + logf(l) : -INFINITY);
+  gather_one_row_any<E, PATTERN>(A, b, h, r, scratch_all[wave], lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -150,13 +57,6 @@ __global__ __launch_bounds__(256) void gather_fwd_kernel(GatherArgs A) {
 // differs).
 template <Elem E, int D, bool PATTERN>
 __global__ __launch_bounds__(256, 2) void gather_rows_kernel(GatherArgs A) {
-  using T = typename ElemT<E>::T;
-  constexpr int EPL = ElemT<E>::kPerChunk;  // elements per lane per load
-  constexpr int LPK = D / EPL;              // lanes per row
-  constexpr int KPI = 64 / LPK;             // rows per load instruction
-  constexpr int SK = 16 * KPI < 64 ? 16 * KPI : 64;  // keys per chunk
-  constexpr int NI = SK / KPI;              // load instructions per chunk
-  static_assert(LPK <= 64 && 64 % LPK == 0 && NI <= 16, "row split");
   __shared__ float sc_all[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t wv = (int64_t)blockIdx.x * 4 + wave;
@@ -164,99 +64,7 @@ __global__ __launch_bounds__(256, 2) void gather_rows_kernel(GatherArgs A) {
   if (wv >= (int64_t)A.B * A.H * A.q_len) return;
   const int r = (int)(wv % A.q_len);
   const int h = (int)((wv / A.q_len) % A.H), b = (int)(wv / ((int64_t)A.q_len * A.H));
-  const int kvh = h / A.groups;
-  float* sc = sc_all[wave];
-  const int gk = lane / LPK;  // row of an instruction this lane loads
-  const int ln = lane % LPK;  // its 16-byte piece: elements EPL ln .. + EPL
-
-  float qv[EPL];
-  {
-    const T* qrow = (const T*)A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)r * A.qss;
-    const u32x4 raw = *(const u32x4*)(qrow + EPL * ln);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) qv[e] = ElemT<E>::chunk(raw, e);
-  }
-  const T* kbase = (const T*)A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh + EPL * ln;
-  const T* vbase = (const T*)A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh + EPL * ln;
-  RowEntries row;
-  row.init<PATTERN>(A.src, h, r);
-
-  auto dot16 = [&](const u32x4& raw) {
-    float acc = 0.f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc += qv[e] * ElemT<E>::chunk(raw, e);
-    return acc;
-  };
-
-  float m = -INFINITY, l = 0.f;
-  float acc[EPL];
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-  const int w = A.src.w;
-  for (int c0 = 0; c0 < w; c0 += SK) {
-    // slot `lane` of the chunk: entry c0 + lane
-    const int j = c0 + lane;
-    bool valid = false;
-    int64_t key = 0;
-    if (lane < SK && j < w) row.entry<PATTERN>(A.src, h, r, j, valid, key);
-    const bool in_range = key >= 0 && key < A.kv_len;
-    const int kaddr = (valid && in_range) ? (int)key : 0;  // a row that exists
-    u32x4 kd[NI], vd[NI];
-#pragma unroll
-    for (int t = 0; t < NI; ++t) {
-      const int kk = __shfl(kaddr, KPI * t + gk, 64);
-      kd[t] = *(const u32x4*)(kbase + (int64_t)kk * A.kss);
-      vd[t] = *(const u32x4*)(vbase + (int64_t)kk * A.vss);
-    }
-#pragma unroll
-    for (int t = 0; t < NI; ++t) {
-      const float part = group_sum<LPK>(dot16(kd[t]));
-      if (ln == 0) sc[KPI * t + gk] = part;
-    }
-    wave_sync_lds();
-    float s = -INFINITY;
-    if (lane < SK && valid) s = in_range ? sc[lane] * A.sm_scale : 0.f;
-    const float cmax = wave_max(s);
-    const float m_new = fmaxf(m, cmax);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float p = valid ? expf(s - m_use) : 0.f;
-    const float alpha = expf(m - m_use);
-    l = l * alpha + wave_sum(p);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] *= alpha;
-    m = m_new;
-    wave_sync_lds();
-    // PV weight of the slot (dropout keep factor applied)
-    if (lane < SK) {
-      const float keep = j < w ? drop_factor(A.drop, b, h, r, j, A.H, A.q_len, w) : 0.f;
-      sc[lane] = (valid && in_range) ? p * keep : 0.f;
-    }
-    wave_sync_lds();
-#pragma unroll
-    for (int t = 0; t < NI; ++t) {
-      const float pt = sc[KPI * t + gk];
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[e] += pt * ElemT<E>::chunk(vd[t], e);
-    }
-    wave_sync_lds();
-  }
-  // the KPI row groups' partial sums: lanes ln, ln + LPK, ...
-#pragma unroll
-  for (int off = LPK; off < 64; off <<= 1)
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] += __shfl_xor(acc[e], off, 64);
-
-  const float inv = row.bad_pos ? __builtin_nanf("") : (l > 0.f ? 1.f / l : 0.f);
-  if (gk == 0) {
-    T* orow = (T*)A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)r * A.oss + EPL * ln;
-    float x[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) x[e] = acc[e] * inv;
-    *(u32x4*)orow = ElemT<E>::pack_chunk(x);
-  }
-  if (A.lse && lane == 0)
-    A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + r] =
-        row.bad_pos ? __builtin_nanf("") : (l > 0.f ? m + logf(l) : -INFINITY);
+  gather_one_row<E, D, PATTERN>(A, b, h, r, sc_all[wave], lane);
 }
 
 // ---------------------------------------------------------------------------

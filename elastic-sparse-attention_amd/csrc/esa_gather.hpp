@@ -102,4 +102,215 @@ __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// One query row (b, h, r) of the per-row gather forward, by one wave (the
+// body of gather_rows_kernel, esa_fwd_gather.hip, which describes it; also
+// the band forward's path for rows whose positions are not consecutive):
+// D = 64, 128 or 256 with 16-byte aligned rows; sc: 64 floats of LDS private
+// to the wave.
+template <Elem E, int D, bool PATTERN>
+__device__ __forceinline__ void gather_one_row(const GatherArgs& A, int b, int h, int r,
+                                               float* sc, int lane) {
+  using T = typename ElemT<E>::T;
+  constexpr int EPL = ElemT<E>::kPerChunk;  // elements per lane per load
+  constexpr int LPK = D / EPL;              // lanes per row
+  constexpr int KPI = 64 / LPK;             // rows per load instruction
+  constexpr int SK = 16 * KPI < 64 ? 16 * KPI : 64;  // keys per chunk
+  constexpr int NI = SK / KPI;              // load instructions per chunk
+  static_assert(LPK <= 64 && 64 % LPK == 0 && NI <= 16, "row split");
+  const int kvh = h / A.groups;
+  const int gk = lane / LPK;  // row of an instruction this lane loads
+  const int ln = lane % LPK;  // its 16-byte piece: elements EPL ln .. + EPL
+
+  float qv[EPL];
+  {
+    const T* qrow = (const T*)A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)r * A.qss;
+    const u32x4 raw = *(const u32x4*)(qrow + EPL * ln);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) qv[e] = ElemT<E>::chunk(raw, e);
+  }
+  const T* kbase = (const T*)A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh + EPL * ln;
+  const T* vbase = (const T*)A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh + EPL * ln;
+  RowEntries row;
+  row.init<PATTERN>(A.src, h, r);
+
+  auto dot16 = [&](const u32x4& raw) {
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc += qv[e] * ElemT<E>::chunk(raw, e);
+    return acc;
+  };
+
+  float m = -INFINITY, l = 0.f;
+  float acc[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+  const int w = A.src.w;
+  for (int c0 = 0; c0 < w; c0 += SK) {
+    // slot `lane` of the chunk: entry c0 + lane
+    const int j = c0 + lane;
+    bool valid = false;
+    int64_t key = 0;
+    if (lane < SK && j < w) row.entry<PATTERN>(A.src, h, r, j, valid, key);
+    const bool in_range = key >= 0 && key < A.kv_len;
+    const int kaddr = (valid && in_range) ? (int)key : 0;  // a row that exists
+    u32x4 kd[NI], vd[NI];
+#pragma unroll
+    for (int t = 0; t < NI; ++t) {
+      const int kk = __shfl(kaddr, KPI * t + gk, 64);
+      kd[t] = *(const u32x4*)(kbase + (int64_t)kk * A.kss);
+      vd[t] = *(const u32x4*)(vbase + (int64_t)kk * A.vss);
+    }
+#pragma unroll
+    for (int t = 0; t < NI; ++t) {
+      const float part = group_sum<LPK>(dot16(kd[t]));
+      if (ln == 0) sc[KPI * t + gk] = part;
+    }
+    wave_sync_lds();
+    float s = -INFINITY;
+    if (lane < SK && valid) s = in_range ? sc[lane] * A.sm_scale : 0.f;
+    const float cmax = wave_max(s);
+    const float m_new = fmaxf(m, cmax);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float p = valid ? expf(s - m_use) : 0.f;
+    const float alpha = expf(m - m_use);
+    l = l * alpha + wave_sum(p);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] *= alpha;
+    m = m_new;
+    wave_sync_lds();
+    // PV weight of the slot (dropout keep factor applied)
+    if (lane < SK) {
+      const float keep = j < w ? drop_factor(A.drop, b, h, r, j, A.H, A.q_len, w) : 0.f;
+      sc[lane] = (valid && in_range) ? p * keep : 0.f;
+    }
+    wave_sync_lds();
+#pragma unroll
+    for (int t = 0; t < NI; ++t) {
+      const float pt = sc[KPI * t + gk];
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] += pt * ElemT<E>::chunk(vd[t], e);
+    }
+    wave_sync_lds();
+  }
+  // the KPI row groups' partial sums: lanes ln, ln + LPK, ...
+#pragma unroll
+  for (int off = LPK; off < 64; off <<= 1)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] += __shfl_xor(acc[e], off, 64);
+
+  const float inv = row.bad_pos ? __builtin_nanf("") : (l > 0.f ? 1.f / l : 0.f);
+  if (gk == 0) {
+    T* orow = (T*)A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)r * A.oss + EPL * ln;
+    float x[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) x[e] = acc[e] * inv;
+    *(u32x4*)orow = ElemT<E>::pack_chunk(x);
+  }
+  if (A.lse && lane == 0)
+    A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + r] =
+        row.bad_pos ? __builtin_nanf("") : (l > 0.f ? m + logf(l) : -INFINITY);
+}
+
+// dot(q, k_row) over D (D % 4 == 0); q in LDS as float
+template <Elem E>
+__device__ __forceinline__ float row_dot(const float* __restrict__ qs,
+                                         const typename ElemT<E>::T* __restrict__ kr, int D) {
+  float acc = 0.f;
+  if constexpr (E == Elem::f32) {
+    for (int d = 0; d < D; d += 4) {
+      const f32x4 kv = *(const f32x4*)(kr + d);
+      acc += qs[d] * kv[0];
+      acc += qs[d + 1] * kv[1];
+      acc += qs[d + 2] * kv[2];
+      acc += qs[d + 3] * kv[3];
+    }
+  } else {
+    for (int d = 0; d < D; d += 4) {
+      const u32x2 kv = *(const u32x2*)(kr + d);
+      const u32x4 raw = {kv[0], kv[1], 0u, 0u};
+      acc += qs[d] * ElemT<E>::chunk(raw, 0);
+      acc += qs[d + 1] * ElemT<E>::chunk(raw, 1);
+      acc += qs[d + 2] * ElemT<E>::chunk(raw, 2);
+      acc += qs[d + 3] * ElemT<E>::chunk(raw, 3);
+    }
+  }
+  return acc;
+}
+
+// One query row (b, h, r) of the per-row gather forward for any head_dim (a
+// multiple of 4, up to 256), by one wave (the body of gather_fwd_kernel,
+// esa_fwd_gather.hip, which describes it; also the band forward's path for
+// rows whose positions are not consecutive): scratch is 384 floats of LDS
+// private to the wave (q, the chunk's probabilities and keys).
+template <Elem E, bool PATTERN>
+__device__ __forceinline__ void gather_one_row_any(const GatherArgs& A, int b, int h, int r,
+                                                   float* scratch, int lane) {
+  using T = typename ElemT<E>::T;
+  const int kvh = h / A.groups;
+  const int D = A.D;
+  float* qs = scratch;                // D <= 256 floats
+  float* ps = scratch + 256;          // 64
+  int* ks = (int*)(scratch + 320);    // 64
+
+  const T* qrow = (const T*)A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)r * A.qss;
+  for (int d = lane; d < D; d += 64) qs[d] = ElemT<E>::load(qrow + d);
+  wave_sync_lds();
+
+  const T* kbase = (const T*)A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh;
+  const T* vbase = (const T*)A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh;
+  RowEntries row;
+  row.init<PATTERN>(A.src, h, r);
+
+  float m = -INFINITY, l = 0.f;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const int w = A.src.w;
+  for (int c0 = 0; c0 < w; c0 += 64) {
+    const int j = c0 + lane;
+    bool valid = false;
+    int64_t key = 0;
+    if (j < w) row.entry<PATTERN>(A.src, h, r, j, valid, key);
+    const bool in_range = key >= 0 && key < A.kv_len;
+    float s = -INFINITY;
+    if (valid) s = in_range ? row_dot<E>(qs, kbase + key * A.kss, D) * A.sm_scale : 0.f;
+    const float cmax = wave_max(s);
+    const float m_new = fmaxf(m, cmax);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float p = valid ? expf(s - m_use) : 0.f;
+    const float alpha = expf(m - m_use);
+    l = l * alpha + wave_sum(p);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] *= alpha;
+    m = m_new;
+    const float keep = j < w ? drop_factor(A.drop, b, h, r, j, A.H, A.q_len, w) : 0.f;
+    ps[lane] = p * keep;
+    ks[lane] = (valid && in_range) ? (int)key : -1;
+    wave_sync_lds();
+    const int nj = min(64, w - c0);
+    for (int jj = 0; jj < nj; ++jj) {
+      const float pj = ps[jj];
+      const int kj = ks[jj];
+      if (kj >= 0 && pj != 0.f) {
+        const T* vr = vbase + (int64_t)kj * A.vss;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int d = lane + 64 * e;
+          if (d < D) acc[e] += pj * ElemT<E>::load(vr + d);
+        }
+      }
+    }
+    wave_sync_lds();
+  }
+
+  const float inv = row.bad_pos ? __builtin_nanf("") : (l > 0.f ? 1.f / l : 0.f);
+  T* orow = (T*)A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)r * A.oss;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int d = lane + 64 * e;
+    if (d < D) ElemT<E>::store(orow + d, acc[e] * inv);
+  }
+  if (A.lse && lane == 0)
+    A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + r] =
+        row.bad_pos ? __builtin_nanf("") : (l > 0.f ? m + logf(l) : -INFINITY);
+}
+
 }  // namespace esa

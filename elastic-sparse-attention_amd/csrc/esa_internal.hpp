@@ -59,6 +59,11 @@ struct BandArgs {
   float scale_log2;  // sm_scale * log2(e)
   PatternConsts pc;
   int elem;      // Elem of q, k, v, o: bf16 or f16
+  // query positions (cache_position): row r is position positions[r] (a
+  // negative one counting from kv_len), or r when NULL
+  const int64_t* positions;
+  int kv_len;
+  float sm_scale;
 };
 
 // Where a query row's w entries come from: the elastic pattern (regenerated

@@ -463,6 +463,12 @@ BWD_DQ_CROSSOVER = {128: 16.5, 64: 13.0}
 BWD_DKDV_CROSSOVER = {128: 16.5, 64: 17.0}
 
 
+# cache_position calls with at least this many query rows (a chunked
+# prefill) run the band kernel at their positions; fewer (decode) the per-row
+# gather kernel
+BAND_POSITION_MIN_ROWS = 32
+
+
 def _band_beats_tile(layout: ElasticLayout, q_len: int, batch: int, head_dim: int,
                      crossover: Dict[int, float]) -> bool:
     p = layout.pattern
@@ -569,23 +575,28 @@ def _prefill_fwd(q, k, v, layout, scaling, return_lse, out, key_block, query_blo
 
 def elastic_attention_band(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                            pattern: EsaPattern, scaling: float, return_lse: bool = True,
-                           out: Optional[torch.Tensor] = None
+                           out: Optional[torch.Tensor] = None,
+                           positions: Optional[torch.Tensor] = None
                            ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
-    """Band-gathered MFMA forward (prefill: query row r is position r), no
-    layout needed: each wave takes 16 query rows and, for every entry j of
-    their index lists, gathers the at most 16 consecutive keys those rows use
-    at entry j.  Returns ``o`` ``[B, Lq, H, D]`` and, if asked, ``lse``
-    float32 ``[B, H, Lq]``, as :func:`elastic_attention_fwd`."""
+    """Band-gathered MFMA forward, no layout needed: each wave takes 16 query
+    rows and, for every entry j of their index lists, gathers the at most 16
+    consecutive keys those rows use at entry j.  Query row r is position r,
+    or ``positions[r]`` (int64 on the device, as cache_position: a chunked
+    prefill's consecutive positions run as prefill groups, any other 16-row
+    group through the per-row gather).  Returns ``o`` ``[B, Lq, H, D]`` and,
+    if asked, ``lse`` float32 ``[B, H, Lq]``, as
+    :func:`elastic_attention_fwd`."""
     _check_qkv(q, k, v)
     B, H, Lq, D = q.shape
     q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
     o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
+    positions, pos_ptr = _positions_ptr(positions, Lq, q.device)
     if B == 0 or Lq == 0:
         return o, lse
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
-    check(load().esa_elastic_fwd_band(ctypes.byref(a), ctypes.byref(pattern), _stream(q.device)),
-          "esa_elastic_fwd_band")
+    check(load().esa_elastic_fwd_band(ctypes.byref(a), ctypes.byref(pattern), pos_ptr,
+                                      _stream(q.device)), "esa_elastic_fwd_band")
     return o, lse
 
 
@@ -896,6 +907,27 @@ class _ElasticTileAttention(torch.autograd.Function):
         return dq, dk, dv, None, None, None
 
 
+class _ElasticBandRowsAttention(torch.autograd.Function):
+    """The band forward at cache_position rows (chunked prefill) with the
+    gather backward at the same positions:
+    ``apply(q, k, v, pattern, scaling, positions) -> o [B, Lq, H, D]``."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, pattern, scaling, positions):
+        o, lse = elastic_attention_band(q, k, v, pattern, scaling, return_lse=True,
+                                        positions=positions)
+        ctx.save_for_backward(q, k, v, o, lse, positions)
+        ctx.pattern, ctx.scaling = pattern, scaling
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, lse, positions = ctx.saved_tensors
+        dq, dk, dv = elastic_attention_bwd_rows(q, k, v, o, lse, do, ctx.pattern, ctx.scaling,
+                                                positions)
+        return dq, dk, dv, None, None, None
+
+
 class ElasticSparseAttentionFunction(torch.autograd.Function):
     """The reference's operator (:235-339): ``apply(q, k, v, sparse_indices,
     sparse_mask, sm_scale, num_kv_groups) -> o [B, H, Lq, D]``, with its
@@ -1148,6 +1180,16 @@ class ElasticSparseAttention(nn.Module):
                 return o.reshape(B, Lq, H * D), None
             o, _ = _prefill_fwd(q, k, v, self.layout(q.device), self.scaling, False, None, None,
                                 None, self.prefill_kernel, True)
+            return o.view(B, Lq, H * D), None                              # :761-763
+        if pos is not None and not naive and dropout_p == 0.0 and q.dtype in MFMA_DTYPES \
+                and D in (64, 128) and Lq >= BAND_POSITION_MIN_ROWS \
+                and self.attention_length <= 64 and kv_len < (1 << 24):
+            # a chunked prefill: the band kernel at the given positions
+            if grad:
+                o = _ElasticBandRowsAttention.apply(q, k, v, self.pattern, self.scaling, pos)
+                return o.reshape(B, Lq, H * D), None
+            o, _ = elastic_attention_band(q, k, v, self.pattern, self.scaling, return_lse=False,
+                                          positions=pos)
             return o.view(B, Lq, H * D), None                              # :761-763
         # per-row gather: decode rows, float32 / float16, other head dims, the
         # naive path; keep decisions of dropout drawn from torch's generator

@@ -148,7 +148,7 @@ def load() -> ctypes.CDLL:
     lib.esa_build_stage_masks.restype = st
     lib.esa_build_stage_masks.argtypes = [P(EsaPattern), vp, vp, vp, vp, ctypes.c_int64, vp]
     lib.esa_elastic_fwd_band.restype = st
-    lib.esa_elastic_fwd_band.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp]
+    lib.esa_elastic_fwd_band.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp, vp]
     lib.esa_elastic_fwd_rows.restype = st
     lib.esa_elastic_fwd_rows.argtypes = [P(EsaFwdArgs), P(EsaPattern), vp, vp]
     lib.esa_sparse_fwd.restype = st

@@ -209,11 +209,18 @@ esa_status esa_build_stage_masks(const esa_pattern* p, const int32_t* row_ptr,
                                  const int32_t* col_idx, const int32_t* row_ptr_host,
                                  uint32_t* masks, int64_t capacity_words, void* stream);
 
-/* Band-gathered forward over the elastic pattern, prefill rows 0 .. q_len-1
- * (no layout needed).  Replaces the forward branch of the Triton kernel
- * (elastic_sparse_attention.py:117-166) as _triton_forward launches it for
- * prefill (:592-622), with each row's index list regenerated on the device
- * (bit-exact with :470-535).  Entry j of the rows' index lists (a band)
+/* Band-gathered forward over the elastic pattern, prefill rows 0 .. q_len-1,
+ * or the rows at positions[r] (int64 device array, as cache_position,
+ * :602-608; NULL = rows 0 .. q_len-1) (no layout needed).  Replaces the
+ * forward branch of the Triton kernel (elastic_sparse_attention.py:117-166)
+ * as _triton_forward launches it for prefill and chunked prefill (:592-622),
+ * with each row's index list regenerated on the device (bit-exact with
+ * :470-535).  With positions, each group of 16 rows whose positions are
+ * consecutive and in [0, kv_len) (negative ones counting from kv_len) runs
+ * as below from its first row's position; any other group computes its rows
+ * one at a time with esa_elastic_fwd_rows' arithmetic (float32), a row whose
+ * position lies outside [-kv_len, kv_len) getting NaN; q_len and kv_len are
+ * then not compared.  Entry j of the rows' index lists (a band)
  * moves by at most one key per row (two at a few rows of some heads), so 16
  * consecutive rows mostly use at most 16 consecutive keys of each band
  * (wider bands are handled, more slowly):
@@ -224,7 +231,8 @@ esa_status esa_build_stage_masks(const esa_pattern* p, const int32_t* row_ptr,
  * (kv_len + 16) * K/V row stride * 2 < 2^31, row strides >= head_dim,
  * q_len <= kv_len, q_len <= p->seq_len, finite sm_scale > 0, 16-byte
  * aligned q, k, v, o and strides (elements) that are multiples of 8. */
-esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p, void* stream);
+esa_status esa_elastic_fwd_band(const esa_fwd_args* a, const esa_pattern* p,
+                                const int64_t* positions, void* stream);
 
 /* Per-row gather forward over the elastic pattern for arbitrary query
  * positions: row r of q is position positions[r] (int64 device array, as

@@ -164,7 +164,7 @@ def test_forward_entry_points_reject_bad_arguments():
             a = fwd_args()
             setattr(a, f"{t}_stride_s", big)
             assert call(a) == en.ESA_ERR_UNSUPPORTED, (t, big)
-            assert lib.esa_elastic_fwd_band(ctypes.byref(a), ctypes.byref(p), None) \
+            assert lib.esa_elastic_fwd_band(ctypes.byref(a), ctypes.byref(p), None, None) \
                 == en.ESA_ERR_UNSUPPORTED, (t, big)
     assert call(fwd_args(), pp=pat(L=1024, H=4, bm=64)) == en.ESA_ERR_UNSUPPORTED
     for bad_scale in (0.0, -0.1, float("inf"), float("nan")):
