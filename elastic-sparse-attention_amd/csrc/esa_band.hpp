@@ -28,16 +28,20 @@ struct BandCfg {
 };
 
 // physical 16-byte chunk of logical chunk lc in row r of a V slot: the 16
-// lanes of a transposed read hit 16 distinct bank groups
+// lanes of a transposed read hit 16 distinct bank groups (at D = 256 a
+// 16-lane group reads chunks 8 k + c, k = 0..3, of 4 rows: chunks 16 apart
+// share a bank group, so bit 4 of the chunk also moves it; every form is its
+// own inverse, as the DMA offsets need)
 template <int D>
 __device__ __forceinline__ int vswz(int r, int lc) {
-  return D == 128 ? lc ^ (r & 3) : lc ^ ((r >> 1) & 1);
+  return D == 256 ? lc ^ (r & 3) ^ ((lc >> 4) << 2)
+                  : (D == 128 ? lc ^ (r & 3) : lc ^ ((r >> 1) & 1));
 }
 // the same for a K slot: 16 lanes reading one chunk of rows 0..15 hit 16
 // distinct bank groups
 template <int D>
 __device__ __forceinline__ int kswz(int r, int lc) {
-  return D == 128 ? lc ^ (r & 15) : lc ^ ((r >> 1) & 7);
+  return D >= 128 ? lc ^ (r & 15) : lc ^ ((r >> 1) & 7);
 }
 
 __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {

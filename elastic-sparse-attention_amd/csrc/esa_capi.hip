@@ -482,7 +482,9 @@ esa_status band_args_of(const esa_fwd_args* a, const esa_pattern* p, const int64
   s = check_pattern(p);
   if (s != ESA_OK) return s;
   if (a->dtype != ESA_BF16 && a->dtype != ESA_F16) return ESA_ERR_DTYPE;
-  if (a->head_dim != 64 && a->head_dim != 128) return ESA_ERR_UNSUPPORTED;
+  // kernels at D = 64, 128 and 256; a head_dim between them (a multiple of
+  // 8: whole 16-byte chunks) runs the next one up with zero padding
+  if (a->head_dim < 8 || a->head_dim > 256 || a->head_dim % 8 != 0) return ESA_ERR_UNSUPPORTED;
   // one wave holds a row's band descriptors for at most 64 bands; indices
   // rise with the band (0 <= alpha <= 1)
   if (p->attention_length > 64) return ESA_ERR_UNSUPPORTED;
@@ -531,6 +533,7 @@ esa_status band_args_of(const esa_fwd_args* a, const esa_pattern* p, const int64
   t.positions = positions;
   t.kv_len = a->kv_len;
   t.sm_scale = a->sm_scale;
+  t.d_real = a->head_dim;
   return ESA_OK;
 }
 

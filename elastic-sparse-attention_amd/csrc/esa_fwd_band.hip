@@ -137,7 +137,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
 #pragma unroll
     for (int s = 0; s < C::NS; ++s) {
       u32x4 raw = {0u, 0u, 0u, 0u};
-      if (row_ok) raw = *(const u32x4*)(qrow + 32 * s + 8 * q);
+      if (row_ok && 32 * s + 8 * q < A.d_real) raw = *(const u32x4*)(qrow + 32 * s + 8 * q);
       qop[s] = __builtin_bit_cast(V8, raw);
     }
   }
@@ -172,12 +172,15 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
 
   // DMA t, lane l fills slot row R = (64 t + l) / CPR, physical chunk
   // l % CPR: its byte offset from the band's first row, fixed per lane
+  // (a chunk past the inputs' head_dim gets an offset past every buffer's
+  // num_records: it loads zeros)
   int kofs[C::VLOADS], vofs[C::VLOADS];
 #pragma unroll
   for (int t = 0; t < C::VLOADS; ++t) {
     const int R = (64 * t + lane) / C::CPR, pc = lane % C::CPR;
-    kofs[t] = R * kss2 + 16 * kswz<D>(R, pc);
-    vofs[t] = R * vss2 + 16 * vswz<D>(R, pc);
+    const int kc = kswz<D>(R, pc), vc = vswz<D>(R, pc);
+    kofs[t] = 8 * kc < A.d_real ? R * kss2 + 16 * kc : 0x7ffffff0;
+    vofs[t] = 8 * vc < A.d_real ? R * vss2 + 16 * vc : 0x7ffffff0;
   }
   // K or V rows of band info word `bi` -> slot dst, through a buffer resource
   // that starts at the band's first row and holds its W rows: rows past the
@@ -206,7 +209,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   };
   auto load_k = [&](int bi, lds_u16* dst) { load_rows(kbase, kss2, kofs, bi, dst, !KSKIP); };
   auto load_v = [&](int bi, lds_u16* dst) { load_rows(vbase, vss2, vofs, bi, dst, true); };
-  // s_waitcnt vmcnt(n) for a count known only at run time (0 .. 8)
+  // s_waitcnt vmcnt(n) for a count known only at run time (0 .. 16)
   auto wait_vm = [&](int n) {
     switch (n) {
       case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
@@ -217,10 +220,18 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
       case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
       case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
       case 7: __builtin_amdgcn_s_waitcnt(0x0F77); break;
-      default: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+      case 8: __builtin_amdgcn_s_waitcnt(0x0F78); break;
+      case 9: __builtin_amdgcn_s_waitcnt(0x0F79); break;
+      case 10: __builtin_amdgcn_s_waitcnt(0x0F7A); break;
+      case 11: __builtin_amdgcn_s_waitcnt(0x0F7B); break;
+      case 12: __builtin_amdgcn_s_waitcnt(0x0F7C); break;
+      case 13: __builtin_amdgcn_s_waitcnt(0x0F7D); break;
+      case 14: __builtin_amdgcn_s_waitcnt(0x0F7E); break;
+      case 15: __builtin_amdgcn_s_waitcnt(0x0F7F); break;
+      default: __builtin_amdgcn_s_waitcnt(0x4F70); break;  // vmcnt(16)
     }
   };
-  static_assert(2 * C::VLOADS <= 8, "wait_vm covers at most 8 DMAs in flight");
+  static_assert(2 * C::VLOADS <= 16, "wait_vm covers at most 16 DMAs in flight");
 
   // K operand read addresses (bytes within a slot) for k-step s: lane
   // (m = n, q) reads key row n, dims 32 s + 8 q .. + 8
@@ -343,6 +354,30 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     }
   };
 
+  // O^T += V^T P^T reading each 16-dim slice's V^T operands next to its MFMA
+  // (D = 256: all slices of both bands at once would hold 64 VGPRs)
+  auto pv_sliced = [&](auto san, const uint16_t* va, const uint16_t* vb, uint64_t pa,
+                       uint64_t pb) {
+    const u32x4 pq = {(uint32_t)pa, (uint32_t)(pa >> 32), (uint32_t)pb, (uint32_t)(pb >> 32)};
+    const V8 pop = __builtin_bit_cast(V8, pq);
+#pragma unroll
+    for (int s = 0; s < C::NV; ++s) {
+      s16x4 vv[2] = {
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((const char*)va + vrd[s])),
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((const char*)vb + vrd[s]))};
+      if constexpr (decltype(san)::value) {
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          u32x2 w = __builtin_bit_cast(u32x2, vv[h2]);
+          w[0] = sanitize2<E>(w[0]);
+          w[1] = sanitize2<E>(w[1]);
+          vv[h2] = __builtin_bit_cast(s16x4, w);
+        }
+      }
+      oacc[s] = M::mfma16(__builtin_bit_cast(V8, vv), pop, oacc[s]);
+    }
+  };
+
   // ---- the bands: the main loop over band pairs, then the tail.  san: the
   // rerun with sanitised V operands (see below).
   auto run_bands = [&](auto san) {
@@ -384,6 +419,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
         const int n_nxt = KSKIP ? n_loads(na) + n_loads(nb) : 2 * C::VLOADS;  // next K DMAs
         V8 kopa[C::NS], kopb[C::NS];
         s16x4 ta[C::NV], tb[C::NV];
+        f32x4 sa, sb;
         if constexpr (VEARLY) {
           __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this pair's K and V are in LDS
           if (live) {
@@ -400,7 +436,14 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
           __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's K is in LDS
           if (live) {
             read_k(ks0, kopa);
-            read_k(ks1, kopb);
+            if constexpr (D == 256) {
+              // (one band's K operands at a time: both would hold 64 VGPRs)
+              sa = scores(kopa);
+              read_k(ks1, kopa);
+              sb = scores(kopa);
+            } else {
+              read_k(ks1, kopb);
+            }
           }
           __builtin_amdgcn_s_waitcnt(kWaitLds);  // K slots read: refill them
           load_k(na, lk0);
@@ -413,8 +456,10 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
               (uint32_t)__builtin_amdgcn_ds_bpermute(lane_key + 64 * qj, (int)kd[rp >> 1]);
           const int da = (int)((dw >> (16 * (rp & 1))) & 0xFFu);
           const int db = (int)((dw >> (16 * (rp & 1) + 8)) & 0xFFu);
-          const f32x4 sa = scores(kopa);
-          const f32x4 sb = scores(kopb);
+          if constexpr (VEARLY || D != 256) {
+            sa = scores(kopa);
+            sb = scores(kopb);
+          }
           bool ha, hb;
           int ea, eb;
           const float xa = pick(sa, da, ha, ea);
@@ -427,9 +472,12 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
               wait_vm(n_nxt);
             else
               __builtin_amdgcn_s_waitcnt(kWaitPair);
-            read_vt(san, vs0, vs1, ta, tb);
+            if constexpr (D != 256) read_vt(san, vs0, vs1, ta, tb);
           }
-          pv(ta, tb, pa, pbw);
+          if constexpr (!VEARLY && D == 256)
+            pv_sliced(san, vs0, vs1, pa, pbw);
+          else
+            pv(ta, tb, pa, pbw);
         }
         if constexpr (!VEARLY) {
           // this pair's V has landed (and been read): refill the V slots
@@ -470,10 +518,14 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
         const float xt = pick(st, d == 0xFF ? -1 : d - (c0 - lo), ht, et);
         uint64_t pt, pz;
         pair_softmax(xt, ht, et, -INFINITY, false, 0, pt, pz);
-        // the second band of the pair contributes p = 0 (vs1 holds finite rows)
-        s16x4 ta[C::NV], tb[C::NV];
-        read_vt(san, vs0, vs1, ta, tb);
-        pv(ta, tb, pt, 0ull);
+        // the second band of the pair contributes p = 0
+        if constexpr (D == 256) {
+          pv_sliced(san, vs0, vs1, pt, 0ull);
+        } else {
+          s16x4 ta[C::NV], tb[C::NV];
+          read_vt(san, vs0, vs1, ta, tb);
+          pv(ta, tb, pt, 0ull);
+        }
       }
     }
   };
@@ -507,7 +559,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
         ov[e] = (typename M::s)(oacc[2 * t][e] * inv);
         ov[4 + e] = (typename M::s)(oacc[2 * t + 1][e] * inv);
       }
-      *(V8*)(orow + C::CW * q + 8 * t) = ov;
+      if (C::CW * q + 8 * t < A.d_real) *(V8*)(orow + C::CW * q + 8 * t) = ov;
     }
     if (A.lse && q == 0) {
       const float lse = l_run > 0.f ? (m_run + __log2f(l_run)) * 0.69314718055994530942f
@@ -546,16 +598,31 @@ void launch_band_d(const BandArgs& a, dim3 grid, bool kskip, bool vearly, hipStr
   }
 }
 
+// D = 256 runs only the late V order: the early one holds both bands' K and
+// V^T operands at once (128 VGPRs at D = 256, about 264 in all)
+template <Elem E, bool POS>
+void launch_band_d256(const BandArgs& a, dim3 grid, bool kskip, hipStream_t stream) {
+  if (kskip)
+    band_fwd_kernel<256, true, false, E, POS><<<grid, 64, 0, stream>>>(a);
+  else
+    band_fwd_kernel<256, false, false, E, POS><<<grid, 64, 0, stream>>>(a);
+}
+
+// the kernel's D: the head_dim, or the next of 64, 128, 256 above it
 template <Elem E>
 void launch_band_elem(const BandArgs& a, int head_dim, dim3 grid, bool kskip, bool vearly,
                       hipStream_t stream) {
   if (a.positions) {
-    if (head_dim == 128)
+    if (head_dim > 128)
+      launch_band_d256<E, true>(a, grid, kskip, stream);
+    else if (head_dim > 64)
       launch_band_d<128, E, true>(a, grid, kskip, vearly, stream);
     else
       launch_band_d<64, E, true>(a, grid, kskip, vearly, stream);
   } else {
-    if (head_dim == 128)
+    if (head_dim > 128)
+      launch_band_d256<E, false>(a, grid, kskip, stream);
+    else if (head_dim > 64)
       launch_band_d<128, E, false>(a, grid, kskip, vearly, stream);
     else
       launch_band_d<64, E, false>(a, grid, kskip, vearly, stream);

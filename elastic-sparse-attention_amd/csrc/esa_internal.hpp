@@ -64,6 +64,9 @@ struct BandArgs {
   const int64_t* positions;
   int kv_len;
   float sm_scale;
+  // the inputs' head_dim (a multiple of 8) when it is below the kernel's D:
+  // dims d_real .. D - 1 of Q, K and V read as zeros and O's are not stored
+  int d_real;
 };
 
 // Where a query row's w entries come from: the elastic pattern (regenerated

@@ -19,8 +19,12 @@ hand-written gfx950 HIP kernels:
   band-gathered MFMA kernel (each row's index-list entries as 16-key bands)
   or the block-sparse MFMA kernel over the block layout (CSR of active
   128x128 tiles, built once per device by the HIP layout builder),
-  whichever is faster for the shape (``prefill_kernel``);
-* decode (``cache_position`` given), float32, or other head dims: the
+  whichever is faster for the shape (``prefill_kernel``); other head dims
+  that are multiples of 8 up to 256: the band kernel (at D = 256, or padded
+  to 64, 128 or 256);
+* chunked prefill (``cache_position`` of at least 32 rows), bf16 or fp16:
+  the band kernel at those positions;
+* decode (fewer ``cache_position`` rows), float32, or other head dims: the
   per-row gather kernel that regenerates each row's elastic indices on the
   device.
 
@@ -44,9 +48,9 @@ Differences from the reference, all deliberate:
 * Every path backpropagates, deterministically (no atomics on the
   gradients): bf16 or fp16 prefill with head_dim 64 or 128 through
   hand-written MFMA kernels (band-gathered or block-sparse like the
-  forward); the others (decode rows, float32, other head dims, dropout,
-  explicit index lists) through the gather backward (row pass, stable key
-  sort, key-major pass).
+  forward); the others (decode and chunked-prefill rows, float32, other
+  head dims, dropout, explicit index lists) through the gather backward (row
+  pass, stable key sort, key-major pass).
 * A query row with no valid entry (impossible for the elastic pattern, only
   reachable through explicit masks) gives output 0 rather than NaN.
 * A cache_position on the device is not range-checked on the host (that
@@ -469,6 +473,13 @@ BWD_DKDV_CROSSOVER = {128: 16.5, 64: 17.0}
 BAND_POSITION_MIN_ROWS = 32
 
 
+def band_head_dim(head_dim: int) -> bool:
+    """Head dims the band forward runs on MFMA: 64, 128 and 256, and any
+    other multiple of 8 up to 256 through the next of them with zero
+    padding (the tile kernels and the MFMA backward take 64 and 128)."""
+    return 8 <= head_dim <= 256 and head_dim % 8 == 0
+
+
 def _band_beats_tile(layout: ElasticLayout, q_len: int, batch: int, head_dim: int,
                      crossover: Dict[int, float]) -> bool:
     p = layout.pattern
@@ -481,7 +492,12 @@ def _band_beats_tile(layout: ElasticLayout, q_len: int, batch: int, head_dim: in
 
 def prefill_kernel(layout: ElasticLayout, q_len: int, batch: int, head_dim: int) -> str:
     """"band" or "tile": the faster prefill kernel for this pattern and shape
-    (the band kernel needs attention_length <= 64 and kv_len < 2^24)."""
+    (the band kernel needs attention_length <= 64 and kv_len < 2^24; at head
+    dims other than 64 and 128 only the band kernel runs)."""
+    p = layout.pattern
+    if head_dim not in BAND_CROSSOVER and band_head_dim(head_dim) and \
+            p.attention_length <= 64 and p.seq_len < (1 << 24):
+        return "band"
     return "band" if _band_beats_tile(layout, q_len, batch, head_dim, BAND_CROSSOVER) else "tile"
 
 
@@ -908,8 +924,9 @@ class _ElasticTileAttention(torch.autograd.Function):
 
 
 class _ElasticBandRowsAttention(torch.autograd.Function):
-    """The band forward at cache_position rows (chunked prefill) with the
-    gather backward at the same positions:
+    """The band forward at cache_position rows (chunked prefill; positions
+    None: rows 0 .. Lq - 1), or at a head_dim the MFMA backward does not
+    take, with the gather backward at the same positions:
     ``apply(q, k, v, pattern, scaling, positions) -> o [B, Lq, H, D]``."""
 
     @staticmethod
@@ -1172,6 +1189,17 @@ class ElasticSparseAttention(nn.Module):
         naive = self.implementation == "naive"
         dropout_p = (float(self.attention_dropout)
                      if self.training and self.implementation != "triton" else 0.0)
+        band_ok = (q.dtype in MFMA_DTYPES and band_head_dim(D) and self.attention_length <= 64
+                   and kv_len < (1 << 24))
+        if pos is None and not naive and dropout_p == 0.0 and q.dtype in MFMA_DTYPES \
+                and D not in (64, 128) and band_ok:
+            # other head dims: the band forward on MFMA (zero padding up to 64,
+            # 128 or 256), the gather backward
+            if grad:
+                o = _ElasticBandRowsAttention.apply(q, k, v, self.pattern, self.scaling, None)
+                return o.reshape(B, Lq, H * D), None
+            o, _ = elastic_attention_band(q, k, v, self.pattern, self.scaling, return_lse=False)
+            return o.view(B, Lq, H * D), None                              # :761-763
         if pos is None and not naive and dropout_p == 0.0 and q.dtype in MFMA_DTYPES \
                 and D in (64, 128):
             if grad:
@@ -1181,9 +1209,8 @@ class ElasticSparseAttention(nn.Module):
             o, _ = _prefill_fwd(q, k, v, self.layout(q.device), self.scaling, False, None, None,
                                 None, self.prefill_kernel, True)
             return o.view(B, Lq, H * D), None                              # :761-763
-        if pos is not None and not naive and dropout_p == 0.0 and q.dtype in MFMA_DTYPES \
-                and D in (64, 128) and Lq >= BAND_POSITION_MIN_ROWS \
-                and self.attention_length <= 64 and kv_len < (1 << 24):
+        if pos is not None and not naive and dropout_p == 0.0 and band_ok \
+                and Lq >= BAND_POSITION_MIN_ROWS:
             # a chunked prefill: the band kernel at the given positions
             if grad:
                 o = _ElasticBandRowsAttention.apply(q, k, v, self.pattern, self.scaling, pos)

@@ -227,7 +227,9 @@ esa_status esa_build_stage_masks(const esa_pattern* p, const int32_t* row_ptr,
  * one wave gathers each band's keys once for its 16 rows and runs QK^T and
  * PV on bf16 MFMA with float32 accumulation and online softmax.  Same
  * outputs as esa_elastic_fwd within bf16 rounding.  Requires dtype
- * ESA_BF16 or ESA_F16, head_dim 64 or 128, attention_length <= 64, kv_len < 2^24,
+ * ESA_BF16 or ESA_F16, head_dim a multiple of 8 up to 256 (kernels at 64,
+ * 128 and 256; other head dims run the next of them with zero padding),
+ * attention_length <= 64, kv_len < 2^24,
  * (kv_len + 16) * K/V row stride * 2 < 2^31, row strides >= head_dim,
  * q_len <= kv_len, q_len <= p->seq_len, finite sm_scale > 0, 16-byte
  * aligned q, k, v, o and strides (elements) that are multiples of 8. */

@@ -167,6 +167,10 @@ def test_forward_entry_points_reject_bad_arguments():
             assert lib.esa_elastic_fwd_band(ctypes.byref(a), ctypes.byref(p), None, None) \
                 == en.ESA_ERR_UNSUPPORTED, (t, big)
     assert call(fwd_args(), pp=pat(L=1024, H=4, bm=64)) == en.ESA_ERR_UNSUPPORTED
+    # the band forward takes head dims that are multiples of 8 up to 256
+    for bad_d in (100, 264, 4):
+        assert lib.esa_elastic_fwd_band(ctypes.byref(fwd_args(D=bad_d)), ctypes.byref(p), None,
+                                        None) in (en.ESA_ERR_UNSUPPORTED, en.ESA_ERR_SHAPE), bad_d
     for bad_scale in (0.0, -0.1, float("inf"), float("nan")):
         a = fwd_args()
         a.sm_scale = bad_scale

@@ -349,9 +349,11 @@ def test_band_rejects_unsupported():
         elastic_attention_band(q, q, q, make_pattern(64, 65, 3, 8, 2), 0.1)  # w > 64
     with pytest.raises(ValueError):
         elastic_attention_band(q.float(), q.float(), q.float(), make_pattern(64, 64, 3, 8, 2), 0.1)
-    qd = torch.zeros(1, 2, 64, 96, dtype=torch.bfloat16, device=DEV)
-    with pytest.raises(RuntimeError):
-        elastic_attention_band(qd, qd, qd, make_pattern(64, 64, 3, 8, 2), 0.1)
+    # head dims: multiples of 8 up to 256 (others padded up to 64, 128, 256)
+    for bad_d in (100, 264):
+        qd = torch.zeros(1, 2, 64, bad_d, dtype=torch.bfloat16, device=DEV)
+        with pytest.raises(RuntimeError):
+            elastic_attention_band(qd, qd, qd, make_pattern(64, 64, 3, 8, 2), 0.1)
 
 
 @pytest.mark.parametrize("layer", [4, 7])
