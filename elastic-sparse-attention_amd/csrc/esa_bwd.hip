@@ -393,6 +393,14 @@ __global__ __launch_bounds__(512, D == 64 ? 4 : 1) void dkdv_kernel(BwdArgs A, c
   exchange(dvacc);
   exchange(dkacc);
 
+  // the non-finite flags of this wave's two 16-key blocks (bwd_fix_kernel
+  // recomputes flagged blocks)
+  if (qh == 0) {
+    const bool bad = wave_any(!sum_finite(dkacc) || !sum_finite(dvacc));
+    const int blk = (kb * KB + kw * 32) / 16;
+    if (lane < 2 && blk + lane < A.nkb16)
+      A.flags[A.n_qflags + (int64_t)bkv * A.nkb16 + blk + lane] = bad ? 1 : 0;
+  }
   // dK = scale * (dK^T)^T, dV = (dV^T)^T: lane holds key l32, d = 32 d' +
   // 8 (r / 4) + 4 hf + r % 4
   if (qh == 0 && key_ok) {
@@ -589,6 +597,14 @@ __global__ __launch_bounds__(256, 2) void dq_kernel(BwdArgs A, const float* lse2
     block(k_st1, v_st1, 1, mb[3]);
   }
 
+  // the non-finite flags of this wave's two 16-row groups (bwd_fix_kernel
+  // recomputes flagged groups)
+  {
+    const bool bad = wave_any(!sum_finite(dqacc));
+    const int grp = (qb * 128 + wave * 32) / 16;
+    if (lane < 2 && grp + lane < A.ng)
+      A.flags[((int64_t)b * A.H + h) * A.ng + grp + lane] = bad ? 1 : 0;
+  }
   // dQ = scale * (dQ^T)^T: lane holds row i, d = 32 d' + 8 (r / 4) + 4 hf + r % 4
   if (row_ok) {
     uint16_t* dqr = A.dq + (int64_t)b * A.dqsb + (int64_t)h * A.dqsh + (int64_t)i * A.dqss;
@@ -624,7 +640,9 @@ static hipError_t launch_tile_bwd_elem(const BwdArgs& a, int head_dim, int64_t n
     // the split counters) on its way, then dK / dV reads them
     hipError_t e0 = launch_band_dq(a, head_dim, lse2, true, stream);
     if (e0 != hipSuccess) return e0;
-    return launch_band_dkdv(a, head_dim, lse2, stream);
+    e0 = launch_band_dkdv(a, head_dim, lse2, stream);
+    if (e0 != hipSuccess) return e0;
+    return launch_bwd_fix(a, head_dim, stream);
   }
   const unsigned n_rb = (unsigned)((a.q_len + PREP_ROWS - 1) / PREP_ROWS);
   // heads fastest where O interleaves heads within a row and the row blocks
@@ -649,7 +667,11 @@ static hipError_t launch_tile_bwd_elem(const BwdArgs& a, int head_dim, int64_t n
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if (num_q_items < 0) return launch_band_dq(a, head_dim, lse2, false, stream);  // no work list
+  if (num_q_items < 0) {  // no work list
+    e = launch_band_dq(a, head_dim, lse2, false, stream);
+    if (e != hipSuccess) return e;
+    return launch_bwd_fix(a, head_dim, stream);
+  }
   if (num_q_items > 0) {
     const dim3 grid((unsigned)num_q_items);
     if (head_dim == 128 && a.qmask)
@@ -661,8 +683,9 @@ static hipError_t launch_tile_bwd_elem(const BwdArgs& a, int head_dim, int64_t n
     else
       dq_kernel<64, E, false><<<grid, 256, 0, stream>>>(a, lse2);
     e = hipGetLastError();
+    if (e != hipSuccess) return e;
   }
-  return e;
+  return launch_bwd_fix(a, head_dim, stream);
 }
 
 hipError_t launch_tile_bwd(const BwdArgs& a, int head_dim, int64_t num_q_items,

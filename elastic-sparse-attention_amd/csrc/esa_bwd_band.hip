@@ -388,6 +388,13 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
     }
   }
 
+  // ---- the group's non-finite flag (staged K rows a row does not list meet
+  // dS = 0 in dQ^T, and 0 * Inf is NaN: bwd_fix_kernel recomputes such a
+  // group exactly)
+  {
+    const bool bad = wave_any(!sum_finite(dqacc));
+    if (lane == 0) A.flags[g] = bad ? 1 : 0;
+  }
   // ---- dQ = scale * dQ^T^T: lane (n, q) holds dims CW q + 4 s + e of row n
   if (row_ok) {
     uint16_t* dqr = A.dq + (int64_t)b * A.dqsb + (int64_t)h * A.dqsh + (int64_t)i * A.dqss;
@@ -828,6 +835,11 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
     }
   }
 
+  // ---- the block's non-finite flag (bwd_fix_kernel recomputes it)
+  {
+    const bool bad = wave_any(!sum_finite(dkacc) || !sum_finite(dvacc));
+    if (lane == 0) A.flags[A.n_qflags + g] = bad ? 1 : 0;
+  }
   // ---- dK = scale dK^T^T, dV = dV^T^T: lane (key n, q) holds dims
   // CW q + 4 s + e of key u0 + n
   if (key_ok) {

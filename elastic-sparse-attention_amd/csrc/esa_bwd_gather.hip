@@ -14,7 +14,10 @@
 //                     coefficient m_j p and dK coefficient scale * dS go to
 //                     the workspace (0 for an entry that is masked or whose
 //                     key lies outside [0, kv_len): the Triton kernel's
-//                     atomics skip those, :209-213, :226-228).
+//                     atomics skip those, :209-213, :226-228).  A row
+//                     with a non-finite delta and an entry it does not
+//                     attend gets a NaN dQ, as the Triton kernel's
+//                     (0 - delta) * 0 term for that entry gives it.
 //   bwd_sort_keys     key of each entry: kv_head * kv_len + key for a valid
 //                     in-range entry, else a sentinel past every key.
 //   radix sort        a stable LSD radix sort of (key, entry id), 8 bits per
@@ -34,32 +37,6 @@
 namespace esa {
 
 namespace {
-
-// dot of a float row in LDS with a row of T in memory (D % 4 == 0)
-template <Elem E>
-__device__ __forceinline__ float lds_row_dot(const float* __restrict__ xs,
-                                             const typename ElemT<E>::T* __restrict__ row, int D) {
-  float acc = 0.f;
-  if constexpr (E == Elem::f32) {
-    for (int d = 0; d < D; d += 4) {
-      const f32x4 kv = *(const f32x4*)(row + d);
-      acc += xs[d] * kv[0];
-      acc += xs[d + 1] * kv[1];
-      acc += xs[d + 2] * kv[2];
-      acc += xs[d + 3] * kv[3];
-    }
-  } else {
-    for (int d = 0; d < D; d += 4) {
-      const u32x2 kv = *(const u32x2*)(row + d);
-      const u32x4 raw = {kv[0], kv[1], 0u, 0u};
-      acc += xs[d] * ElemT<E>::chunk(raw, 0);
-      acc += xs[d + 1] * ElemT<E>::chunk(raw, 1);
-      acc += xs[d + 2] * ElemT<E>::chunk(raw, 2);
-      acc += xs[d + 3] * ElemT<E>::chunk(raw, 3);
-    }
-  }
-  return acc;
-}
 
 template <Elem E, bool PATTERN>
 __global__ __launch_bounds__(256) void bwd_rows_kernel(GatherBwdArgs A) {
@@ -104,6 +81,7 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(GatherBwdArgs A) {
   float* cs = A.cs + (int64_t)b * A.E;
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  bool dead = false;
   for (int c0 = 0; c0 < w; c0 += 64) {
     const int j = c0 + lane;
     bool valid = false;
@@ -111,10 +89,11 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(GatherBwdArgs A) {
     if (j < w) row.entry<PATTERN>(A.src, h, r, j, valid, key);
     const bool in_range = key >= 0 && key < A.kv_len;
     const bool live = valid && in_range && !row.bad_pos;
+    dead |= j < w && !live;
     float dsc = 0.f, pc = 0.f;
     if (live) {
-      const float s = lds_row_dot<E>(qs, kbase + key * A.kss, D) * A.sm_scale;
-      const float dp = lds_row_dot<E>(dos, vbase + key * A.vss, D);
+      const float s = row_dot<E>(qs, kbase + key * A.kss, D) * A.sm_scale;
+      const float dp = row_dot<E>(dos, vbase + key * A.vss, D);
       const float p = expf(s - lse);
       const float keep = drop_factor(A.drop, b, h, r, j, A.H, A.q_len, w);
       pc = keep * p;
@@ -131,7 +110,7 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(GatherBwdArgs A) {
     for (int jj = 0; jj < nj; ++jj) {
       const float g = dsl[jj];
       const int kj = ksl[jj];
-      if (kj >= 0 && g != 0.f) {
+      if (kj >= 0) {
         const T* kr = kbase + (int64_t)kj * A.kss;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -143,11 +122,14 @@ __global__ __launch_bounds__(256) void bwd_rows_kernel(GatherBwdArgs A) {
     wave_sync_lds();
   }
   T* dqrow = (T*)A.dq + (int64_t)b * A.dqsb + (int64_t)h * A.dqsh + (int64_t)r * A.dqss;
-  const float nan_or_one = row.bad_pos ? __builtin_nanf("") : 1.f;
+  // an entry the row does not attend (masked, or a key outside [0, kv_len))
+  // adds dS * 0 in the Triton kernel with dS = p (0 - delta) scale (:202-221):
+  // NaN throughout when delta is not finite
+  const bool all_nan = row.bad_pos || (__builtin_amdgcn_ballot_w64(dead) != 0 && !__builtin_isfinite(delta));
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int d = lane + 64 * e;
-    if (d < D) ElemT<E>::store(dqrow + d, acc[e] * nan_or_one);
+    if (d < D) ElemT<E>::store(dqrow + d, all_nan ? __builtin_nanf("") : acc[e]);
   }
 }
 
@@ -223,8 +205,9 @@ __global__ __launch_bounds__(256) void bwd_kv_kernel(GatherBwdArgs A) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int d = lane + 64 * q;
-        qv[u][q] = d < D ? ElemT<E>::load(qrow + d) : 0.f;
-        gv[u][q] = d < D ? ElemT<E>::load(dorow + d) : 0.f;
+        // (a padding slot's row counts 0, not 0 times that row)
+        qv[u][q] = in && d < D ? ElemT<E>::load(qrow + d) : 0.f;
+        gv[u][q] = in && d < D ? ElemT<E>::load(dorow + d) : 0.f;
       }
     }
 #pragma unroll

@@ -737,20 +737,40 @@ int bwd_split_parts(const esa_bwd_args* a) {
 }
 int bwd_split_blocks(const esa_bwd_args*) { return 1; }
 
+// Byte offsets of the MFMA backward's workspace regions: delta and lse2 per
+// row (rows of each (b, h) padded to qpad, bwd_qpad), the split dK / dV's
+// float32 partial sums and arrival counters (when it splits), then the
+// non-finite flags (one byte per 16-row dQ group and per 16-key dK / dV
+// block), 256-byte aligned; the total is a multiple of 256 bytes.
+struct BwdWsLayout {
+  size_t part_buf, part_cnt, flags, total;
+  int64_t n_qflags, n_kvflags;
+};
+
+static BwdWsLayout bwd_ws_layout(const esa_bwd_args* a) {
+  BwdWsLayout L{};
+  size_t bytes = (size_t)2 * a->batch * a->num_heads * bwd_qpad(a->q_len) * sizeof(float);
+  L.part_buf = L.part_cnt = bytes;
+  const int parts = bwd_split_parts(a);
+  if (parts > 1) {
+    const size_t n_split = (size_t)a->batch * a->num_kv_heads * bwd_split_blocks(a);
+    bytes += n_split * parts * 2 * 16 * a->head_dim * sizeof(float);
+    L.part_cnt = bytes;
+    bytes += (n_split * sizeof(int) + 15) / 16 * 16;
+  }
+  L.flags = (bytes + 255) / 256 * 256;
+  L.n_qflags = (int64_t)a->batch * a->num_heads * ((a->q_len + 15) / 16);
+  L.n_kvflags = (int64_t)a->batch * a->num_kv_heads * ((std::max(a->kv_len, 0) + 15) / 16);
+  L.total = (L.flags + (size_t)(L.n_qflags + L.n_kvflags) + 255) / 256 * 256;
+  return L;
+}
+
 esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes) {
   if (!a || !workspace_bytes) return ESA_ERR_NULL;
   if (a->batch < 0 || a->num_heads < 1 || a->num_kv_heads < 1 || a->q_len < 0 ||
       a->head_dim < 1)
     return ESA_ERR_SHAPE;
-  // delta and lse2 per row, rows of each (b, h) padded to qpad (bwd_qpad)
-  size_t bytes = (size_t)2 * a->batch * a->num_heads * bwd_qpad(a->q_len) * sizeof(float);
-  const int parts = bwd_split_parts(a);
-  if (parts > 1) {  // split partial sums and arrival counters
-    const size_t n_split = (size_t)a->batch * a->num_kv_heads * bwd_split_blocks(a);
-    bytes += n_split * parts * 2 * 16 * a->head_dim * sizeof(float);
-    bytes += (n_split * sizeof(int) + 15) / 16 * 16;
-  }
-  *workspace_bytes = bytes;
+  *workspace_bytes = bwd_ws_layout(a).total;
   return ESA_OK;
 }
 
@@ -935,9 +955,14 @@ esa_status elastic_bwd_impl(const esa_bwd_args* a, const esa_pattern* p, const i
     const int64_t n_split = (int64_t)t.n_bkv * t.split_blocks;
     if (n_split * (t.split_parts - 1) > INT32_MAX / 2) return ESA_ERR_SHAPE;
     t.n_extra = (int)((n_split * (t.split_parts - 1) + 7) / 8 * 8);
-    t.part_buf = (float*)workspace + (int64_t)2 * a->batch * a->num_heads * t.qpad;
-    t.part_cnt = (int*)(t.part_buf + n_split * t.split_parts * 2 * 16 * a->head_dim);
   }
+  const BwdWsLayout wl = bwd_ws_layout(a);
+  t.part_buf = (float*)((char*)workspace + wl.part_buf);
+  t.part_cnt = (int*)((char*)workspace + wl.part_cnt);
+  t.flags = (uint8_t*)workspace + wl.flags;
+  if (wl.n_qflags + wl.n_kvflags > INT32_MAX / 2) return ESA_ERR_SHAPE;
+  t.n_qflags = (int)wl.n_qflags;
+  t.n_kvflags = (int)wl.n_kvflags;
   return hip_status(launch_tile_bwd(t, a->head_dim, band_dq ? -1 : num_q_items,
                                     band_dkdv ? -1 : num_kv_items, (hipStream_t)stream));
 }

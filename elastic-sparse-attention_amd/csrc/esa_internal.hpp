@@ -207,6 +207,12 @@ struct BwdArgs {
   float* part_buf;
   int* part_cnt;
   int elem;  // Elem of the 16-bit tensors: bf16 or f16
+  // non-finite output flags (workspace): one byte per 16-row dQ group
+  // ((b * H + h) * ng + row / 16) then one per 16-key dK / dV block (n_qflags
+  // + (b * Hkv + kvh) * nkb16 + key / 16), each written 0 or 1 by the kernel
+  // that stores the unit; bwd_fix_kernel recomputes the flagged units
+  uint8_t* flags;
+  int n_qflags, n_kvflags;
 };
 
 hipError_t launch_indices(const PatternConsts& pc, int row0, int nrows, void* indices, void* mask,
@@ -224,6 +230,7 @@ hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
                            hipStream_t stream);
 hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream);
 // prep: the kernel forms and stores delta / lse2 itself (see band_dq_kernel)
+hipError_t launch_bwd_fix(const BwdArgs& a, int head_dim, hipStream_t stream);
 hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2, bool prep,
                           hipStream_t stream);
 hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,

@@ -860,7 +860,7 @@ def elastic_attention_bwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: 
         ws = ctypes.c_size_t()
         check(lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(ws)),
               "esa_bwd_workspace_size")
-        work = torch.empty(max(ws.value // 4, 4), dtype=torch.float32, device=q.device)
+        work = torch.empty(max((ws.value + 3) // 4, 4), dtype=torch.float32, device=q.device)
     auto_dq, auto_dkdv = bwd_kernels(layout, Lq, B, D)
     dq_kernel = auto_dq if dq_kernel == "auto" else dq_kernel
     dkdv_kernel = auto_dkdv if dkdv_kernel == "auto" else dkdv_kernel

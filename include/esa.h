@@ -360,8 +360,11 @@ esa_status esa_build_tile_masks(const esa_pattern* p, const int32_t* row_ptr,
  * 32 (per-row delta and log2 LSE), and, when the band dK/dV may split key
  * block 0 (num_heads / num_kv_heads * q_len > 6144), P float32 partial
  * sums of 2 * 16 * head_dim floats and one counter per (batch, kv head),
- * P = that product / 6144 rounded up, at most 32.  Requires num_kv_heads
- * and head_dim >= 1. */
+ * P = that product / 6144 rounded up, at most 32, then, from the next
+ * 256-byte boundary, one byte per 16-row dQ group (batch * num_heads *
+ * ceil(q_len / 16)) and per 16-key dK / dV block (batch * num_kv_heads *
+ * ceil(kv_len / 16)): the kernels' non-finite flags.  The total is a
+ * multiple of 256.  Requires num_kv_heads and head_dim >= 1. */
 esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes);
 
 /* Backward over the elastic pattern: replaces the backward branch of the
@@ -392,6 +395,10 @@ esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes
  * q_len; q_masks: esa_stage_masks_size) from row_ptr_host, the host copy of
  * row_ptr, which is required (ESA_ERR_NULL) whenever mask_t or q_masks is
  * read; a shorter buffer is rejected (ESA_ERR_CAPACITY).
+ * Inf and NaN in the inputs reach exactly the gradients the reference's
+ * gather reaches: each kernel flags the 16-row dQ groups and 16-key dK / dV
+ * blocks it stores with a non-finite value, and a last kernel recomputes
+ * those on the listed (row, entry) pairs only.
  * Requires dtype ESA_BF16 or ESA_F16, head_dim 64 or 128, block 128 x 128, a finite
  * sm_scale > 0, q_len <= kv_len, 16-byte aligned rows. */
 esa_status esa_elastic_bwd(const esa_bwd_args* a, const esa_pattern* p,

@@ -376,7 +376,9 @@ def test_bwd_entry_points_reject_bad_arguments():
     a.sm_scale = 128 ** -0.5
     ws = ctypes.c_size_t()
     assert lib.esa_bwd_workspace_size(ctypes.byref(a), ctypes.byref(ws)) == en.ESA_OK
-    assert ws.value == 2 * 1 * 4 * (256 + 32) * 4   # rows padded to 32, + 32
+    # delta and lse2 (rows padded to 32, + 32), then a flag byte per 16-row
+    # dQ group and per 16-key dK / dV block
+    assert ws.value == (2 * 1 * 4 * (256 + 32) * 4 + 4 * 16 + 4 * 16 + 255) // 256 * 256
 
     # host copy of the 128 x 128 layout's row_ptr (8 query blocks x 4 heads,
     # 3 tiles each)
@@ -461,7 +463,9 @@ def test_bwd_workspace_size_with_split():
     split of key block 0: P = ceil(groups * q_len / 6144) (at most 32)
     float32 partial sums of 2 * 16 * D floats and one counter per (batch, kv
     head), after the 2 * B * H * qpad floats of delta and lse2 (each part of
-    the workspace 16-byte aligned, the total rounded up to 256 bytes)."""
+    the workspace 16-byte aligned); then, from the next 256-byte boundary,
+    one non-finite flag byte per 16-row dQ group and per 16-key dK / dV
+    block, the total a multiple of 256 bytes."""
     lib = en.load()
 
     def size(B, H, Hkv, q_len, D):
@@ -479,13 +483,14 @@ def test_bwd_workspace_size_with_split():
         parts = min(max(-(-(H // Hkv) * q_len // 6144), 1), 32)
         if parts > 1:
             n += B * Hkv * parts * 2 * 16 * D * 4 + (B * Hkv * 4 + 15) // 16 * 16
-        return n
+        n = (n + 255) // 256 * 256 + B * H * ((q_len + 15) // 16) + B * Hkv * ((q_len + 15) // 16)
+        return (n + 255) // 256 * 256
 
     for shape in [(1, 8, 2, 8192, 128), (2, 4, 4, 6144, 64), (1, 4, 4, 6145, 64),
                   (1, 32, 8, 32768, 128), (1, 64, 1, 131072, 128), (3, 6, 3, 100, 64)]:
         assert size(*shape) == expect(*shape), shape
     # 6144 rows of one group: no split; one more row: two parts
-    assert size(1, 1, 1, 6144, 64) == expect(1, 1, 1, 6144, 64) == 2 * (6144 + 32) * 4
+    assert size(1, 1, 1, 6144, 64) == expect(1, 1, 1, 6144, 64) == 2 * (6144 + 32) * 4 + 768
 
 
 def test_reachability_rejects_bad_arguments():

@@ -10,13 +10,17 @@ group or item whose output met a non-finite value runs again with the staged
 V operands sanitised and the reference's non-finite values put back from the
 row's own entries.  So for them too, rows that do not attend a planted key
 are bit-identical to a clean run, and rows that do are non-finite exactly
-where the per-row gather path is.
+where the per-row gather path is.  The MFMA backward flags every unit it
+stores with a non-finite value and recomputes those on the reference's pairs,
+so its gradients too are non-finite exactly where the per-row gather
+backward's are.
 """
 import pytest
 import torch
 
 from esa_oracle import elastic_indices, seeded_inputs
-from elastic_sparse_attention import (ElasticLayout, elastic_attention_fwd,
+from elastic_sparse_attention import (ElasticLayout, elastic_attention_bwd,
+                                      elastic_attention_bwd_rows, elastic_attention_fwd,
                                       elastic_attention_rows, make_pattern)
 
 pytestmark = pytest.mark.gpu
@@ -179,3 +183,56 @@ def test_mfma_paths_nonfinite_k(kernel, layer, L, H, D, w, dtype):
     assert same_nonfinite(bad, ref)
     fin = torch.isfinite(ref.float()) & torch.isfinite(bad.float())
     assert float((bad.float() - ref.float())[fin].abs().max()) <= 2e-2
+
+
+# (dQ kernel / dK-dV kernel, layer, L, H, Hkv, D, dtype): each pair of the
+# MFMA backward kernels, GQA, both head dims, float16, and the last layer's
+# split of key block 0 over several waves (band dK/dV, groups * L > 6144)
+BWD_NF_CASES = [("band/band", 4, 1024, 4, 2, 128, torch.bfloat16),
+                ("tile/tile", 4, 1024, 4, 2, 128, torch.bfloat16),
+                ("band/tile", 0, 1024, 4, 4, 64, torch.bfloat16),
+                ("tile/band", 7, 1024, 4, 2, 64, torch.float16),
+                ("tile/tile", 2, 700, 2, 1, 64, torch.float16),
+                ("band/band", 7, 2048, 8, 2, 128, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("where", ["v", "k"])
+@pytest.mark.parametrize("kernels,layer,L,H,Hkv,D,dtype", BWD_NF_CASES)
+def test_mfma_backward_reference_semantics(kernels, layer, L, H, Hkv, D, dtype, where):
+    """V (or K) planted with +Inf, NaN and -Inf / +Inf at three keys, the
+    forward output and log-sum-exp of the per-row gather (the reference's
+    semantics): every gradient of the MFMA backward is non-finite exactly
+    where the per-row gather backward's is, with the same kind (the kernels
+    flag each 16-row dQ group and 16-key dK / dV block that met a non-finite
+    value and bwd_fix_kernel recomputes those on the reference's pairs), and
+    the finite values agree to the bf16 bar."""
+    dq_kernel, dkdv_kernel = kernels.split("/")
+    print(f"nonfinite bwd {where} {kernels} layer={layer} L={L} H={H} Hkv={Hkv} D={D} {dtype}",
+          flush=True)
+    q, k, v = seeded_inputs(1, H, Hkv, L, D, dtype, seed=31, scale=1.0)
+    keys = [L // 2 + 1, L // 3, L - 5]
+    t = (v if where == "v" else k).clone()
+    t[:, :, keys[0], 3] = float("inf")
+    t[:, :, keys[1], D - 1] = float("nan")
+    t[:, :, keys[2], 7] = float("-inf")
+    t[:, :, keys[2], 8] = float("inf")
+    kb, vb = (k, t) if where == "v" else (t, v)
+    pat = make_pattern(L, 64, layer, 8, H)
+    lay = ElasticLayout(pat, DEV)
+    qd, kd, vd = q.to(DEV), kb.to(DEV), vb.to(DEV)
+    sc = D ** -0.5
+    o, lse = elastic_attention_rows(qd, kd, vd, pat, sc)
+    do = torch.randn(o.shape, generator=torch.Generator().manual_seed(5)).to(dtype).to(DEV)
+    ref = elastic_attention_bwd_rows(qd, kd, vd, o, lse, do, pat, sc)
+    got = elastic_attention_bwd(qd, kd, vd, o, lse, do, lay, sc, dq_kernel=dq_kernel,
+                                dkdv_kernel=dkdv_kernel)
+    for name, g, r in zip(("dq", "dk", "dv"), got, ref):
+        rf, gf = r.float(), g.float()
+        fin = torch.isfinite(rf)
+        print(f"  {name}: {int((~fin).sum())} non-finite of {rf.numel()}", flush=True)
+        assert same_nonfinite(g, r), name
+        assert bool(fin.any()), name
+        err = float((gf - rf)[fin].abs().max())
+        assert err <= 2e-2 * float(rf[fin].abs().max()), (name, err)
+    # some gradient holds a non-finite value only because of the planted keys
+    assert any(not bool(torch.isfinite(r.float()).all()) for r in ref)
