@@ -185,12 +185,13 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   // K or V rows of band info word `bi` -> slot dst, through a buffer resource
   // that starts at the band's first row and holds its W rows: rows past the
   // band fall outside num_records and read as zeros without a fetch.  V
-  // always takes VLOADS DMAs, so its slot rows past the band are zeros (they
-  // meet p = 0 in PV, and 0 * Inf would be NaN).  K takes VLOADS too, or
-  // with KSKIP only the ceil(W / RPI) that reach a band row (each DMA costs
-  // the texture unit a full 64-lane transfer, rows past W included): K rows
-  // past the band then keep older finite contents, whose scores belong to
-  // keys no row picks.
+  // takes only the ceil(W / RPI) DMAs that reach a band row (each DMA costs
+  // the texture unit a full 64-lane transfer, rows past W included); its
+  // slot rows past them keep an earlier band's rows, which meet p = 0 in PV
+  // (0 * Inf = NaN for a non-finite one sends the group to the sanitised
+  // rerun below, which gives the bits of a run without it).  K takes VLOADS
+  // DMAs, or with KSKIP only those that reach a band row: K rows past the
+  // band then keep older contents, whose scores belong to keys no row picks.
   constexpr int RPI = 64 / C::CPR;  // slot rows per DMA
   auto n_loads = [&](int bi) { return (min((int)((uint32_t)bi >> 24), 16) + RPI - 1) / RPI; };
   auto load_rows = [&](const char* base, int ss2, const int* ofs, int bi, lds_u16* dst,
@@ -208,7 +209,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     }
   };
   auto load_k = [&](int bi, lds_u16* dst) { load_rows(kbase, kss2, kofs, bi, dst, !KSKIP); };
-  auto load_v = [&](int bi, lds_u16* dst) { load_rows(vbase, vss2, vofs, bi, dst, true); };
+  auto load_v = [&](int bi, lds_u16* dst) { load_rows(vbase, vss2, vofs, bi, dst, false); };
   // s_waitcnt vmcnt(n) for a count known only at run time (0 .. 16)
   auto wait_vm = [&](int n) {
     switch (n) {
@@ -385,9 +386,9 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     //   VEARLY: wait for the pair's K and V DMAs (the only ones outstanding),
     //   read the K and V^T operands, request the next pair's K and V into the
     //   same slots, then compute from registers.
-    //   Otherwise: before the K wait exactly this pair's 2 VLOADS V DMAs may be
-    //   newer; before the V wait the next pair's K DMAs (2 VLOADS of them, or
-    //   with KSKIP as many as load_k issued).
+    //   Otherwise: before the K wait exactly this pair's V DMAs (as many as
+    //   load_v issued) may be newer; before the V wait the next pair's K DMAs
+    //   (2 VLOADS of them, or with KSKIP as many as load_k issued).
     constexpr int kWaitPair = (0xF70 & ~0xF) | ((2 * C::VLOADS) & 0xF) |
                               (((2 * C::VLOADS) >> 4) << 14);  // vmcnt(2 VLOADS)
     constexpr int kWaitLds = 0xC07F;                           // lgkmcnt(0)
@@ -433,7 +434,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
           load_v(na, lv0);
           load_v(nb, lv1);
         } else {
-          __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's K is in LDS
+          wait_vm(n_loads(ia) + n_loads(ib));  // this pair's K is in LDS
           if (live) {
             read_k(ks0, kopa);
             if constexpr (D == 256) {
