@@ -25,9 +25,9 @@
 
 namespace esa {
 
-// VSKIP: issue only the V DMAs that reach a band row (see load_rows); the
-// host picks it where many bands are narrower than 16 keys, as for the
-// forward's K DMA skip.
+// VSKIP: issue only the K and V DMAs that reach a band row (see
+// load_rows); the host picks it where many bands are narrower than 16 keys,
+// as for the forward's K DMA skip.
 // PREP: the kernel forms its rows' delta = rowsum(dO * O) and lse2 = lse *
 // log2(e) itself (instead of reading them) and stores both for the band
 // dK/dV kernel, which then runs after it; block 0 also clears the split
@@ -181,12 +181,12 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
     vofs[t] = R * vss2 + 16 * kswz<D>(R, pc);
   }
   // K or V rows of band `bi` -> slot dst, through a buffer resource over the
-  // band's W rows (rows past the band read as zeros without a fetch).  K
-  // always takes VLOADS DMAs: its slot rows past the band meet dS = 0 in
-  // dQ^T += K^T dS^T and must be zeros (0 * Inf would be NaN).  V takes
-  // VLOADS too, or with VSKIP only the ceil(W / RPI) DMAs that reach a band
-  // row: V rows past the band then keep older slot contents, which only
-  // feed dP of keys no row picks.  The vmcnt waits count the DMAs issued.
+  // band's W rows (rows past the band read as zeros without a fetch).  Each
+  // takes VLOADS DMAs, or with VSKIP only the ceil(W / RPI) that reach a
+  // band row: slot rows past them then keep older contents.  Old V rows only
+  // feed dP of keys no row picks; old K rows meet dS = 0 in dQ^T += K^T dS^T
+  // (0 * Inf = NaN for a non-finite one flags the group, and bwd_fix_kernel
+  // recomputes it).  The vmcnt waits count the DMAs issued.
   constexpr int RPI = 64 / C::CPR;  // slot rows per DMA
   auto n_loads = [&](int bi) { return (min((int)((uint32_t)bi >> 24), 16) + RPI - 1) / RPI; };
   auto load_rows = [&](const char* base, int ss2, const int* ofs, int bi, lds_u16* dst,
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
                                                  0, 0);
     }
   };
-  auto load_k = [&](int bi, lds_u16* dst) { load_rows(kbase, kss2, kofs, bi, dst, true); };
+  auto load_k = [&](int bi, lds_u16* dst) { load_rows(kbase, kss2, kofs, bi, dst, !VSKIP); };
   auto load_v = [&](int bi, lds_u16* dst) { load_rows(vbase, vss2, vofs, bi, dst, !VSKIP); };
   // s_waitcnt vmcnt(n) for a count known only at run time (0 .. 8)
   auto wait_vm = [&](int n) {
@@ -285,9 +285,9 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   };
 
   // ---- band pairs: per pair, K reads, then K of the next pair; V reads,
-  // then V of the next pair.  So before the V wait exactly the next pair's
-  // 2 VLOADS K DMAs may be newer, and before the K wait this pair's V DMAs
-  // (2 VLOADS of them, or with VSKIP as many as load_v issued).
+  // then V of the next pair.  So before the V wait exactly the next pair's K
+  // DMAs may be newer, and before the K wait this pair's V DMAs (2 VLOADS of
+  // each, or with VSKIP as many as load_k / load_v issued).
   constexpr int kWaitPair = (0xF70 & ~0xF) | ((2 * C::VLOADS) & 0xF) |
                             (((2 * C::VLOADS) >> 4) << 14);  // vmcnt(2 VLOADS)
   constexpr int kWaitLds = 0xC07F;                           // lgkmcnt(0)
@@ -337,7 +337,11 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
       __builtin_amdgcn_s_waitcnt(kWaitLds);  // K slots read: refill them
       load_k(na, lk0);
       load_k(nb, lk1);
-      __builtin_amdgcn_s_waitcnt(kWaitPair);  // this pair's V is in LDS
+      // this pair's V is in LDS
+      if constexpr (VSKIP)
+        wait_vm(n_loads(na) + n_loads(nb));
+      else
+        __builtin_amdgcn_s_waitcnt(kWaitPair);
       V8 va[C::NS], vb[C::NS];
       if (live) {
         read_rows(vs0, va);
@@ -360,7 +364,7 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   }
 
   // ---- tail: keys of bands wider than 16, one 16-key chunk at a time (the
-  // pair's second half is ks1 with dS = 0; ks1 holds finite rows)
+  // pair's second half is ks1 with dS = 0)
   __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   const bool wide = wave_any(((uint32_t)info1 >> 24) > 16u);  // some slot's band
   for (int j = 0; j < 64 && wide; ++j) {
@@ -884,7 +888,7 @@ hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,
 
 template <int D, bool PREP, Elem E>
 static void launch_band_dq_d(const BwdArgs& a, dim3 grid, const float* lse2, hipStream_t stream) {
-  // V DMA skipping from interpolation weight 1/2 on, as for the forward's K
+  // K and V DMA skipping from interpolation weight 1/2 on, as for the forward
   if (a.pc.a >= 0.5f)
     band_dq_kernel<D, true, PREP, E><<<grid, 64, 0, stream>>>(a, lse2);
   else

@@ -633,10 +633,6 @@ void launch_band_elem(const BandArgs& a, int head_dim, dim3 grid, bool kskip, bo
 hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) {
   if (a.n_groups <= 0) return hipSuccess;
   dim3 grid((unsigned)(8 * a.per_xcd));
-  // K DMA skipping from interpolation weight 1/2 on: measured at B=1, H=32,
-  // L=32768, D=128, w=64 over 8 layers: 1-7% faster at weights 4/7 .. 1,
-  // even at 3/7, 3-4% slower at 1/7 and 2/7
-  const bool kskip = a.pc.a >= 0.5f;
   // The refill order by the entry spacing at the last row, (q_len a + c) / w
   // query rows between one entry's keys and the next's: at B=1 H=8 L=131072
   // D=128 the early V requests were 9-11% faster at spacings 586 and 878
@@ -648,6 +644,14 @@ hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) 
   const float last = (float)(a.positions ? a.kv_len : a.q_len);
   const float spacing = (last * a.pc.a + a.pc.c) / (float)a.pc.w;
   const bool vearly = spacing < 1000.0f;
+  // K DMA skipping: with the late V order from interpolation weight 1/2 on
+  // (measured at B=1, H=32, L=32768, D=128, w=64 over 8 layers: 1-7% faster
+  // at weights 4/7 .. 1, even at 3/7, 3-4% slower at 1/7 and 2/7, where
+  // nearly every band is 16 keys wide and the run-time waits cost more than
+  // the DMAs saved); with the early V order (one vmcnt(0) wait per pair,
+  // whatever the count) always: 2-5% faster at weights 2/7 and 3/7 of
+  // L=8192 .. 131072, within 1% at 1/7
+  const bool kskip = a.pc.a >= 0.5f || vearly;
   if (a.elem == (int)Elem::f16)
     launch_band_elem<Elem::f16>(a, head_dim, grid, kskip, vearly, stream);
   else
