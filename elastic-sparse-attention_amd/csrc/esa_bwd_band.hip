@@ -370,7 +370,11 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   for (int j = 0; j < 64 && wide; ++j) {
     const int qj = j >> 4, r = j & 15;
     const int bi = __builtin_amdgcn_readlane(info1, j);  // slot (qj, r)
-    const uint32_t w4 = r < 8 ? (r < 4 ? kd[0] : kd[1]) : (r < 12 ? kd[2] : kd[3]);
+    // (the words as opaque values first: selects between loads of kd would
+    // become a load at a selected address, which puts kd in scratch)
+    uint32_t k0 = kd[0], k1 = kd[1], k2 = kd[2], k3 = kd[3];
+    asm volatile("" : "+v"(k0), "+v"(k1), "+v"(k2), "+v"(k3));
+    const uint32_t w4 = (r & 8) ? ((r & 4) ? k3 : k2) : ((r & 4) ? k1 : k0);
     const uint32_t dw = (uint32_t)__builtin_amdgcn_ds_bpermute(lane_key + 64 * qj, (int)w4);
     const int d = (int)((dw >> (8 * (r & 3))) & 0xFFu);  // 0xFF: no key
     const int lo = bi & 0xffffff, wdt = (int)((uint32_t)bi >> 24);
