@@ -1,12 +1,13 @@
 // Rate probes (gfx950): dense bf16 MFMA, HBM read, L2 -> LDS or HBM -> LDS
 // through the buffer_load ... lds path the MFMA kernels stage K and V with,
 // 256-byte row gathers into LDS (the band kernels' pattern) and from HBM
-// into registers (the decode step's).
+// into registers (the decode step's), and the band kernels' LDS operand
+// reads (bank-conflict rates of each read form).
 // Built into libesa_probe.so; declared in include/esa_probe.h.
 #include <hip/hip_runtime.h>
 
 #include "esa_probe.h"
-#include "esa_tile.hpp"
+#include "esa_band.hpp"
 
 namespace esa {
 namespace {
@@ -148,6 +149,66 @@ __global__ __launch_bounds__(kThreads) void gather_probe_kernel(const u32x4* src
   sink[gid] = acc;
 }
 
+// The band forward's LDS operand reads at D = 128, from one 16-row slot per
+// wave (16 rows x 256 bytes, filled with 16-bit ones), `iters` rounds:
+//   0: K operand, ds_read_b128, lane (n, q) row n, chunk kswz(n, 4 s + q),
+//      s = 0..3 (the kernels' swizzle)
+//   1: V^T operand, ds_read_b64_tr_b16, lane x of group q row 4 q + x / 4,
+//      dims 32 (x % 4) + 4 s, s = 0..7, chunks by vswz (the kernels')
+//   2: V^T operand over contiguous 16-dim slices, dims 16 s + 4 (x % 4),
+//      chunks swizzled by 2 (row % 4), so each 16-lane group reads eight
+//      chunks in distinct 16-byte bank groups, both halves of each
+//   3: pattern 0 without the swizzle (row n, chunk 4 s + q)
+// sink[t] = the sum of every 16-bit word thread t read = 32 iters.
+template <int MODE>
+__global__ __launch_bounds__(kThreads) void lds_read_probe_kernel(int iters, uint32_t* sink) {
+  constexpr int D = 128, ROWB = 2 * D, NS = D / 32, NV = D / 16, CW = D / 4;
+  __shared__ __attribute__((aligned(1024))) uint16_t slots[4][16 * D];
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63, n = lane & 15, q = lane >> 4;
+  uint16_t* const slot = slots[wave];
+  for (int i = lane; i < 16 * D / 8; i += 64)
+    *(u32x4*)(slot + 8 * i) = u32x4{0x00010001u, 0x00010001u, 0x00010001u, 0x00010001u};
+  __syncthreads();
+  int adr[NV];
+#pragma unroll
+  for (int s = 0; s < NV; ++s) {
+    const int R = 4 * q + (n >> 2);
+    if (MODE == 0) adr[s] = n * ROWB + 16 * kswz<D>(n, 4 * (s % NS) + q);
+    if (MODE == 3) adr[s] = n * ROWB + 16 * (4 * (s % NS) + q);
+    if (MODE == 1) {
+      const int dim0 = CW * (n & 3) + 4 * s;
+      adr[s] = R * ROWB + 16 * vswz<D>(R, dim0 >> 3) + 2 * (dim0 & 7);
+    }
+    if (MODE == 2) {
+      const int dim0 = 16 * s + 4 * (n & 3);
+      adr[s] = R * ROWB + 16 * ((dim0 >> 3) ^ (2 * (R & 3))) + 2 * (dim0 & 7);
+    }
+  }
+  typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+  typedef __attribute__((address_space(3))) char lds_char;
+  uint32_t acc = 0;
+  for (int it = 0; it < iters; ++it) {
+    if constexpr (MODE == 0 || MODE == 3) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const u32x4 v = *(volatile lds_u32x4*)((lds_char*)slot + adr[s]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc += (v[e] & 0xffffu) + (v[e] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < NV; ++s) {
+        const s16x4 v =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((lds_char*)slot + adr[s]));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc += (uint32_t)(uint16_t)v[e];
+        asm volatile("" ::: "memory");
+      }
+    }
+  }
+  sink[(int64_t)blockIdx.x * kThreads + t] = acc;
+}
+
 esa_status launched() { return hipGetLastError() == hipSuccess ? ESA_OK : ESA_ERR_HIP; }
 
 }  // namespace
@@ -218,6 +279,24 @@ esa_status esa_probe_gather_read(const void* src, int64_t src_rows, const int32_
   if (sink_elems < (int64_t)workgroups * kThreads) return ESA_ERR_CAPACITY;
   gather_probe_kernel<<<workgroups, kThreads, 0, (hipStream_t)stream>>>(
       (const u32x4*)src, src_rows, rows, n_rows, sink);
+  return launched();
+}
+
+esa_status esa_probe_lds_read(int32_t pattern, int32_t workgroups, int32_t iters, uint32_t* sink,
+                              int64_t sink_elems, void* stream) {
+  using namespace esa;
+  if (!sink) return ESA_ERR_NULL;
+  if (pattern < 0 || pattern > 3 || workgroups < 1 || workgroups > (1 << 20) || iters < 1 ||
+      iters > (1 << 20))
+    return ESA_ERR_SHAPE;
+  if (sink_elems < (int64_t)workgroups * kThreads) return ESA_ERR_CAPACITY;
+  const hipStream_t st = (hipStream_t)stream;
+  switch (pattern) {
+    case 0: lds_read_probe_kernel<0><<<workgroups, kThreads, 0, st>>>(iters, sink); break;
+    case 1: lds_read_probe_kernel<1><<<workgroups, kThreads, 0, st>>>(iters, sink); break;
+    case 2: lds_read_probe_kernel<2><<<workgroups, kThreads, 0, st>>>(iters, sink); break;
+    default: lds_read_probe_kernel<3><<<workgroups, kThreads, 0, st>>>(iters, sink); break;
+  }
   return launched();
 }
 

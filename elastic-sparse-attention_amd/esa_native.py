@@ -191,7 +191,7 @@ def load() -> ctypes.CDLL:
 
 
 PROBE_EXPORTED = ("esa_probe_mfma_bf16", "esa_probe_l2_to_lds", "esa_probe_hbm_read",
-                  "esa_probe_gather_to_lds", "esa_probe_gather_read")
+                  "esa_probe_gather_to_lds", "esa_probe_gather_read", "esa_probe_lds_read")
 _probe: Optional[ctypes.CDLL] = None
 
 
@@ -217,6 +217,8 @@ def load_probe() -> ctypes.CDLL:
     lib.esa_probe_gather_to_lds.argtypes = [vp, i64, vp, i64, i32, i32, vp, i64, vp]
     lib.esa_probe_gather_read.restype = st
     lib.esa_probe_gather_read.argtypes = [vp, i64, vp, i64, i32, vp, i64, vp]
+    lib.esa_probe_lds_read.restype = st
+    lib.esa_probe_lds_read.argtypes = [i32, i32, i32, vp, i64, vp]
     _probe = lib
     return lib
 

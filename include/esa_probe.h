@@ -83,6 +83,19 @@ esa_status esa_probe_gather_read(const void* src, int64_t src_rows, const int32_
                                  int64_t n_rows, int32_t workgroups, uint32_t* sink,
                                  int64_t sink_elems, void* stream);
 
+/* LDS operand reads of the band forward at head_dim 128: each wave of
+ * `workgroups` 256-thread workgroups reads its own 16-row slot (16 x 256
+ * bytes of 16-bit ones) `iters` rounds in one pattern: 0 = the K operand's
+ * ds_read_b128 with the kernels' swizzle, 1 = the V^T operand's
+ * ds_read_b64_tr_b16 with the kernels' swizzle, 2 = ds_read_b64_tr_b16 over
+ * contiguous 16-dim slices with a swizzle that gives each 16-lane group
+ * eight distinct 16-byte bank groups, 3 = pattern 0 unswizzled.  LDS
+ * instructions per wave: 4 iters (patterns 0, 3) or 8 iters (1, 2).
+ * sink[t] = 32 * iters (the sum of the 16-bit words thread t read).
+ * pattern in [0, 3], workgroups and iters in [1, 2^20]. */
+esa_status esa_probe_lds_read(int32_t pattern, int32_t workgroups, int32_t iters, uint32_t* sink,
+                              int64_t sink_elems, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -67,6 +67,12 @@ def test_probe_library_exports_and_rejects():
         == en.ESA_ERR_ALIGN
     assert lib.esa_probe_gather_read(fake, 10, fake, 10, 8, fake, 2047, None) \
         == en.ESA_ERR_CAPACITY
+    assert lib.esa_probe_lds_read(0, 8, 4, None, 2048, None) == en.ESA_ERR_NULL
+    assert lib.esa_probe_lds_read(4, 8, 4, fake, 2048, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_lds_read(-1, 8, 4, fake, 2048, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_lds_read(1, 0, 4, fake, 2048, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_lds_read(1, 8, 0, fake, 2048, None) == en.ESA_ERR_SHAPE
+    assert lib.esa_probe_lds_read(2, 8, 4, fake, 2047, None) == en.ESA_ERR_CAPACITY
 
 
 def pat(L=32768, w=64, layer=4, nl=8, H=32, bm=128, bn=128):

@@ -85,3 +85,16 @@ def test_gather_to_lds_probe_closed_form():
                                          _stream()), "esa_probe_gather_to_lds")
     torch.cuda.synchronize()
     assert torch.all(sink == 8 * 5)
+
+
+@pytest.mark.parametrize("pattern", [0, 1, 2, 3])
+def test_lds_read_probe_closed_form(pattern):
+    """Every read of every pattern lands in the wave's slot of 16-bit ones:
+    32 words per round per thread (four 16-byte or eight 8-byte reads)."""
+    lib = en.load_probe()
+    wg, iters = 24, 37
+    sink = torch.zeros(wg * 256, dtype=torch.int32, device=DEV)
+    en.check(lib.esa_probe_lds_read(pattern, wg, iters, ctypes.c_void_p(sink.data_ptr()),
+                                    sink.numel(), _stream()), "esa_probe_lds_read")
+    torch.cuda.synchronize()
+    assert torch.all(sink == 32 * iters)
