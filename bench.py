@@ -341,12 +341,21 @@ def peaks(torch, steps: int = 10) -> None:
     print(json.dumps({"peaks": out}), flush=True)
 
 
+WARM_MS = 50.0  # the GPU's clocks climb over tens of ms of work after idle time
+
+
 def event_ms(torch, fn, steps: int, warmup: int) -> float:
-    """Median time of `fn` over `steps` calls after `warmup` untimed ones,
-    each between two HIP events on torch's current stream (the stream the
-    library launches on)."""
+    """Median time of `fn` over `steps` calls after `warmup` untimed ones (and
+    more until WARM_MS of them have run), each between two HIP events on
+    torch's current stream (the stream the library launches on)."""
+    t0 = time.perf_counter()
     for _ in range(warmup):
         fn()
+    torch.cuda.synchronize()
+    while (time.perf_counter() - t0) * 1e3 < WARM_MS:
+        for _ in range(max(warmup, 1)):
+            fn()
+        torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(steps)]
@@ -361,12 +370,19 @@ def event_ms(torch, fn, steps: int, warmup: int) -> float:
 
 def executed_blocks(torch, lay, L: int) -> int:
     """Number of (active tile, 32-row block, 32-key block) triples in which
-    some row has a valid key, per batch element: the blocks the tile
-    forward issues MFMAs for.  From the layout's key-major tile masks (32 row
-    bits per key)."""
+    some row has a valid key, per batch element, over the query blocks of
+    an L-row prefill: the blocks the tile forward issues MFMAs for.  From
+    the layout's key-major tile masks (32 row bits per key)."""
     masks = lay.tile_masks(L)
     n = lay.mask_tiles(L)
-    return int(masks[:n * 512].view(n, 4, 4, 32).ne(0).any(-1).sum().item())
+    H, nqb = lay.pattern.num_heads, lay.num_qblocks
+    rp = lay.row_ptr_host.to(torch.int64)
+    # the mask buffer holds the tiles of every query block of the heads
+    # before the last: keep those of the blocks below ceil(L / block_m)
+    tile_qb = torch.repeat_interleave(torch.arange(H * nqb) % nqb, rp[1:] - rp[:-1])[:n]
+    keep = (tile_qb < (L + lay.pattern.block_m - 1) // lay.pattern.block_m).to(masks.device)
+    blocks = masks[:n * 512].view(n, 4, 4, 32).ne(0).any(-1)
+    return int(blocks[keep].sum().item())
 
 
 def band_executed_flops(B: int, H: int, L: int, D: int, w: int) -> float:
@@ -410,9 +426,15 @@ def band_bwd_executed_flops(torch, lay, B: int, H: int, Hkv: int, L: int, D: int
     return {"dq": dq, "dkdv": dkdv}
 
 
-def executed_flops(torch, kernel: str, lay, B: int, H: int, L: int, D: int) -> float:
+def executed_flops(torch, kernel: str, lay, B: int, H: int, L: int, D: int,
+                   split: int = 0) -> float:
+    """kernel "tile" or "band" over all L rows, or "split": the tile kernel's
+    blocks over rows [0, split) and the band kernel's pairs over the rest."""
     if kernel == "tile":
         return B * executed_blocks(torch, lay, L) * 4.0 * 32 * 32 * D
+    if kernel == "split":
+        band = band_executed_flops(B, H, L, D, W) - band_executed_flops(B, H, split, D, W)
+        return B * executed_blocks(torch, lay, split) * 4.0 * 32 * 32 * D + band
     return band_executed_flops(B, H, L, D, W)
 
 
@@ -513,21 +535,23 @@ def time_backward(torch, lay, q, k, v, scaling, counted_fwd, steps, warmup) -> d
 def one_config(torch, cfg: str, layer: int, dev, steps: int, warmup: int, with_bwd: bool) -> dict:
     """Forward (and backward) kernel time of one configured workload and
     layer, through the module's kernel choice."""
-    from elastic_sparse_attention import ElasticSparseAttention, elastic_attention_fwd, prefill_kernel
+    from elastic_sparse_attention import ElasticSparseAttention, elastic_attention_fwd, prefill_split
     B, H, L, D, _, _ = CONFIGS[cfg]
     q, k, v = make_inputs(torch, cfg, dev, on_device=True)
     m = ElasticSparseAttention(layer_idx=layer, num_hidden_layers=NL, num_attention_heads=H,
                                head_dim=D, attention_length=W, max_seq_len=L)
     lay = m.layout(dev)
-    kernel = prefill_kernel(lay, L, B, D)
-    if kernel == "tile":
-        lay.stages().schedule(L, B)
+    split = prefill_split(lay, L, B, D)
+    kernel = "band" if split == 0 else ("tile" if split == L else "split")
+    if kernel != "band":
+        lay.stages(64, 128).schedule(split, B)
+        lay.stages(64, 128).stage_masks()
     counted = lay.tiles_for(L) * B * 4.0 * 128 * 128 * D
     with torch.no_grad():
         ms = event_ms(torch, lambda: elastic_attention_fwd(q, k, v, lay, m.scaling,
-                                                           return_lse=False, kernel=kernel),
+                                                           return_lse=False),
                       steps, warmup)
-    executed = executed_flops(torch, kernel, lay, B, H, L, D)
+    executed = executed_flops(torch, kernel, lay, B, H, L, D, split)
     prof = f"{kernel}_fwd_kernel_bf16_B{B}_H{H}_L{L}_D{D}_layer{layer}_pmc.md"
     out = {"workload": f"bf16 B={B} H={H} L={L} D={D}, w={W}, layer {layer} of {NL}",
            "kernel": kernel, "fwd_ms": round(ms, 4),
@@ -535,6 +559,8 @@ def one_config(torch, cfg: str, layer: int, dev, steps: int, warmup: int, with_b
            "executed_flop_fraction": round(executed / counted, 4),
            "roofline": roofline_of(layer, ms, executed, alg_bytes_of(B, H, L, D),
                                    figure_from_profile(prof))}
+    if kernel == "split":
+        out["split_row"] = split  # tile kernel on rows [0, split), band kernel on the rest
     if with_bwd:
         try:
             bwd = time_backward(torch, lay, q, k, v, m.scaling, counted, steps, warmup)
@@ -673,7 +699,7 @@ def main() -> None:
     if args.lds_probe:
         print(json.dumps({"lds_read": lds_probe(torch)}), flush=True)
         return
-    from elastic_sparse_attention import ElasticSparseAttention, prefill_kernel
+    from elastic_sparse_attention import ElasticSparseAttention, prefill_split
 
     B, H, L, D, _, _ = CONFIGS[args.config]
     dev = torch.device("cuda", 0)
@@ -686,13 +712,17 @@ def main() -> None:
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     lay = m.layout(dev)           # 128 x 128 tiles: the declared (counted) tile
-    kernel = prefill_kernel(lay, L, B, D) if args.kernel == "auto" else args.kernel
-    if kernel == "tile":
+    # the module's choice: one kernel, or the tile kernel on rows [0, split)
+    # and the band kernel on the rest
+    split = prefill_split(lay, L, B, D) if args.kernel == "auto" else \
+        (0 if args.kernel == "band" else L)
+    kernel = "band" if split == 0 else ("tile" if split == L else "split")
+    if kernel != "band":
         st = lay.stages(64, 128)      # 128 x 64 blocks: the tile kernel's staging unit
-        st.schedule(L, B)
+        st.schedule(split, B)
         if args.layer > 0:
             st.stage_masks()          # per-stage row masks, once per pattern
-    m.prefill_kernel = kernel
+    m.prefill_kernel = "auto" if kernel == "split" else kernel
     torch.cuda.synchronize()
     layout_ms = (time.perf_counter() - t0) * 1e3
 
@@ -703,9 +733,13 @@ def main() -> None:
     alg_bytes = alg_bytes_of(B, H, L, D)
 
     with torch.no_grad():
+        t0 = time.perf_counter()
         for _ in range(args.warmup):
             m(q, k, v)
         torch.cuda.synchronize()
+        while (time.perf_counter() - t0) * 1e3 < WARM_MS:  # clocks up before timing
+            m(q, k, v)
+            torch.cuda.synchronize()
         # timed region: K forwards, each bracketed by HIP events on the stream
         # the module launches on (torch's current stream), wall clock around all K
         stream = torch.cuda.current_stream(dev)
@@ -722,7 +756,7 @@ def main() -> None:
     kern_ms = statistics.mean(s.elapsed_time(e) for s, e in evs)
 
     value = counted / wall / 1e12
-    executed = executed_flops(torch, kernel, lay, B, H, L, D)
+    executed = executed_flops(torch, kernel, lay, B, H, L, D, split)
     prof = f"{kernel}_fwd_kernel_bf16_B{B}_H{H}_L{L}_D{D}_layer{args.layer}_pmc.md"
     traffic = figure_from_profile(prof)
     l2_bytes = figure_from_profile(prof, "l2_to_cu_bytes_per_launch")
@@ -744,7 +778,8 @@ def main() -> None:
                                 f"128x128 tiles"),
                    "batch": B, "heads": H, "seq_len": L, "head_dim": D,
                    "attention_length": W, "layer_idx": args.layer, "num_hidden_layers": NL,
-                   "block": [128, 128], "active_tiles": tiles, "kernel": kernel},
+                   "block": [128, 128], "active_tiles": tiles, "kernel": kernel,
+                   **({"split_row": split} if kernel == "split" else {})},
         "counted_pct_of_bf16_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
         "kernel_ms": round(kern_ms, 4),
         "executed_flop_fraction": round(executed / counted, 4),

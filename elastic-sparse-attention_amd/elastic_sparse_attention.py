@@ -251,6 +251,9 @@ class ElasticLayout:
         self._stages = _LRU(self.STAGE_CACHE)         # (block_m, block_n) -> layout
         self._stage_masks = None  # tensor, False (none: over budget), or unbuilt
         self._tiles_for = _LRU(self.COUNT_CACHE)      # q_len -> active tiles
+        self._splits = _LRU(self.COUNT_CACHE)         # (q_len, batch, D) -> split row
+        self._positions = _LRU(self.SCHEDULE_CACHE)   # (row0, q_len) -> device positions
+        self._block_cum = None  # cumulative listed blocks per query block, all heads
 
     # cache capacities: work lists and backward plans are device arrays sized
     # by the batch and the tile count (about 563K tiles at H=32 L=32768 layer
@@ -322,6 +325,25 @@ class ElasticLayout:
         nxt = self.row_ptr_host.view(-1)[1:].view(self.pattern.num_heads, self.num_qblocks)
         got = int((nxt[:, :nq] - rp[:, :nq]).sum())
         self._tiles_for[int(q_len)] = got
+        return got
+
+    def block_cumsum(self) -> torch.Tensor:
+        """float64 ``[nqb + 1]``: blocks listed for query blocks 0 .. i - 1,
+        summed over heads (one batch element); host, cached."""
+        if self._block_cum is None:
+            H = self.pattern.num_heads
+            rp = self.row_ptr_host.to(torch.int64)
+            per = (rp[1:] - rp[:-1]).view(H, self.num_qblocks).sum(0).double()
+            self._block_cum = torch.cat([torch.zeros(1, dtype=torch.float64), per.cumsum(0)])
+        return self._block_cum
+
+    def positions(self, row0: int, q_len: int) -> torch.Tensor:
+        """int64 ``arange(row0, q_len)`` on the layout's device, cached."""
+        key = (int(row0), int(q_len))
+        got = self._positions.get(key)
+        if got is None:
+            got = torch.arange(row0, q_len, dtype=torch.int64, device=self.device)
+            self._positions[key] = got
         return got
 
     def schedule(self, q_len: int, batch: int) -> Tuple[torch.Tensor, int]:
@@ -501,6 +523,63 @@ def prefill_kernel(layout: ElasticLayout, q_len: int, batch: int, head_dim: int)
     return "band" if _band_beats_tile(layout, q_len, batch, head_dim, BAND_CROSSOVER) else "tile"
 
 
+# A prefill split by rows: the tile kernel on rows [0, R), the band kernel
+# (at positions R ..) on [R, q_len).  A dilated layer's low rows list few
+# blocks (narrow windows: the tile kernel's work grows with them) and its
+# high rows many (the band kernel's work per 16-row group is about fixed),
+# so where both kernels are close over the whole prefill, each taking its
+# own rows beats either.  Cost model (ms) fitted to the two kernels timed on
+# row ranges at every split in 1/8 steps of B=8 H=16 L=4096 D=64 and B=1
+# H=32 L=8192 / 32768 D=128, layers 2, 4 and 7 (MI355X): a x (64 x 32
+# blocks the tile rows list) + (b0 + b1 alpha) x (16-row groups of the band
+# rows) + per-launch overheads (alpha = the layer's interpolation weight:
+# later layers have narrower bands and cheaper groups).  The split is taken
+# only where the model puts it SPLIT_MIN_GAIN below the better single
+# kernel.  Measured with the split the model picks: B=8 H=16 L=4096 D=64
+# layer 7 (rows from 1664) 0.258 vs 0.281 ms for the band kernel alone,
+# B=1 H=32 L=8192 D=128 layer 4 (from 3584) 0.287 vs 0.308 ms, B=1 H=32
+# L=32768 layer 2 (from 7552) 1.281 vs 1.387 ms; L=8192 layer 7, where the
+# model predicts 7%, 0.277 vs 0.271 ms (the band kernel alone stays there).
+# The two launches run in sequence: on two streams they were 1-5% slower.
+SPLIT_MODEL = {64: (6.66e-7, 1.048e-5, -1.916e-6, 0.0126, 0.0244),
+               128: (1.157e-6, 2.118e-5, -3.321e-6, 0.0124, 0.0167)}
+SPLIT_MIN_GAIN = 0.08
+
+
+def prefill_split(layout: ElasticLayout, q_len: int, batch: int, head_dim: int) -> int:
+    """The row R from which the band kernel takes a prefill's rows, the tile
+    kernel taking rows [0, R): q_len for the tile kernel alone, 0 for the
+    band kernel alone, else a multiple of 128 (see SPLIT_MODEL); cached per
+    shape."""
+    key = (int(q_len), int(batch), int(head_dim))
+    got = layout._splits.get(key)
+    if got is not None:
+        return got
+    single = prefill_kernel(layout, q_len, batch, head_dim)
+    R = 0 if single == "band" else q_len
+    p = layout.pattern
+    if head_dim in SPLIT_MODEL and p.layer_idx > 0 and q_len >= 256 and \
+            p.attention_length <= 64 and p.seq_len < (1 << 24):
+        a, b0, b1, o_tile, o_band = SPLIT_MODEL[head_dim]
+        alpha = p.layer_idx / (p.num_hidden_layers - 1) if p.num_hidden_layers > 1 else 0.0
+        st = layout.stages()
+        cum = st.block_cumsum()
+        bm = st.pattern.block_m
+        per_group = (b0 + b1 * alpha) * batch * p.num_heads
+        rows = torch.arange(128, q_len, 128, dtype=torch.int64)
+        if rows.numel() > 0:
+            tile = a * batch * cum[torch.clamp((rows + bm - 1) // bm, max=cum.numel() - 1)]
+            band = per_group * ((q_len - rows + 15) // 16).double()
+            cost = tile + band + o_tile + o_band
+            i = int(torch.argmin(cost))
+            tile_only = a * batch * float(cum[min((q_len + bm - 1) // bm, cum.numel() - 1)]) + o_tile
+            band_only = per_group * ((q_len + 15) // 16) + o_band
+            if float(cost[i]) <= (1.0 - SPLIT_MIN_GAIN) * min(tile_only, band_only):
+                R = int(rows[i])
+    layout._splits[key] = R
+    return R
+
+
 def bwd_kernels(layout: ElasticLayout, q_len: int, batch: int, head_dim: int
                 ) -> Tuple[str, str]:
     """("band" | "tile", "band" | "tile"): the faster dQ and dK/dV kernels for
@@ -553,22 +632,35 @@ def _prefill_fwd(q, k, v, layout, scaling, return_lse, out, key_block, query_blo
     B, H, Lq, D = q.shape
     if kernel not in ("auto", "tile", "band"):
         raise ValueError(f"kernel must be 'auto', 'tile' or 'band', got {kernel!r}")
+    split = Lq
     if kernel == "auto":
-        kernel = prefill_kernel(layout, Lq, B, D)
+        split = prefill_split(layout, Lq, B, D)
+        kernel = "band" if split == 0 else "tile"
         if out is not None and out.data_ptr() % 16 != 0:
-            kernel = "tile"
+            kernel, split = "tile", Lq
     if kernel == "band":
         return elastic_attention_band(q, k, v, layout.pattern, scaling, return_lse, out)
     q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
     o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
+    if 0 < split < Lq:
+        # rows [split, Lq) by the band kernel at their positions, then rows
+        # [0, split) by the tile kernel below (views of the same o and lse)
+        _band_launch(q[:, :, split:], k, v, o[:, split:], None if lse is None else
+                     lse[:, :, split:], layout.pattern, scaling, layout.positions(split, Lq))
+        q, o_all, lse_all = q[:, :, :split], o, lse
+        o = o[:, :split]
+        lse = None if lse is None else lse[:, :, :split]
+        Lq = split
+    else:
+        o_all, lse_all = o, lse
     if query_block is None and key_block is None:
         query_block, key_block = 128, 64
     if (query_block, key_block) not in ((128, 64), (128, 128), (64, 32)):
         raise ValueError(f"(query_block, key_block) must be (128, 64), (128, 128) or (64, 32), "
                          f"got ({query_block}, {key_block})")
     if B == 0 or Lq == 0:
-        return o, lse  # no rows: nothing to launch (empty tensors may have no address)
+        return o_all, lse_all  # no rows: nothing to launch (empty tensors may have no address)
     st = layout if (query_block, key_block) == (128, 128) else layout.stages(key_block,
                                                                              query_block)
     items, n = st.schedule(Lq, B)
@@ -586,7 +678,7 @@ def _prefill_fwd(q, k, v, layout, scaling, return_lse, out, key_block, query_blo
                                  masks.numel() if masks is not None else 0,
                                  ctypes.c_void_p(items.data_ptr()), n, _stream(q.device)),
           "esa_elastic_fwd")
-    return o, lse
+    return o_all, lse_all
 
 
 def elastic_attention_band(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -607,13 +699,20 @@ def elastic_attention_band(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     q, k, v = _prep(q, 8), _prep(k, 8), _prep(v, 8)
     o = out if out is not None else torch.empty(B, Lq, H, D, dtype=q.dtype, device=q.device)
     lse = torch.empty(B, H, Lq, dtype=torch.float32, device=q.device) if return_lse else None
+    _band_launch(q, k, v, o, lse, pattern, scaling, positions)
+    return o, lse
+
+
+def _band_launch(q, k, v, o, lse, pattern, scaling, positions) -> None:
+    """esa_elastic_fwd_band into o ``[B, Lq, H, D]`` (and lse) for q's rows
+    (q, k, v prepared, o's rows 16-byte aligned)."""
+    B, H, Lq, D = q.shape
     positions, pos_ptr = _positions_ptr(positions, Lq, q.device)
     if B == 0 or Lq == 0:
-        return o, lse
+        return
     a = _fwd_args(q, k, v, o, (o.stride(0), o.stride(2), o.stride(1)), lse, scaling)
     check(load().esa_elastic_fwd_band(ctypes.byref(a), ctypes.byref(pattern), pos_ptr,
                                       _stream(q.device)), "esa_elastic_fwd_band")
-    return o, lse
 
 
 def _positions_ptr(positions: Optional[torch.Tensor], q_len: int, device: torch.device):

@@ -606,3 +606,36 @@ def test_empty_inputs(D):
             if kg.grad.numel():
                 assert torch.count_nonzero(kg.grad) == 0 and torch.count_nonzero(vg.grad) == 0
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("L,H,B,D,layer,split", [
+    (4096, 16, 8, 64, 7, True), (8192, 32, 1, 128, 4, True), (4096, 16, 8, 64, 4, False),
+    (1024, 4, 1, 128, 5, None),
+])
+def test_split_prefill(L, H, B, D, layer, split):
+    """The module's row split (tile kernel on rows [0, R), band kernel at
+    positions R .. on the rest): taken where the cost model puts it well
+    below either kernel alone; its output and log-sum-exp agree with each
+    kernel alone to bf16 rounding, and rows below R are the tile kernel's
+    bits (the band kernel's rows start their entry walks at other entries
+    than in a launch over all rows, so they agree to rounding)."""
+    from elastic_sparse_attention import prefill_split
+    print(f"split B={B} H={H} L={L} D={D} layer={layer}", flush=True)
+    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+    R = prefill_split(lay, L, B, D)
+    if split is True:
+        assert 0 < R < L and R % 128 == 0
+    elif split is False:
+        assert R in (0, L)
+    q, k, v = seeded_inputs(B, H, H, L, D, torch.bfloat16, seed=layer, scale=1.0)
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    sc = D ** -0.5
+    o, lse = elastic_attention_fwd(q, k, v, lay, sc)
+    ot, lt = elastic_attention_fwd(q, k, v, lay, sc, kernel="tile")
+    ob, lb = elastic_attention_fwd(q, k, v, lay, sc, kernel="band")
+    assert float((o.float() - ot.float()).abs().max()) <= 2e-2
+    assert float((lse - lt).abs().max()) <= 2e-3
+    assert float((o.float() - ob.float()).abs().max()) <= 2e-2
+    assert float((lse - lb).abs().max()) <= 2e-3
+    if 0 < R < L:
+        assert torch.equal(o[:, :R], ot[:, :R]) and torch.equal(lse[..., :R], lt[..., :R])
