@@ -26,7 +26,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 SOURCES = ["esa_capi.hip", "esa_layout.hip", "esa_fwd_tile.hip", "esa_fwd_band.hip",
            "esa_bwd_band.hip", "esa_fwd_gather.hip", "esa_bwd_gather.hip", "esa_bwd.hip",
-           "esa_reach.hip", "esa_bwd_fix.hip"]
+           "esa_reach.hip", "esa_bwd_fix.hip", "esa_fwd_window.hip"]
 PROBE_SOURCES = ["esa_probe.hip"]
 LIB = os.path.join(HERE, "libesa.so")
 PROBE_LIB = os.path.join(HERE, "libesa_probe.so")

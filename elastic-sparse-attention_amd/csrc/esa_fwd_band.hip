@@ -636,6 +636,9 @@ void launch_band_elem(const BandArgs& a, int head_dim, dim3 grid, bool kskip, bo
 
 hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) {
   if (a.n_groups <= 0) return hipSuccess;
+  // interpolation weight 0 (a sliding window): every group's bands overlap
+  // in all but one key per step, so the window kernel stages each key once
+  if (window_fwd_applies(a, head_dim)) return launch_window_fwd(a, head_dim, stream);
   dim3 grid((unsigned)(8 * a.per_xcd));
   // The refill order by the entry spacing at the last row, (q_len a + c) / w
   // query rows between one entry's keys and the next's: at B=1 H=8 L=131072

@@ -229,6 +229,9 @@ hipError_t launch_stage_masks(const PatternConsts& pc, const LayoutDims& ld, con
 hipError_t launch_tile_fwd(const TileArgs& a, int head_dim, int64_t num_items,
                            hipStream_t stream);
 hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream);
+// the sliding-window kernel takes the band forward's layer-0 prefills
+bool window_fwd_applies(const BandArgs& a, int head_dim);
+hipError_t launch_window_fwd(const BandArgs& a, int head_dim, hipStream_t stream);
 // prep: the kernel forms and stores delta / lse2 itself (see band_dq_kernel)
 hipError_t launch_bwd_fix(const BwdArgs& a, int head_dim, hipStream_t stream);
 hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2, bool prep,

@@ -517,8 +517,15 @@ def prefill_kernel(layout: ElasticLayout, q_len: int, batch: int, head_dim: int)
     (the band kernel needs attention_length <= 64 and kv_len < 2^24; at head
     dims other than 64 and 128 only the band kernel runs)."""
     p = layout.pattern
-    if head_dim not in BAND_CROSSOVER and band_head_dim(head_dim) and \
-            p.attention_length <= 64 and p.seq_len < (1 << 24):
+    band_ok = band_head_dim(head_dim) and p.attention_length <= 64 and p.seq_len < (1 << 24)
+    if head_dim not in BAND_CROSSOVER and band_ok:
+        return "band"
+    if p.layer_idx == 0 and band_ok:
+        # interpolation weight 0, a sliding window: the band entry point runs
+        # the window kernel, which stages each key of a 32-row group once
+        # (measured against the tile kernel: B=1 H=32 L=32768 D=128 0.240 vs
+        # 0.246 ms, B=8 H=16 L=4096 D=64 0.050 vs 0.055, B=1 H=8 L=131072
+        # 0.251 vs 0.254, B=1 H=32 L=8192 within 1%)
         return "band"
     return "band" if _band_beats_tile(layout, q_len, batch, head_dim, BAND_CROSSOVER) else "tile"
 

@@ -297,6 +297,14 @@ def test_band_all_layers(D):
     # that requests V after PV (the other refill order)
     (1, 3, 3, 16384, 16384, 64, 7, 16, 8),  # odd head count, D = 64
     (2, 2, 1, 12000, 12000, 128, 7, 12, 8),  # GQA, D = 128, spacing exactly 1000
+    # interpolation weight 0: the sliding-window kernel
+    (2, 4, 2, 1000, 1000, 64, 0, 64, 8),    # GQA, partial last group
+    (1, 4, 4, 1024, 700, 128, 0, 64, 8),    # q_len < kv_len
+    (1, 2, 2, 5, 5, 64, 0, 64, 8),          # shorter than one group
+    (1, 3, 3, 1024, 1024, 128, 0, 48, 6),   # w = 48
+    (1, 4, 4, 1024, 1024, 128, 0, 17, 4),   # w = 17: one chunk pair per group
+    (3, 2, 1, 777, 777, 128, 0, 64, 1),     # one layer (weight 0), MQA, ragged length
+    (1, 2, 2, 4096, 4096, 64, 0, 64, 8),    # many groups per XCD range
 ])
 def test_band_shapes(B, H, Hkv, L, Lq, D, layer, w, nl):
     print(f"band shape B={B} H={H} Hkv={Hkv} L={L} Lq={Lq} D={D} layer={layer} w={w} nl={nl}",
@@ -325,7 +333,7 @@ def test_band_sharp_softmax_outliers():
 
 
 @pytest.mark.parametrize("L,H,B,D,layer,want,want_bwd", [
-    (32768, 32, 1, 128, 4, "band", "band/band"), (32768, 32, 1, 128, 0, "tile", "tile/tile"),
+    (32768, 32, 1, 128, 4, "band", "band/band"), (32768, 32, 1, 128, 0, "band", "tile/tile"),
     (8192, 32, 1, 128, 3, "tile", "tile/tile"), (8192, 32, 1, 128, 4, "band", "band/band"),
     (4096, 32, 4, 128, 7, "tile", "tile/tile"),
     (8192, 32, 1, 128, 5, "band", "band/band"), (4096, 16, 8, 64, 6, "band", "band/tile"),

@@ -85,11 +85,14 @@ def rows_path(q, k, v, pat, D):
 
 # (kernel, layer, L, H, D, w, dtype): the band kernel's early and late V
 # refill orders (w = 2 at the last layer puts the entry spacing past 1000
-# rows), both head dims, float16, and the tile kernel's three staging shapes
+# rows), both head dims, float16, its layer-0 (sliding-window) kernel, and
+# the tile kernel's three staging shapes
 NF_CASES = [("band", 4, 2048, 4, 128, 64, torch.bfloat16),
             ("band", 7, 2048, 4, 64, 64, torch.bfloat16),
             ("band", 7, 2048, 4, 128, 2, torch.bfloat16),
             ("band", 5, 1500, 3, 128, 64, torch.float16),
+            ("band", 0, 2048, 4, 128, 64, torch.bfloat16),
+            ("band", 0, 1500, 3, 64, 48, torch.float16),
             ("tile", 4, 2048, 4, 128, 64, torch.bfloat16),
             ("tile", 0, 2048, 4, 128, 64, torch.bfloat16),
             ("tile", 2, 1024, 4, 64, 64, torch.float16),
@@ -152,7 +155,7 @@ def test_mfma_paths_reference_semantics(kernel, layer, L, H, D, w, dtype):
     assert float((bad.float() - ref.float())[fin].abs().max()) <= 2e-2
 
 
-@pytest.mark.parametrize("kernel,layer,L,H,D,w,dtype", NF_CASES[:2] + NF_CASES[4:8])
+@pytest.mark.parametrize("kernel,layer,L,H,D,w,dtype", NF_CASES[:2] + NF_CASES[4:10])
 def test_mfma_paths_nonfinite_k(kernel, layer, L, H, D, w, dtype):
     """K planted with +Inf, -Inf and NaN: a row attending a planted key gets a
     non-finite score there (NaN output, or, for a -Inf score, that key's
