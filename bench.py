@@ -454,6 +454,12 @@ def roofline_of(layer: int, kern_ms: float, executed: float, alg_bytes: int, tra
             "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4), "traffic": traffic}
 
 
+def profiled_kernel(kernel: str, layer: int) -> str:
+    """The kernel whose profiles/ summary covers a prefill: the band entry
+    point runs the sliding-window kernel at layer 0."""
+    return "window_fwd_kernel" if kernel == "band" and layer == 0 else f"{kernel}_fwd_kernel"
+
+
 def figure_from_profile(name: str, key: str = "traffic_bytes_per_launch"):
     """A per-launch figure of a kernel (HBM bytes by default) from the
     committed rocprofv3 --pmc summary for this workload (profiles/<name>), or
@@ -552,7 +558,7 @@ def one_config(torch, cfg: str, layer: int, dev, steps: int, warmup: int, with_b
                                                            return_lse=False),
                       steps, warmup)
     executed = executed_flops(torch, kernel, lay, B, H, L, D, split)
-    prof = f"{kernel}_fwd_kernel_bf16_B{B}_H{H}_L{L}_D{D}_layer{layer}_pmc.md"
+    prof = f"{profiled_kernel(kernel, layer)}_bf16_B{B}_H{H}_L{L}_D{D}_layer{layer}_pmc.md"
     out = {"workload": f"bf16 B={B} H={H} L={L} D={D}, w={W}, layer {layer} of {NL}",
            "kernel": kernel, "fwd_ms": round(ms, 4),
            "counted_tflops": round(counted / (ms * 1e-3) / 1e12, 3),
@@ -757,7 +763,7 @@ def main() -> None:
 
     value = counted / wall / 1e12
     executed = executed_flops(torch, kernel, lay, B, H, L, D, split)
-    prof = f"{kernel}_fwd_kernel_bf16_B{B}_H{H}_L{L}_D{D}_layer{args.layer}_pmc.md"
+    prof = f"{profiled_kernel(kernel, args.layer)}_bf16_B{B}_H{H}_L{L}_D{D}_layer{args.layer}_pmc.md"
     traffic = figure_from_profile(prof)
     l2_bytes = figure_from_profile(prof, "l2_to_cu_bytes_per_launch")
     out = {
