@@ -25,17 +25,23 @@
 // in contiguous ranges (rows ascending within a head), so consecutive groups
 // of one head, which share all but 16 of their keys, run on one L2.
 //
+// POS: rows at positions A.positions[r] (a chunked prefill's cache_position).
+// A group whose rows sit at consecutive positions, all in [0, kv_len), runs
+// from its first row's position; any other group computes its rows one at a
+// time with the per-row gather, as band_fwd_kernel does.
+//
 // Non-finite K / V: as in band_fwd_kernel, a group whose output met a
 // non-finite value (V rows of keys outside a row's window meet p = 0, and
 // 0 * Inf = NaN) runs again with the staged V operands sanitised, and each
 // row's own non-finite V values are put back from its entries.
 #include "esa_band.hpp"
+#include "esa_gather.hpp"
 
 namespace esa {
 
 namespace {
 
-template <int D, int G, Elem E>
+template <int D, int G, Elem E, bool POS>
 __global__ __launch_bounds__(64, 2) void window_fwd_kernel(BandArgs A) {
   using C = BandCfg<D>;
   using M = MmaT<E>;
@@ -56,19 +62,55 @@ __global__ __launch_bounds__(64, 2) void window_fwd_kernel(BandArgs A) {
 
   const int lane = threadIdx.x;
   const int n = lane & 15, q = lane >> 4;
-  const int r0 = gq * 16 * G;
+  const int r0 = gq * 16 * G;  // the group's first row (of q, o and lse)
   const int w = A.pc.w;
-  // the group's keys [k0, k1): the windows of its rows (rows past q_len
-  // attend nothing)
-  const int k0 = max(r0 - w + 1, 0);
-  const int k1 = min(r0 + 16 * G, A.q_len);
+  const int n_rows = min(16 * G, A.q_len - r0);
+  int base = r0;  // the first row's position
+  if constexpr (POS) {
+    int64_t p0 = A.positions[r0];
+    p0 = p0 < 0 ? p0 + A.kv_len : p0;
+    base = __builtin_amdgcn_readfirstlane((int)(p0 >= 0 && p0 < A.kv_len ? p0 : 0));
+    bool bad = !(p0 >= 0 && p0 < A.kv_len);
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const int r = r0 + 16 * u + n;
+      if (r < A.q_len) {
+        int64_t p = A.positions[r];
+        p = p < 0 ? p + A.kv_len : p;
+        bad |= !(p >= 0 && p < A.kv_len && p == (int64_t)base + 16 * u + n);
+      }
+    }
+    if (wave_any(bad)) {
+      // positions not consecutive (or out of range): the rows one at a time,
+      // by the per-row gather, with the first K slot as its 384-float scratch
+      GatherArgs Gr{};
+      Gr.q = A.q; Gr.k = A.k; Gr.v = A.v; Gr.o = A.o; Gr.lse = A.lse;
+      Gr.qsb = A.qsb; Gr.qsh = A.qsh; Gr.qss = A.qss;
+      Gr.ksb = A.ksb; Gr.ksh = A.ksh; Gr.kss = A.kss;
+      Gr.vsb = A.vsb; Gr.vsh = A.vsh; Gr.vss = A.vss;
+      Gr.osb = A.osb; Gr.osh = A.osh; Gr.oss = A.oss;
+      Gr.lsb = A.lsb; Gr.lsh = A.lsh;
+      Gr.H = A.H; Gr.groups = A.groups; Gr.q_len = A.q_len; Gr.kv_len = A.kv_len; Gr.D = D;
+      Gr.sm_scale = A.sm_scale;
+      Gr.elem = A.elem;
+      Gr.src.w = A.pc.w; Gr.src.kv_len = A.kv_len; Gr.src.pc = A.pc;
+      Gr.src.positions = A.positions;
+      for (int rr = 0; rr < n_rows; ++rr)
+        gather_one_row_any<E, true>(Gr, b, h, r0 + rr, (float*)ks0, lane);
+      return;
+    }
+  }
+  // the group's keys [k0, k1): the windows of its rows (positions base ..
+  // base + n_rows - 1)
+  const int k0 = max(base - w + 1, 0);
+  const int k1 = base + n_rows;
   const int n_pairs = (k1 - k0 + 31) / 32;
   // row 16 u + n of the group: its window as offsets from k0
   int lo[G], hi[G];
 #pragma unroll
   for (int u = 0; u < G; ++u) {
-    const int i = r0 + 16 * u + n;
-    const bool ok = i < A.q_len;
+    const int i = base + 16 * u + n;
+    const bool ok = 16 * u + n < n_rows;
     lo[u] = ok ? max(i - w + 1, 0) - k0 : 1;
     hi[u] = ok ? i - k0 : 0;
   }
@@ -85,12 +127,12 @@ __global__ __launch_bounds__(64, 2) void window_fwd_kernel(BandArgs A) {
   V8 qop[G][C::NS];
 #pragma unroll
   for (int u = 0; u < G; ++u) {
-    const int i = r0 + 16 * u + n;
-    const uint16_t* qrow = A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)i * A.qss;
+    const int r = r0 + 16 * u + n;
+    const uint16_t* qrow = A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)r * A.qss;
 #pragma unroll
     for (int s = 0; s < C::NS; ++s) {
       u32x4 raw = {0u, 0u, 0u, 0u};
-      if (i < A.q_len) raw = *(const u32x4*)(qrow + 32 * s + 8 * q);
+      if (r < A.q_len) raw = *(const u32x4*)(qrow + 32 * s + 8 * q);
       qop[u][s] = __builtin_bit_cast(V8, raw);
     }
   }
@@ -271,10 +313,10 @@ __global__ __launch_bounds__(64, 2) void window_fwd_kernel(BandArgs A) {
     l_tot += __shfl_xor(l_tot, 32, 64);
     n_tot += __shfl_xor(n_tot, 16, 64);
     n_tot += __shfl_xor(n_tot, 32, 64);
-    const int i = r0 + 16 * u + n;
-    if (i >= A.q_len) continue;
+    const int r = r0 + 16 * u + n, i = base + 16 * u + n;  // row, position
+    if (r >= A.q_len) continue;
     const float inv = n_tot > 0.f ? 1.f / n_tot : 0.f;
-    uint16_t* orow = A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)i * A.oss;
+    uint16_t* orow = A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)r * A.oss;
 #pragma unroll
     for (int t = 0; t < C::NV / 2; ++t) {
       V8 ov;
@@ -288,7 +330,7 @@ __global__ __launch_bounds__(64, 2) void window_fwd_kernel(BandArgs A) {
     if (A.lse && q == 0) {
       const float lse = l_tot > 0.f ? (m_run[u] + __log2f(l_tot)) * 0.69314718055994530942f
                                     : -INFINITY;
-      A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + i] = lse;
+      A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + r] = lse;
     }
     if (rerun) {
       int dim0[C::CW / 4];
@@ -308,8 +350,7 @@ __global__ __launch_bounds__(64, 2) void window_fwd_kernel(BandArgs A) {
 }  // namespace
 
 bool window_fwd_applies(const BandArgs& a, int head_dim) {
-  return a.pc.a == 0.0f && !a.positions && a.d_real == head_dim &&
-         (head_dim == 64 || head_dim == 128);
+  return a.pc.a == 0.0f && a.d_real == head_dim && (head_dim == 64 || head_dim == 128);
 }
 
 // rows per wave: 16 WINDOW_G (two 16-row groups share each chunk's staging)
@@ -322,7 +363,11 @@ void launch_window_d(const BandArgs& a, hipStream_t stream) {
   const int64_t n = (int64_t)a.n_groups / a.ng * w.ng;  // batch * H * ng
   w.n_groups = (int)n;
   w.per_xcd = (int)((n + 7) / 8);
-  window_fwd_kernel<D, WINDOW_G, E><<<dim3((unsigned)(8 * w.per_xcd)), 64, 0, stream>>>(w);
+  const dim3 grid((unsigned)(8 * w.per_xcd));
+  if (a.positions)
+    window_fwd_kernel<D, WINDOW_G, E, true><<<grid, 64, 0, stream>>>(w);
+  else
+    window_fwd_kernel<D, WINDOW_G, E, false><<<grid, 64, 0, stream>>>(w);
 }
 
 hipError_t launch_window_fwd(const BandArgs& a, int head_dim, hipStream_t stream) {

@@ -126,3 +126,26 @@ def test_module_chunked_prefill(dtype):
     for got, ref in ((qd.grad, qf.grad), (kd.grad, kf.grad), (vd.grad, vf.grad)):
         err = (got.float().cpu() - ref).abs().max().item()
         assert err <= 2e-2 * ref.abs().max().item(), err
+
+
+@pytest.mark.parametrize("p0,Lq,D,w", [(1500, 548, 128, 64), (37, 300, 64, 64), (0, 100, 128, 17),
+                                       (2000, 48, 64, 48)])
+def test_window_chunk_at_offset(p0, Lq, D, w):
+    """Layer 0 (the sliding-window kernel) at cache_position rows: 32-row
+    groups of consecutive positions from p0 (not a multiple of 16, ragged
+    last group) run from their first position."""
+    print(f"window positions p0={p0} Lq={Lq} D={D} w={w}", flush=True)
+    pos = torch.arange(p0, p0 + Lq, dtype=torch.int64)
+    check_rows(1, 4, 2, 2048, D, 0, pos, w=w)
+
+
+def test_window_mixed_and_negative_positions():
+    """Layer 0: groups that are not consecutive take the per-row gather
+    (a jump inside a 32-row group, repeated and shuffled positions), and
+    negative positions count from kv_len."""
+    L = 1500
+    g = torch.Generator().manual_seed(4)
+    runs = [torch.arange(100, 150), torch.arange(700, 714), torch.tensor([5, 5, 5]),
+            torch.randperm(L, generator=g)[:40], torch.arange(1470, 1500) - L]
+    pos = torch.cat(runs).to(torch.int64)
+    check_rows(2, 8, 2, L, 128, 0, pos)
