@@ -225,8 +225,12 @@ esa_status esa_build_stage_masks(const esa_pattern* p, const int32_t* row_ptr,
  * consecutive rows mostly use at most 16 consecutive keys of each band
  * (wider bands are handled, more slowly):
  * one wave gathers each band's keys once for its 16 rows and runs QK^T and
- * PV on bf16 MFMA with float32 accumulation and online softmax.  Same
- * outputs as esa_elastic_fwd within bf16 rounding.  Requires dtype
+ * PV on bf16 MFMA with float32 accumulation and online softmax.  At
+ * interpolation weight 0 (layer 0: every row attends the keys
+ * max(0, i - w + 1) .. i) with head_dim 64 or 128, a sliding-window kernel
+ * runs instead: one wave per 32 rows (groups of 32 at positions), each key
+ * of their windows staged once.  Same outputs as esa_elastic_fwd within
+ * bf16 rounding.  Requires dtype
  * ESA_BF16 or ESA_F16, head_dim a multiple of 8 up to 256 (kernels at 64,
  * 128 and 256; other head dims run the next of them with zero padding),
  * attention_length <= 64, kv_len < 2^24,
