@@ -408,12 +408,24 @@ def band_bwd_executed_flops(torch, lay, B: int, H: int, Hkv: int, L: int, D: int
     (row, entry) pairs whose key lies in the block (ceil(pairs / 32) steps),
     2 D/32 for S, 2 D/32 for dP, D/16 each for dV^T and dK^T.  The pairs per
     (head, block) are counted from the pattern's index lists built on the
-    GPU."""
+    GPU.  At layer 0 (interpolation weight 0, a sliding window) the kernels
+    walk the window directly: band_dq_kernel per group and pair of 16-key
+    chunks of keys [max(16 g - w + 1, 0), min(16 g + 16, L)), band_dkdv_kernel
+    per block, query head and 32-row step of rows [16 b, min(16 b + 15 + w,
+    L)), with the same MFMAs per pair and step."""
     from elastic_sparse_attention import build_indices
+    dq_unit = (4 * (D // 32) + D // 16) * 16384
+    dkdv_unit = (4 * (D // 32) + 2 * (D // 16)) * 16384
+    if lay.pattern.layer_idx == 0:
+        pairs = steps = 0
+        for g in range((L + 15) // 16):
+            pairs += (min(16 * g + 16, L) - max(16 * g - w + 1, 0) + 31) // 32
+            steps += (min(16 * g + 15 + w, L) - 16 * g + 31) // 32
+        return {"dq": float(B * H * pairs * dq_unit), "dkdv": float(B * H * steps * dkdv_unit)}
     pairs = 0
     for g in range((L + 15) // 16):
         pairs += (min(w, 16 * g + 16) + 1) // 2
-    dq = float(B * H * pairs * (4 * (D // 32) + D // 16) * 16384)
+    dq = float(B * H * pairs * dq_unit)
     idx, msk = build_indices(lay.pattern, lay.device, torch.int32)
     nblk = (L + 15) // 16
     steps = 0
@@ -422,7 +434,7 @@ def band_bwd_executed_flops(torch, lay, B: int, H: int, Hkv: int, L: int, D: int
         cnt = torch.bincount(keys, minlength=nblk)
         steps += int(((cnt + 31) // 32).sum().item())
     del idx, msk
-    dkdv = float(B * steps * (4 * (D // 32) + 2 * (D // 16)) * 16384)
+    dkdv = float(B * steps * dkdv_unit)
     return {"dq": dq, "dkdv": dkdv}
 
 

@@ -33,7 +33,11 @@ namespace esa {
 // dK/dV kernel, which then runs after it; block 0 also clears the split
 // arrival counters.  Used when both halves are band kernels, so no separate
 // pass re-reads O and dO.
-template <int D, bool VSKIP, bool PREP, Elem E>
+// WIN: interpolation weight 0 (layer 0, a sliding window): row i attends
+// the keys max(0, i - w + 1) .. i, so the group's keys come in 16-key
+// chunks (two per MFMA k-step, about three pairs at w = 64) and every key of
+// a row's window is kept, instead of 64 bands of one key per row.
+template <int D, bool VSKIP, bool PREP, Elem E, bool WIN = false>
 __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* lse2) {
   using M = MmaT<E>;
   using V8 = typename M::v8;
@@ -160,8 +164,9 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   // unchanged at B=1 H=32 L=32768 (and 9/64 at D = 64 within 1% of 12/64)
   // (unsigned: the product wraps for grids near 2^31 blocks; only the value
   // mod 64 matters)
-  band_rows(A.pc, h, i, row_ok, q, n,
-            (int)(((unsigned)(bid >> 3) * (D == 128 ? 19u : 12u) / 64u) & 63u), kd, info1);
+  if constexpr (!WIN)
+    band_rows(A.pc, h, i, row_ok, q, n,
+              (int)(((unsigned)(bid >> 3) * (D == 128 ? 19u : 12u) / 64u) & 63u), kd, info1);
 
   const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
   const char* const vbase = (const char*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh);
@@ -284,6 +289,70 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
     }
   };
 
+  if constexpr (WIN) {
+    // ---- the window's 16-key chunks [k0 + 16 c, ..), two per pair: per
+    // pair, both chunks' K and V are waited for together, read, and the next
+    // pair's requested (every wait is vmcnt(0))
+    const int w = A.pc.w;
+    const int r0 = gq * 16;
+    const int k0 = max(r0 - w + 1, 0), k1 = min(r0 + 16, A.q_len);
+    const int n_pairs = (k1 - k0 + 31) / 32;
+    // this lane's row window as offsets from k0 (none past q_len)
+    const int lo_k = row_ok ? max(i - w + 1, 0) - k0 : 1;
+    const int hi_k = row_ok ? i - k0 : 0;
+    auto desc = [&](int c) {
+      const int c0 = k0 + 16 * c;
+      const int rows = max(min(k1 - c0, 16), 0);
+      return rows > 0 ? (c0 | (rows << 24)) : 0;
+    };
+    // dS of this lane's 4 keys kb0 .. kb0 + 3 (offsets from k0) for its row
+    // as 16-bit values at their register slots; 0 outside the row's window
+    auto win_words = [&](const f32x4& sacc, const f32x4& pacc, int kb0) -> uint64_t {
+      uint64_t wv = 0ull;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool in = kb0 + e >= lo_k && kb0 + e <= hi_k;
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[e], scale2, -l2));
+        const uint64_t bits = (uint64_t)(uint32_t)M::bits(p * (pacc[e] - dl));
+        wv |= in ? bits << (16 * e) : 0ull;
+      }
+      return wv;
+    };
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // the slot zeros are in LDS
+    load_k(desc(0), lk0);
+    load_k(desc(1), lk1);
+    load_v(desc(0), lv0);
+    load_v(desc(1), lv1);
+    for (int p = 0; p < n_pairs; ++p) {
+      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this pair's K and V are in LDS
+      f32x4 sa, sb;
+      s16x4 ta[C::NV], tb[C::NV];
+      V8 va[C::NS], vb[C::NS];
+      {
+        V8 ka[C::NS], kb[C::NS];
+        read_rows(ks0, ka);
+        read_rows(ks1, kb);
+        sa = product(ka, qop);
+        sb = product(kb, qop);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      read_tr(ks0, ta);
+      read_tr(ks1, tb);
+      read_rows(vs0, va);
+      read_rows(vs1, vb);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // slots read: refill them
+      if (p + 1 < n_pairs) {
+        load_k(desc(2 * p + 2), lk0);
+        load_k(desc(2 * p + 3), lk1);
+        load_v(desc(2 * p + 2), lv0);
+        load_v(desc(2 * p + 3), lv1);
+      }
+      const f32x4 pa = product(va, dop);
+      const f32x4 pb = product(vb, dop);
+      dq_step(ta, tb, win_words(sa, pa, 32 * p + 4 * q), win_words(sb, pb, 32 * p + 16 + 4 * q));
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  } else {
   // ---- band pairs: per pair, K reads, then K of the next pair; V reads,
   // then V of the next pair.  So before the V wait exactly the next pair's K
   // DMAs may be newer, and before the K wait this pair's V DMAs (2 VLOADS of
@@ -396,6 +465,8 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
     }
   }
 
+  }
+
   // ---- the group's non-finite flag (staged K rows a row does not list meet
   // dS = 0 in dQ^T, and 0 * Inf is NaN: bwd_fix_kernel recomputes such a
   // group exactly)
@@ -460,8 +531,14 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
 // and the part that arrives last (an atomic counter) adds the parts in part
 // order and writes the block, so results do not depend on which wave is
 // last.
+//
+// WIN: interpolation weight 0 (layer 0, a sliding window).  Key u is
+// attended by rows u .. u + w - 1, so the block's rows are the one range
+// [u0, u0 + 15 + w) (clipped to q_len), walked once per query head, and a
+// slot row keeps every block key of its window (key <= row < key + w)
+// instead of the one key of an entry.
 
-template <int D, Elem E>
+template <int D, Elem E, bool WIN = false>
 __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float* lse2) {
   using M = MmaT<E>;
   using V8 = typename M::v8;
@@ -501,8 +578,8 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
   // dO rows in L2.  The parts of a split block walk one sequence: no
   // rotation there.
   const int rot =
-      split ? 0
-            : (int)(((unsigned)((bid - A.n_extra) >> 3) * (D == 128 ? 19u : 12u) / 64u) & 63u);
+      split || WIN ? 0
+                   : (int)(((unsigned)((bid - A.n_extra) >> 3) * (D == 128 ? 19u : 12u) / 64u) & 63u);
   const int kvh = bkv % A.Hkv, b = bkv / A.Hkv;
   const int u0 = 16 * kb;
 
@@ -587,7 +664,10 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
     r0 = 0;
     len = 0;
     const int ej = (lane + rot) & 63;
-    if (ej < A.pc.w) {
+    if constexpr (WIN) {
+      r0 = u0;
+      len = lane == 0 ? max(min(u0 + 15 + A.pc.w, A.q_len) - u0, 0) : 0;
+    } else if (ej < A.pc.w) {
       int a0 = u0, a1 = A.q_len;  // first row >= u0 with key >= u0
       while (a0 < a1) {
         const int mid = (a0 + a1) >> 1;
@@ -710,7 +790,9 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
       if (P + ROWS < p_end) map_step(P + ROWS, e, row_n, ent_n);
       // the key of slot row (lane % 32), -1 when masked or empty
       int rkey = -1;
-      if (row_c >= 0) {
+      if constexpr (WIN) {
+        rkey = row_c;
+      } else if (row_c >= 0) {
         const int kk = key_at(row_c, (ent_c + rot) & 63);
         rkey = kk <= row_c ? kk : -1;
       }
@@ -779,7 +861,8 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
 #pragma unroll
         for (int e2 = 0; e2 < 4; ++e2) {
           const int rk = __builtin_amdgcn_ds_bpermute(4 * (16 * c + 4 * q + e2), rkey);
-          const bool has = rk == key;
+          // (WIN: rk is the slot row, -1 for none)
+          const bool has = WIN ? rk >= 0 && key <= rk && key > rk - A.pc.w : rk == key;
           const float p =
               __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[c][e2], scale2, -l2v[c][e2]));
           pv[e2] = has ? p : 0.f;
@@ -872,10 +955,19 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
 template <Elem E>
 static void launch_band_dkdv_elem(const BwdArgs& a, int head_dim, dim3 grid, const float* lse2,
                                   hipStream_t stream) {
-  if (head_dim == 128)
-    band_dkdv_kernel<128, E><<<grid, 64, 0, stream>>>(a, lse2);
-  else
-    band_dkdv_kernel<64, E><<<grid, 64, 0, stream>>>(a, lse2);
+  // a sliding window at interpolation weight 0
+  const bool win = a.pc.a == 0.0f;
+  if (head_dim == 128) {
+    if (win)
+      band_dkdv_kernel<128, E, true><<<grid, 64, 0, stream>>>(a, lse2);
+    else
+      band_dkdv_kernel<128, E><<<grid, 64, 0, stream>>>(a, lse2);
+  } else {
+    if (win)
+      band_dkdv_kernel<64, E, true><<<grid, 64, 0, stream>>>(a, lse2);
+    else
+      band_dkdv_kernel<64, E><<<grid, 64, 0, stream>>>(a, lse2);
+  }
 }
 
 hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,
@@ -892,8 +984,11 @@ hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,
 
 template <int D, bool PREP, Elem E>
 static void launch_band_dq_d(const BwdArgs& a, dim3 grid, const float* lse2, hipStream_t stream) {
-  // K and V DMA skipping from interpolation weight 1/2 on, as for the forward
-  if (a.pc.a >= 0.5f)
+  // a sliding window at interpolation weight 0; K and V DMA skipping from
+  // interpolation weight 1/2 on, as for the forward
+  if (a.pc.a == 0.0f)
+    band_dq_kernel<D, false, PREP, E, true><<<grid, 64, 0, stream>>>(a, lse2);
+  else if (a.pc.a >= 0.5f)
     band_dq_kernel<D, true, PREP, E><<<grid, 64, 0, stream>>>(a, lse2);
   else
     band_dq_kernel<D, false, PREP, E><<<grid, 64, 0, stream>>>(a, lse2);

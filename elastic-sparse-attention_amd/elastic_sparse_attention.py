@@ -592,6 +592,15 @@ def bwd_kernels(layout: ElasticLayout, q_len: int, batch: int, head_dim: int
     """("band" | "tile", "band" | "tile"): the faster dQ and dK/dV kernels for
     this pattern and shape, each half switching to its band kernel at its own
     measured crossover (BWD_DQ_CROSSOVER, BWD_DKDV_CROSSOVER)."""
+    p = layout.pattern
+    if (p.layer_idx == 0 and head_dim in BWD_DQ_CROSSOVER and p.attention_length <= 64
+            and p.seq_len < (1 << 24)):
+        # interpolation weight 0, a sliding window: both band kernels walk the
+        # window's keys and rows directly (measured against tile / tile: B=1
+        # H=32 L=32768 D=128 0.803 vs 0.952 ms, B=1 H=32 L=8192 0.225 vs
+        # 0.261, B=8 H=16 L=4096 D=64 0.220 vs 0.245, B=1 H=8 L=131072 0.810
+        # vs 0.962; band / band is also faster than either mixed pair)
+        return "band", "band"
     dq = _band_beats_tile(layout, q_len, batch, head_dim, BWD_DQ_CROSSOVER)
     dkdv = _band_beats_tile(layout, q_len, batch, head_dim, BWD_DKDV_CROSSOVER)
     return "band" if dq else "tile", "band" if dkdv else "tile"

@@ -389,7 +389,9 @@ esa_status esa_bwd_workspace_size(const esa_bwd_args* a, size_t* workspace_bytes
  * kv_items NULL computes dK and dV with the band-gathered key-major kernel
  * instead (same limits; tile_row, kv_ptr, kv_tiles, mask_t and num_kv_items
  * are ignored).  With both NULL no layout is read (row_ptr, col_idx may be
- * NULL).  q_masks: NULL (the block-sparse dQ computes each row's valid keys
+ * NULL).  At interpolation weight 0 (layer_idx 0: a sliding window, row i
+ * attends keys max(0, i - w + 1) .. i) both band kernels walk the window's
+ * key chunks and row ranges directly.  q_masks: NULL (the block-sparse dQ computes each row's valid keys
  * per tile from the pattern), or esa_build_stage_masks' masks of this 128 x
  * 128 layout (16-byte aligned; only with q_items, ESA_ERR_UNSUPPORTED
  * otherwise): same results bit for bit, without the per-row index walk.

@@ -46,6 +46,9 @@ def rel_err(got, ref):
     (1, 2, 2, 64, 64, 128, 3),       # one row block, rows 0 .. w - 1 only
     (1, 8, 2, 2048, 2048, 128, 7),   # last layer, GQA: band dK/dV splits key block 0 (2 parts)
     (2, 4, 1, 3000, 3000, 64, 7),    # the same with batch 2, MQA, D = 64, ragged rows
+    (2, 8, 2, 640, 640, 64, 0),      # layer 0 (a window): GQA, batch, D = 64
+    (1, 4, 4, 1000, 700, 128, 0),    # layer 0, q_len < kv_len, ragged blocks
+    (1, 2, 1, 40, 40, 128, 0),       # layer 0, fewer rows than the window
 ])
 def test_backward_matches_autograd(B, H, Hkv, L, Lq, D, layer, kernels):
     """kernels: dQ kernel / dK-dV kernel."""
@@ -80,6 +83,8 @@ def test_backward_matches_autograd(B, H, Hkv, L, Lq, D, layer, kernels):
     (1, 4, 2, 1000, 128, 5, 33),   # odd index-list length: lanes 33 .. 63 idle
     (1, 3, 1, 700, 64, 7, 16),     # short lists, last layer, MQA
     (2, 1, 1, 513, 128, 3, 64),    # one head (interpolation weight 0), ragged
+    (1, 4, 2, 1000, 128, 0, 33),   # layer 0, odd window
+    (1, 3, 1, 700, 64, 0, 16),     # layer 0, short window, MQA
 ])
 def test_backward_attention_lengths(B, H, Hkv, L, D, layer, w, kernels):
     """Index lists shorter than 64 entries and a single head, both halves of

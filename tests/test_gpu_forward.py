@@ -333,7 +333,7 @@ def test_band_sharp_softmax_outliers():
 
 
 @pytest.mark.parametrize("L,H,B,D,layer,want,want_bwd", [
-    (32768, 32, 1, 128, 4, "band", "band/band"), (32768, 32, 1, 128, 0, "band", "tile/tile"),
+    (32768, 32, 1, 128, 4, "band", "band/band"), (32768, 32, 1, 128, 0, "band", "band/band"),
     (8192, 32, 1, 128, 3, "tile", "tile/tile"), (8192, 32, 1, 128, 4, "band", "band/band"),
     (4096, 32, 4, 128, 7, "tile", "tile/tile"),
     (8192, 32, 1, 128, 5, "band", "band/band"), (4096, 16, 8, 64, 6, "band", "band/tile"),

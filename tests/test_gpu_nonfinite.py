@@ -196,7 +196,9 @@ BWD_NF_CASES = [("band/band", 4, 1024, 4, 2, 128, torch.bfloat16),
                 ("band/tile", 0, 1024, 4, 4, 64, torch.bfloat16),
                 ("tile/band", 7, 1024, 4, 2, 64, torch.float16),
                 ("tile/tile", 2, 700, 2, 1, 64, torch.float16),
-                ("band/band", 7, 2048, 8, 2, 128, torch.bfloat16)]
+                ("band/band", 7, 2048, 8, 2, 128, torch.bfloat16),
+                ("band/band", 0, 1024, 4, 2, 128, torch.bfloat16),
+                ("tile/band", 0, 700, 2, 1, 64, torch.float16)]
 
 
 @pytest.mark.parametrize("where", ["v", "k"])
