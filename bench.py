@@ -455,6 +455,12 @@ def alg_bytes_of(B: int, H: int, L: int, D: int) -> int:
     return 2 * B * (2 * H * L * D + 2 * H * L * D) + 4 * B * H * L
 
 
+def bwd_alg_bytes_of(B: int, H: int, Hkv: int, L: int, D: int) -> int:
+    """The backward's: Q, O, dO read and dQ written (H heads), K, V read and
+    dK, dV written (Hkv heads) once in bf16, LSE read in float32."""
+    return 2 * B * L * D * 4 * (H + Hkv) + 4 * B * H * L
+
+
 def roofline_of(layer: int, kern_ms: float, executed: float, alg_bytes: int, traffic) -> dict:
     if layer == 0:
         # a plain sliding window: ~127 flop/B, below the MFMA ridge -> HBM-bound
@@ -536,10 +542,20 @@ def time_backward(torch, lay, q, k, v, scaling, counted_fwd, steps, warmup) -> d
         ex = band_bwd_executed_flops(torch, lay, B, H, k.shape[1], L, D, W)
         tf = (ex["dq"] + ex["dkdv"]) / (ms * 1e-3) / 1e12
         out["executed_mfma_flops"] = {"dq": ex["dq"], "dkdv": ex["dkdv"]}
-        # executed bf16 MFMA work of both kernels over the whole backward's
-        # time (per-kernel rates: the committed trace and counter summary)
-        out["roofline"] = {"bound": "mfma", "achieved": round(tf, 3), "peak": PEAK_BF16_TFLOPS,
-                           "unit": "TFLOP/s", "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+        if lay.pattern.layer_idx == 0:
+            # a sliding window: HBM-bound (about 85 executed flop per
+            # algorithmic byte); the backward's algorithmic bytes over its time
+            alg = bwd_alg_bytes_of(B, H, k.shape[1], L, D)
+            gbs = alg / (ms * 1e-3) / 1e9
+            out["algorithmic_bytes"] = alg
+            out["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                               "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        else:
+            # executed bf16 MFMA work of both kernels over the whole backward's
+            # time (per-kernel rates: the committed trace and counter summary)
+            out["roofline"] = {"bound": "mfma", "achieved": round(tf, 3),
+                               "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                               "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
         prof = f"band_bwd_kernels_bf16_B{B}_H{H}_L{L}_D{D}_layer{lay.pattern.layer_idx}.md"
         l2 = figure_from_profile(prof, "l2_to_cu_bytes_per_launch")
         hbm = figure_from_profile(prof)
@@ -547,6 +563,8 @@ def time_backward(torch, lay, q, k, v, scaling, counted_fwd, steps, warmup) -> d
             out["l2_to_cu_bytes"] = l2
         if hbm is not None:
             out["traffic"] = hbm
+            if out["roofline"]["bound"] == "hbm":
+                out["roofline"]["traffic"] = hbm
     return out
 
 
