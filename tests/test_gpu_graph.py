@@ -43,7 +43,8 @@ def warm_up(fn):
 
 @pytest.mark.parametrize("kernel,layer,L,H,D", [("band", 4, 2048, 8, 128), ("tile", 4, 2048, 8, 128),
                                                 ("tile", 0, 1024, 4, 128), ("tile", 2, 1024, 4, 64),
-                                                ("band", 7, 1536, 4, 64)])
+                                                ("band", 7, 1536, 4, 64),
+                                                ("band", 0, 1024, 4, 128)])
 def test_module_forward_graph_replays(kernel, layer, L, H, D):
     print(f"graph forward {kernel} layer={layer} L={L} H={H} D={D}", flush=True)
     m = ElasticSparseAttention(layer, 8, H, D, 64, L)
@@ -102,7 +103,8 @@ def test_noalloc_first_call_captured_after_init():
 @pytest.mark.parametrize("kernel,layer,L,H,Hkv,D", [("band", 4, 2048, 8, 8, 128),
                                                     ("tile", 3, 1024, 4, 2, 64),
                                                     ("band", 7, 2048, 4, 4, 128),
-                                                    ("tile", 7, 1024, 4, 4, 128)])
+                                                    ("tile", 7, 1024, 4, 4, 128),
+                                                    ("band", 0, 1024, 4, 2, 128)])
 def test_noalloc_backward_graph_replays(kernel, layer, L, H, Hkv, D):
     print(f"graph noalloc backward {kernel} layer={layer} L={L} H={H} Hkv={Hkv} D={D}", flush=True)
     B = 1
