@@ -60,6 +60,23 @@ __device__ __forceinline__ float row4_max(float v) {
   return __builtin_elementwise_maximum(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// row4_max of a and of b at once: the first swap pairs a's lanes l, l + 32
+// in lanes 0..31 and b's in lanes 32..63, one l ^ 16 swap finishes both
+// halves, and a last l ^ 32 swap hands each value to every lane (7 VALU
+// instructions for the two instead of 12; the same maxima, NaN included)
+__device__ __forceinline__ void row4_max2(float& a, float& b) {
+  const auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                                   false);
+  const float m1 = __builtin_elementwise_maximum(__uint_as_float(s1[0]), __uint_as_float(s1[1]));
+  const auto s2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m1), __float_as_uint(m1),
+                                                   false, false);
+  const float m2 = __builtin_elementwise_maximum(__uint_as_float(s2[0]), __uint_as_float(s2[1]));
+  const auto s3 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m2), __float_as_uint(m2),
+                                                   false, false);
+  a = __uint_as_float(s3[0]);
+  b = __uint_as_float(s3[1]);
+}
+
 // min / max over the 16 lanes of a lane group (DPP row rotations)
 // (a row rotation writes every lane, so the moves carry no old value and
 // fold into the min / max as DPP operands)

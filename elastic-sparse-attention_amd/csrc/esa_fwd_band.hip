@@ -265,13 +265,23 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   // d >= 16), the same in the row's 4 lanes; -inf when the row has no key
   // there.  has / e: this lane holds the key, at register e (d >> 2 == q
   // only for d in 4 q .. 4 q + 3, an arithmetic shift keeping d < 0 out).
-  auto pick = [&](const f32x4& sacc, int d, bool& has, int& e) -> float {
+  auto lane_score = [&](const f32x4& sacc, int d, bool& has, int& e) -> float {
     has = (d >> 2) == q;
     e = d & 3;
     const float s01 = (e & 1) ? sacc[1] : sacc[0];
     const float s23 = (e & 1) ? sacc[3] : sacc[2];
     const float s = (e & 2) ? s23 : s01;
-    return row4_max(has ? s * scale : -INFINITY);
+    return has ? s * scale : -INFINITY;
+  };
+  auto pick = [&](const f32x4& sacc, int d, bool& has, int& e) -> float {
+    return row4_max(lane_score(sacc, d, has, e));
+  };
+  // both bands of a pair (one fused 4-lane max)
+  auto pick2 = [&](const f32x4& sa, int da, bool& ha, int& ea, float& xa, const f32x4& sb,
+                   int db, bool& hb, int& eb, float& xb) {
+    xa = lane_score(sa, da, ha, ea);
+    xb = lane_score(sb, db, hb, eb);
+    row4_max2(xa, xb);
   };
   // Online softmax over two bands' scores xa, xb (one running-max update per
   // pair, so both probabilities share one scale) -> P words (the input type
@@ -306,8 +316,8 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     // O is normalised by the probabilities PV used (rounded to the input type)
     n_run += M::val(b0);
     n_run += M::val(b1);
-    pa = ha ? ((uint64_t)b0 << (16 * ea)) : 0ull;
-    pb = hb ? ((uint64_t)b1 << (16 * eb)) : 0ull;
+    pa = (uint64_t)(ha ? b0 : 0u) << (16 * ea);
+    pb = (uint64_t)(hb ? b1 : 0u) << (16 * eb);
   };
 
   auto scores = [&](const V8 (&kb)[C::NS]) {
@@ -463,8 +473,8 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
           }
           bool ha, hb;
           int ea, eb;
-          const float xa = pick(sa, da, ha, ea);
-          const float xb = pick(sb, db, hb, eb);
+          float xa, xb;
+          pick2(sa, da, ha, ea, xa, sb, db, hb, eb, xb);
           uint64_t pa, pbw;
           pair_softmax(xa, ha, ea, xb, hb, eb, pa, pbw);
           if constexpr (!VEARLY) {
