@@ -20,7 +20,10 @@
 // chunk (bands wider than 16 keys get a tail pass), so every valid (row,
 // key) pair contributes once, as in :191-228.  band_dkdv_kernel (below) is
 // the key-major counterpart for dK and dV; dkdv_kernel (esa_bwd.hip) is the
-// block-sparse one.  Operand layouts: esa_band.hpp.
+// block-sparse one.  At interpolation weight 0 (a sliding window) both run
+// their WIN form: the group's window keys, or the block's window rows, as
+// contiguous 16-key chunks / 32-row steps in place of 64 bands.  Operand
+// layouts: esa_band.hpp.
 #include "esa_band.hpp"
 
 namespace esa {
