@@ -398,6 +398,18 @@ def band_executed_flops(B: int, H: int, L: int, D: int, w: int) -> float:
     return float(B * H * pairs * (2 * (D // 32) + D // 16) * 16384)
 
 
+def window_executed_flops(B: int, H: int, L: int, D: int, w: int, G: int = 2) -> float:
+    """MFMA flops the window kernel (the band entry point at interpolation
+    weight 0) issues: per 16 G-row group, its keys [max(r0 - w + 1, 0),
+    min(r0 + 16 G, L)) in pairs of 16-key chunks, and per pair and 16-row
+    group 2 D/32 QK^T MFMAs (one per chunk) and D/16 PV MFMAs (the pair as
+    one 32-key step), 16384 flops each."""
+    pairs = 0
+    for r0 in range(0, L, 16 * G):
+        pairs += (min(r0 + 16 * G, L) - max(r0 - w + 1, 0) + 31) // 32
+    return float(B * H * pairs * G * (2 * (D // 32) + D // 16) * 16384)
+
+
 def band_bwd_executed_flops(torch, lay, B: int, H: int, Hkv: int, L: int, D: int,
                             w: int) -> dict:
     """MFMA flops the band backward kernels issue in their main loops
@@ -447,6 +459,8 @@ def executed_flops(torch, kernel: str, lay, B: int, H: int, L: int, D: int,
     if kernel == "split":
         band = band_executed_flops(B, H, L, D, W) - band_executed_flops(B, H, split, D, W)
         return B * executed_blocks(torch, lay, split) * 4.0 * 32 * 32 * D + band
+    if lay.pattern.layer_idx == 0:
+        return window_executed_flops(B, H, L, D, W)  # the band entry point's window kernel
     return band_executed_flops(B, H, L, D, W)
 
 
