@@ -109,7 +109,9 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
       G.vsb = A.vsb; G.vsh = A.vsh; G.vss = A.vss;
       G.osb = A.osb; G.osh = A.osh; G.oss = A.oss;
       G.lsb = A.lsb; G.lsh = A.lsh;
-      G.H = A.H; G.groups = A.groups; G.q_len = A.q_len; G.kv_len = A.kv_len; G.D = D;
+      // (the inputs' head dim: at a head dim padded up to the kernel's D the
+      // rows hold d_real elements, and the gather reads and writes that many)
+      G.H = A.H; G.groups = A.groups; G.q_len = A.q_len; G.kv_len = A.kv_len; G.D = A.d_real;
       G.sm_scale = A.sm_scale;
       G.elem = A.elem;
       G.src.w = A.pc.w; G.src.kv_len = A.kv_len; G.src.pc = A.pc;

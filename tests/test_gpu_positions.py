@@ -84,6 +84,37 @@ def test_mixed_and_negative_positions():
     check_rows(2, 8, 2, L, 128, 5, pos)
 
 
+@pytest.mark.parametrize("D", [96, 80, 40, 200])
+def test_mixed_positions_padded_head_dims(D):
+    """Head dims padded up to the kernel's (96 and 80 run the D = 128
+    kernel, 40 the 64 one, 200 the 256 one) with groups that are not
+    consecutive: those groups' rows go to the per-row gather, which must use
+    the inputs' own head dim.  O is written into the front of a larger
+    buffer; the elements after it must keep their sentinel (no row is
+    written past its D elements)."""
+    B, H, Hkv, L, layer = 2, 4, 2, 900, 5
+    g = torch.Generator().manual_seed(7)
+    pos = torch.cat([torch.arange(200, 248), torch.randperm(L, generator=g)[:40],
+                     torch.arange(860, 900) - L]).to(torch.int64)
+    Lq = pos.numel()
+    _, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=9, scale=1.0)
+    q = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=10, scale=1.0, Lq=Lq)[0]
+    sc = scaling_for(D)
+    pat = make_pattern(L, 64, layer, 8, H)
+    n = B * Lq * H * D
+    buf = torch.full((n + 512,), 7.0, dtype=torch.bfloat16, device=DEV)
+    o = buf[:n].view(B, Lq, H, D)
+    o, lse = elastic_attention_band(q.to(DEV), k.to(DEV), v.to(DEV), pat, sc, out=o,
+                                    positions=pos.to(DEV))
+    torch.cuda.synchronize()
+    assert bool((buf[n:] == 7.0).all())
+    idx, msk = elastic_indices(L, layer, 8, H, 64)
+    pi, pm = prepared_rows(idx, msk, Lq, L, L, pos % L)
+    ro, rl = forward_fp32(q, k, v, pi, pm, sc, H // Hkv)
+    assert (o.float().permute(0, 2, 1, 3).cpu() - ro).abs().max().item() <= BF16_TOL
+    assert (lse.cpu() - rl).abs().max().item() <= BF16_LSE_TOL
+
+
 def test_out_of_range_positions_give_nan_rows():
     B, H, L, D = 1, 4, 600, 64
     _, k, v = seeded_inputs(B, H, H, L, D, torch.bfloat16, seed=2, scale=1.0)

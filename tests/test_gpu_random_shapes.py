@@ -174,6 +174,49 @@ def test_random_decode_positions_through_module(seed):
     assert err <= tol, err
 
 
+def draw_chunk(seed):
+    r = random.Random(3000 + seed)
+    H = r.choice([2, 4, 8])
+    Hkv = r.choice([d for d in range(1, H + 1) if H % d == 0])
+    L = r.randint(200, 2000)
+    nq = r.randint(32, min(600, L))
+    p0 = r.randint(0, L - nq)
+    nl = r.choice([1, 2, 8, 12])
+    layer = r.randrange(nl)
+    w = r.choice([16, 33, 64, 64])
+    D = r.choice([64, 128, 128, 96])
+    dtype = r.choice([torch.bfloat16, torch.bfloat16, torch.float16])
+    B = r.choice([1, 2])
+    pos = torch.arange(p0, p0 + nq, dtype=torch.int64)
+    if r.random() < 0.25:  # a few rows moved or given as negatives: those groups take the gather
+        for _ in range(r.randint(1, 3)):
+            j = r.randrange(nq)
+            pos[j] = r.randrange(-L, L)
+    return B, H, Hkv, L, nq, nl, layer, w, D, dtype, pos
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_chunk_positions_through_module(seed):
+    """The module's cache_position branch with a chunk of 32 or more rows (a
+    chunked prefill: the band kernel, or the window kernel at layer 0, at the
+    rows' positions; groups whose positions are not consecutive take the
+    per-row gather) at random offsets, lengths, layers, GQA, bf16 / fp16 and
+    head dims 64 / 96 / 128, against the oracle's rows at those positions."""
+    from elastic_sparse_attention import ElasticSparseAttention
+    B, H, Hkv, L, nq, nl, layer, w, D, dtype, pos = draw_chunk(seed)
+    print(f"chunk seed={seed} B={B} H={H} Hkv={Hkv} L={L} rows={nq} p0={int(pos[0])} D={D} "
+          f"nl={nl} layer={layer} w={w} {dtype}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, dtype, seed=500 + seed, scale=D ** -0.25, Lq=nq)
+    idx, msk = elastic_indices(L, layer, nl, H, w)
+    pi, pm = prepared_rows(idx, msk, nq, L, L, cache_position=pos)
+    m = ElasticSparseAttention(layer, nl, H, D, w, L, num_key_value_heads=Hkv)
+    ro, _ = forward_fp32(q, k, v, pi, pm, m.scaling, H // Hkv)
+    out, _ = m(q.to(DEV), k.to(DEV), v.to(DEV), cache_position=pos.to(DEV))
+    ref = ro.transpose(1, 2).reshape(B, nq, H * D)
+    err = (out.float().cpu() - ref).abs().max().item()
+    assert err <= TOL[dtype][0], err
+
+
 @pytest.mark.parametrize("seed", range(16))
 def test_random_strided_inputs_same_bits(seed):
     """q, k, v as the [B, L, H, D] tensors attention layers hold, seen as
