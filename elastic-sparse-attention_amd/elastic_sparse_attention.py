@@ -16,14 +16,15 @@ Underneath, every call goes through libesa.so's C ABI (include/esa.h) to
 hand-written gfx950 HIP kernels:
 
 * prefill (``cache_position is None``), bf16 or fp16, head_dim 64 or 128: the
-  band-gathered MFMA kernel (each row's index-list entries as 16-key bands)
-  or the block-sparse MFMA kernel over the block layout (CSR of active
-  128x128 tiles, built once per device by the HIP layout builder),
-  whichever is faster for the shape (``prefill_kernel``); other head dims
-  that are multiples of 8 up to 256: the band kernel (at D = 256, or padded
-  to 64, 128 or 256);
+  band-gathered MFMA kernel (each row's index-list entries as 16-key bands;
+  at layer 0, a sliding window, its window kernel) or the block-sparse MFMA
+  kernel over the block layout (CSR of active 128x128 tiles, built once per
+  device by the HIP layout builder), whichever is faster for the shape, or
+  the two split by rows (``prefill_split``); other head dims that are
+  multiples of 8 up to 256: the band kernel (at D = 256, or padded to 64,
+  128 or 256);
 * chunked prefill (``cache_position`` of at least 32 rows), bf16 or fp16:
-  the band kernel at those positions;
+  the band (or window) kernel at those positions;
 * decode (fewer ``cache_position`` rows), float32, or other head dims: the
   per-row gather kernel that regenerates each row's elastic indices on the
   device.
@@ -47,8 +48,8 @@ Differences from the reference, all deliberate:
   stream, so the mask differs from torch.dropout's draw for the same seed.
 * Every path backpropagates, deterministically (no atomics on the
   gradients): bf16 or fp16 prefill with head_dim 64 or 128 through
-  hand-written MFMA kernels (band-gathered or block-sparse like the
-  forward); the others (decode and chunked-prefill rows, float32, other
+  hand-written MFMA kernels (band-gathered, their window forms at layer 0,
+  or block-sparse, each half picked per shape); the others (decode and chunked-prefill rows, float32, other
   head dims, dropout, explicit index lists) through the gather backward (row
   pass, stable key sort, key-major pass).
 * A query row with no valid entry (impossible for the elastic pattern, only
