@@ -23,7 +23,12 @@
 // The next pair's K and V are requested once this pair's operands are in
 // registers (the band kernel's early refill order).  Groups go to the XCDs
 // in contiguous ranges (rows ascending within a head), so consecutive groups
-// of one head, which share all but 16 of their keys, run on one L2.
+// of one head, which share all but 32 of their keys, run on one L2.  The
+// next group's pair p is this group's pair p + 1, so each group starts at
+// pair (-group) mod n_pairs and wraps around: the groups sharing a pair load
+// it at the same step instead of one to two pairs apart, by which time it had
+// often left L2 (layer 0 forward at B=1 H=32 L=8192 0.059 -> 0.050 ms,
+// L=32768 -2%).
 //
 // POS: rows at positions A.positions[r] (a chunked prefill's cache_position).
 // A group whose rows sit at consecutive positions, all in [0, kv_len), runs
@@ -105,6 +110,11 @@ __global__ __launch_bounds__(64, 2) void window_fwd_kernel(BandArgs A) {
   const int k0 = max(base - w + 1, 0);
   const int k1 = base + n_rows;
   const int n_pairs = (k1 - k0 + 31) / 32;
+  // pair order: the group at position base starts at pair (-base / 16 G) mod
+  // n_pairs and wraps around.  The next group's keys start 16 G keys later,
+  // so its pair p is this group's pair p + 1: with this order the n_pairs
+  // groups that share a pair all load it at the same step, while it is in L2
+  const int pstart = (n_pairs - (base / (16 * G)) % n_pairs) % n_pairs;
   // row 16 u + n of the group: its window as offsets from k0
   int lo[G], hi[G];
 #pragma unroll
@@ -202,12 +212,12 @@ __global__ __launch_bounds__(64, 2) void window_fwd_kernel(BandArgs A) {
     }
     {
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the slot zeros are in LDS
-      load_chunk(kbase, kss2, kofs, 0, lk0);
-      load_chunk(kbase, kss2, kofs, 1, lk1);
-      load_chunk(vbase, vss2, vofs, 0, lv0);
-      load_chunk(vbase, vss2, vofs, 1, lv1);
+      load_chunk(kbase, kss2, kofs, 2 * pstart, lk0);
+      load_chunk(kbase, kss2, kofs, 2 * pstart + 1, lk1);
+      load_chunk(vbase, vss2, vofs, 2 * pstart, lv0);
+      load_chunk(vbase, vss2, vofs, 2 * pstart + 1, lv1);
     }
-    for (int p = 0; p < n_pairs; ++p) {
+    for (int st = 0, p = pstart; st < n_pairs; ++st, p = p + 1 == n_pairs ? 0 : p + 1) {
       __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this pair's K and V are in LDS
       V8 ka[C::NS], kb[C::NS];
       s16x4 ta[C::NV], tb[C::NV];
@@ -235,11 +245,12 @@ __global__ __launch_bounds__(64, 2) void window_fwd_kernel(BandArgs A) {
         }
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);  // slots read: refill them
-      if (p + 1 < n_pairs) {
-        load_chunk(kbase, kss2, kofs, 2 * p + 2, lk0);
-        load_chunk(kbase, kss2, kofs, 2 * p + 3, lk1);
-        load_chunk(vbase, vss2, vofs, 2 * p + 2, lv0);
-        load_chunk(vbase, vss2, vofs, 2 * p + 3, lv1);
+      if (st + 1 < n_pairs) {
+        const int pn = p + 1 == n_pairs ? 0 : p + 1;
+        load_chunk(kbase, kss2, kofs, 2 * pn, lk0);
+        load_chunk(kbase, kss2, kofs, 2 * pn + 1, lk1);
+        load_chunk(vbase, vss2, vofs, 2 * pn, lv0);
+        load_chunk(vbase, vss2, vofs, 2 * pn + 1, lv1);
       }
       // this lane's keys: 32 p + 4 q + e (chunk a) and 32 p + 16 + 4 q + e
       // (chunk b), as offsets from k0
