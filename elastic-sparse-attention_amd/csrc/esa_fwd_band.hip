@@ -149,19 +149,12 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   // group's band descriptors (slot (q, r)'s in lane 16 q + r of info1)
   uint32_t kd[4];
   int info1;
-  // entry rotation, in 64ths of an entry per group dispatched on the XCD:
-  // an XCD keeps 320 waves resident at D = 128 (ten per CU, by LDS) and 640
-  // at D = 64 (twenty, by LDS and registers alike), so a group is dispatched
-  // about every 64 / 320 = 12.8/64 or 64 / 640 = 6.4/64 of a wave's walk;
-  // the rotation leads that.  Measured rates per 64th: 15 and 9 are the best
-  // or within 2% of it at every layer of B=1 H=8 L=131072, where an XCD's L2
-  // cannot hold the resident groups' rows across entries (12/64 there was
-  // 8-11% slower at D = 128 layers 4-7 and 17-22% at D = 64), and shapes up
-  // to L=32768 do not move with the rate (7 and 8 at D = 64 within 1% of 9).
+  // entry rotation, A.rot_rate 64ths of an entry per group dispatched on the
+  // XCD (launch_band_fwd picks the rate)
   // (unsigned: the product wraps for grids near 2^31 blocks; only the value
   // mod 64 matters)
   band_rows(A.pc, h, i, row_ok, q, n,
-            (int)(((unsigned)(bid >> 3) * (D == 128 ? 15u : 9u) / 64u) & 63u), kd, info1);
+            (int)(((unsigned)(bid >> 3) * (unsigned)A.rot_rate / 64u) & 63u), kd, info1);
 
   const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
   const char* const vbase = (const char*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh);
@@ -663,6 +656,32 @@ hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) 
   const float last = (float)(a.positions ? a.kv_len : a.q_len);
   const float spacing = (last * a.pc.a + a.pc.c) / (float)a.pc.w;
   const bool vearly = spacing < 1000.0f;
+  // Entry rotation.  An XCD keeps 40960 / D waves resident (by LDS: 320 at
+  // D = 128, 640 at D = 64, 160 at D = 256).  Where the grid fills many
+  // rounds of them, waves finish and are replaced one at a time, a group
+  // about every 64 / 320 = 12.8/64 (D = 128) or 6.4/64 (D = 64) of a wave's
+  // walk, and a rotation a little ahead of that rate (15/64, 9/64) puts the
+  // resident groups on neighbouring entries, whose keys share L2: 15 and 9
+  // are the best or within 2% of it at every layer of B=1 H=8 L=131072
+  // (12/64 there was 8-11% slower at D = 128 layers 4-7, 17-22% at D = 64).
+  // A grid of a few rounds starts each round nearly at once instead, and the
+  // same rate spreads a round's groups over all 64 entries, so an XCD's L2
+  // must hold the keys of every entry of the resident rows.  Where a head's
+  // K and V (4 head_dim bytes per key) exceed the 4 MB L2, a grid of up to
+  // four rounds therefore starts every group at entry 0.  Same box,
+  // rotation against none: the last 1024 / 2048 / 4096 rows of B=1 H=32
+  // L=32768 D=128 layer 4 as a chunk (0.8 / 1.6 / 3.2 rounds) 0.108 ->
+  // 0.066, 0.179 -> 0.106, 0.271 -> 0.197 ms, layer 7 -7% / -30%, the last
+  // 16384 rows of B=1 H=8 L=131072 -31% at layer 4 (+3% at layer 7); at 6.4
+  // rounds within +-3%, at 12.8 the rotation 1-9% faster, at 25.6 (the full
+  // L=32768 prefill) 9%.  At L=8192 (4 MB of K and V per head) none was
+  // 1-4% slower at 0.8-3.6 rounds.
+  const int dk = head_dim > 128 ? 256 : head_dim > 64 ? 128 : 64;
+  const int64_t resident = 8 * (40960 / dk);
+  const bool few_rounds = (int64_t)a.n_groups <= 4 * resident;
+  const bool head_past_l2 = (int64_t)a.kv_len * 4 * a.d_real > (int64_t(4) << 20);
+  BandArgs r = a;
+  r.rot_rate = few_rounds && head_past_l2 ? 0 : dk == 128 ? 15 : 9;
   // K DMA skipping: with the late V order from interpolation weight 1/2 on
   // (measured at B=1, H=32, L=32768, D=128, w=64 over 8 layers: 1-7% faster
   // at weights 4/7 .. 1, even at 3/7, 3-4% slower at 1/7 and 2/7, where
@@ -672,9 +691,9 @@ hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) 
   // L=8192 .. 131072, within 1% at 1/7
   const bool kskip = a.pc.a >= 0.5f || vearly;
   if (a.elem == (int)Elem::f16)
-    launch_band_elem<Elem::f16>(a, head_dim, grid, kskip, vearly, stream);
+    launch_band_elem<Elem::f16>(r, head_dim, grid, kskip, vearly, stream);
   else
-    launch_band_elem<Elem::bf16>(a, head_dim, grid, kskip, vearly, stream);
+    launch_band_elem<Elem::bf16>(r, head_dim, grid, kskip, vearly, stream);
   return hipGetLastError();
 }
 

@@ -67,6 +67,9 @@ struct BandArgs {
   // the inputs' head_dim (a multiple of 8) when it is below the kernel's D:
   // dims d_real .. D - 1 of Q, K and V read as zeros and O's are not stored
   int d_real;
+  // entry rotation of the band forward, in 64ths of an entry per group
+  // dispatched on an XCD (set by launch_band_fwd from the grid's size)
+  int rot_rate;
 };
 
 // Where a query row's w entries come from: the elastic pattern (regenerated
