@@ -160,16 +160,13 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
 
   uint32_t kd[4];  // the row's key offsets (band_rows)
   int info1;       // slot (q, r)'s descriptor in lane 16 q + r
-  // entry rotation, in 64ths of an entry per group dispatched on the XCD: a
-  // little ahead of the dispatch rate, 64 / (resident waves per XCD) = 16/64
-  // at D = 128 (256 resident) and 8/64 at D = 64 (512), as in the forward;
-  // measured 1-4% faster than 16/64 at B=1 H=8 L=131072 layers 4 and 7,
-  // unchanged at B=1 H=32 L=32768 (and 9/64 at D = 64 within 1% of 12/64)
+  // entry rotation, A.rot_dq 64ths of an entry per group dispatched on the
+  // XCD (launch_band_dq picks the rate)
   // (unsigned: the product wraps for grids near 2^31 blocks; only the value
   // mod 64 matters)
   if constexpr (!WIN)
     band_rows(A.pc, h, i, row_ok, q, n,
-              (int)(((unsigned)(bid >> 3) * (D == 128 ? 19u : 12u) / 64u) & 63u), kd, info1);
+              (int)(((unsigned)(bid >> 3) * (unsigned)A.rot_dq / 64u) & 63u), kd, info1);
 
   const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
   const char* const vbase = (const char*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh);
@@ -575,14 +572,13 @@ __global__ __launch_bounds__(64, 2) void band_dkdv_kernel(BwdArgs A, const float
   const int bkv = g / A.nkb16, kb = g % A.nkb16;
   const bool split = A.split_parts > 1 && kb < A.split_blocks;
   // entry rotation (as in band_rows): lane r of the walk holds entry
-  // (r + rot) mod 64, rot growing by 19/64 (D = 128: 256 resident waves per
-  // XCD) or 12/64 (D = 64: 384) of an entry per block dispatched on the XCD,
-  // so the blocks resident at once walk neighbouring entries and share Q /
-  // dO rows in L2.  The parts of a split block walk one sequence: no
-  // rotation there.
+  // (r + rot) mod 64, rot growing by A.rot_dkdv 64ths of an entry per block
+  // dispatched on the XCD (launch_band_dkdv picks the rate), so the blocks
+  // resident at once walk neighbouring entries and share Q / dO rows in L2.
+  // The parts of a split block walk one sequence: no rotation there.
   const int rot =
       split || WIN ? 0
-                   : (int)(((unsigned)((bid - A.n_extra) >> 3) * (D == 128 ? 19u : 12u) / 64u) & 63u);
+                   : (int)(((unsigned)((bid - A.n_extra) >> 3) * (unsigned)A.rot_dkdv / 64u) & 63u);
   const int kvh = bkv % A.Hkv, b = bkv / A.Hkv;
   const int u0 = 16 * kb;
 
@@ -978,10 +974,19 @@ hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,
   if (a.n_kblk <= 0 || a.kchunk <= 0) return hipSuccess;
   const int64_t chunks = (a.n_kblk + 8 * (int64_t)a.kchunk - 1) / (8 * (int64_t)a.kchunk);
   const dim3 grid((unsigned)(a.n_extra + chunks * 8 * a.kchunk));
+  // Entry rotation: 19/64 (D = 128: 256 resident waves per XCD) or 12/64
+  // (D = 64: 384), a little ahead of the dispatch rate; none for a grid of
+  // a few rounds whose heads' Q and dO rows exceed L2 (band_rotation).  Same
+  // box, without against with: B=1 H=4 L=32768 D=128 (four rounds) backward
+  // -4% at layer 4, -9% at layer 7, B=1 H=2 L=65536 -5.5%; at eight rounds
+  // (H=8) +1.4%, at 32 (H=32) +4.3%.
+  BwdArgs r = a;
+  r.rot_dkdv = band_rotation(a.n_kblk, head_dim == 128 ? 256 : 384,
+                             (int64_t)a.q_len * 4 * head_dim, head_dim == 128 ? 19 : 12);
   if (a.elem == (int)Elem::f16)
-    launch_band_dkdv_elem<Elem::f16>(a, head_dim, grid, lse2, stream);
+    launch_band_dkdv_elem<Elem::f16>(r, head_dim, grid, lse2, stream);
   else
-    launch_band_dkdv_elem<Elem::bf16>(a, head_dim, grid, lse2, stream);
+    launch_band_dkdv_elem<Elem::bf16>(r, head_dim, grid, lse2, stream);
   return hipGetLastError();
 }
 
@@ -1017,10 +1022,19 @@ hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2, boo
                           hipStream_t stream) {
   if (a.n_groups <= 0) return hipSuccess;
   dim3 grid((unsigned)(8 * a.per_xcd));
+  // Entry rotation: 19/64 (D = 128: 256 resident waves per XCD) or 12/64
+  // (D = 64: 512), a little ahead of the dispatch rate 64 / 256 = 16/64 or
+  // 8/64 (19/64 measured 1-4% faster than 16/64 at B=1 H=8 L=131072 layers
+  // 4 and 7, unchanged at B=1 H=32 L=32768; 9/64 at D = 64 within 1% of
+  // 12/64); none for a grid of a few rounds whose heads' K and V exceed L2
+  // (band_rotation, measured with the dK / dV's in launch_band_dkdv)
+  BwdArgs r = a;
+  r.rot_dq = band_rotation(a.n_groups, head_dim == 128 ? 256 : 512,
+                           (int64_t)a.kv_len * 4 * head_dim, head_dim == 128 ? 19 : 12);
   if (a.elem == (int)Elem::f16)
-    launch_band_dq_elem<Elem::f16>(a, head_dim, grid, lse2, prep, stream);
+    launch_band_dq_elem<Elem::f16>(r, head_dim, grid, lse2, prep, stream);
   else
-    launch_band_dq_elem<Elem::bf16>(a, head_dim, grid, lse2, prep, stream);
+    launch_band_dq_elem<Elem::bf16>(r, head_dim, grid, lse2, prep, stream);
   return hipGetLastError();
 }
 

@@ -677,11 +677,9 @@ hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) 
   // L=32768 prefill) 9%.  At L=8192 (4 MB of K and V per head) none was
   // 1-4% slower at 0.8-3.6 rounds.
   const int dk = head_dim > 128 ? 256 : head_dim > 64 ? 128 : 64;
-  const int64_t resident = 8 * (40960 / dk);
-  const bool few_rounds = (int64_t)a.n_groups <= 4 * resident;
-  const bool head_past_l2 = (int64_t)a.kv_len * 4 * a.d_real > (int64_t(4) << 20);
   BandArgs r = a;
-  r.rot_rate = few_rounds && head_past_l2 ? 0 : dk == 128 ? 15 : 9;
+  r.rot_rate = band_rotation(a.n_groups, 40960 / dk, (int64_t)a.kv_len * 4 * a.d_real,
+                             dk == 128 ? 15 : 9);
   // K DMA skipping: with the late V order from interpolation weight 1/2 on
   // (measured at B=1, H=32, L=32768, D=128, w=64 over 8 layers: 1-7% faster
   // at weights 4/7 .. 1, even at 3/7, 3-4% slower at 1/7 and 2/7, where

@@ -216,7 +216,21 @@ struct BwdArgs {
   // that stores the unit; bwd_fix_kernel recomputes the flagged units
   uint8_t* flags;
   int n_qflags, n_kvflags;
+  // entry rotation of the band dQ / dK-dV walks, in 64ths of an entry per
+  // group or block dispatched on an XCD (set by their launchers)
+  int rot_dq, rot_dkdv;
 };
+
+// Entry rotation rate of a band kernel's launch (64ths of an entry per unit
+// dispatched on an XCD).  A grid of many rounds of resident waves refills
+// them one unit at a time, and `rate`, a little ahead of 64 / (resident
+// waves per XCD), keeps the resident units on neighbouring entries, whose
+// rows share L2.  A grid of up to four rounds starts each round nearly at
+// once, where the same rate spreads a round over all 64 entries: when a
+// head's gathered rows exceed an XCD's 4 MB L2 every unit starts at entry 0.
+inline int band_rotation(int64_t units, int64_t resident_per_xcd, int64_t head_bytes, int rate) {
+  return units <= 4 * 8 * resident_per_xcd && head_bytes > (int64_t(4) << 20) ? 0 : rate;
+}
 
 hipError_t launch_indices(const PatternConsts& pc, int row0, int nrows, void* indices, void* mask,
                           int elem_bytes, hipStream_t stream);

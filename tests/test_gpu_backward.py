@@ -307,6 +307,45 @@ def test_backward_identities_full_size(B, H, Hkv, L, D, layer, kernels):
     assert r_v <= 1e-3 and r_k <= 1e-3
 
 
+@pytest.mark.parametrize("B,H,Hkv,L,D,layer", [
+    (1, 2, 2, 65536, 128, 4),
+    (1, 4, 1, 32768, 128, 7),     # GQA, the last layer's split key block
+    (1, 4, 4, 32768, 64, 5),
+])
+def test_few_heads_long_band_matches_tile(B, H, Hkv, L, D, layer):
+    """Few heads at long lengths: grids of up to four rounds of resident
+    waves whose heads' K / V (Q / dO) exceed an XCD's L2, where the band
+    kernels walk every group or block from entry 0 instead of rotating.
+    Forward O and LSE and all three gradients of the band kernels against
+    the block-sparse kernels (independent paths), and a second band backward
+    bit-identical."""
+    print(f"few heads band vs tile B={B} H={H} Hkv={Hkv} L={L} D={D} layer={layer}", flush=True)
+    q, k, v = seeded_inputs(B, H, Hkv, L, D, torch.bfloat16, seed=130 + layer, scale=D ** -0.25)
+    sc = scaling_for(D)
+    lay = ElasticLayout(make_pattern(L, 64, layer, 8, H), DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    ob, lb = elastic_attention_fwd(qd, kd, vd, lay, sc, kernel="band")
+    ot, lt = elastic_attention_fwd(qd, kd, vd, lay, sc, kernel="tile")
+    eo = (ob.float() - ot.float()).abs().max().item()
+    el = (lb - lt).abs().max().item()
+    print(f"  forward max|O band - O tile| {eo:.3e}  max|lse diff| {el:.3e}", flush=True)
+    assert eo <= 2e-2 and el <= 2e-3
+    do = torch.randn(B, L, H, D, generator=torch.Generator().manual_seed(layer))
+    do = do.to(torch.bfloat16).to(DEV)
+    tt = elastic_attention_bwd(qd, kd, vd, ot, lt, do, lay, sc, dq_kernel="tile",
+                               dkdv_kernel="tile")
+    bb = elastic_attention_bwd(qd, kd, vd, ot, lt, do, lay, sc, dq_kernel="band",
+                               dkdv_kernel="band")
+    for name, x, y in zip(("dq", "dk", "dv"), tt, bb):
+        assert bool(torch.isfinite(y.float()).all())
+        r = ((y.float() - x.float()).abs().max() / x.float().abs().max()).item()
+        print(f"  max|{name} band - {name} tile| / max|{name}| {r:.3e}", flush=True)
+        assert r <= REL
+    again = elastic_attention_bwd(qd, kd, vd, ot, lt, do, lay, sc, dq_kernel="band",
+                                  dkdv_kernel="band")
+    assert all(torch.equal(x, y) for x, y in zip(bb, again))
+
+
 @pytest.mark.parametrize("layer,Hkv", [(0, 32), (4, 32), (7, 32), (7, 8)])
 def test_band_matches_tile_full_size(layer, Hkv):
     """The headline shape: dQ, dK and dV from the band kernels against the
