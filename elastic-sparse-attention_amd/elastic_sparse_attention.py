@@ -526,7 +526,9 @@ def prefill_kernel(layout: ElasticLayout, q_len: int, batch: int, head_dim: int)
         # the window kernel, which stages each key of a 32-row group once
         # (measured against the tile kernel: B=1 H=32 L=32768 D=128 0.240 vs
         # 0.246 ms, B=8 H=16 L=4096 D=64 0.050 vs 0.055, B=1 H=8 L=131072
-        # 0.251 vs 0.254, B=1 H=32 L=8192 within 1%)
+        # 0.251 vs 0.254, B=1 H=32 L=8192 within 1%; since then the window
+        # kernel's groups load each shared pair at the same step: 0.237,
+        # 0.048, 0.244 and 0.050 ms)
         return "band"
     return "band" if _band_beats_tile(layout, q_len, batch, head_dim, BAND_CROSSOVER) else "tile"
 
