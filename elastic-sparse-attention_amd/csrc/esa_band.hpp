@@ -121,7 +121,9 @@ __device__ __forceinline__ int row16_max(int v) {
 // give their measured rates) keeps the resident groups on neighbouring
 // entries, whose keys overlap: an L2 model of one XCD (4 MB LRU, 320
 // resident waves) at B=1 H=32 L=32768 layer 4 puts the hit rate at 0.79
-// without and 0.94 with the rotation.
+// without and 0.94 with the rotation.  That holds once waves are replaced
+// one at a time; a grid of a few rounds starts each round at once, where
+// the callers pass rot = 0 (band_rotation).
 __device__ __forceinline__ void band_rows(const PatternConsts& pc, int h, int i, bool row_ok,
                                           int q, int n, int rot, uint32_t (&kd)[4],
                                           int& info1) {

@@ -523,8 +523,9 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
 // balance the heavy low blocks over the XCDs), and each block starts its
 // walk at entry rot, a little more than 64 / (resident waves per XCD) of an
 // entry further per block dispatched on the XCD, so the resident blocks walk
-// neighbouring entries (the rotation of band_rows).  At the last layer of a pattern key block 0 takes far more
-// rows than the rest (entry 0 of the heads with small interpolation weight
+// neighbouring entries (the rotation of band_rows; none for a grid of a few
+// rounds, band_rotation).  At the last layer of a pattern key block 0 takes
+// far more rows than the rest (entry 0 of the heads with small interpolation weight
 // stays in it for thousands of rows), so the host splits blocks
 // 0 .. split_blocks - 1 (block 0) over split_parts waves each: each part
 // walks a fixed range of the block's steps (unrotated), stores float32 sums,
