@@ -20,10 +20,10 @@
 // chunk (bands wider than 16 keys get a tail pass), so every valid (row,
 // key) pair contributes once, as in :191-228.  band_dkdv_kernel (below) is
 // the key-major counterpart for dK and dV; dkdv_kernel (esa_bwd.hip) is the
-// block-sparse one.  At interpolation weight 0 (a sliding window) both run
-// their WIN form: the group's window keys, or the block's window rows, as
-// contiguous 16-key chunks / 32-row steps in place of 64 bands.  Operand
-// layouts: esa_band.hpp.
+// block-sparse one.  At interpolation weight 0 (a sliding window) dQ runs
+// window_dq_kernel (32-row groups over the window keys in 16-key chunks) and
+// dK / dV band_dkdv_kernel's WIN form (the block's window rows in 32-row
+// steps), in place of 64 bands.  Operand layouts: esa_band.hpp.
 #include "esa_band.hpp"
 
 namespace esa {
@@ -36,11 +36,7 @@ namespace esa {
 // dK/dV kernel, which then runs after it; block 0 also clears the split
 // arrival counters.  Used when both halves are band kernels, so no separate
 // pass re-reads O and dO.
-// WIN: interpolation weight 0 (layer 0, a sliding window): row i attends
-// the keys max(0, i - w + 1) .. i, so the group's keys come in 16-key
-// chunks (two per MFMA k-step, about three pairs at w = 64) and every key of
-// a row's window is kept, instead of 64 bands of one key per row.
-template <int D, bool VSKIP, bool PREP, Elem E, bool WIN = false>
+template <int D, bool VSKIP, bool PREP, Elem E>
 __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* lse2) {
   using M = MmaT<E>;
   using V8 = typename M::v8;
@@ -164,8 +160,7 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
   // XCD (launch_band_dq picks the rate)
   // (unsigned: the product wraps for grids near 2^31 blocks; only the value
   // mod 64 matters)
-  if constexpr (!WIN)
-    band_rows(A.pc, h, i, row_ok, q, n,
+  band_rows(A.pc, h, i, row_ok, q, n,
               (int)(((unsigned)(bid >> 3) * (unsigned)A.rot_dq / 64u) & 63u), kd, info1);
 
   const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
@@ -289,70 +284,6 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
     }
   };
 
-  if constexpr (WIN) {
-    // ---- the window's 16-key chunks [k0 + 16 c, ..), two per pair: per
-    // pair, both chunks' K and V are waited for together, read, and the next
-    // pair's requested (every wait is vmcnt(0))
-    const int w = A.pc.w;
-    const int r0 = gq * 16;
-    const int k0 = max(r0 - w + 1, 0), k1 = min(r0 + 16, A.q_len);
-    const int n_pairs = (k1 - k0 + 31) / 32;
-    // this lane's row window as offsets from k0 (none past q_len)
-    const int lo_k = row_ok ? max(i - w + 1, 0) - k0 : 1;
-    const int hi_k = row_ok ? i - k0 : 0;
-    auto desc = [&](int c) {
-      const int c0 = k0 + 16 * c;
-      const int rows = max(min(k1 - c0, 16), 0);
-      return rows > 0 ? (c0 | (rows << 24)) : 0;
-    };
-    // dS of this lane's 4 keys kb0 .. kb0 + 3 (offsets from k0) for its row
-    // as 16-bit values at their register slots; 0 outside the row's window
-    auto win_words = [&](const f32x4& sacc, const f32x4& pacc, int kb0) -> uint64_t {
-      uint64_t wv = 0ull;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool in = kb0 + e >= lo_k && kb0 + e <= hi_k;
-        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[e], scale2, -l2));
-        const uint64_t bits = (uint64_t)(uint32_t)M::bits(p * (pacc[e] - dl));
-        wv |= in ? bits << (16 * e) : 0ull;
-      }
-      return wv;
-    };
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // the slot zeros are in LDS
-    load_k(desc(0), lk0);
-    load_k(desc(1), lk1);
-    load_v(desc(0), lv0);
-    load_v(desc(1), lv1);
-    for (int p = 0; p < n_pairs; ++p) {
-      __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this pair's K and V are in LDS
-      f32x4 sa, sb;
-      s16x4 ta[C::NV], tb[C::NV];
-      V8 va[C::NS], vb[C::NS];
-      {
-        V8 ka[C::NS], kb[C::NS];
-        read_rows(ks0, ka);
-        read_rows(ks1, kb);
-        sa = product(ka, qop);
-        sb = product(kb, qop);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      read_tr(ks0, ta);
-      read_tr(ks1, tb);
-      read_rows(vs0, va);
-      read_rows(vs1, vb);
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // slots read: refill them
-      if (p + 1 < n_pairs) {
-        load_k(desc(2 * p + 2), lk0);
-        load_k(desc(2 * p + 3), lk1);
-        load_v(desc(2 * p + 2), lv0);
-        load_v(desc(2 * p + 3), lv1);
-      }
-      const f32x4 pa = product(va, dop);
-      const f32x4 pb = product(vb, dop);
-      dq_step(ta, tb, win_words(sa, pa, 32 * p + 4 * q), win_words(sb, pb, 32 * p + 16 + 4 * q));
-    }
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  } else {
   // ---- band pairs: per pair, K reads, then K of the next pair; V reads,
   // then V of the next pair.  So before the V wait exactly the next pair's K
   // DMAs may be newer, and before the K wait this pair's V DMAs (2 VLOADS of
@@ -465,8 +396,6 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
     }
   }
 
-  }
-
   // ---- the group's non-finite flag (staged K rows a row does not list meet
   // dS = 0 in dQ^T, and 0 * Inf is NaN: bwd_fix_kernel recomputes such a
   // group exactly)
@@ -486,6 +415,302 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
         ov[4 + e] = (typename M::s)(dqacc[2 * t + 1][e] * A.sm_scale);
       }
       *(V8*)(dqr + C::CW * q + 8 * t) = ov;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Window dQ over 32-row groups (interpolation weight 0, layer 0): one wave
+// per (batch, head, 32-row group [r0, r0 + 32)), two 16-row halves u that
+// share every staged pair.  The group's keys [max(r0 - w + 1, 0),
+// min(r0 + 32, q_len)) go through the slots in 16-key chunks, two per pair
+// (four pairs at w = 64 for 32 rows, against three for each 16-row group
+// walked alone), so each row waits for about half as many pairs.  Same box,
+// layer-0 backward against 16-row groups: B=1 H=32 L=32768 0.805 -> 0.768
+// ms, B=1 H=8 L=131072 -4%, B=8 H=16 L=4096 D=64 -5% (the pair order below
+// 0.8-1.8% of that).  Per
+// pair: S^T = K Q^T and dP^T = V dO^T for each half, dS at the keys of each
+// row's window, dQ^T += K^T dS^T.  The group's pair p is the next group's
+// pair p - 1, so each group starts at pair (-group) mod n_pairs and wraps
+// around: the groups sharing a pair load it at the same step.  Each half
+// writes the flag byte and delta / lse2 (PREP) of its 16-row group as
+// band_dq_kernel does, so bwd_fix_kernel and the dK / dV kernel read the
+// same workspace.
+template <int D, bool PREP, Elem E>
+__global__ __launch_bounds__(64, 2) void window_dq_kernel(BwdArgs A, const float* lse2) {
+  using M = MmaT<E>;
+  using V8 = typename M::v8;
+  using C = BandCfg<D>;
+  constexpr int G = 2;
+  if (PREP && A.split_parts > 1 && blockIdx.x == 0)
+    for (int t = threadIdx.x; t < A.n_bkv * A.split_blocks; t += 64) A.part_cnt[t] = 0;
+  __shared__ __attribute__((aligned(1024))) uint16_t ks0[C::SLOT];
+  __shared__ __attribute__((aligned(1024))) uint16_t ks1[C::SLOT];
+  __shared__ __attribute__((aligned(1024))) uint16_t vs0[C::SLOT];
+  __shared__ __attribute__((aligned(1024))) uint16_t vs1[C::SLOT];
+  uint16_t* const slot[4] = {ks0, ks1, vs0, vs1};
+
+  // ---- group: XCD x takes the contiguous range [x per, (x + 1) per)
+  const int ng2 = (A.q_len + 16 * G - 1) / (16 * G);
+  const int n2 = A.B * A.H * ng2;
+  const int per2 = (n2 + 7) / 8;
+  const int bid = blockIdx.x;
+  const int g = (bid & 7) * per2 + (bid >> 3);
+  if (g >= n2) return;
+  const int bh = g / ng2, gq = g % ng2;
+  const int h = bh % A.H, b = bh / A.H;
+  const int kvh = h / A.groups;
+
+  const int lane = threadIdx.x;
+  const int n = lane & 15, q = lane >> 4;
+  const int r0 = gq * 16 * G;
+
+  {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int c = 0; c < C::SLOT / 512; ++c) *(u32x4*)(slot[s] + (c * 64 + lane) * 8) = z;
+  }
+
+  // Q and dO of row 16 u + n as B operands: dims 32 s + 8 q .. + 8
+  V8 qop[G][C::NS], dop[G][C::NS];
+  float l2[G], dl[G];
+#pragma unroll
+  for (int u = 0; u < G; ++u) {
+    const int i = r0 + 16 * u + n;
+    const bool row_ok = i < A.q_len;
+    const uint16_t* qr = A.q + (int64_t)b * A.qsb + (int64_t)h * A.qsh + (int64_t)i * A.qss;
+    const uint16_t* dr =
+        A.dout + (int64_t)b * A.dosb + (int64_t)h * A.dosh + (int64_t)i * A.doss;
+#pragma unroll
+    for (int s = 0; s < C::NS; ++s) {
+      u32x4 qraw = {0u, 0u, 0u, 0u}, draw = {0u, 0u, 0u, 0u};
+      if (row_ok) {
+        qraw = *(const u32x4*)(qr + 32 * s + 8 * q);
+        draw = *(const u32x4*)(dr + 32 * s + 8 * q);
+      }
+      qop[u][s] = __builtin_bit_cast(V8, qraw);
+      dop[u][s] = __builtin_bit_cast(V8, draw);
+    }
+    l2[u] = 0.f;
+    dl[u] = 0.f;
+    if constexpr (PREP) {
+      // rowsum(dO * O) in prep_kernel's order (as band_dq_kernel forms it)
+      float hs[C::NS][2];
+      {
+        u32x4 raw[C::NS];
+        const uint16_t* orow =
+            A.o + (int64_t)b * A.osb + (int64_t)h * A.osh + (int64_t)i * A.oss;
+#pragma unroll
+        for (int s = 0; s < C::NS; ++s) {
+          raw[s] = u32x4{0u, 0u, 0u, 0u};
+          if (row_ok) raw[s] = *(const u32x4*)(orow + 32 * s + 8 * q);
+        }
+        constexpr int PER = D / 16;
+#pragma unroll
+        for (int s = 0; s < C::NS; ++s)
+#pragma unroll
+          for (int k = 0; k < 8 / PER; ++k) {
+            float acc = 0.f;
+#pragma unroll
+            for (int e = PER * k; e < PER * k + PER; ++e) {
+              const uint32_t w = raw[s][e / 2];
+              const float ov = M::val((e & 1) ? (w >> 16) : (w & 0xffffu));
+              acc += ov * (float)dop[u][s][e];
+            }
+            hs[s][k] = acc;
+          }
+      }
+      if constexpr (D == 128) {
+        float t = (hs[0][0] + hs[2][0]) + (hs[1][0] + hs[3][0]);
+        t += __shfl_xor(t, 32, 64);
+        t += __shfl_xor(t, 16, 64);
+        dl[u] = t;
+      } else {
+        float t0 = hs[0][0] + hs[1][0], t1 = hs[0][1] + hs[1][1];
+        t0 += __shfl_xor(t0, 32, 64);
+        t1 += __shfl_xor(t1, 32, 64);
+        t0 += __shfl_xor(t0, 16, 64);
+        t1 += __shfl_xor(t1, 16, 64);
+        dl[u] = t0 + t1;
+      }
+      if (row_ok) {
+        // kept finite: masked scores enter as -inf, and -inf - (-inf) would be NaN
+        l2[u] = fmaxf(A.lse[(int64_t)b * A.lsb + (int64_t)h * A.lsh + i] * 1.4426950408889634f,
+                      -3.0e38f);
+        if (q == 0) {
+          const int64_t at = ((int64_t)b * A.H + h) * A.qpad + i;
+          A.delta[at] = dl[u];
+          A.delta[(int64_t)A.B * A.H * A.qpad + at] = l2[u];
+        }
+      }
+    } else {
+      if (row_ok) {
+        const int64_t at = ((int64_t)b * A.H + h) * A.qpad + i;
+        l2[u] = lse2[at];
+        dl[u] = A.delta[at];
+      }
+    }
+  }
+
+  const char* const kbase = (const char*)(A.k + (int64_t)b * A.ksb + (int64_t)kvh * A.ksh);
+  const char* const vbase = (const char*)(A.v + (int64_t)b * A.vsb + (int64_t)kvh * A.vsh);
+  const int kss2 = (int)A.kss * 2, vss2 = (int)A.vss * 2;
+  lds_u16* const lk0 = (lds_u16*)ks0;
+  lds_u16* const lk1 = (lds_u16*)ks1;
+  lds_u16* const lv0 = (lds_u16*)vs0;
+  lds_u16* const lv1 = (lds_u16*)vs1;
+  int kofs[C::VLOADS], vofs[C::VLOADS];
+#pragma unroll
+  for (int t = 0; t < C::VLOADS; ++t) {
+    const int R = (64 * t + lane) / C::CPR, pc = lane % C::CPR;
+    kofs[t] = R * kss2 + 16 * kswz<D>(R, pc);
+    vofs[t] = R * vss2 + 16 * kswz<D>(R, pc);
+  }
+  const int w = A.pc.w;
+  const int k0 = max(r0 - w + 1, 0), k1 = min(r0 + 16 * G, A.q_len);
+  const int n_pairs = (k1 - k0 + 31) / 32;
+  // chunk c (keys k0 + 16 c ..) -> slot dst: only the DMAs that reach one of
+  // the group's keys (rows past k1 are not loaded; a slot's rows past them
+  // keep older contents, which meet dS = 0)
+  constexpr int RPI = 64 / C::CPR;
+  auto load_chunk = [&](const char* base, int ss2, const int* ofs, int c, lds_u16* dst) {
+    const int c0 = k0 + 16 * c;
+    const int rows = __builtin_amdgcn_readfirstlane(max(min(k1 - c0, 16), 0));
+    const int nl = (rows + RPI - 1) / RPI;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(base + (int64_t)min(c0, k1) * ss2), (short)0, rows * ss2, 0x00020000);
+#pragma unroll
+    for (int t = 0; t < C::VLOADS; ++t) {
+      if (t < nl)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(dst + 512 * t), 16, ofs[t], 0,
+                                                 0, 0);
+    }
+  };
+  int rrd[C::NS];
+#pragma unroll
+  for (int s = 0; s < C::NS; ++s) rrd[s] = n * C::ROWB + 16 * kswz<D>(n, 4 * s + q);
+  int trd[C::NV];
+#pragma unroll
+  for (int s = 0; s < C::NV; ++s) {
+    const int R = 4 * q + (n >> 2), dim0 = C::CW * (n & 3) + 4 * s;
+    trd[s] = R * C::ROWB + 16 * kswz<D>(R, dim0 >> 3) + 2 * (dim0 & 7);
+  }
+  auto read_rows = [&](const uint16_t* src, V8 (&op)[C::NS]) {
+#pragma unroll
+    for (int s = 0; s < C::NS; ++s) op[s] = *(const V8*)((const char*)src + rrd[s]);
+  };
+  auto read_tr = [&](const uint16_t* src, s16x4 (&op)[C::NV]) {
+#pragma unroll
+    for (int s = 0; s < C::NV; ++s)
+      op[s] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((const char*)src + trd[s]));
+  };
+  auto product = [&](const V8 (&a)[C::NS], const V8 (&bop)[C::NS]) {
+    f32x4 acc = M::mfma16(a[0], bop[0], f32x4{});
+#pragma unroll
+    for (int s = 1; s < C::NS; ++s) acc = M::mfma16(a[s], bop[s], acc);
+    return acc;
+  };
+  const float scale2 = A.scale_log2;
+  // row 16 u + n's window as offsets from k0 (none past q_len)
+  int lo_k[G], hi_k[G];
+#pragma unroll
+  for (int u = 0; u < G; ++u) {
+    const int i = r0 + 16 * u + n;
+    const bool ok = i < A.q_len;
+    lo_k[u] = ok ? max(i - w + 1, 0) - k0 : 1;
+    hi_k[u] = ok ? i - k0 : 0;
+  }
+  // dS of this lane's 4 keys kb0 .. kb0 + 3 (offsets from k0) for row
+  // 16 u + n as 16-bit values at their register slots; 0 outside its window
+  auto win_words = [&](int u, const f32x4& sacc, const f32x4& pacc, int kb0) -> uint64_t {
+    uint64_t wv = 0ull;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool in = kb0 + e >= lo_k[u] && kb0 + e <= hi_k[u];
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[e], scale2, -l2[u]));
+      const uint64_t bits = (uint64_t)(uint32_t)M::bits(p * (pacc[e] - dl[u]));
+      wv |= in ? bits << (16 * e) : 0ull;
+    }
+    return wv;
+  };
+  f32x4 dqacc[G][C::NV];
+#pragma unroll
+  for (int u = 0; u < G; ++u)
+#pragma unroll
+    for (int s = 0; s < C::NV; ++s) dqacc[u][s] = f32x4{};
+
+  const int pstart = (n_pairs - gq % n_pairs) % n_pairs;
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // the slot zeros are in LDS
+  load_chunk(kbase, kss2, kofs, 2 * pstart, lk0);
+  load_chunk(kbase, kss2, kofs, 2 * pstart + 1, lk1);
+  load_chunk(vbase, vss2, vofs, 2 * pstart, lv0);
+  load_chunk(vbase, vss2, vofs, 2 * pstart + 1, lv1);
+  for (int st = 0, p = pstart; st < n_pairs; ++st, p = p + 1 == n_pairs ? 0 : p + 1) {
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // this pair's K and V are in LDS
+    f32x4 sa[G], sb[G];
+    s16x4 ta[C::NV], tb[C::NV];
+    V8 va[C::NS], vb[C::NS];
+    {
+      V8 ka[C::NS], kb[C::NS];
+      read_rows(ks0, ka);
+      read_rows(ks1, kb);
+#pragma unroll
+      for (int u = 0; u < G; ++u) {
+        sa[u] = product(ka, qop[u]);
+        sb[u] = product(kb, qop[u]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    read_tr(ks0, ta);
+    read_tr(ks1, tb);
+    read_rows(vs0, va);
+    read_rows(vs1, vb);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // slots read: refill them
+    if (st + 1 < n_pairs) {
+      const int pn = p + 1 == n_pairs ? 0 : p + 1;
+      load_chunk(kbase, kss2, kofs, 2 * pn, lk0);
+      load_chunk(kbase, kss2, kofs, 2 * pn + 1, lk1);
+      load_chunk(vbase, vss2, vofs, 2 * pn, lv0);
+      load_chunk(vbase, vss2, vofs, 2 * pn + 1, lv1);
+    }
+    const int kb0 = 32 * p + 4 * q;
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const f32x4 pa = product(va, dop[u]);
+      const f32x4 pb = product(vb, dop[u]);
+      const uint64_t wa = win_words(u, sa[u], pa, kb0), wb = win_words(u, sb[u], pb, kb0 + 16);
+      const u32x4 sq = {(uint32_t)wa, (uint32_t)(wa >> 32), (uint32_t)wb, (uint32_t)(wb >> 32)};
+      const V8 sop = __builtin_bit_cast(V8, sq);
+#pragma unroll
+      for (int s = 0; s < C::NV; ++s) {
+        const s16x4 kk[2] = {ta[s], tb[s]};
+        dqacc[u][s] = M::mfma16(__builtin_bit_cast(V8, kk), sop, dqacc[u][s]);
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+
+#pragma unroll
+  for (int u = 0; u < G; ++u) {
+    // the 16-row group's non-finite flag (see band_dq_kernel)
+    const int g16 = 2 * gq + u;
+    const bool bad = wave_any(!sum_finite(dqacc[u]));
+    if (lane == 0 && g16 < A.ng) A.flags[(int64_t)bh * A.ng + g16] = bad ? 1 : 0;
+    const int i = r0 + 16 * u + n;
+    if (i < A.q_len) {
+      uint16_t* dqr = A.dq + (int64_t)b * A.dqsb + (int64_t)h * A.dqsh + (int64_t)i * A.dqss;
+#pragma unroll
+      for (int t = 0; t < C::NV / 2; ++t) {
+        V8 ov;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ov[e] = (typename M::s)(dqacc[u][2 * t][e] * A.sm_scale);
+          ov[4 + e] = (typename M::s)(dqacc[u][2 * t + 1][e] * A.sm_scale);
+        }
+        *(V8*)(dqr + C::CW * q + 8 * t) = ov;
+      }
     }
   }
 }
@@ -995,9 +1220,11 @@ template <int D, bool PREP, Elem E>
 static void launch_band_dq_d(const BwdArgs& a, dim3 grid, const float* lse2, hipStream_t stream) {
   // a sliding window at interpolation weight 0; K and V DMA skipping from
   // interpolation weight 1/2 on, as for the forward
-  if (a.pc.a == 0.0f)
-    band_dq_kernel<D, false, PREP, E, true><<<grid, 64, 0, stream>>>(a, lse2);
-  else if (a.pc.a >= 0.5f)
+  if (a.pc.a == 0.0f) {
+    // 32-row groups (window_dq_kernel), XCD-contiguous like the 16-row grid
+    const int64_t n2 = (int64_t)a.B * a.H * ((a.q_len + 31) / 32);
+    window_dq_kernel<D, PREP, E><<<dim3((unsigned)(8 * ((n2 + 7) / 8))), 64, 0, stream>>>(a, lse2);
+  } else if (a.pc.a >= 0.5f)
     band_dq_kernel<D, true, PREP, E><<<grid, 64, 0, stream>>>(a, lse2);
   else
     band_dq_kernel<D, false, PREP, E><<<grid, 64, 0, stream>>>(a, lse2);
