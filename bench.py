@@ -421,17 +421,19 @@ def band_bwd_executed_flops(torch, lay, B: int, H: int, Hkv: int, L: int, D: int
     2 D/32 for S, 2 D/32 for dP, D/16 each for dV^T and dK^T.  The pairs per
     (head, block) are counted from the pattern's index lists built on the
     GPU.  At layer 0 (interpolation weight 0, a sliding window) the kernels
-    walk the window directly: band_dq_kernel per group and pair of 16-key
-    chunks of keys [max(16 g - w + 1, 0), min(16 g + 16, L)), band_dkdv_kernel
-    per block, query head and 32-row step of rows [16 b, min(16 b + 15 + w,
-    L)), with the same MFMAs per pair and step."""
+    walk the window directly: window_dq_kernel per 32-row group and pair of
+    16-key chunks of keys [max(32 g - w + 1, 0), min(32 g + 32, L)), the
+    MFMAs of a pair for each of the group's two 16-row halves;
+    band_dkdv_kernel per block, query head and 32-row step of rows
+    [16 b, min(16 b + 15 + w, L)), with the same MFMAs per step."""
     from elastic_sparse_attention import build_indices
     dq_unit = (4 * (D // 32) + D // 16) * 16384
     dkdv_unit = (4 * (D // 32) + 2 * (D // 16)) * 16384
     if lay.pattern.layer_idx == 0:
         pairs = steps = 0
+        for g in range((L + 31) // 32):
+            pairs += 2 * ((min(32 * g + 32, L) - max(32 * g - w + 1, 0) + 31) // 32)
         for g in range((L + 15) // 16):
-            pairs += (min(16 * g + 16, L) - max(16 * g - w + 1, 0) + 31) // 32
             steps += (min(16 * g + 15 + w, L) - 16 * g + 31) // 32
         return {"dq": float(B * H * pairs * dq_unit), "dkdv": float(B * H * steps * dkdv_unit)}
     pairs = 0

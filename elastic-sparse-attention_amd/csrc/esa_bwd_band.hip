@@ -424,8 +424,9 @@ __global__ __launch_bounds__(64, 2) void band_dq_kernel(BwdArgs A, const float* 
 // per (batch, head, 32-row group [r0, r0 + 32)), two 16-row halves u that
 // share every staged pair.  The group's keys [max(r0 - w + 1, 0),
 // min(r0 + 32, q_len)) go through the slots in 16-key chunks, two per pair
-// (four pairs at w = 64 for 32 rows, against three for each 16-row group
-// walked alone), so each row waits for about half as many pairs.  Same box,
+// (three pairs, 95 keys, at w = 64 for 32 rows, against three, 79 keys,
+// for each 16-row group walked alone), so each row waits for half as many
+// pairs for the same MFMAs.  Same box,
 // layer-0 backward against 16-row groups: B=1 H=32 L=32768 0.805 -> 0.768
 // ms, B=1 H=8 L=131072 -4%, B=8 H=16 L=4096 D=64 -5% (the pair order below
 // 0.8-1.8% of that).  Per
