@@ -25,8 +25,8 @@ hand-written gfx950 HIP kernels:
   128 or 256);
 * chunked prefill (``cache_position`` of at least 32 rows), bf16 or fp16:
   the band (or window) kernel at those positions, except at a dilated layer
-  for calls of at most 4096 (batch, head, row) units, where the per-row
-  gather is faster;
+  for calls of at most 4096 · 128 / head_dim (batch, head, row) units, where
+  the per-row gather is faster;
 * decode (fewer ``cache_position`` rows), float32, or other head dims: the
   per-row gather kernel that regenerates each row's elastic indices on the
   device.
@@ -497,14 +497,18 @@ BWD_DKDV_CROSSOVER = {128: 16.5, 64: 17.0}
 # gather kernel
 BAND_POSITION_MIN_ROWS = 32
 # ... except at a dilated layer when the call has at most this many (batch,
-# head, row) units: a grid under one round of resident waves takes the band
-# kernel one group's whole 64-band walk (about 28 us at D = 128), while the
-# per-row gather costs about 5 us plus 4.5 us per 1024 units.  Same box, the
-# last rows of L=32768 H=32 D=128 at layers 4 and 7: B=1, 32 / 64 / 128 rows,
-# gather 9.5 / 14 / 24 us against band 29 / 29 / 29; 256 rows 41 against 36;
-# B=4, 32 rows 24 against 29, 64 rows 43 against 44, 128 rows 83 against 69.
-# At layer 0 the band entry point runs the window kernel, 10 us from 32 rows
-# on, faster than the gather at every size but B=1 with 32 rows (9 us).
+# head, row) units at head_dim 128 (scaled by 128 / head_dim: the gather's
+# cost per unit follows the row bytes): a grid under one round of resident
+# waves takes the band kernel one group's whole 64-band walk (about 28 us at
+# D = 128, 21 us at D = 64), while the per-row gather costs about 5 us plus
+# 4.5 us per 1024 units at D = 128.  Same box, the last rows of L=32768 at
+# layers 4 and 7, gather against band: H=32 D=128, B=1, 32 / 64 / 128 rows
+# 9.5 / 14 / 24 us against 29 / 29 / 29, 256 rows 41 against 36; B=4, 32
+# rows 24 against 29, 64 rows 43 against 44, 128 rows 83 against 69.  H=16
+# D=64, B=1, 512 rows (8192 units) 19-21 against 23-24 us, 1024 rows 30-32
+# against 25; B=4, 128 rows 19-22 against 23-24, 256 rows 31-36 against
+# 29-35.  At layer 0 the band entry point runs the window kernel, 10 us from
+# 32 rows on, faster than the gather at every size but B=1 with 32 rows.
 BAND_POSITION_MIN_UNITS = 4096
 
 
@@ -1341,7 +1345,7 @@ class ElasticSparseAttention(nn.Module):
             return o.view(B, Lq, H * D), None                              # :761-763
         if pos is not None and not naive and dropout_p == 0.0 and band_ok \
                 and Lq >= BAND_POSITION_MIN_ROWS \
-                and (self.layer_idx == 0 or B * H * Lq > BAND_POSITION_MIN_UNITS):
+                and (self.layer_idx == 0 or B * H * Lq * D > BAND_POSITION_MIN_UNITS * 128):
             # a chunked prefill: the band kernel at the given positions
             if grad:
                 o = _ElasticBandRowsAttention.apply(q, k, v, self.pattern, self.scaling, pos)

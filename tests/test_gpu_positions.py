@@ -135,12 +135,12 @@ def test_out_of_range_positions_give_nan_rows():
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_module_chunked_prefill(dtype):
     """ElasticSparseAttention.forward with a device cache_position of at least
-    BAND_POSITION_MIN_ROWS rows and more than BAND_POSITION_MIN_UNITS (batch,
-    head, row) units runs the band kernel; its output and its gradients (the
+    BAND_POSITION_MIN_ROWS rows and more than BAND_POSITION_MIN_UNITS * 128 /
+    head_dim (batch, head, row) units runs the band kernel; its output and its gradients (the
     gather backward at the same positions) match the oracle and torch
     autograd through it."""
     B, H, Hkv, L, D, layer, p0, Lq = 2, 8, 2, 1024, 128, 4, 333, 300
-    assert Lq >= BAND_POSITION_MIN_ROWS and B * H * Lq > BAND_POSITION_MIN_UNITS
+    assert Lq >= BAND_POSITION_MIN_ROWS and B * H * Lq * D > BAND_POSITION_MIN_UNITS * 128
     m = ElasticSparseAttention(layer, 8, H, D, 64, L, num_key_value_heads=Hkv)
     _, k, v = seeded_inputs(B, H, Hkv, L, D, dtype, seed=11, scale=1.0)
     q = seeded_inputs(B, H, Hkv, L, D, dtype, seed=12, scale=1.0, Lq=Lq)[0]
