@@ -1206,10 +1206,11 @@ hipError_t launch_band_dkdv(const BwdArgs& a, int head_dim, const float* lse2,
   // a few rounds whose heads' Q and dO rows exceed L2 (band_rotation).  Same
   // box, without against with: B=1 H=4 L=32768 D=128 (four rounds) backward
   // -4% at layer 4, -9% at layer 7, B=1 H=2 L=65536 -5.5%; at eight rounds
-  // (H=8) +1.4%, at 32 (H=32) +4.3%.
+  // (H=8) +1.4%, at 32 (H=32) +4.3%.  A few-round rate of 3/64 (the
+  // forward's) was 3-10% slower than none here.
   BwdArgs r = a;
   r.rot_dkdv = band_rotation(a.n_kblk, head_dim == 128 ? 256 : 384,
-                             (int64_t)a.q_len * 4 * head_dim, head_dim == 128 ? 19 : 12);
+                             (int64_t)a.q_len * 4 * head_dim, head_dim == 128 ? 19 : 12, 0);
   if (a.elem == (int)Elem::f16)
     launch_band_dkdv_elem<Elem::f16>(r, head_dim, grid, lse2, stream);
   else
@@ -1259,7 +1260,7 @@ hipError_t launch_band_dq(const BwdArgs& a, int head_dim, const float* lse2, boo
   // (band_rotation, measured with the dK / dV's in launch_band_dkdv)
   BwdArgs r = a;
   r.rot_dq = band_rotation(a.n_groups, head_dim == 128 ? 256 : 512,
-                           (int64_t)a.kv_len * 4 * head_dim, head_dim == 128 ? 19 : 12);
+                           (int64_t)a.kv_len * 4 * head_dim, head_dim == 128 ? 19 : 12, 0);
   if (a.elem == (int)Elem::f16)
     launch_band_dq_elem<Elem::f16>(r, head_dim, grid, lse2, prep, stream);
   else

@@ -668,18 +668,21 @@ hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) 
   // same rate spreads a round's groups over all 64 entries, so an XCD's L2
   // must hold the keys of every entry of the resident rows.  Where a head's
   // K and V (4 head_dim bytes per key) exceed the 4 MB L2, a grid of up to
-  // four rounds therefore starts every group at entry 0.  Same box,
-  // rotation against none: the last 1024 / 2048 / 4096 rows of B=1 H=32
-  // L=32768 D=128 layer 4 as a chunk (0.8 / 1.6 / 3.2 rounds) 0.108 ->
-  // 0.066, 0.179 -> 0.106, 0.271 -> 0.197 ms, layer 7 -7% / -30%, the last
-  // 16384 rows of B=1 H=8 L=131072 -31% at layer 4 (+3% at layer 7); at 6.4
-  // rounds within +-3%, at 12.8 the rotation 1-9% faster, at 25.6 (the full
-  // L=32768 prefill) 9%.  At L=8192 (4 MB of K and V per head) none was
-  // 1-4% slower at 0.8-3.6 rounds.
+  // four rounds therefore rotates by 3/64 only.  Same box, rotation against
+  // none: the last 1024 / 2048 / 4096 rows of B=1 H=32 L=32768 D=128 layer
+  // 4 as a chunk (0.8 / 1.6 / 3.2 rounds) 0.108 -> 0.066, 0.179 -> 0.106,
+  // 0.271 -> 0.197 ms, layer 7 -7% / -30%, the last 16384 rows of B=1 H=8
+  // L=131072 -31% at layer 4 (+3% at layer 7); at 6.4 rounds within +-3%,
+  // at 12.8 the rotation 1-9% faster, at 25.6 (the full L=32768 prefill) 9%.
+  // At L=8192 (4 MB of K and V per head) none was 1-4% slower at 0.8-3.6
+  // rounds.  3/64 against none, same box: the 3.2-round chunks above -2.6%
+  // (layer 4) and -5% (layer 7), the L=131072 chunk -9% at layers 4 and 7,
+  // B=1 H=2 L=65536 prefill -10%; 0.8-round chunks +1-2%; 2/64 and 4/64
+  // each worse at some of these.
   const int dk = head_dim > 128 ? 256 : head_dim > 64 ? 128 : 64;
   BandArgs r = a;
   r.rot_rate = band_rotation(a.n_groups, 40960 / dk, (int64_t)a.kv_len * 4 * a.d_real,
-                             dk == 128 ? 15 : 9);
+                             dk == 128 ? 15 : 9, 3);
   // K DMA skipping: with the late V order from interpolation weight 1/2 on
   // (measured at B=1, H=32, L=32768, D=128, w=64 over 8 layers: 1-7% faster
   // at weights 4/7 .. 1, even at 3/7, 3-4% slower at 1/7 and 2/7, where

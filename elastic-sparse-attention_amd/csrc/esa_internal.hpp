@@ -227,9 +227,12 @@ struct BwdArgs {
 // waves per XCD), keeps the resident units on neighbouring entries, whose
 // rows share L2.  A grid of up to four rounds starts each round nearly at
 // once, where the same rate spreads a round over all 64 entries: when a
-// head's gathered rows exceed an XCD's 4 MB L2 every unit starts at entry 0.
-inline int band_rotation(int64_t units, int64_t resident_per_xcd, int64_t head_bytes, int rate) {
-  return units <= 4 * 8 * resident_per_xcd && head_bytes > (int64_t(4) << 20) ? 0 : rate;
+// head's gathered rows exceed an XCD's 4 MB L2 such a grid takes `few`
+// instead (0, or a small rate that the waves' drift over a few rounds
+// favours).
+inline int band_rotation(int64_t units, int64_t resident_per_xcd, int64_t head_bytes, int rate,
+                         int few) {
+  return units <= 4 * 8 * resident_per_xcd && head_bytes > (int64_t(4) << 20) ? few : rate;
 }
 
 hipError_t launch_indices(const PatternConsts& pc, int row0, int nrows, void* indices, void* mask,
