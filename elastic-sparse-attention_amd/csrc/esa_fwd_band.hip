@@ -681,8 +681,15 @@ hipError_t launch_band_fwd(const BandArgs& a, int head_dim, hipStream_t stream) 
   // each worse at some of these.
   const int dk = head_dim > 128 ? 256 : head_dim > 64 ? 128 : 64;
   BandArgs r = a;
+  // Chunks (positions) from interpolation weight 1/2 on keep 3/64 up to
+  // eight rounds: their rows all have wide windows, and the late 6144- and
+  // 8192-row chunks of L=32768 (4.8 and 6.4 rounds) ran 13-33% faster at
+  // layers 4 and 7, the late 32768-row chunks of L=131072 6-34%, early
+  // chunks (position 0) within 1%; full prefills at 6.4 rounds up to 15%
+  // slower, and late chunks at layer 2 of L=131072 18-36% slower.
+  const int max_rounds = a.positions && a.pc.a >= 0.5f ? 8 : 4;
   r.rot_rate = band_rotation(a.n_groups, 40960 / dk, (int64_t)a.kv_len * 4 * a.d_real,
-                             dk == 128 ? 15 : 9, 3);
+                             dk == 128 ? 15 : 9, 3, max_rounds);
   // K DMA skipping: with the late V order from interpolation weight 1/2 on
   // (measured at B=1, H=32, L=32768, D=128, w=64 over 8 layers: 1-7% faster
   // at weights 4/7 .. 1, even at 3/7, 3-4% slower at 1/7 and 2/7, where

@@ -227,12 +227,13 @@ struct BwdArgs {
 // waves per XCD), keeps the resident units on neighbouring entries, whose
 // rows share L2.  A grid of up to four rounds starts each round nearly at
 // once, where the same rate spreads a round over all 64 entries: when a
-// head's gathered rows exceed an XCD's 4 MB L2 such a grid takes `few`
-// instead (0, or a small rate that the waves' drift over a few rounds
-// favours).
+// head's gathered rows exceed an XCD's 4 MB L2 such a grid (up to
+// max_rounds) takes `few` instead (0, or a small rate that the waves' drift
+// over a few rounds favours).
 inline int band_rotation(int64_t units, int64_t resident_per_xcd, int64_t head_bytes, int rate,
-                         int few) {
-  return units <= 4 * 8 * resident_per_xcd && head_bytes > (int64_t(4) << 20) ? few : rate;
+                         int few, int max_rounds = 4) {
+  return units <= max_rounds * 8 * resident_per_xcd && head_bytes > (int64_t(4) << 20) ? few
+                                                                                     : rate;
 }
 
 hipError_t launch_indices(const PatternConsts& pc, int row0, int nrows, void* indices, void* mask,
