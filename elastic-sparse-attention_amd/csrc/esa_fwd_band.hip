@@ -65,18 +65,30 @@ namespace esa {
 // not a multiple of 16); any other group computes its rows one at a time
 // with the per-row gather (gather_one_row_any: float32, the arithmetic of
 // esa_elastic_fwd_rows).  Q, O and the log-sum-exp stay indexed by the row r.
-template <int D, bool KSKIP, bool VEARLY, Elem E, bool POS>
-__global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
+// S: waves per group (S = 2 for grids that fit one round of resident
+// workgroups, whose time is one group's whole walk): wave w walks the slots of
+// lane groups 4 w / S .. 4 (w + 1) / S - 1 with slots of its own, and wave 0
+// merges the other wave's softmax state (handed over through that wave's
+// slots across one barrier) before the epilogue.
+template <int D, bool KSKIP, bool VEARLY, Elem E, bool POS, int S = 1>
+__global__ __launch_bounds__(64 * S, 2) void band_fwd_kernel(BandArgs A) {
   using C = BandCfg<D>;
   using M = MmaT<E>;
   using V8 = typename M::v8;
+  static_assert(S == 1 || S == 2, "one or two waves per group");
   // K and V slots of the pair's two bands (separate objects, so the compiler
-  // can tell reads of one slot from the direct loads into another)
-  __shared__ __attribute__((aligned(1024))) uint16_t ks0[C::SLOT];
-  __shared__ __attribute__((aligned(1024))) uint16_t ks1[C::SLOT];
-  __shared__ __attribute__((aligned(1024))) uint16_t vs0[C::SLOT];
-  __shared__ __attribute__((aligned(1024))) uint16_t vs1[C::SLOT];
+  // can tell reads of one slot from the direct loads into another), S sets
+  __shared__ __attribute__((aligned(1024))) uint16_t ks0_[C::SLOT * S];
+  __shared__ __attribute__((aligned(1024))) uint16_t ks1_[C::SLOT * S];
+  __shared__ __attribute__((aligned(1024))) uint16_t vs0_[C::SLOT * S];
+  __shared__ __attribute__((aligned(1024))) uint16_t vs1_[C::SLOT * S];
+  const int wv = S > 1 ? __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)) : 0;
+  uint16_t* const ks0 = ks0_ + wv * C::SLOT;
+  uint16_t* const ks1 = ks1_ + wv * C::SLOT;
+  uint16_t* const vs0 = vs0_ + wv * C::SLOT;
+  uint16_t* const vs1 = vs1_ + wv * C::SLOT;
   uint16_t* const slot[4] = {ks0, ks1, vs0, vs1};
+  const int q0 = wv * (4 / S);  // this wave's first lane group of slots
 
   // ---- group: XCD x takes the contiguous range [x per, (x + 1) per)
   const int bid = blockIdx.x;
@@ -86,7 +98,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   const int h = bh % A.H, b = bh / A.H;
   const int kvh = h / A.groups;
 
-  const int lane = threadIdx.x;
+  const int lane = S > 1 ? (int)(threadIdx.x & 63) : (int)threadIdx.x;
   const int n = lane & 15, q = lane >> 4;
   const int r = gq * 16 + n;  // this lane's query row (of q, o and lse)
   const bool row_ok = r < A.q_len;
@@ -116,6 +128,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
       G.elem = A.elem;
       G.src.w = A.pc.w; G.src.kv_len = A.kv_len; G.src.pc = A.pc;
       G.src.positions = A.positions;
+      if (S > 1 && wv != 0) return;  // (every wave of the group takes this branch)
       for (int rr = 0; rr < 16 && gq * 16 + rr < A.q_len; ++rr)
         gather_one_row_any<E, true>(G, b, h, gq * 16 + rr, (float*)ks0, lane);
       return;
@@ -399,16 +412,16 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     constexpr int kWaitLds = 0xC07F;                           // lgkmcnt(0)
     const int lane_key = 4 * n;  // ds_bpermute byte address of row n in group 0
     {
-      const int i0 = __builtin_amdgcn_readlane(info1, 0);
-      const int i1 = __builtin_amdgcn_readlane(info1, 1);
+      const int i0 = __builtin_amdgcn_readlane(info1, 16 * q0);
+      const int i1 = __builtin_amdgcn_readlane(info1, 16 * q0 + 1);
       __builtin_amdgcn_s_waitcnt(kWaitLds);  // the slot zeros are in LDS
       load_k(i0, lk0);
       load_k(i1, lk1);
       load_v(i0, lv0);
       load_v(i1, lv1);
     }
-    for (int qj = 0; qj < 4; ++qj) {
-      const bool more = qj < 3;
+    for (int qj = q0; qj < q0 + 4 / S; ++qj) {
+      const bool more = qj < q0 + 4 / S - 1;
   #pragma unroll
       for (int rp = 0; rp < 8; ++rp) {
         const int ra = 2 * rp, rb = 2 * rp + 1;
@@ -502,7 +515,7 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
     // ---- tail: keys of bands wider than 16, one 16-key chunk at a time
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     const bool wide = wave_any(((uint32_t)info1 >> 24) > 16u);  // some slot's band
-    for (int j = 0; j < 64 && wide; ++j) {
+    for (int j = 16 * q0; j < 16 * (q0 + 4 / S) && wide; ++j) {
       const int qj = j >> 4, r = j & 15;
       const int bi = __builtin_amdgcn_readlane(info1, j);  // slot (qj, r)
       // (the words as opaque values first: selects between loads of kd would
@@ -546,7 +559,10 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   // runs again with the V operands sanitised: rows whose entries bring no
   // non-finite value then get exactly the bits a run without it gives, and
   // the reference's non-finite values go back in below.
-  const bool rerun = wave_any(!sum_finite(oacc));
+  // (with S waves each decides for its own bands: a wave whose sums are
+  // finite met no non-finite value, and its sanitised run would give the
+  // same bits)
+  bool rerun = wave_any(!sum_finite(oacc));
   if (rerun) {
     m_run = -INFINITY;
     l_run = 0.f;
@@ -554,6 +570,38 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
 #pragma unroll
     for (int s = 0; s < C::NV; ++s) oacc[s] = f32x4{};
     run_bands(std::integral_constant<bool, true>{});
+  }
+  if constexpr (S > 1) {
+    // wave 1 hands its state to wave 0 through its own slots: O^T slices
+    // (64 lanes x 16 bytes each, SLOT / 512 per slot) in ks0 and ks1, and
+    // (m, l, n, rerun) per lane in vs0
+    constexpr int SPS = C::SLOT / 512;
+    static_assert(C::NV <= 2 * SPS, "two slots hold the O^T slices");
+    f32x4* const ox0 = (f32x4*)(ks0_ + C::SLOT);
+    f32x4* const ox1 = (f32x4*)(ks1_ + C::SLOT);
+    f32x4* const sx = (f32x4*)(vs0_ + C::SLOT);
+    if (wv == 1) {
+      __builtin_amdgcn_s_waitcnt(0);  // its DMAs into these slots have landed
+#pragma unroll
+      for (int s = 0; s < C::NV; ++s) (s < SPS ? ox0 : ox1)[(s % SPS) * 64 + lane] = oacc[s];
+      sx[lane] = f32x4{m_run, l_run, n_run, rerun ? 1.f : 0.f};
+    }
+    __syncthreads();
+    if (wv == 1) return;
+    const f32x4 st = sx[lane];
+    const float m = fmaxf(m_run, st[0]);
+    const float a0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m);
+    const float a1 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(st[0] - m);
+    l_run = l_run * a0 + st[1] * a1;
+    n_run = n_run * a0 + st[2] * a1;
+#pragma unroll
+    for (int s = 0; s < C::NV; ++s) {
+      const f32x4 o1 = (s < SPS ? ox0 : ox1)[(s % SPS) * 64 + lane];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) oacc[s][e] = oacc[s][e] * a0 + o1[e] * a1;
+    }
+    m_run = m;
+    rerun = rerun || st[3] != 0.f;
   }
 
   // ---- epilogue: lane (n, q) holds O^T[dim][row n] for dims CW q .. CW q + CW
@@ -593,19 +641,31 @@ __global__ __launch_bounds__(64, 2) void band_fwd_kernel(BandArgs A) {
   }
 }
 
-template <int D, Elem E, bool POS>
-void launch_band_d(const BandArgs& a, dim3 grid, bool kskip, bool vearly, hipStream_t stream) {
+template <int D, Elem E, bool POS, int S>
+void launch_band_ds(const BandArgs& a, dim3 grid, bool kskip, bool vearly, hipStream_t stream) {
   if (kskip) {
     if (vearly)
-      band_fwd_kernel<D, true, true, E, POS><<<grid, 64, 0, stream>>>(a);
+      band_fwd_kernel<D, true, true, E, POS, S><<<grid, 64 * S, 0, stream>>>(a);
     else
-      band_fwd_kernel<D, true, false, E, POS><<<grid, 64, 0, stream>>>(a);
+      band_fwd_kernel<D, true, false, E, POS, S><<<grid, 64 * S, 0, stream>>>(a);
   } else {
     if (vearly)
-      band_fwd_kernel<D, false, true, E, POS><<<grid, 64, 0, stream>>>(a);
+      band_fwd_kernel<D, false, true, E, POS, S><<<grid, 64 * S, 0, stream>>>(a);
     else
-      band_fwd_kernel<D, false, false, E, POS><<<grid, 64, 0, stream>>>(a);
+      band_fwd_kernel<D, false, false, E, POS, S><<<grid, 64 * S, 0, stream>>>(a);
   }
+}
+
+// Two waves per group where the whole grid fits one round of two-wave
+// workgroups (n_groups at most 8 * 40960 / D / 2: 1280 at D = 128, 2560 at
+// D = 64), so each group's walk over its 64 bands, the grid's whole time
+// there, is split in half
+template <int D, Elem E, bool POS>
+void launch_band_d(const BandArgs& a, dim3 grid, bool kskip, bool vearly, hipStream_t stream) {
+  if (a.n_groups <= 8 * (40960 / D) / 2)
+    launch_band_ds<D, E, POS, 2>(a, grid, kskip, vearly, stream);
+  else
+    launch_band_ds<D, E, POS, 1>(a, grid, kskip, vearly, stream);
 }
 
 // D = 256 runs only the late V order: the early one holds both bands' K and

@@ -25,7 +25,7 @@ hand-written gfx950 HIP kernels:
   128 or 256);
 * chunked prefill (``cache_position`` of at least 32 rows), bf16 or fp16:
   the band (or window) kernel at those positions, except at a dilated layer
-  for calls of at most 4096 · 128 / head_dim (batch, head, row) units, where
+  for calls of at most 3072 · 128 / head_dim (batch, head, row) units, where
   the per-row gather is faster;
 * decode (fewer ``cache_position`` rows), float32, or other head dims: the
   per-row gather kernel that regenerates each row's elastic indices on the
@@ -498,18 +498,18 @@ BWD_DKDV_CROSSOVER = {128: 16.5, 64: 17.0}
 BAND_POSITION_MIN_ROWS = 32
 # ... except at a dilated layer when the call has at most this many (batch,
 # head, row) units at head_dim 128 (scaled by 128 / head_dim: the gather's
-# cost per unit follows the row bytes): a grid under one round of resident
-# waves takes the band kernel one group's whole 64-band walk (about 28 us at
-# D = 128, 21 us at D = 64), while the per-row gather costs about 5 us plus
-# 4.5 us per 1024 units at D = 128.  Same box, the last rows of L=32768 at
-# layers 4 and 7, gather against band: H=32 D=128, B=1, 32 / 64 / 128 rows
-# 9.5 / 14 / 24 us against 29 / 29 / 29, 256 rows 41 against 36; B=4, 32
-# rows 24 against 29, 64 rows 43 against 44, 128 rows 83 against 69.  H=16
-# D=64, B=1, 512 rows (8192 units) 19-21 against 23-24 us, 1024 rows 30-32
-# against 25; B=4, 128 rows 19-22 against 23-24, 256 rows 31-36 against
-# 29-35.  At layer 0 the band entry point runs the window kernel, 10 us from
-# 32 rows on, faster than the gather at every size but B=1 with 32 rows.
-BAND_POSITION_MIN_UNITS = 4096
+# cost per unit follows the row bytes): a grid under one round takes the band
+# kernel one group's walk over its 64 bands (split over two waves there:
+# about 19 us at D = 128, 15 us at D = 64), while the per-row gather costs
+# about 5 us plus 4.5 us per 1024 units at D = 128.  Same box, the last rows
+# of L=32768 at layers 4 and 7, gather against band: H=32 D=128, B=1, 32 /
+# 64 / 96 / 128 rows 9 / 12-14 / 18-19 / 21-24 us against 19 / 19 / 19-20 /
+# 20-21; B=4, 32 rows 21-23 against 19-21.  H=16 D=64, B=1 up to 256 rows
+# 9-14 against 15-16; B=4, 96 rows (6144 units) 16-18 against 17-19, 128
+# rows 19-22 against 18-21.  At layer 0 the band entry point runs the window
+# kernel, 10 us from 32 rows on, faster than the gather at every size but
+# B=1 with 32 rows.
+BAND_POSITION_MIN_UNITS = 3072
 
 
 def band_head_dim(head_dim: int) -> bool:
